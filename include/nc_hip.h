@@ -1,0 +1,125 @@
+/* nc_hip.h: the C ABI of nanocompile_amd's HIP library (libnc_hip.so), gfx950.
+ *
+ * Kernel entry points keep the reference's generated-kernel calling
+ * convention (codegen_c.py:5-10, 254, 282-283):
+ *
+ *     int32_t nc_name(void **p, const int64_t *s);
+ *
+ * p[0] is the (first) output, p[1..] the operands, all DEVICE pointers to
+ * contiguous row-major arrays; s holds the sizes (the reference's s[] holds
+ * its graph symbols seq and past, runtime.py:255). A call only enqueues work
+ * on the library stream and returns 0, NC_BAD_ARGS (a shape or pointer the
+ * launcher rejects) or NC_LAUNCH_FAILED. A kernel that finds bad input at run
+ * time (the reference's loopir.Fail, loopir.py:280-285, used by gather with
+ * code 1, fusion.py:722) records its code in a device word that nc_sync()
+ * returns, which the Python runtime maps to KernelError as the reference's
+ * runtime.py:298-318 does. nc_last_error() explains the last non-zero code.
+ *
+ * Dtypes: i8 = int8_t, i32 = int32_t, f32 = float, i64 = int64_t.
+ */
+#ifndef NC_HIP_H
+#define NC_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NC_OK 0
+#define NC_FAIL_INDEX 1
+#define NC_BAD_ARGS 2
+#define NC_LAUNCH_FAILED 3
+
+/* -- runtime ------------------------------------------------------------------
+ * Replaces the reference's library loading and executor binding
+ * (runtime.py:62-83 pool loading, codegen_c.py:71-81 nc_bind_pool): one
+ * device, one stream, instead of one thread pool. */
+
+const char *nc_last_error(void);
+int32_t nc_device_count(void);
+/* Bind the library to a device and create its stream (runtime.py:200-203). */
+int32_t nc_init(int32_t device);
+int32_t nc_device_info(char *arch, int64_t arch_len, int64_t *compute_units, int64_t *lds_bytes,
+                       int64_t *hbm_bytes, int64_t *clock_khz);
+
+/* Device memory: the reference's one 64-byte-aligned arena (runtime.py:39,
+ * 239-243) becomes one hipMalloc arena the Python runtime carves up. */
+void *nc_malloc(int64_t bytes);
+int32_t nc_free(void *ptr);
+void *nc_host_malloc(int64_t bytes);       /* pinned host staging */
+int32_t nc_host_free(void *ptr);
+int32_t nc_memcpy_h2d(void *dst, const void *src, int64_t bytes);      /* waits */
+int32_t nc_memcpy_d2h(void *dst, const void *src, int64_t bytes);      /* waits */
+int32_t nc_memcpy_h2d_async(void *dst, const void *src, int64_t bytes);
+int32_t nc_memcpy_d2h_async(void *dst, const void *src, int64_t bytes);
+int32_t nc_memcpy_d2d(void *dst, const void *src, int64_t bytes);
+
+/* Wait for the stream; returns the first kernel failure code since the last
+ * call (clearing it), NC_LAUNCH_FAILED, or 0 (runtime.py:298-299). */
+int32_t nc_sync(void);
+void *nc_stream_handle(void);
+void *nc_error_word(void);
+
+/* Events on the library stream: the reference times kernels with a C loop
+ * around calls (autotune.py:89-122); here the GPU timestamps them. */
+void *nc_event_create(void);
+int32_t nc_event_record(void *event);
+int32_t nc_event_elapsed_ms(void *start, void *stop, float *ms);
+int32_t nc_event_destroy(void *event);
+
+/* Graph capture of the library stream: a decode step's launches recorded
+ * once and replayed (the reference's planned phase 7, docs/ROADMAP.md:209-228). */
+int32_t nc_capture_begin(void);
+int32_t nc_capture_end(void **graph_exec);
+int32_t nc_graph_launch(void *graph_exec);
+int32_t nc_graph_destroy(void *graph_exec);
+
+/* -- int8 quantizers ---------------------------------------------------------- */
+
+/* Per-row symmetric int8 weights (quantize.py:55-70, the reference's
+ * quantize_int8, done on the host there).
+ * p: [q i8[N,K], scales f32[N], w f32[N,K]];  s: [N, K] */
+int32_t nc_quantize_rows_i8(void **p, const int64_t *s);
+
+/* Per-token int8 activations: the reference's block quantizer
+ * (quantize.py:102-124) with one block spanning the row.
+ * p: [xq i8[M,K], xs f32[M], x f32[M,K]];  s: [M, K] */
+int32_t nc_quantize_token_i8(void **p, const int64_t *s);
+
+/* rms_norm (nn.py:34-38, one row kernel as fusion.py:631-650 makes it) fused
+ * with the per-token quantizer.
+ * p: [normed f32[M,K] or NULL, xq i8[M,K], xs f32[M], x f32[M,K], gamma f32[K]];
+ * s: [M, K, eps as the bits of a float32] */
+int32_t nc_rms_norm_quant(void **p, const int64_t *s);
+
+/* -- int8 projections --------------------------------------------------------- */
+
+/* matmul_i8_token: per-token int8 activations times per-row int8 weights,
+ * int32 accumulation, fp32 epilogue y = (f32(acc) * xs[m]) * scales[n],
+ * then + bias[n], then residual[m,n] + y. Extends the reference's int8
+ * matmuls (ir.py:392-439, lowered at lower.py:400-417 and fused with bias,
+ * residual and SwiGLU epilogues at fusion.py:677-711) with the per-token mode
+ * the reference lacks.
+ * p: [y f32[M,N], xq i8[M,K], xs f32[M], q i8[N,K], scales f32[N],
+ *     bias f32[N] or NULL, residual f32[M,N] or NULL];
+ * s: [M, N, K, schedule] (schedule 0 is the default) */
+int32_t nc_matmul_i8_token(void **p, const int64_t *s);
+
+/* The raw int32 accumulators of matmul_i8_token, for bit-exact checking.
+ * p: [acc i32[M,N], xq i8[M,K], q i8[N,K]];  s: [M, N, K, schedule] */
+int32_t nc_matmul_i8_token_acc(void **p, const int64_t *s);
+
+/* B independent matmul_i8_token problems in one launch, problem b reading its
+ * own weights: a stream of decode projections over distinct weights (the
+ * reference streams rotated weight copies for the same reason,
+ * autotune.py:82-83, 181-182), measured as one kernel.
+ * p: [y f32[B,M,N], xq i8[B,M,K], xs f32[B,M], q i8[B,N,K], scales f32[B,N]];
+ * s: [B, M, N, K, schedule] */
+int32_t nc_matmul_i8_token_stacked(void **p, const int64_t *s);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NC_HIP_H */

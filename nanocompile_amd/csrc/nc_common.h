@@ -1,0 +1,118 @@
+// Shared device helpers for the gfx950 kernels of nanocompile_amd.
+//
+// Everything here is exact or has one stated order:
+//  * int8 dot products go through v_dot4_i32_i8 (__builtin_amdgcn_sdot4),
+//    which is exact in int32 for every operand this library produces
+//    (|acc| <= 127 * 127 * K, below 2^31 for K < 133,000);
+//  * float reductions across a wavefront are a fixed xor butterfly
+//    (offsets 32, 16, 8, 4, 2, 1), so every lane ends with the same bits and
+//    the host oracle can replay the same tree;
+//  * rounding follows the reference's two rules: C's roundf (half away from
+//    zero, exact) for activations (ir.py:244-247, interpreter.py:192-201), and
+//    the weight quantizer's float32 floor(|s| + 0.5) (quantize.py:68).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define NC_EXPORT extern "C" __attribute__((visibility("default")))
+
+#define NC_OK 0
+#define NC_FAIL_INDEX 1      // a gather index out of range (loopir.Fail code 1)
+#define NC_BAD_ARGS 2        // the host launcher rejected a shape or pointer
+#define NC_LAUNCH_FAILED 3   // the HIP runtime refused the launch
+
+namespace nc {
+
+// 16 int8 values as four dwords: one global_load_dwordx4.
+struct alignas(16) i8x16 { int32_t w[4]; };
+
+__device__ __forceinline__ int32_t dot4(int32_t a, int32_t b, int32_t acc) {
+    return __builtin_amdgcn_sdot4(a, b, acc, false);
+}
+
+__device__ __forceinline__ int32_t dot16(const i8x16 &a, const i8x16 &b, int32_t acc) {
+    acc = dot4(a.w[0], b.w[0], acc);
+    acc = dot4(a.w[1], b.w[1], acc);
+    acc = dot4(a.w[2], b.w[2], acc);
+    acc = dot4(a.w[3], b.w[3], acc);
+    return acc;
+}
+
+__device__ __forceinline__ i8x16 load16(const int8_t *p) {
+    return *reinterpret_cast<const i8x16 *>(p);
+}
+
+__device__ __forceinline__ i8x16 load16_stream(const int8_t *p) {
+    // Weights are read once per step: a non-temporal load keeps them from
+    // evicting the activations and the KV cache from L2.
+    i8x16 v;
+    const int32_t *q = reinterpret_cast<const int32_t *>(p);
+    v.w[0] = __builtin_nontemporal_load(q + 0);
+    v.w[1] = __builtin_nontemporal_load(q + 1);
+    v.w[2] = __builtin_nontemporal_load(q + 2);
+    v.w[3] = __builtin_nontemporal_load(q + 3);
+    return v;
+}
+
+// Sum over the L lanes of an aligned group (L a power of two <= 64). Integer
+// addition is exact, so the order is immaterial.
+template <int L>
+__device__ __forceinline__ int32_t group_sum_i32(int32_t v) {
+#pragma unroll
+    for (int off = L / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Sum over a whole wavefront, the butterfly (v[i] + v[i ^ off]) for
+// off = 32, 16, 8, 4, 2, 1. Addition commutes, so all lanes agree bitwise.
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = v + __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// C's roundf: half away from zero, exact for every float.
+__device__ __forceinline__ float round_half_away(float v) { return __builtin_roundf(v); }
+
+// Per-token activation quantization of one value (the reference's
+// quantize_activations with one block spanning the row, quantize.py:116-121):
+// clamp(round(x / scale), -127, 127).
+__device__ __forceinline__ int8_t quantize_value(float x, float scale) {
+    float r = round_half_away(__fdiv_rn(x, scale));
+    r = r <= 127.0f ? r : 127.0f;
+    r = -127.0f <= r ? r : -127.0f;
+    return static_cast<int8_t>(r);
+}
+
+// The activation scale from a row maximum: where(mag <= 0, 1, mag / 127).
+__device__ __forceinline__ float token_scale(float magnitude) {
+    return magnitude <= 0.0f ? 1.0f : __fdiv_rn(magnitude, 127.0f);
+}
+
+}  // namespace nc
+
+// Host side: the library stream and error word (nc_runtime.hip), shared by
+// every launcher.
+namespace nc {
+hipStream_t stream();
+int32_t *error_word();
+// NC_OK, or NC_LAUNCH_FAILED with the message recorded for nc_last_error().
+int32_t launched(const char *what);
+void set_message(const char *text);
+}  // namespace nc
+
+// A launcher's argument checks: on failure, record why and return NC_BAD_ARGS.
+#define NC_REQUIRE(cond, text)                 \
+    do {                                       \
+        if (!(cond)) {                         \
+            nc::set_message(text);             \
+            return NC_BAD_ARGS;                \
+        }                                      \
+    } while (0)

@@ -1,0 +1,227 @@
+// The per-token int8 projection, decode shape: y[m, n] for a few tokens m and
+// every weight row n, streamed from HBM once.
+//
+//   acc[m, n] = sum_k xq[m, k] * q[n, k]           exact, int32
+//   y[m, n]   = (f32(acc) * xs[m]) * scales[n]      two rounded multiplies
+//             (+ bias[n]) (residual[m, n] + ...)    each one rounded add
+//
+// This is the build's primitive matmul_i8_token. The reference has no
+// per-token mode (its int8 modes are ir.py:392-439); the epilogue order above
+// is the one this library freezes, and the oracle restates it. The weight
+// format is the reference's per-row int8 (quantize.py:55-70): q row-major
+// [N, K], one f32 scale per row.
+//
+// Layout on the chip: a group of L lanes owns one weight row. Each lane reads
+// 16 bytes at a time (global_load_dwordx4), and the L lanes of a group read
+// L * 16 consecutive bytes, so at L = 8 each load instruction takes whole
+// 128-byte lines. Activations are staged once per workgroup in LDS. The L
+// partial sums are added with lane shuffles, exact in int32, and lane 0 of
+// the group applies the epilogue.
+#include "nc_common.h"
+
+namespace {
+
+using nc::i8x16;
+
+template <int KS, int L, int WAVES, int MT, bool ACC_OUT, bool STACKED>
+__global__ __launch_bounds__(64 * WAVES) void gemv_i8_token(
+    void *__restrict__ out, const int8_t *__restrict__ xq, const float *__restrict__ xs,
+    const int8_t *__restrict__ q, const float *__restrict__ ws, const float *__restrict__ bias,
+    const float *__restrict__ residual, int M, int N, int Kr) {
+    constexpr int ROWS = (64 / L) * WAVES;
+    constexpr int STEP = L * 16;
+    const int K = KS ? KS : Kr;
+    extern __shared__ __align__(16) int8_t sx[];
+    if constexpr (STACKED) {   // nc_matmul_i8_token_stacked: problem z has its own operands
+        const size_t z = blockIdx.z;
+        q += z * (size_t)N * K;
+        ws += z * (size_t)N;
+        xq += z * (size_t)M * K;
+        xs += z * (size_t)M;
+        out = static_cast<char *>(out) + z * (size_t)M * N * 4;
+    }
+
+    const int m0 = blockIdx.y * MT;
+    const int mt = min(MT, M - m0);
+    const int chunks = K / 16;
+    for (int i = threadIdx.x; i < MT * chunks; i += 64 * WAVES) {
+        const int m = i / chunks, c = i - m * chunks;
+        i8x16 v = {};
+        if (m < mt) v = nc::load16(xq + (size_t)(m0 + m) * K + c * 16);
+        *reinterpret_cast<i8x16 *>(sx + m * K + c * 16) = v;
+    }
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane & (L - 1), grp = lane / L;
+    const int n = blockIdx.x * ROWS + wave * (64 / L) + grp;
+
+    int32_t acc[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[m] = 0;
+    if (n < N) {
+        const int8_t *row = q + (size_t)n * K;
+        const int iters = (K + STEP - 1) / STEP;
+#pragma unroll
+        for (int it = 0; it < iters; ++it) {
+            const int c = it * STEP + sub * 16;
+            if (K % STEP == 0 || c < K) {
+                const i8x16 w = nc::load16_stream(row + c);
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+                    acc[m] = nc::dot16(w, *reinterpret_cast<const i8x16 *>(sx + m * K + c), acc[m]);
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[m] = nc::group_sum_i32<L>(acc[m]);
+
+    if (sub == 0 && n < N) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            if (m >= mt) break;
+            const size_t at = (size_t)(m0 + m) * N + n;
+            if constexpr (ACC_OUT) {
+                static_cast<int32_t *>(out)[at] = acc[m];
+            } else {
+                float v = __fmul_rn(__fmul_rn((float)acc[m], xs[m0 + m]), ws[n]);
+                if (bias) v = __fadd_rn(v, bias[n]);
+                if (residual) v = __fadd_rn(residual[at], v);
+                static_cast<float *>(out)[at] = v;
+            }
+        }
+    }
+}
+
+// Any K, byte by byte: the path for widths that are not a whole number of
+// 16-byte chunks (the reference's test widths 77 and 40, say). One wave per
+// row; the same exact sum and the same epilogue.
+template <bool ACC_OUT>
+__global__ __launch_bounds__(64) void gemv_i8_token_bytes(
+    void *__restrict__ out, const int8_t *__restrict__ xq, const float *__restrict__ xs,
+    const int8_t *__restrict__ q, const float *__restrict__ ws, const float *__restrict__ bias,
+    const float *__restrict__ residual, int M, int N, int K) {
+    const int n = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
+    const int8_t *row = q + (size_t)n * K;
+    const int8_t *x = xq + (size_t)m * K;
+    int32_t acc = 0;
+    for (int k = lane; k < K; k += 64) acc += (int32_t)row[k] * (int32_t)x[k];
+    acc = nc::group_sum_i32<64>(acc);
+    if (lane == 0) {
+        const size_t at = (size_t)m * N + n;
+        if constexpr (ACC_OUT) {
+            static_cast<int32_t *>(out)[at] = acc;
+        } else {
+            float v = __fmul_rn(__fmul_rn((float)acc, xs[m]), ws[n]);
+            if (bias) v = __fadd_rn(v, bias[n]);
+            if (residual) v = __fadd_rn(residual[at], v);
+            static_cast<float *>(out)[at] = v;
+        }
+    }
+}
+
+struct Args {
+    void *out;
+    const int8_t *xq;
+    const float *xs;
+    const int8_t *q;
+    const float *ws;
+    const float *bias;
+    const float *residual;
+    int M, N, K;
+    int batch;
+};
+
+template <int KS, int L, int WAVES, int MT, bool ACC_OUT>
+int32_t launch(const Args &a) {
+    constexpr int ROWS = (64 / L) * WAVES;
+    dim3 grid((a.N + ROWS - 1) / ROWS, (a.M + MT - 1) / MT, a.batch);
+    size_t lds = (size_t)MT * a.K;
+    if (a.batch > 1)
+        hipLaunchKernelGGL((gemv_i8_token<KS, L, WAVES, MT, ACC_OUT, true>), grid, dim3(64 * WAVES), lds,
+                           nc::stream(), a.out, a.xq, a.xs, a.q, a.ws, a.bias, a.residual, a.M, a.N, a.K);
+    else
+        hipLaunchKernelGGL((gemv_i8_token<KS, L, WAVES, MT, ACC_OUT, false>), grid, dim3(64 * WAVES), lds,
+                           nc::stream(), a.out, a.xq, a.xs, a.q, a.ws, a.bias, a.residual, a.M, a.N, a.K);
+    return nc::launched("gemv_i8_token");
+}
+
+template <bool ACC_OUT>
+int32_t launch_bytes(const Args &a) {
+    hipLaunchKernelGGL((gemv_i8_token_bytes<ACC_OUT>), dim3(a.N, a.M), dim3(64), 0, nc::stream(), a.out, a.xq, a.xs,
+                       a.q, a.ws, a.bias, a.residual, a.M, a.N, a.K);
+    return nc::launched("gemv_i8_token_bytes");
+}
+
+// The schedule space of the decode GEMV: lanes per row L and waves per
+// workgroup. Index 0 is the default. The token tile MT follows M.
+template <int KS, int MT, bool ACC_OUT>
+int32_t dispatch_schedule(const Args &a, int schedule) {
+    switch (schedule) {
+        case 0: return launch<KS, 8, 1, MT, ACC_OUT>(a);
+        case 1: return launch<KS, 4, 1, MT, ACC_OUT>(a);
+        case 2: return launch<KS, 16, 1, MT, ACC_OUT>(a);
+        case 3: return launch<KS, 8, 2, MT, ACC_OUT>(a);
+        case 4: return launch<KS, 8, 4, MT, ACC_OUT>(a);
+        case 5: return launch<KS, 4, 2, MT, ACC_OUT>(a);
+        case 6: return launch<KS, 16, 2, MT, ACC_OUT>(a);
+        default: nc::set_message("gemv_i8_token: no such schedule"); return NC_BAD_ARGS;
+    }
+}
+
+template <int KS, bool ACC_OUT>
+int32_t dispatch_tokens(const Args &a, int schedule) {
+    if (a.M == 1) return dispatch_schedule<KS, 1, ACC_OUT>(a, schedule);
+    if (a.M == 2) return dispatch_schedule<KS, 2, ACC_OUT>(a, schedule);
+    if (a.M <= 4) return dispatch_schedule<KS, 4, ACC_OUT>(a, schedule);
+    return dispatch_schedule<KS, 8, ACC_OUT>(a, schedule);
+}
+
+template <bool ACC_OUT>
+int32_t run(const Args &a, int schedule) {
+    if (a.M == 0 || a.N == 0) return NC_OK;
+    if (a.K % 16 != 0 || (size_t)8 * a.K > 65536) {
+        if (a.batch != 1) { nc::set_message("stacked GEMV needs K a multiple of 16"); return NC_BAD_ARGS; }
+        return launch_bytes<ACC_OUT>(a);
+    }
+    if (a.K == 896) return dispatch_tokens<896, ACC_OUT>(a, schedule);
+    if (a.K == 4864) return dispatch_tokens<4864, ACC_OUT>(a, schedule);
+    return dispatch_tokens<0, ACC_OUT>(a, schedule);
+}
+
+}  // namespace
+
+// p: [y f32[M,N], xq i8[M,K], xs f32[M], q i8[N,K], scales f32[N], bias f32[N] | NULL,
+//     residual f32[M,N] | NULL];  s: [M, N, K, schedule]
+NC_EXPORT int32_t nc_matmul_i8_token(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3] && p[4], "nc_matmul_i8_token: null operand");
+    NC_REQUIRE(s[0] >= 0 && s[1] >= 0 && s[2] > 0 && s[0] < (1 << 24) && s[1] < (1 << 24) && s[2] < (1 << 24),
+               "nc_matmul_i8_token: bad shape");
+    Args a{p[0], (const int8_t *)p[1], (const float *)p[2], (const int8_t *)p[3], (const float *)p[4],
+           (const float *)p[5], (const float *)p[6], (int)s[0], (int)s[1], (int)s[2], 1};
+    return run<false>(a, (int)s[3]);
+}
+
+// p: [acc i32[M,N], xq i8[M,K], q i8[N,K]];  s: [M, N, K, schedule]
+NC_EXPORT int32_t nc_matmul_i8_token_acc(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2], "nc_matmul_i8_token_acc: null operand");
+    NC_REQUIRE(s[0] >= 0 && s[1] >= 0 && s[2] > 0 && s[0] < (1 << 24) && s[1] < (1 << 24) && s[2] < (1 << 24),
+               "nc_matmul_i8_token_acc: bad shape");
+    Args a{p[0], (const int8_t *)p[1], nullptr, (const int8_t *)p[2], nullptr, nullptr, nullptr,
+           (int)s[0], (int)s[1], (int)s[2], 1};
+    return run<true>(a, (int)s[3]);
+}
+
+// B independent projections in one launch, problem z reading its own weights:
+// the steady state of a stream of decode GEMVs over rotated weight copies.
+// p: [y f32[B,M,N], xq i8[B,M,K], xs f32[B,M], q i8[B,N,K], scales f32[B,N]];
+// s: [B, M, N, K, schedule]
+NC_EXPORT int32_t nc_matmul_i8_token_stacked(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3] && p[4], "nc_matmul_i8_token_stacked: null operand");
+    NC_REQUIRE(s[0] > 0 && s[0] < 65536 && s[1] >= 0 && s[2] >= 0 && s[3] > 0 && s[1] < (1 << 24) &&
+                   s[2] < (1 << 24) && s[3] < (1 << 24),
+               "nc_matmul_i8_token_stacked: bad shape");
+    Args a{p[0], (const int8_t *)p[1], (const float *)p[2], (const int8_t *)p[3], (const float *)p[4],
+           nullptr, nullptr, (int)s[1], (int)s[2], (int)s[3], (int)s[0]};
+    return run<false>(a, (int)s[4]);
+}

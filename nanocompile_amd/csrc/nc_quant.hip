@@ -1,0 +1,157 @@
+// Row kernels that produce int8: the per-row weight quantizer, the per-token
+// activation quantizer, and rms_norm fused with the activation quantizer.
+//
+// One workgroup of 256 threads per row. Maxima are exact in any order. The
+// one float sum here (rms_norm's sum of squares) has this order, which the
+// host oracle replays bit for bit:
+//   thread t: s_t = x[t]^2 + x[t+256]^2 + ... in index order, from 0;
+//   wave w:   the butterfly of nc::wave_sum_f32 over its 64 threads;
+//   block:    (w0 + w1) + (w2 + w3).
+// The reference sums the row in index order (fusion.py:631-650); the two
+// orders agree to float rounding, which the tests bound.
+#include "nc_common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ float block_max(float v, float *scratch) {
+    v = nc::wave_max_f32(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(scratch[0], scratch[1]), fmaxf(scratch[2], scratch[3]));
+}
+
+__device__ float block_sum(float v, float *scratch) {
+    v = nc::wave_sum_f32(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    return __fadd_rn(__fadd_rn(scratch[0], scratch[1]), __fadd_rn(scratch[2], scratch[3]));
+}
+
+// quantize.py:55-70, operation for operation, in float32:
+//   scale = max|row| / 127 (1 for an all-zero row); s = w / scale;
+//   q = clip(sign(s) * floor(|s| + 0.5), -127, 127).
+__global__ __launch_bounds__(kThreads) void quantize_rows(int8_t *__restrict__ q, float *__restrict__ scales,
+                                                          const float *__restrict__ w, int K) {
+    __shared__ float scratch[4];
+    const float *row = w + (size_t)blockIdx.x * K;
+    float mag = 0.0f;
+    for (int k = threadIdx.x; k < K; k += kThreads) mag = fmaxf(mag, fabsf(row[k]));
+    mag = block_max(mag, scratch);
+    float scale = __fdiv_rn(mag, 127.0f);
+    if (scale == 0.0f) scale = 1.0f;
+    int8_t *out = q + (size_t)blockIdx.x * K;
+    for (int k = threadIdx.x; k < K; k += kThreads) {
+        const float s = __fdiv_rn(row[k], scale);
+        const float r = floorf(__fadd_rn(fabsf(s), 0.5f));
+        float v = s > 0.0f ? r : (s < 0.0f ? -r : 0.0f);
+        v = fminf(fmaxf(v, -127.0f), 127.0f);
+        out[k] = (int8_t)v;
+    }
+    if (threadIdx.x == 0) scales[blockIdx.x] = scale;
+}
+
+// Per-token quantization of a row already in registers/LDS-free form.
+__global__ __launch_bounds__(kThreads) void quantize_token(int8_t *__restrict__ xq, float *__restrict__ xs,
+                                                           const float *__restrict__ x, int K) {
+    __shared__ float scratch[4];
+    const float *row = x + (size_t)blockIdx.x * K;
+    float mag = 0.0f;
+    for (int k = threadIdx.x; k < K; k += kThreads) mag = fmaxf(mag, fabsf(row[k]));
+    const float scale = nc::token_scale(block_max(mag, scratch));
+    int8_t *out = xq + (size_t)blockIdx.x * K;
+    for (int k = threadIdx.x; k < K; k += kThreads) out[k] = nc::quantize_value(row[k], scale);
+    if (threadIdx.x == 0) xs[blockIdx.x] = scale;
+}
+
+// rms_norm (nn.py:34-38: (x * (1 / sqrt(sum(x*x) / K + eps))) * gamma) and
+// then the per-token quantizer on the normed row, one pass over x. normed may
+// be null when only the int8 row is wanted.
+template <int PER_THREAD>
+__global__ __launch_bounds__(kThreads) void rms_norm_quant(float *__restrict__ normed, int8_t *__restrict__ xq,
+                                                           float *__restrict__ xs, const float *__restrict__ x,
+                                                           const float *__restrict__ gamma, int K, float eps) {
+    __shared__ float scratch[4];
+    const float *row = x + (size_t)blockIdx.x * K;
+    float v[PER_THREAD];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+        const int k = threadIdx.x + i * kThreads;
+        v[i] = k < K ? row[k] : 0.0f;
+        if (k < K) ss = __fadd_rn(ss, __fmul_rn(v[i], v[i]));
+    }
+    ss = block_sum(ss, scratch);
+    const float rcp = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)K), eps)));
+    float mag = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+        const int k = threadIdx.x + i * kThreads;
+        v[i] = k < K ? __fmul_rn(__fmul_rn(v[i], rcp), gamma[k]) : 0.0f;
+        mag = fmaxf(mag, fabsf(v[i]));
+    }
+    const float scale = nc::token_scale(block_max(mag, scratch));
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+        const int k = threadIdx.x + i * kThreads;
+        if (k < K) {
+            if (normed) normed[(size_t)blockIdx.x * K + k] = v[i];
+            xq[(size_t)blockIdx.x * K + k] = nc::quantize_value(v[i], scale);
+        }
+    }
+    if (threadIdx.x == 0) xs[blockIdx.x] = scale;
+}
+
+template <int PER_THREAD>
+int32_t launch_rms(void **p, int M, int K, float eps) {
+    hipLaunchKernelGGL((rms_norm_quant<PER_THREAD>), dim3(M), dim3(kThreads), 0, nc::stream(), (float *)p[0],
+                       (int8_t *)p[1], (float *)p[2], (const float *)p[3], (const float *)p[4], K, eps);
+    return nc::launched("rms_norm_quant");
+}
+
+float bits_to_float(int64_t bits) {
+    union { uint32_t u; float f; } c;
+    c.u = (uint32_t)bits;
+    return c.f;
+}
+
+}  // namespace
+
+// p: [q i8[N,K], scales f32[N], w f32[N,K]];  s: [N, K]
+NC_EXPORT int32_t nc_quantize_rows_i8(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2], "nc_quantize_rows_i8: null operand");
+    NC_REQUIRE(s[0] >= 0 && s[1] > 0 && s[0] < (1 << 26) && s[1] < (1 << 26), "nc_quantize_rows_i8: bad shape");
+    if (s[0] == 0) return NC_OK;
+    hipLaunchKernelGGL(quantize_rows, dim3((unsigned)s[0]), dim3(kThreads), 0, nc::stream(), (int8_t *)p[0],
+                       (float *)p[1], (const float *)p[2], (int)s[1]);
+    return nc::launched("quantize_rows");
+}
+
+// p: [xq i8[M,K], xs f32[M], x f32[M,K]];  s: [M, K]
+NC_EXPORT int32_t nc_quantize_token_i8(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2], "nc_quantize_token_i8: null operand");
+    NC_REQUIRE(s[0] >= 0 && s[1] > 0 && s[0] < (1 << 26) && s[1] < (1 << 26), "nc_quantize_token_i8: bad shape");
+    if (s[0] == 0) return NC_OK;
+    hipLaunchKernelGGL(quantize_token, dim3((unsigned)s[0]), dim3(kThreads), 0, nc::stream(), (int8_t *)p[0],
+                       (float *)p[1], (const float *)p[2], (int)s[1]);
+    return nc::launched("quantize_token");
+}
+
+// p: [normed f32[M,K] | NULL, xq i8[M,K], xs f32[M], x f32[M,K], gamma f32[K]];
+// s: [M, K, eps as float32 bits]
+NC_EXPORT int32_t nc_rms_norm_quant(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[1] && p[2] && p[3] && p[4], "nc_rms_norm_quant: null operand");
+    NC_REQUIRE(s[0] >= 0 && s[1] > 0 && s[0] < (1 << 26) && s[1] <= 32 * kThreads, "nc_rms_norm_quant: bad shape");
+    const int M = (int)s[0], K = (int)s[1];
+    const float eps = bits_to_float(s[2]);
+    if (M == 0) return NC_OK;
+    if (K <= 4 * kThreads) return launch_rms<4>(p, M, K, eps);
+    if (K <= 8 * kThreads) return launch_rms<8>(p, M, K, eps);
+    if (K <= 20 * kThreads) return launch_rms<20>(p, M, K, eps);
+    return launch_rms<32>(p, M, K, eps);
+}

@@ -1,0 +1,133 @@
+"""The hot path's operators on device arrays, with the reference's typing contracts.
+
+Each function checks its operands the way the reference's IR checks a node's
+(ir.py:381-439: one f32 scale per i8 weight row, activations of the weights'
+width) and raises :class:`ShapeError` with the same kind of message, then
+enqueues one kernel of the HIP library. Results are :class:`DeviceArray`\\ s;
+nothing is copied to the host unless the caller asks.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from nanocompile_amd import hip
+from nanocompile_amd.hip import DeviceArray
+
+F32, I8, I32 = np.dtype(np.float32), np.dtype(np.int8), np.dtype(np.int32)
+
+
+class ShapeError(ValueError):
+    """Operands that do not fit the primitive (the reference's ir.ShapeError)."""
+
+
+def _device(x, dtype=None) -> DeviceArray:
+    if isinstance(x, DeviceArray):
+        if dtype is not None and x.dtype != np.dtype(dtype):
+            raise ShapeError(f"expected {np.dtype(dtype)}, got {x.dtype}")
+        return x
+    array = np.asarray(x)
+    if dtype is not None and array.dtype != np.dtype(dtype):
+        raise ShapeError(f"expected {np.dtype(dtype)}, got {array.dtype}")
+    return DeviceArray.from_host(array)
+
+
+def float_bits(value: float) -> int:
+    return int(np.array(value, dtype=np.float32).view(np.uint32))
+
+
+def _int8_weight(op: str, q: DeviceArray, scales: DeviceArray, k: int) -> int:
+    """Check ``q: i8[N, K]`` and ``scales: f32[N]`` against width ``k``; return N (ir.py:381-389)."""
+    if q.dtype != I8 or len(q.shape) != 2:
+        raise ShapeError(f"{op}: weights must be i8[N, K], got {q.dtype}{list(q.shape)}")
+    if scales.dtype != F32 or len(scales.shape) != 1 or scales.shape[0] != q.shape[0]:
+        raise ShapeError(f"{op}: expected one f32 scale per row of i8{list(q.shape)}, "
+                         f"got {scales.dtype}{list(scales.shape)}")
+    if q.shape[1] != k:
+        raise ShapeError(f"{op}: activations have width {k}, weights i8{list(q.shape)} expect {q.shape[1]}")
+    return q.shape[0]
+
+
+def quantize_int8(w) -> tuple[DeviceArray, DeviceArray]:
+    """Per-row symmetric int8 of an ``[N, K]`` f32 matrix: (values, scales) (quantize.py:55-70)."""
+    w = _device(w, F32)
+    if len(w.shape) != 2:
+        raise ValueError(f"expected a 2-D weight matrix, got shape {w.shape}")
+    n, k = w.shape
+    q, scales = DeviceArray((n, k), I8), DeviceArray((n,), F32)
+    if n and k:
+        hip.call("nc_quantize_rows_i8", [q, scales, w], [n, k])
+    return q, scales
+
+
+def quantize_token(x) -> tuple[DeviceArray, DeviceArray]:
+    """``x: f32[M, K]`` to ``(xq i8[M, K], xs f32[M])``: one scale per token."""
+    x = _device(x, F32)
+    if len(x.shape) != 2:
+        raise ShapeError(f"quantize_token: activations must be f32[M, K], got {list(x.shape)}")
+    m, k = x.shape
+    xq, xs = DeviceArray((m, k), I8), DeviceArray((m,), F32)
+    if m and k:
+        hip.call("nc_quantize_token_i8", [xq, xs, x], [m, k])
+    return xq, xs
+
+
+def rms_norm_quant(x, gamma, eps: float, normed: bool = True):
+    """rms_norm then per-token int8, one kernel: ``(normed | None, xq, xs)``."""
+    x, gamma = _device(x, F32), _device(gamma, F32)
+    if len(x.shape) != 2 or gamma.shape != (x.shape[1],):
+        raise ShapeError(f"rms_norm_quant: x f32[M, K] and gamma f32[K], got {list(x.shape)}, {list(gamma.shape)}")
+    m, k = x.shape
+    out = DeviceArray((m, k), F32) if normed else None
+    xq, xs = DeviceArray((m, k), I8), DeviceArray((m,), F32)
+    if m:
+        hip.call("nc_rms_norm_quant", [out, xq, xs, x, gamma], [m, k, float_bits(eps)])
+    return out, xq, xs
+
+
+def matmul_i8_token(xq, xs, q, scales, bias=None, residual=None, schedule: int = 0) -> DeviceArray:
+    """``(f32(xq @ q.T) * xs[:, None]) * scales (+ bias) (+ residual)``, accumulated exactly in int32."""
+    xq, xs, q, scales = _device(xq, I8), _device(xs, F32), _device(q, I8), _device(scales, F32)
+    if len(xq.shape) != 2:
+        raise ShapeError(f"matmul_i8_token: activations must be i8[M, K], got {list(xq.shape)}")
+    m, k = xq.shape
+    if xs.shape != (m,):
+        raise ShapeError(f"matmul_i8_token: expected f32[{m}] token scales, got {list(xs.shape)}")
+    n = _int8_weight("matmul_i8_token", q, scales, k)
+    if bias is not None:
+        bias = _device(bias, F32)
+        if bias.shape != (n,):
+            raise ShapeError(f"matmul_i8_token: bias must be f32[{n}]")
+    if residual is not None:
+        residual = _device(residual, F32)
+        if residual.shape != (m, n):
+            raise ShapeError(f"matmul_i8_token: residual must be f32[{m}, {n}]")
+    y = DeviceArray((m, n), F32)
+    hip.call("nc_matmul_i8_token", [y, xq, xs, q, scales, bias, residual], [m, n, k, schedule])
+    return y
+
+
+def matmul_i8_token_acc(xq, q, schedule: int = 0) -> DeviceArray:
+    """The int32 accumulators ``xq @ q.T`` alone, for checking them bit for bit."""
+    xq, q = _device(xq, I8), _device(q, I8)
+    if len(xq.shape) != 2 or len(q.shape) != 2 or xq.shape[1] != q.shape[1]:
+        raise ShapeError(f"matmul_i8_token_acc: i8[M, K] @ i8[N, K].T, got {list(xq.shape)}, {list(q.shape)}")
+    m, k = xq.shape
+    acc = DeviceArray((m, q.shape[0]), I32)
+    hip.call("nc_matmul_i8_token_acc", [acc, xq, q], [m, q.shape[0], k, schedule])
+    return acc
+
+
+def matmul_i8_token_stacked(xq, xs, q, scales, out: DeviceArray | None = None, schedule: int = 0) -> DeviceArray:
+    """``B`` independent projections in one launch: ``xq i8[B,M,K]``, ``q i8[B,N,K]`` -> ``f32[B,M,N]``."""
+    xq, xs, q, scales = _device(xq, I8), _device(xs, F32), _device(q, I8), _device(scales, F32)
+    if len(xq.shape) != 3 or len(q.shape) != 3 or xq.shape[0] != q.shape[0] or xq.shape[2] != q.shape[2]:
+        raise ShapeError(f"matmul_i8_token_stacked: i8[B,M,K] and i8[B,N,K], got {list(xq.shape)}, {list(q.shape)}")
+    b, m, k = xq.shape
+    n = q.shape[1]
+    if xs.shape != (b, m) or scales.shape != (b, n):
+        raise ShapeError("matmul_i8_token_stacked: scales must be f32[B,M] and f32[B,N]")
+    if out is None:
+        out = DeviceArray((b, m, n), F32)
+    hip.call("nc_matmul_i8_token_stacked", [out, xq, xs, q, scales], [b, m, n, k, schedule])
+    return out
