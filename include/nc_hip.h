@@ -93,6 +93,12 @@ int32_t nc_quantize_token_i8(void **p, const int64_t *s);
  * s: [M, K, eps as the bits of a float32] */
 int32_t nc_rms_norm_quant(void **p, const int64_t *s);
 
+/* Diagnostic: the device's float32 a / b, sqrt(|a|) and roundf(a), so tests can
+ * hold them to IEEE correct rounding as the reference's C is (libm sqrtf and
+ * '/', codegen_c.py:58, 141; roundf half away from zero, loopir.py:88-90).
+ * p: [quotient f32[n], root f32[n], rounded f32[n], a f32[n], b f32[n]];  s: [n] */
+int32_t nc_probe_fp32_ops(void **p, const int64_t *s);
+
 /* -- int8 projections --------------------------------------------------------- */
 
 /* matmul_i8_token: per-token int8 activations times per-row int8 weights,

@@ -26,6 +26,7 @@ ARCH = "gfx950"
 
 HIPCC_FLAGS = (
     "-O3", "-std=c++17", f"--offload-arch={ARCH}", "-fPIC", "-ffp-contract=off",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-fvisibility=hidden", "-munsafe-fp-atomics",
     # Packed fp32 instructions have given wrong results on these machines:
     # hipcc must not form them from ordinary float code.

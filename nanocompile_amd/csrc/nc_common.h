@@ -78,6 +78,14 @@ __device__ __forceinline__ float wave_max_f32(float v) {
     return v;
 }
 
+// Correctly rounded float32 square root. Not __fsqrt_rn: without
+// OCML_BASIC_ROUNDED_OPERATIONS, HIP maps that to the approximate native
+// sqrt. llvm.sqrt.f32 is expanded to the correctly rounded sequence under
+// -fhip-fp32-correctly-rounded-divide-sqrt, which the build passes (and which
+// also makes plain float division correctly rounded).
+__device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
+__device__ __forceinline__ float div_rn(float a, float b) { return a / b; }
+
 // C's roundf: half away from zero, exact for every float.
 __device__ __forceinline__ float round_half_away(float v) { return __builtin_roundf(v); }
 
@@ -85,7 +93,7 @@ __device__ __forceinline__ float round_half_away(float v) { return __builtin_rou
 // quantize_activations with one block spanning the row, quantize.py:116-121):
 // clamp(round(x / scale), -127, 127).
 __device__ __forceinline__ int8_t quantize_value(float x, float scale) {
-    float r = round_half_away(__fdiv_rn(x, scale));
+    float r = round_half_away(div_rn(x, scale));
     r = r <= 127.0f ? r : 127.0f;
     r = -127.0f <= r ? r : -127.0f;
     return static_cast<int8_t>(r);
@@ -93,7 +101,7 @@ __device__ __forceinline__ int8_t quantize_value(float x, float scale) {
 
 // The activation scale from a row maximum: where(mag <= 0, 1, mag / 127).
 __device__ __forceinline__ float token_scale(float magnitude) {
-    return magnitude <= 0.0f ? 1.0f : __fdiv_rn(magnitude, 127.0f);
+    return magnitude <= 0.0f ? 1.0f : div_rn(magnitude, 127.0f);
 }
 
 }  // namespace nc

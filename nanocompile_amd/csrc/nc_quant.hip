@@ -43,11 +43,11 @@ __global__ __launch_bounds__(kThreads) void quantize_rows(int8_t *__restrict__ q
     float mag = 0.0f;
     for (int k = threadIdx.x; k < K; k += kThreads) mag = fmaxf(mag, fabsf(row[k]));
     mag = block_max(mag, scratch);
-    float scale = __fdiv_rn(mag, 127.0f);
+    float scale = nc::div_rn(mag, 127.0f);
     if (scale == 0.0f) scale = 1.0f;
     int8_t *out = q + (size_t)blockIdx.x * K;
     for (int k = threadIdx.x; k < K; k += kThreads) {
-        const float s = __fdiv_rn(row[k], scale);
+        const float s = nc::div_rn(row[k], scale);
         const float r = floorf(__fadd_rn(fabsf(s), 0.5f));
         float v = s > 0.0f ? r : (s < 0.0f ? -r : 0.0f);
         v = fminf(fmaxf(v, -127.0f), 127.0f);
@@ -87,7 +87,7 @@ __global__ __launch_bounds__(kThreads) void rms_norm_quant(float *__restrict__ n
         if (k < K) ss = __fadd_rn(ss, __fmul_rn(v[i], v[i]));
     }
     ss = block_sum(ss, scratch);
-    const float rcp = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)K), eps)));
+    const float rcp = nc::div_rn(1.0f, nc::sqrt_rn(__fadd_rn(nc::div_rn(ss, (float)K), eps)));
     float mag = 0.0f;
 #pragma unroll
     for (int i = 0; i < PER_THREAD; ++i) {
@@ -154,4 +154,30 @@ NC_EXPORT int32_t nc_rms_norm_quant(void **p, const int64_t *s) {
     if (K <= 8 * kThreads) return launch_rms<8>(p, M, K, eps);
     if (K <= 20 * kThreads) return launch_rms<20>(p, M, K, eps);
     return launch_rms<32>(p, M, K, eps);
+}
+
+namespace {
+__global__ void fp32_ops(float *__restrict__ quotient, float *__restrict__ root, float *__restrict__ rounded,
+                         const float *__restrict__ a, const float *__restrict__ b, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        quotient[i] = nc::div_rn(a[i], b[i]);
+        root[i] = nc::sqrt_rn(fabsf(a[i]));
+        rounded[i] = nc::round_half_away(a[i]);
+    }
+}
+}  // namespace
+
+// The device's float32 division, square root and roundf, elementwise, so a
+// test can hold them to IEEE correct rounding (the reference's C uses libm's
+// correctly rounded sqrtf and '/', codegen_c.py:58, 141).
+// p: [a / b f32[n], sqrt(|a|) f32[n], roundf(a) f32[n], a f32[n], b f32[n]];  s: [n]
+NC_EXPORT int32_t nc_probe_fp32_ops(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3] && p[4], "nc_probe_fp32_ops: null operand");
+    NC_REQUIRE(s[0] >= 0 && s[0] < (1 << 28), "nc_probe_fp32_ops: bad size");
+    if (s[0] == 0) return NC_OK;
+    const int n = (int)s[0];
+    hipLaunchKernelGGL(fp32_ops, dim3((n + 255) / 256), dim3(256), 0, nc::stream(), (float *)p[0], (float *)p[1],
+                       (float *)p[2], (const float *)p[3], (const float *)p[4], n);
+    return nc::launched("fp32_ops");
 }

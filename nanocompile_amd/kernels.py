@@ -21,15 +21,16 @@ class ShapeError(ValueError):
     """Operands that do not fit the primitive (the reference's ir.ShapeError)."""
 
 
+SHORT = {F32: "f32", I8: "i8", I32: "i32", np.dtype(np.int64): "i64"}
+
+
 def _device(x, dtype=None) -> DeviceArray:
-    if isinstance(x, DeviceArray):
-        if dtype is not None and x.dtype != np.dtype(dtype):
-            raise ShapeError(f"expected {np.dtype(dtype)}, got {x.dtype}")
-        return x
-    array = np.asarray(x)
-    if dtype is not None and array.dtype != np.dtype(dtype):
-        raise ShapeError(f"expected {np.dtype(dtype)}, got {array.dtype}")
-    return DeviceArray.from_host(array)
+    """``x`` on the device (uploaded if it is a host array), checked to be ``dtype``."""
+    have = x.dtype if isinstance(x, DeviceArray) else np.asarray(x).dtype
+    if dtype is not None and have != np.dtype(dtype):
+        want = SHORT.get(np.dtype(dtype), str(dtype))
+        raise ShapeError(f"operand must be {want}, got {SHORT.get(have, str(have))}")
+    return x if isinstance(x, DeviceArray) else DeviceArray.from_host(np.asarray(x))
 
 
 def float_bits(value: float) -> int:
