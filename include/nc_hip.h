@@ -124,6 +124,68 @@ int32_t nc_matmul_i8_token_acc(void **p, const int64_t *s);
  * s: [B, M, N, K, schedule] */
 int32_t nc_matmul_i8_token_stacked(void **p, const int64_t *s);
 
+/* SwiGLU's gate and up projections sharing one pass over the activations
+ * (fusion.py:677-711 shares their k loop), then h = silu(gate) * up
+ * (nn.py:41-54) in the epilogue; each projection's epilogue as above.
+ * p: [h f32[M,N], xq i8[M,K], xs f32[M], qg i8[N,K], sg f32[N], qu i8[N,K], su f32[N]];
+ * s: [M, N, K] (K a multiple of 16, at most 8192) */
+int32_t nc_matmul_i8_token_swiglu(void **p, const int64_t *s);
+
+/* -- fused groups around the projections (nn.py, models/qwen2.py) ------------ */
+
+/* y = silu(g) * u elementwise: p = 0 <= g, e = exp(p ? -g : g),
+ * sigmoid = (p ? 1 : e) / (e + 1), y = (g * sigmoid) * u (nn.py:41-54).
+ * p: [y f32[n], g f32[n], u f32[n]];  s: [n] */
+int32_t nc_silu_mul(void **p, const int64_t *s);
+
+/* RoPE with the half-split pairing (nn.py:69-106) at positions past..past+seq-1.
+ * p: [y f32[heads,seq,D], x f32[heads,seq,D], inv_freq f32[D/2]];  s: [heads, seq, D, past] */
+int32_t nc_rope(void **p, const int64_t *s);
+
+/* softmax(s + causal mask) row by row (nn.py:57-66 with nn.py:123-135, one
+ * row kernel as fusion makes it); masked entries come out 0.
+ * p: [y f32[heads,seq,past+seq], s f32[heads,seq,past+seq]];  s: [heads, seq, past] */
+int32_t nc_softmax_causal(void **p, const int64_t *s);
+
+/* Rotates the q and k heads of each qkv row by RoPE (q in place) and appends
+ * k and v to the cache at positions past+i (models/qwen2.py:134-145: keys are
+ * cached after rotation).
+ * p: [qkv f32[M,(heads+2*kv)*D], kcache f32[kv,C,D], vcache f32[kv,C,D], inv_freq f32[D/2]];
+ * s: [M, heads, kv, D, past, C] */
+int32_t nc_rope_append(void **p, const int64_t *s);
+
+/* Grouped-query attention of each new row over the cache, causal
+ * (models/qwen2.py:113-155; query head h reads KV head h / (heads / kv), the
+ * reference's repeat_kv as index arithmetic, nn.py:109-120).
+ * p: [ctx f32[M,heads*D], qkv (q rotated), kcache, vcache];
+ * s: [M, heads, kv, D, past, C, scale as float32 bits] (D <= 64) */
+int32_t nc_attention(void **p, const int64_t *s);
+
+/* -- the model's ends ---------------------------------------------------------- */
+
+/* Embedding gather (lower.py:420-444); an id outside 0..V-1 records failure
+ * code 1 for nc_sync, as the reference's gather Fail does (fusion.py:722).
+ * p: [x f32[M,H], table f32[V,H], ids i64[M]];  s: [M, H, V] */
+int32_t nc_embed(void **p, const int64_t *s);
+
+/* The LM head's packed table: blocks of 64 rows, 4 consecutive k per row
+ * together (the reference's pack, schedule.py:362-395).
+ * p: [packed f32[ceil(V/64)*64, H], table f32[V,H]];  s: [V, H] */
+int32_t nc_pack_rows64(void **p, const int64_t *s);
+
+/* logits = x @ table.T with each row summed in k order, multiply then add
+ * (the reference's float32 matmul kernel, lower.py:255-269), and best[m] the
+ * 64-bit argmax key of row m (first index of the maximum).
+ * p: [logits f32[M,V] or NULL, best u64[M] or NULL, x f32[M,H], packed table];
+ * s: [M, V, H] */
+int32_t nc_lm_head(void **p, const int64_t *s);
+
+/* p: [best u64[n]];  s: [n]  (zeroes the argmax keys before nc_lm_head) */
+int32_t nc_argmax_clear(void **p, const int64_t *s);
+
+/* p: [index i64[n], best u64[n]];  s: [n]  (argmax keys to token ids) */
+int32_t nc_argmax_index(void **p, const int64_t *s);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,6 +18,7 @@
 // partial sums are added with lane shuffles, exact in int32, and lane 0 of
 // the group applies the epilogue.
 #include "nc_common.h"
+#include "nc_math.h"
 
 namespace {
 
@@ -89,6 +90,78 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_i8_token(
                 if (residual) v = __fadd_rn(residual[at], v);
                 static_cast<float *>(out)[at] = v;
             }
+        }
+    }
+}
+
+// silu(g) * u in the reference's float32 order (nn.py:41-54):
+// p = 0 <= g; e = exp(p ? -g : g); sigmoid = (p ? 1 : e) / (e + 1); (g * sigmoid) * u.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    const bool p = 0.0f <= g;
+    const float e = nc_expf(p ? -g : g);
+    const float sig = nc::div_rn(p ? 1.0f : e, __fadd_rn(e, 1.0f));
+    return __fmul_rn(__fmul_rn(g, sig), u);
+}
+
+// The SwiGLU pair: gate row n and up row n read by the same lane group, sharing
+// the activation chunks (the reference's gate and up share one k loop,
+// fusion.py:677-711), then h[m, n] = silu(gate) * up with each projection's
+// own epilogue (f32(acc) * xs[m]) * scales[n].
+template <int KS, int L, int MT>
+__global__ __launch_bounds__(64) void gemv_i8_token_swiglu(
+    float *__restrict__ h, const int8_t *__restrict__ xq, const float *__restrict__ xs,
+    const int8_t *__restrict__ qg, const float *__restrict__ wsg, const int8_t *__restrict__ qu,
+    const float *__restrict__ wsu, int M, int N, int Kr) {
+    constexpr int ROWS = 64 / L;
+    constexpr int STEP = L * 16;
+    const int K = KS ? KS : Kr;
+    extern __shared__ __align__(16) int8_t sx[];
+    const int m0 = blockIdx.y * MT;
+    const int mt = min(MT, M - m0);
+    const int chunks = K / 16;
+    for (int i = threadIdx.x; i < MT * chunks; i += 64) {
+        const int m = i / chunks, c = i - m * chunks;
+        i8x16 v = {};
+        if (m < mt) v = nc::load16(xq + (size_t)(m0 + m) * K + c * 16);
+        *reinterpret_cast<i8x16 *>(sx + m * K + c * 16) = v;
+    }
+    __syncthreads();
+    const int lane = threadIdx.x;
+    const int sub = lane & (L - 1), grp = lane / L;
+    const int n = blockIdx.x * ROWS + grp;
+    int32_t ag[MT], au[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) ag[m] = au[m] = 0;
+    if (n < N) {
+        const int8_t *rg = qg + (size_t)n * K, *ru = qu + (size_t)n * K;
+        const int iters = (K + STEP - 1) / STEP;
+#pragma unroll
+        for (int it = 0; it < iters; ++it) {
+            const int c = it * STEP + sub * 16;
+            if (K % STEP == 0 || c < K) {
+                const i8x16 wg = nc::load16_stream(rg + c), wu = nc::load16_stream(ru + c);
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    const i8x16 x = *reinterpret_cast<const i8x16 *>(sx + m * K + c);
+                    ag[m] = nc::dot16(wg, x, ag[m]);
+                    au[m] = nc::dot16(wu, x, au[m]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        ag[m] = nc::group_sum_i32<L>(ag[m]);
+        au[m] = nc::group_sum_i32<L>(au[m]);
+    }
+    if (sub == 0 && n < N) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            if (m >= mt) break;
+            const float x = xs[m0 + m];
+            const float g = __fmul_rn(__fmul_rn((float)ag[m], x), wsg[n]);
+            const float u = __fmul_rn(__fmul_rn((float)au[m], x), wsu[n]);
+            h[(size_t)(m0 + m) * N + n] = silu_mul(g, u);
         }
     }
 }
@@ -224,4 +297,64 @@ NC_EXPORT int32_t nc_matmul_i8_token_stacked(void **p, const int64_t *s) {
     Args a{p[0], (const int8_t *)p[1], (const float *)p[2], (const int8_t *)p[3], (const float *)p[4],
            nullptr, nullptr, (int)s[1], (int)s[2], (int)s[3], (int)s[0]};
     return run<false>(a, (int)s[4]);
+}
+
+namespace {
+template <int KS, int MT>
+int32_t launch_swiglu(float *h, const int8_t *xq, const float *xs, const int8_t *qg, const float *wsg,
+                      const int8_t *qu, const float *wsu, int M, int N, int K) {
+    constexpr int L = 8;
+    dim3 grid((N + 64 / L - 1) / (64 / L), (M + MT - 1) / MT);
+    hipLaunchKernelGGL((gemv_i8_token_swiglu<KS, L, MT>), grid, dim3(64), (size_t)MT * K, nc::stream(), h, xq, xs,
+                       qg, wsg, qu, wsu, M, N, K);
+    return nc::launched("gemv_i8_token_swiglu");
+}
+
+template <int KS>
+int32_t swiglu_tokens(float *h, const int8_t *xq, const float *xs, const int8_t *qg, const float *wsg,
+                      const int8_t *qu, const float *wsu, int M, int N, int K) {
+    if (M == 1) return launch_swiglu<KS, 1>(h, xq, xs, qg, wsg, qu, wsu, M, N, K);
+    if (M <= 4) return launch_swiglu<KS, 4>(h, xq, xs, qg, wsg, qu, wsu, M, N, K);
+    return launch_swiglu<KS, 8>(h, xq, xs, qg, wsg, qu, wsu, M, N, K);
+}
+}  // namespace
+
+// h = silu((f32(xq @ qg.T) * xs) * sg) * ((f32(xq @ qu.T) * xs) * su), one kernel.
+// p: [h f32[M,N], xq i8[M,K], xs f32[M], qg i8[N,K], sg f32[N], qu i8[N,K], su f32[N]];
+// s: [M, N, K]  (K a multiple of 16, at most 8192)
+NC_EXPORT int32_t nc_matmul_i8_token_swiglu(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3] && p[4] && p[5] && p[6],
+               "nc_matmul_i8_token_swiglu: null operand");
+    NC_REQUIRE(s[0] >= 0 && s[1] >= 0 && s[2] > 0 && s[2] % 16 == 0 && s[2] <= 8192 && s[0] < (1 << 24) &&
+                   s[1] < (1 << 24),
+               "nc_matmul_i8_token_swiglu: bad shape (K must be a multiple of 16, at most 8192)");
+    const int M = (int)s[0], N = (int)s[1], K = (int)s[2];
+    if (M == 0 || N == 0) return NC_OK;
+    float *h = (float *)p[0];
+    auto xq = (const int8_t *)p[1];
+    auto xs = (const float *)p[2];
+    auto qg = (const int8_t *)p[3];
+    auto sg = (const float *)p[4];
+    auto qu = (const int8_t *)p[5];
+    auto su = (const float *)p[6];
+    if (K == 896) return swiglu_tokens<896>(h, xq, xs, qg, sg, qu, su, M, N, K);
+    return swiglu_tokens<0>(h, xq, xs, qg, sg, qu, su, M, N, K);
+}
+
+namespace {
+__global__ void silu_mul_rows(float *__restrict__ y, const float *__restrict__ g, const float *__restrict__ u,
+                              int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = silu_mul(g[i], u[i]);
+}
+}  // namespace
+
+// y = silu(g) * u elementwise (nn.py:41-54, the epilogue fusion puts on gate and up).
+// p: [y f32[n], g f32[n], u f32[n]];  s: [n]
+NC_EXPORT int32_t nc_silu_mul(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2] && s[0] >= 0 && s[0] < (1LL << 40), "nc_silu_mul: bad operand");
+    if (s[0] == 0) return NC_OK;
+    hipLaunchKernelGGL(silu_mul_rows, dim3((unsigned)((s[0] + 255) / 256)), dim3(256), 0, nc::stream(),
+                       (float *)p[0], (const float *)p[1], (const float *)p[2], s[0]);
+    return nc::launched("silu_mul_rows");
 }

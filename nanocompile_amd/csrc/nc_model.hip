@@ -1,0 +1,154 @@
+// The model's ends: the embedding gather, the float32 LM head and the argmax.
+//
+// * Gather (lower.py:420-444, fusion.py:712-731): rows of the table by index;
+//   an index outside 0..V-1 is the reference's Fail code 1, recorded in the
+//   library's device error word (nc_sync returns it) and the row left zero.
+// * LM head (models/qwen2.py:210-221, A15 in the reference's matmul kernel,
+//   lower.py:255-269): logits[n] = sum over k of x[k] * E[n, k], one
+//   accumulator, multiply then add, k in order. That is the reference's own
+//   bit pattern. The table is read in a packed layout (the reference's pack,
+//   schedule.py:362-395, runtime.py:157-164): blocks of 64 rows, and within a
+//   block 4 consecutive k of each row together, so the 64 lanes of a wave read
+//   1 KB contiguous per load while each lane still walks its own row in order.
+// * Argmax: the first index of the largest logit (numpy.argmax), folded into
+//   the LM head as a 64-bit atomic maximum of (ordered value bits, ~index), so
+//   ties go to the smallest index whatever order the waves finish in.
+#include "nc_common.h"
+
+namespace {
+
+__global__ __launch_bounds__(256) void embed_rows(float *__restrict__ x, const float *__restrict__ table,
+                                                  const int64_t *__restrict__ ids, int H, int64_t V,
+                                                  int32_t *__restrict__ error) {
+    const int m = blockIdx.x;
+    const int64_t id = ids[m];
+    const bool bad = id < 0 || id >= V;
+    if (bad && threadIdx.x == 0) atomicCAS(error, 0, NC_FAIL_INDEX);
+    const float *row = table + (bad ? 0 : id) * (int64_t)H;
+    for (int k = threadIdx.x; k < H; k += 256) x[(size_t)m * H + k] = bad ? 0.0f : row[k];
+}
+
+// Packed index of (n, k): ((n / 64) * (H / 4) + k / 4) * 256 + (n % 64) * 4 + k % 4.
+__global__ __launch_bounds__(256) void pack_rows64(float *__restrict__ packed, const float *__restrict__ table,
+                                                   int64_t V, int H) {
+    const int64_t blk = blockIdx.x;
+    const int k4n = H / 4;
+    for (int i = threadIdx.x; i < k4n * 64; i += 256) {
+        const int k4 = i / 64, lane = i % 64;
+        const int64_t n = blk * 64 + lane;
+        float4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (n < V) v = *reinterpret_cast<const float4 *>(table + n * H + k4 * 4);
+        reinterpret_cast<float4 *>(packed)[(blk * k4n + k4) * 64 + lane] = v;
+    }
+}
+
+__device__ __forceinline__ unsigned long long argmax_key(float v, int64_t n) {
+    uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)ord << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)n);
+}
+
+template <int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void lm_head(float *__restrict__ logits, unsigned long long *__restrict__ best,
+                                                      const float *__restrict__ x, const float4 *__restrict__ packed,
+                                                      int64_t V, int H) {
+    extern __shared__ float sxh[];
+    const int m = blockIdx.y;
+    for (int i = threadIdx.x; i < H; i += 64 * WAVES) sxh[i] = x[(size_t)m * H + i];
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t blk = (int64_t)blockIdx.x * WAVES + wave;
+    const int64_t n = blk * 64 + lane;
+    if (blk * 64 >= V) return;
+    const int k4n = H / 4;
+    const float4 *e = packed + blk * k4n * 64 + lane;
+    float acc = 0.0f;
+#pragma unroll 8
+    for (int k4 = 0; k4 < k4n; ++k4) {
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+        const f32x4 w = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(e + (size_t)k4 * 64));
+        const float4 xv = *reinterpret_cast<const float4 *>(sxh + 4 * k4);
+        acc = __fadd_rn(acc, __fmul_rn(xv.x, w.x));
+        acc = __fadd_rn(acc, __fmul_rn(xv.y, w.y));
+        acc = __fadd_rn(acc, __fmul_rn(xv.z, w.z));
+        acc = __fadd_rn(acc, __fmul_rn(xv.w, w.w));
+    }
+    const bool valid = n < V;
+    if (logits && valid) logits[(size_t)m * V + n] = acc;
+    if (best) {
+        unsigned long long key = valid ? argmax_key(acc, n) : 0ull;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const unsigned long long other = __shfl_xor(key, off, 64);
+            key = other > key ? other : key;
+        }
+        if (lane == 0) atomicMax(best + m, key);
+    }
+}
+
+__global__ void fill_u64(unsigned long long *p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0ull;
+}
+
+__global__ void argmax_decode(int64_t *__restrict__ index, const unsigned long long *__restrict__ best, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) index[i] = (int64_t)(0xFFFFFFFFu - (uint32_t)(best[i] & 0xFFFFFFFFull));
+}
+
+}  // namespace
+
+// p: [x f32[M,H], table f32[V,H], ids i64[M]];  s: [M, H, V]
+NC_EXPORT int32_t nc_embed(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2], "nc_embed: null operand");
+    NC_REQUIRE(s[0] >= 0 && s[0] < (1 << 30) && s[1] > 0 && s[1] < (1 << 24) && s[2] > 0, "nc_embed: bad shape");
+    if (s[0] == 0) return NC_OK;
+    hipLaunchKernelGGL(embed_rows, dim3((unsigned)s[0]), dim3(256), 0, nc::stream(), (float *)p[0],
+                       (const float *)p[1], (const int64_t *)p[2], (int)s[1], s[2], nc::error_word());
+    return nc::launched("embed_rows");
+}
+
+// The LM head's packed table: p: [packed f32[ceil(V/64)*64, H], table f32[V,H]];  s: [V, H] (H % 4 == 0)
+NC_EXPORT int32_t nc_pack_rows64(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1], "nc_pack_rows64: null operand");
+    NC_REQUIRE(s[0] > 0 && s[1] > 0 && s[1] % 4 == 0 && s[1] < (1 << 20) && s[0] < (1LL << 31),
+               "nc_pack_rows64: bad shape (H must be a multiple of 4)");
+    hipLaunchKernelGGL(pack_rows64, dim3((unsigned)((s[0] + 63) / 64)), dim3(256), 0, nc::stream(), (float *)p[0],
+                       (const float *)p[1], s[0], (int)s[1]);
+    return nc::launched("pack_rows64");
+}
+
+// logits[m, n] = sum_k x[m, k] * table[n, k] in k order, and best[m] the
+// argmax key of row m (atomic maximum: clear it first with nc_argmax_clear).
+// p: [logits f32[M,V] | NULL, best u64[M] | NULL, x f32[M,H], packed table];  s: [M, V, H]
+NC_EXPORT int32_t nc_lm_head(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[2] && p[3] && (p[0] || p[1]), "nc_lm_head: null operand");
+    NC_REQUIRE(s[0] >= 0 && s[0] < 65536 && s[1] > 0 && s[1] < (1LL << 31) && s[2] > 0 && s[2] % 4 == 0 &&
+                   s[2] <= 16384,
+               "nc_lm_head: bad shape (H a multiple of 4, at most 16384)");
+    if (s[0] == 0) return NC_OK;
+    constexpr int W = 4;
+    const int64_t blocks = (s[1] + 63) / 64;
+    hipLaunchKernelGGL((lm_head<W>), dim3((unsigned)((blocks + W - 1) / W), (unsigned)s[0]), dim3(64 * W),
+                       (size_t)s[2] * sizeof(float), nc::stream(), (float *)p[0], (unsigned long long *)p[1],
+                       (const float *)p[2], (const float4 *)p[3], s[1], (int)s[2]);
+    return nc::launched("lm_head");
+}
+
+// p: [best u64[n]];  s: [n]
+NC_EXPORT int32_t nc_argmax_clear(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && s[0] >= 0 && s[0] < (1 << 24), "nc_argmax_clear: bad operand");
+    if (s[0] == 0) return NC_OK;
+    hipLaunchKernelGGL(fill_u64, dim3((unsigned)((s[0] + 255) / 256)), dim3(256), 0, nc::stream(),
+                       (unsigned long long *)p[0], (int)s[0]);
+    return nc::launched("fill_u64");
+}
+
+// p: [index i64[n], best u64[n]];  s: [n]
+NC_EXPORT int32_t nc_argmax_index(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1] && s[0] >= 0 && s[0] < (1 << 24), "nc_argmax_index: bad operand");
+    if (s[0] == 0) return NC_OK;
+    hipLaunchKernelGGL(argmax_decode, dim3((unsigned)((s[0] + 255) / 256)), dim3(256), 0, nc::stream(),
+                       (int64_t *)p[0], (const unsigned long long *)p[1], (int)s[0]);
+    return nc::launched("argmax_decode");
+}

@@ -1,0 +1,288 @@
+"""Qwen2 on the HIP kernels: the reference's model driver (models/qwen2.py), MI355X-side.
+
+The reference compiles one graph over (seq, past) and runs it a kernel call at
+a time from Python, with the KV cache in host memory (models/qwen2.py:167-345,
+runtime.py:245-301). Here the same forward pass is a fixed sequence of HIP
+kernels per layer, the weights and the KV cache live on the device, and the
+driver only uploads token ids and downloads what the caller asks for:
+
+    rms_norm + per-token int8 ......... nc_rms_norm_quant
+    q, k, v projections + bias ........ nc_matmul_i8_token (rows concatenated)
+    RoPE, cache append ................ nc_rope_append
+    attention (GQA, causal) ........... nc_attention
+    per-token int8 of the context ..... nc_quantize_token_i8
+    o projection + residual ........... nc_matmul_i8_token (in place on x)
+    rms_norm + per-token int8 ......... nc_rms_norm_quant
+    gate, up, silu(gate) * up ......... nc_matmul_i8_token_swiglu
+    per-token int8 of h ............... nc_quantize_token_i8
+    down projection + residual ........ nc_matmul_i8_token (in place on x)
+
+then the final rms_norm, the float32 tied LM head (the reference keeps it
+float32, quantize.py:24-28) and the argmax. ``quantization="int8-token"`` is
+the north star's mode: per-row int8 weights, per-token int8 activations,
+exact int32 accumulation.
+
+Memory: the weights go into one device arena, made once; activations for up
+to ``max_tokens`` new tokens into a second, also made once; the KV cache is a
+device array per sequence (``new_cache``), so a decode step moves nothing but
+a token id in and (optionally) a row of logits out.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Mapping, Sequence
+
+import numpy as np
+
+from nanocompile_amd import hip
+from nanocompile_amd.hip import DeviceArray
+from nanocompile_amd.kernels import float_bits
+from nanocompile_amd.models.config import Qwen2Config
+
+QUANTIZATIONS = ("int8-token",)
+ALIGN = 256
+
+
+def inverse_frequencies(head_dim: int, theta: float) -> np.ndarray:
+    """RoPE's per-plane rates in float32, as the reference computes them (nn.py:69-75)."""
+    exponent = np.arange(0, head_dim, 2, dtype=np.int64).astype(np.float32) / np.float32(head_dim)
+    return (np.float32(1.0) / (np.float32(theta) ** exponent)).astype(np.float32)
+
+
+class Arena:
+    """One device allocation carved into aligned arrays (the reference's arena, runtime.py:39, 97-143)."""
+
+    def __init__(self, nbytes: int) -> None:
+        self.base = DeviceArray((max(1, nbytes),), np.uint8)
+        self.top = 0
+
+    @staticmethod
+    def size(shapes: Sequence[tuple[tuple[int, ...], np.dtype]]) -> int:
+        total = 0
+        for shape, dtype in shapes:
+            total += -(-int(np.prod(shape, dtype=np.int64)) * np.dtype(dtype).itemsize // ALIGN) * ALIGN
+        return total
+
+    def take(self, shape, dtype) -> DeviceArray:
+        nbytes = int(np.prod(shape, dtype=np.int64)) * np.dtype(dtype).itemsize
+        view = self.base.view(shape, dtype, offset_bytes=self.top)
+        self.top += -(-nbytes // ALIGN) * ALIGN
+        return view
+
+
+class KVCache:
+    """Keys and values of one sequence on the device: ``[layers, kv_heads, capacity, head_dim]`` each.
+
+    The reference grows its host cache by doubling (models/qwen2.py:232-271);
+    on the device the capacity is fixed when the cache is made, since 288 GB
+    of HBM leaves room to size it for the whole sequence up front.
+    """
+
+    def __init__(self, config: Qwen2Config, capacity: int = 256) -> None:
+        if capacity <= 0:
+            raise ValueError(f"capacity must be positive, got {capacity}")
+        self.config, self.capacity, self.length = config, capacity, 0
+        shape = (config.num_hidden_layers, config.num_key_value_heads, capacity, config.head_dim)
+        self.keys, self.values = DeviceArray(shape, np.float32), DeviceArray(shape, np.float32)
+        self._layer = config.num_key_value_heads * capacity * config.head_dim * 4
+
+    def layer(self, index: int) -> tuple[int, int]:
+        return self.keys.ptr + index * self._layer, self.values.ptr + index * self._layer
+
+    def past(self) -> tuple[np.ndarray, np.ndarray]:
+        """The filled part, copied to the host (the reference's ``KVCache.past``)."""
+        return self.keys.numpy()[:, :, : self.length], self.values.numpy()[:, :, : self.length]
+
+
+class Qwen2:
+    """The model's front door on the GPU: token ids in, logits out (models/qwen2.py:278-345)."""
+
+    def __init__(self, config: Qwen2Config, weights: Mapping[str, np.ndarray], quantization: str = "int8-token",
+                 max_tokens: int = 512, device: int = 0) -> None:
+        if quantization not in QUANTIZATIONS:
+            raise ValueError(f"quantization must be one of {QUANTIZATIONS}")
+        hip.init(device)
+        self.config, self.quantization, self.max_tokens = config, quantization, max_tokens
+        c = config
+        H, I, D = c.hidden_size, c.intermediate_size, c.head_dim
+        Q, KVW = c.num_attention_heads * D, c.num_key_value_heads * D
+        W = Q + 2 * KVW
+        self.width = W
+        L, V = c.num_hidden_layers, c.vocab_size
+        if H % 4 or H % 16 or I % 16:
+            raise ValueError("hidden and intermediate sizes must be multiples of 16")
+        vblocks = -(-V // 64) * 64
+
+        per_layer = [((H,), np.float32), ((H,), np.float32), ((W, H), np.int8), ((W,), np.float32),
+                     ((W,), np.float32), ((H, Q), np.int8), ((H,), np.float32), ((I, H), np.int8),
+                     ((I,), np.float32), ((I, H), np.int8), ((I,), np.float32), ((H, I), np.int8), ((H,), np.float32)]
+        shapes = per_layer * L + [((V, H), np.float32), ((vblocks, H), np.float32), ((H,), np.float32),
+                                  ((D // 2,), np.float32)]
+        self.weights = Arena(Arena.size(shapes))
+        stage = DeviceArray((max(I * H, W * H, H * Q),), np.float32)     # f32 staging for quantization
+
+        def upload(name: str, into: DeviceArray) -> DeviceArray:
+            into.upload(np.ascontiguousarray(weights[name], np.float32))
+            return into
+
+        def quantized(names: Sequence[str], rows: int, k: int) -> tuple[DeviceArray, DeviceArray]:
+            """Per-row int8 of the named matrices stacked row-wise (quantize.py:55-70, on the device)."""
+            q, s = self.weights.take((rows, k), np.int8), self.weights.take((rows,), np.float32)
+            at = 0
+            for name in names:
+                w = np.ascontiguousarray(weights[name], np.float32)
+                n = w.shape[0]
+                if w.shape[1] != k:
+                    raise ValueError(f"{name} has width {w.shape[1]}, expected {k}")
+                view = stage.view(w.shape, np.float32)
+                view.upload(w)
+                hip.call("nc_quantize_rows_i8", [q.ptr + at * k, s.ptr + at * 4, view], [n, k])
+                hip.sync()
+                at += n
+            if at != rows:
+                raise ValueError(f"{names} have {at} rows, expected {rows}")
+            return q, s
+
+        self.layers = []
+        for i in range(L):
+            p = f"model.layers.{i}"
+            a = f"{p}.self_attn"
+            layer = {
+                "g1": upload(f"{p}.input_layernorm.weight", self.weights.take((H,), np.float32)),
+                "g2": upload(f"{p}.post_attention_layernorm.weight", self.weights.take((H,), np.float32)),
+            }
+            layer["qkv"] = quantized([f"{a}.q_proj.weight", f"{a}.k_proj.weight", f"{a}.v_proj.weight"], W, H)
+            bias = self.weights.take((W,), np.float32)
+            bias.upload(np.concatenate([weights[f"{a}.{n}_proj.bias"] for n in "qkv"]).astype(np.float32))
+            layer["qkv_b"] = bias
+            layer["o"] = quantized([f"{a}.o_proj.weight"], H, Q)
+            layer["gate"] = quantized([f"{p}.mlp.gate_proj.weight"], I, H)
+            layer["up"] = quantized([f"{p}.mlp.up_proj.weight"], I, H)
+            layer["down"] = quantized([f"{p}.mlp.down_proj.weight"], H, I)
+            self.layers.append(layer)
+        self.embed = upload("model.embed_tokens.weight", self.weights.take((V, H), np.float32))
+        head = self.embed
+        if not c.tie_word_embeddings:
+            head = DeviceArray.from_host(np.ascontiguousarray(weights["lm_head.weight"], np.float32))
+        self.head = self.weights.take((vblocks, H), np.float32)
+        hip.call("nc_pack_rows64", [self.head, head], [V, H])
+        self.norm = upload("model.norm.weight", self.weights.take((H,), np.float32))
+        self.inv_freq = self.weights.take((D // 2,), np.float32)
+        self.inv_freq.upload(inverse_frequencies(D, c.rope_theta))
+        self.scale = float(np.float32(D ** -0.5))
+        hip.sync()
+        del stage
+
+        M = max_tokens
+        act = [((M, H), np.float32), ((M, W), np.float32), ((M, Q), np.float32), ((M, I), np.float32),
+               ((M, max(I, H, Q)), np.int8), ((M,), np.float32), ((M, H), np.float32), ((M,), np.int64),
+               ((M,), np.uint64), ((1, V), np.float32), ((M,), np.int64)]
+        self.acts = Arena(Arena.size(act))
+        self.x, self.qkv = self.acts.take((M, H), np.float32), self.acts.take((M, W), np.float32)
+        self.ctx, self.h = self.acts.take((M, Q), np.float32), self.acts.take((M, I), np.float32)
+        self.xq, self.xs = self.acts.take((M, max(I, H, Q)), np.int8), self.acts.take((M,), np.float32)
+        self.normed, self.ids = self.acts.take((M, H), np.float32), self.acts.take((M,), np.int64)
+        self.best, self.logits_row = self.acts.take((M,), np.uint64), self.acts.take((1, V), np.float32)
+        self.argmax = self.acts.take((M,), np.int64)
+
+    # -- running ---------------------------------------------------------------------
+
+    def new_cache(self, capacity: int = 256) -> KVCache:
+        return KVCache(self.config, capacity)
+
+    def _layers(self, m: int, past: int, cache: KVCache) -> None:
+        """The decoder layers over m new tokens at positions past .. past + m - 1."""
+        c = self.config
+        H, I, D = c.hidden_size, c.intermediate_size, c.head_dim
+        heads, kv, W = c.num_attention_heads, c.num_key_value_heads, self.width
+        Q = heads * D
+        eps = float_bits(c.rms_norm_eps)
+        for i, w in enumerate(self.layers):
+            kc, vc = cache.layer(i)
+            hip.call("nc_rms_norm_quant", [None, self.xq, self.xs, self.x, w["g1"]], [m, H, eps])
+            q, s = w["qkv"]
+            hip.call("nc_matmul_i8_token", [self.qkv, self.xq, self.xs, q, s, w["qkv_b"], None], [m, W, H, 0])
+            hip.call("nc_rope_append", [self.qkv, kc, vc, self.inv_freq], [m, heads, kv, D, past, cache.capacity])
+            hip.call("nc_attention", [self.ctx, self.qkv, kc, vc],
+                     [m, heads, kv, D, past, cache.capacity, float_bits(self.scale)])
+            hip.call("nc_quantize_token_i8", [self.xq, self.xs, self.ctx], [m, Q])
+            q, s = w["o"]
+            hip.call("nc_matmul_i8_token", [self.x, self.xq, self.xs, q, s, None, self.x], [m, H, Q, 0])
+            hip.call("nc_rms_norm_quant", [None, self.xq, self.xs, self.x, w["g2"]], [m, H, eps])
+            (qg, sg), (qu, su) = w["gate"], w["up"]
+            hip.call("nc_matmul_i8_token_swiglu", [self.h, self.xq, self.xs, qg, sg, qu, su], [m, I, H])
+            hip.call("nc_quantize_token_i8", [self.xq, self.xs, self.h], [m, I])
+            q, s = w["down"]
+            hip.call("nc_matmul_i8_token", [self.x, self.xq, self.xs, q, s, None, self.x], [m, H, I, 0])
+
+    def forward(self, token_ids: Sequence[int] | np.ndarray, cache: KVCache | None = None,
+                last_only: bool = False) -> np.ndarray:
+        """Logits for ``token_ids``, the tokens not already in ``cache`` (models/qwen2.py:316-345)."""
+        ids = np.asarray(token_ids, dtype=np.int64)
+        if ids.ndim != 1 or ids.size == 0:
+            raise ValueError(f"expected a non-empty 1-D sequence of token IDs, got {ids.shape}")
+        m = int(ids.size)
+        if m > self.max_tokens:
+            raise ValueError(f"{m} tokens in one forward; this model was made for at most {self.max_tokens}")
+        if cache is None:
+            cache = self.new_cache(m)
+        past = cache.length
+        if past + m > cache.capacity:
+            raise ValueError(f"the cache holds {cache.capacity} tokens; {past} + {m} do not fit")
+        c = self.config
+        H, V = c.hidden_size, c.vocab_size
+        self.ids.view((m,)).upload(ids)
+        hip.call("nc_embed", [self.x, self.embed, self.ids], [m, H, V])
+        self._layers(m, past, cache)
+        rows = 1 if last_only else m
+        first = m - rows
+        x_rows = self.x.ptr + first * H * 4
+        hip.call("nc_rms_norm_quant", [self.normed, self.xq, self.xs, x_rows, self.norm],
+                 [rows, H, float_bits(c.rms_norm_eps)])
+        logits = self.logits_row if rows == 1 else DeviceArray((rows, V), np.float32)
+        hip.call("nc_lm_head", [logits, None, self.normed, self.head], [rows, V, H])
+        hip.sync()
+        cache.length = past + m
+        return logits.numpy()[:rows]
+
+    def next_token(self, token_ids, cache: KVCache) -> int:
+        """Greedy's step on the device: forward the new tokens, return the argmax of the last row."""
+        ids = np.asarray(token_ids, dtype=np.int64)
+        m = int(ids.size)
+        past = cache.length
+        if m == 0 or m > self.max_tokens or past + m > cache.capacity:
+            raise ValueError("token count outside the model's or the cache's limits")
+        c = self.config
+        H, V = c.hidden_size, c.vocab_size
+        self.ids.view((m,)).upload(ids)
+        hip.call("nc_embed", [self.x, self.embed, self.ids], [m, H, V])
+        self._layers(m, past, cache)
+        hip.call("nc_rms_norm_quant", [self.normed, self.xq, self.xs, self.x.ptr + (m - 1) * H * 4, self.norm],
+                 [1, H, float_bits(c.rms_norm_eps)])
+        hip.call("nc_argmax_clear", [self.best], [1])
+        hip.call("nc_lm_head", [None, self.best, self.normed, self.head], [1, V, H])
+        hip.call("nc_argmax_index", [self.argmax, self.best], [1])
+        out = np.empty(1, np.int64)
+        hip.load().nc_memcpy_d2h(out.ctypes.data, self.argmax.ptr, 8)
+        hip.sync()
+        cache.length = past + m
+        return int(out[0])
+
+
+def greedy(model: Qwen2, prompt_ids: Sequence[int], max_new_tokens: int, use_cache: bool = True) -> list[int]:
+    """Argmax decoding (models/qwen2.py:348-368)."""
+    if not prompt_ids:
+        raise ValueError("cannot generate from an empty prompt")
+    ids = list(prompt_ids)
+    cache = model.new_cache(len(ids) + max_new_tokens) if use_cache else None
+    pending = ids
+    generated: list[int] = []
+    for _ in range(max_new_tokens):
+        if use_cache:
+            token = model.next_token(pending, cache)
+        else:
+            token = int(np.argmax(model.forward(pending, last_only=True)[0]))
+        generated.append(token)
+        ids.append(token)
+        pending = [token] if use_cache else ids
+    return generated

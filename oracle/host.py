@@ -30,6 +30,7 @@ def load() -> ctypes.CDLL:
         lib.nc_host_time_matmul_i8_token.restype = ctypes.c_double
         lib.nc_host_read_gbps.argtypes = [_P, _I, _I]
         lib.nc_host_read_gbps.restype = ctypes.c_double
+        lib.nc_host_math.argtypes = [ctypes.c_int, _P, _P, _I]
         _LIB = lib
     return _LIB
 
@@ -83,3 +84,75 @@ def time_matmul_i8_token(xq, xs, q_copies, ws_copies, reps: int) -> float:
 def read_gbps(nbytes: int = 1 << 30, reps: int = 3) -> float:
     buf = np.ones(nbytes // 8, np.int64)
     return load().nc_host_read_gbps(_ptr(buf), buf.nbytes, reps)
+
+
+MATH_KINDS = {"nc_exp": 0, "nc_sin": 1, "nc_cos": 2, "exp": 3, "sin": 4, "cos": 5}
+
+
+def math(kind: str, x) -> np.ndarray:
+    """Elementwise nc_expf/nc_sinf/nc_cosf (the shared GPU/host functions) or libm's expf/sinf/cosf."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    load().nc_host_math(MATH_KINDS[kind], _ptr(out), _ptr(x), x.size)
+    return out
+
+
+def _sig(name, n_ptr, n_int, extra=()):
+    fn = getattr(load(), name)
+    fn.argtypes = [_P] * n_ptr + [_I] * n_int + list(extra)
+    return fn
+
+
+def softmax_causal(s, past: int) -> np.ndarray:
+    """softmax(s + causal mask) over rows of s[heads, seq, past + seq], in the GPU kernel's order."""
+    s = np.ascontiguousarray(s, np.float32)
+    heads, seq, _ = s.shape
+    y = np.empty_like(s)
+    _sig("nc_host_softmax_causal", 2, 3)(_ptr(y), _ptr(s), heads, seq, past)
+    return y
+
+
+def rope(x, inv_freq, past: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    heads, seq, d = x.shape
+    y = np.empty_like(x)
+    _sig("nc_host_rope", 3, 4)(_ptr(y), _ptr(x), _ptr(np.ascontiguousarray(inv_freq, np.float32)), heads, seq, d, past)
+    return y
+
+
+def silu_mul(g, u) -> np.ndarray:
+    g, u = np.ascontiguousarray(g, np.float32), np.ascontiguousarray(u, np.float32)
+    y = np.empty_like(g)
+    _sig("nc_host_silu_mul", 3, 1)(_ptr(y), _ptr(g), _ptr(u), g.size)
+    return y
+
+
+def rms_norm_quant(x, gamma, eps: float):
+    x = np.ascontiguousarray(x, np.float32)
+    m, k = x.shape
+    normed, xq, xs = np.empty_like(x), np.empty((m, k), np.int8), np.empty(m, np.float32)
+    _sig("nc_host_rms_norm_quant", 5, 2, [ctypes.c_float])(_ptr(normed), _ptr(xq), _ptr(xs), _ptr(x),
+                                                            _ptr(np.ascontiguousarray(gamma, np.float32)), m, k, eps)
+    return normed, xq, xs
+
+
+def rope_append_attention(qkv, kcache, vcache, inv_freq, heads: int, kv: int, d: int, past: int, scale: float):
+    """RoPE + cache append (in place on qkv and the caches), then attention; returns the context."""
+    m = qkv.shape[0]
+    cap = kcache.shape[1]
+    inv_freq = np.ascontiguousarray(inv_freq, np.float32)
+    _sig("nc_host_rope_append", 4, 6)(_ptr(qkv), _ptr(kcache), _ptr(vcache), _ptr(inv_freq), m, heads, kv, d,
+                                      past, cap)
+    ctx = np.empty((m, heads * d), np.float32)
+    _sig("nc_host_attention", 4, 6, [ctypes.c_float])(_ptr(ctx), _ptr(qkv), _ptr(kcache), _ptr(vcache), m, heads,
+                                                       kv, d, past, cap, scale)
+    return ctx
+
+
+def matmul_i8_token_swiglu(xq, xs, qg, sg, qu, su) -> np.ndarray:
+    m, k = xq.shape
+    n = qg.shape[0]
+    h = np.empty((m, n), np.float32)
+    args = [np.ascontiguousarray(a) for a in (xq, xs, qg, sg, qu, su)]
+    _sig("nc_host_matmul_i8_token_swiglu", 7, 3)(_ptr(h), *[_ptr(a) for a in args], m, n, k)
+    return h

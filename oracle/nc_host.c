@@ -25,11 +25,14 @@
 #include <time.h>
 #include <immintrin.h>
 
+/* The same expf/sinf/cosf the GPU kernels use (one source for both). */
+#include "../nanocompile_amd/csrc/nc_math.h"
+
 #define EXPORT __attribute__((visibility("default")))
 
 /* -- thread pool ----------------------------------------------------------- */
 
-typedef void (*task_fn)(void *ctx, int64_t i);
+#include "nc_host.h"
 
 static pthread_mutex_t g_mu = PTHREAD_MUTEX_INITIALIZER;
 static pthread_cond_t g_start = PTHREAD_COND_INITIALIZER;
@@ -86,7 +89,7 @@ EXPORT int nc_host_threads(void) { return g_threads; }
 /* Runs fn(ctx, i) for i in [0, n) on g_threads threads; returns when all are done.
  * Spawned workers beyond g_threads - 1 take part too (they only claim tasks),
  * which is harmless: the task count, not the thread count, defines the work. */
-static void pool_run(task_fn fn, void *ctx, int64_t n) {
+void nc_pool_run(task_fn fn, void *ctx, int64_t n) {
     if (g_threads <= 1 || n <= 1) {
         for (int64_t i = 0; i < n; ++i) fn(ctx, i);
         return;
@@ -249,11 +252,11 @@ static void gemv(float *y, int32_t *acc, const int8_t *xq, const float *xs, cons
     int32_t *xsum = m <= 64 ? stack_sums : (int32_t *)malloc(sizeof(int32_t) * (size_t)m);
     for (int64_t i = 0; i < m; ++i) xsum[i] = sum_bytes(xq + i * k, k);
     gemv_ctx c = {y, acc, xq, xs, q, ws, bias, residual, xsum, m, n, k, nc_host_isa()};
-    pool_run(gemv_task, &c, (n + ROW_BLOCK - 1) / ROW_BLOCK);
+    nc_pool_run(gemv_task, &c, (n + ROW_BLOCK - 1) / ROW_BLOCK);
     if (xsum != stack_sums) free(xsum);
 }
 
-/* y[M,N] = ((f32(xq @ q.T) * xs[m]) * ws[n]) (+ bias[n]) (residual[m,n] + ...) */
+/* y[M,N] = ((f32(xq @ q.T) * xs[m]) * ws[n]) (+ bias[n]) (residual[m,n] + ...); y may alias residual. */
 EXPORT void nc_host_matmul_i8_token(float *y, const int8_t *xq, const float *xs, const int8_t *q, const float *ws,
                                     const float *bias, const float *residual, int64_t m, int64_t n, int64_t k) {
     gemv(y, NULL, xq, xs, q, ws, bias, residual, m, n, k);
@@ -299,11 +302,28 @@ static void read_task(void *arg, int64_t i) {
 EXPORT double nc_host_read_gbps(const void *buf, int64_t bytes, int64_t reps) {
     int64_t chunks = 256, sums[256];
     read_ctx c = {(const int64_t *)buf, bytes / 8, chunks, sums};
-    pool_run(read_task, &c, chunks);
+    nc_pool_run(read_task, &c, chunks);
     double t0 = now();
-    for (int64_t r = 0; r < reps; ++r) pool_run(read_task, &c, chunks);
+    for (int64_t r = 0; r < reps; ++r) nc_pool_run(read_task, &c, chunks);
     double dt = now() - t0;
     volatile int64_t sink = sums[0];
     (void)sink;
     return (double)bytes * (double)reps / dt / 1e9;
+}
+
+/* Elementwise transcendental functions, for pinning nc_math.h against the C
+ * library the reference calls (codegen_c.py:58): kind 0-2 are nc_expf,
+ * nc_sinf, nc_cosf; 3-5 are libm's expf, sinf, cosf. */
+EXPORT void nc_host_math(int kind, float *out, const float *in, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        float x = in[i];
+        switch (kind) {
+            case 0: out[i] = nc_expf(x); break;
+            case 1: out[i] = nc_sinf(x); break;
+            case 2: out[i] = nc_cosf(x); break;
+            case 3: out[i] = expf(x); break;
+            case 4: out[i] = sinf(x); break;
+            default: out[i] = cosf(x); break;
+        }
+    }
 }

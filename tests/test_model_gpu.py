@@ -1,0 +1,210 @@
+"""The fused groups and the whole model on the GPU, against the host C oracle and the reference.
+
+Against the host oracle (oracle/nc_model.c, the GPU kernels' orders replayed
+in C with the same exp/sin/cos) everything is bitwise: every float, every
+token. Against the reference's own outputs (tests/golden, made by running the
+reference) the fused groups are held to the reference's tolerance.
+"""
+
+from __future__ import annotations
+
+from dataclasses import replace
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from nanocompile_amd.models.config import QWEN25_05B, TINY, TINY_STD, random_weights
+from oracle.host_model import inverse_frequencies
+from tests.conftest import bits
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden" / "golden.npz"
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(GOLDEN, allow_pickle=False)
+
+
+def run(name, outputs, inputs, sizes):
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import DeviceArray
+    outs = [DeviceArray(shape, np.float32) for shape in outputs]
+    ins = [a if a is None else DeviceArray.from_host(np.ascontiguousarray(a)) for a in inputs]
+    hip.call(name, outs + ins, sizes)
+    hip.sync()
+    return [o.numpy() for o in outs]
+
+
+# -- fused groups -------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("seq,past", [(1, 12), (5, 3)])
+def test_softmax_causal(gpu, host, golden, seq, past):
+    key = f"g4_softmax_{seq}_{past}"
+    s = golden[key + "_s"]
+    (y,) = run("nc_softmax_causal", [s.shape], [s], [s.shape[0], seq, past])
+    assert np.array_equal(bits(y), bits(host.softmax_causal(s, past)))
+    np.testing.assert_allclose(y, golden[key + "_y"], rtol=2e-6, atol=1e-6)
+
+
+def test_softmax_long_rows(gpu, host):
+    rng = np.random.default_rng(3)
+    s = (rng.standard_normal((3, 4, 1000 + 4)) * 5).astype(np.float32)
+    (y,) = run("nc_softmax_causal", [s.shape], [s], [3, 4, 1000])
+    assert np.array_equal(bits(y), bits(host.softmax_causal(s, 1000)))
+
+
+def test_silu_mul(gpu, host, golden):
+    g, u = golden["g4_silu_g"], golden["g4_silu_u"]
+    (y,) = run("nc_silu_mul", [g.shape], [g, u], [g.size])
+    assert np.array_equal(bits(y), bits(host.silu_mul(g, u)))
+    np.testing.assert_allclose(y, golden["g4_silu_y"], rtol=2e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("seq,past", [(1, 511), (7, 0), (2, 100000)])
+def test_rope(gpu, host, golden, seq, past):
+    key = f"g4_rope_{seq}_{past}"
+    x = golden[key + "_x"]
+    inv = inverse_frequencies(64, 1e6)
+    (y,) = run("nc_rope", [x.shape], [x, inv], [x.shape[0], seq, 64, past])
+    assert np.array_equal(bits(y), bits(host.rope(x, inv, past)))
+    np.testing.assert_allclose(y, golden[key + "_y"], rtol=2e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("m,past", [(1, 0), (1, 200), (6, 0), (5, 37)])
+def test_rope_append_and_attention(gpu, host, m, past):
+    """Qwen2.5-0.5B's attention shape: 14 query heads over 2 KV heads of 64."""
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import DeviceArray
+    from nanocompile_amd.kernels import float_bits
+    print(f"attention m={m} past={past}", flush=True)
+    heads, kv, d, cap = 14, 2, 64, 256
+    rng = np.random.default_rng(m * 1000 + past)
+    qkv = rng.standard_normal((m, (heads + 2 * kv) * d)).astype(np.float32)
+    kc = np.zeros((kv, cap, d), np.float32)
+    vc = np.zeros((kv, cap, d), np.float32)
+    kc[:, :past] = rng.standard_normal((kv, past, d))
+    vc[:, :past] = rng.standard_normal((kv, past, d))
+    inv = inverse_frequencies(d, 1e6)
+    scale = float(np.float32(d ** -0.5))
+    dq, dk, dv = DeviceArray.from_host(qkv), DeviceArray.from_host(kc), DeviceArray.from_host(vc)
+    ctx = DeviceArray((m, heads * d), np.float32)
+    hip.call("nc_rope_append", [dq, dk, dv, DeviceArray.from_host(inv)], [m, heads, kv, d, past, cap])
+    hip.call("nc_attention", [ctx, dq, dk, dv], [m, heads, kv, d, past, cap, float_bits(scale)])
+    hip.sync()
+    hq, hk, hv = qkv.copy(), kc.copy(), vc.copy()
+    expected = host.rope_append_attention(hq, hk, hv, inv, heads, kv, d, past, scale)
+    assert np.array_equal(bits(dq.numpy()), bits(hq))
+    assert np.array_equal(bits(dk.numpy()), bits(hk)) and np.array_equal(bits(dv.numpy()), bits(hv))
+    assert np.array_equal(bits(ctx.numpy()), bits(expected))
+
+
+def test_swiglu_pair(gpu, host):
+    from nanocompile_amd import kernels
+    rng = np.random.default_rng(9)
+    for m in (1, 3, 9):
+        xq = rng.integers(-127, 128, (m, 896)).astype(np.int8)
+        xs = (rng.random(m) * 0.1).astype(np.float32)
+        qg, qu = (rng.integers(-127, 128, (4864, 896)).astype(np.int8) for _ in range(2))
+        sg, su = ((rng.random(4864) * 1e-3).astype(np.float32) for _ in range(2))
+        (h,) = run("nc_matmul_i8_token_swiglu", [(m, 4864)], [xq, xs, qg, sg, qu, su], [m, 4864, 896])
+        assert np.array_equal(bits(h), bits(host.matmul_i8_token_swiglu(xq, xs, qg, sg, qu, su)))
+    del kernels
+
+
+def test_lm_head_and_argmax(gpu):
+    """The reference's k-order sum (checked in exact arithmetic bounds) and numpy.argmax."""
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import DeviceArray
+    rng = np.random.default_rng(4)
+    v, h = 1000, 96
+    table = (rng.standard_normal((v, h)) * 0.1).astype(np.float32)
+    x = rng.standard_normal((2, h)).astype(np.float32)
+    table[777] = table[123]                                     # a tie: the first index must win
+    x[1] = 0.0
+    packed = DeviceArray((-(-v // 64) * 64, h), np.float32)
+    hip.call("nc_pack_rows64", [packed, DeviceArray.from_host(table)], [v, h])
+    logits, best, index = DeviceArray((2, v), np.float32), DeviceArray((2,), np.uint64), DeviceArray((2,), np.int64)
+    hip.call("nc_argmax_clear", [best], [2])
+    hip.call("nc_lm_head", [logits, best, DeviceArray.from_host(x), packed], [2, v, h])
+    hip.call("nc_argmax_index", [index, best], [2])
+    hip.sync()
+    expected = np.zeros((2, v), np.float32)
+    for k in range(h):                                           # the reference's order, one k at a time
+        expected = (expected + (x[:, k:k + 1] * table[None, :, k]).astype(np.float32)).astype(np.float32)
+    got = logits.numpy()
+    assert np.array_equal(bits(got), bits(expected))
+    assert list(index.numpy()) == [int(np.argmax(expected[0])), 0]
+
+
+# -- the model ------------------------------------------------------------------------
+
+
+@pytest.fixture(scope="module")
+def tiny(gpu, host):
+    from nanocompile_amd.models.qwen2 import Qwen2
+    from oracle.host_model import HostQwen2
+    weights = random_weights(TINY, seed=5, std=TINY_STD)
+    return Qwen2(TINY, weights, max_tokens=64), HostQwen2(TINY, weights, capacity=64)
+
+
+PROMPTS = ([4, 5, 6], [7, 8], [1], [3, 1, 4, 1, 5, 9, 2, 6, 5, 3, 5])
+
+
+def test_tiny_greedy_tokens_are_the_oracles(tiny):
+    from nanocompile_amd.models.qwen2 import greedy
+    model, oracle_model = tiny
+    for prompt in PROMPTS:
+        expected = oracle_model.greedy(prompt, 12)
+        assert greedy(model, prompt, 12) == expected
+        assert greedy(model, prompt, 4, use_cache=False) == expected[:4]
+
+
+def test_tiny_logits_are_bitwise_the_oracles(tiny):
+    model, oracle_model = tiny
+    ids = PROMPTS[3]
+    oracle_model.reset()
+    expected, _ = oracle_model.forward(ids, all_rows=True)
+    got = model.forward(ids)
+    assert np.array_equal(bits(got), bits(expected))
+
+
+def test_tiny_cached_steps_are_one_pass(tiny):
+    """Each row's arithmetic does not depend on how the tokens were batched."""
+    model, _ = tiny
+    ids = PROMPTS[3]
+    whole = model.forward(ids)
+    cache = model.new_cache(16)
+    rows = [model.forward(ids[:5], cache=cache)]
+    rows += [model.forward([t], cache=cache) for t in ids[5:]]
+    assert np.array_equal(bits(np.concatenate(rows)), bits(whole))
+    keys, values = cache.past()
+    assert keys.shape == (2, 2, 11, 32) and np.isfinite(keys).all() and np.isfinite(values).all()
+
+
+def test_tiny_token_out_of_range_is_a_kernel_error(tiny):
+    from nanocompile_amd.hip import KernelError
+    model, _ = tiny
+    with pytest.raises(KernelError, match="out of range"):
+        model.forward([1, 256])
+    with pytest.raises(KernelError, match="out of range"):
+        model.forward([-1])
+    model.forward([1, 2])                                          # and the model still works
+
+
+def test_full_width_model_matches_the_oracle(gpu, host):
+    """Qwen2.5-0.5B's widths and vocabulary, two layers: prefill then decode, bitwise."""
+    from nanocompile_amd.models.qwen2 import Qwen2, greedy
+    from oracle.host_model import HostQwen2
+    config = replace(QWEN25_05B, num_hidden_layers=2)
+    weights = random_weights(config, seed=11)
+    model = Qwen2(config, weights, max_tokens=64)
+    oracle_model = HostQwen2(config, weights, capacity=64)
+    prompt = list(np.random.default_rng(2).integers(0, config.vocab_size, 20))
+    expected = oracle_model.greedy(prompt, 6)
+    assert greedy(model, prompt, 6) == expected
+    oracle_model.reset()
+    logits, _ = oracle_model.forward(prompt)
+    assert np.array_equal(bits(model.forward(prompt, last_only=True)), bits(logits))
