@@ -1,22 +1,27 @@
 """Benchmark of the int8 hot path on one MI355X, with its roofline and the host baseline.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload gemv|decode]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode|gemv]
 
-Prints ONE JSON line. The ``gemv`` workload is BASELINE config 1: the decode
-projection [1, 896] x [4864, 896]^T, per-row int8 weights, per-token int8
-activations, int32 accumulation, fp32 epilogue. Weights are rotated through
-128 device copies (560 MB, past the 256 MB Infinity Cache) so reads come from
-HBM. A step is one launch of the stacked kernel over all 128 copies (one
-decode GEMV per copy); the single-launch rate at the exact shape is reported
-beside it.
+Prints ONE JSON line.
 
-Roofline numerator: the algorithmic bytes of one GEMV,
-N*K + 4N + M*K + 4M + 4MN = 4,397,956 B (int8 weights, f32 scales, int8
-activations, f32 token scale, f32 output), times the GEMVs per launch.
+``decode`` (default): a random-init Qwen2.5-0.5B-shaped
+model (24 layers, hidden 896, 14/2 heads of 64, MLP 4864, vocab 151936, tied
+float32 LM head), all 168 projections per-row int8 with per-token int8
+activations; a 128-token prompt of uniform-random ids, then greedy decoding.
+A step is one decode token: one replay of the captured decode step (every
+layer, the LM head, the argmax, the feedback of the token). K steps are timed
+with HIP events on the library stream (default 255, so 256 tokens in all with
+the prompt's). The host C model (oracle/nc_model.c) decodes the same prompt
+on this machine's cores in the same run; its tokens must equal the GPU's, and
+its decode rate is the CPU baseline.
 
-The CPU baseline is the host C int8 path (oracle/nc_host.c) on this machine's
-cores over the same shapes, its weights rotated through more than twice the
-host's last-level cache.
+``gemv``: the decode projection [1,896] x [4864,896]^T,
+weights rotated through 128 device copies (560 MB, past the 256 MB Infinity
+Cache); also measured in the default run and reported under "gemv".
+
+Roofline numerators are algorithmic bytes:
+  GEMV:    N*K + 4N + M*K + 4M + 4MN = 4,397,956 B per [1,896]x[4864,896]^T.
+  LM head: 4*V*H (float32 table) + 4*H (x) + 8 (argmax key) = 544,542,216 B per step.
 """
 
 from __future__ import annotations
@@ -33,6 +38,7 @@ import numpy as np
 HBM_PEAK_GBPS = 8000.0
 N, K, M = 4864, 896, 1
 COPIES = 128
+PROMPT, NEW_TOKENS = 128, 256
 
 
 def gemv_bytes(m: int, n: int, k: int) -> int:
@@ -43,7 +49,7 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-# -- the GPU leg ---------------------------------------------------------------
+# -- config 1: the decode GEMV -----------------------------------------------------
 
 
 def gpu_gemv(steps: int, warmup: int, seed: int = 0) -> dict:
@@ -51,14 +57,11 @@ def gpu_gemv(steps: int, warmup: int, seed: int = 0) -> dict:
     from nanocompile_amd.hip import DeviceArray, Event
 
     hip.init(0)
-    info = hip.device_info()
     rng = np.random.default_rng(seed)
     w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
     x = rng.standard_normal((M, K)).astype(np.float32)
     q1, s1 = kernels.quantize_int8(w)
     xq1, xs1 = kernels.quantize_token(x)
-
-    # 128 copies of the weights at distinct addresses, and of the activations
     q = DeviceArray((COPIES, N, K), np.int8)
     ws = DeviceArray((COPIES, N), np.float32)
     xq = DeviceArray((COPIES, M, K), np.int8)
@@ -72,23 +75,19 @@ def gpu_gemv(steps: int, warmup: int, seed: int = 0) -> dict:
     hip.sync()
     y = DeviceArray((COPIES, M, N), np.float32)
 
-    # parity of what is timed: every copy's output equals the single GEMV's
     single = kernels.matmul_i8_token(xq1, xs1, q1, s1).numpy()
     kernels.matmul_i8_token_stacked(xq, xs, q, ws, out=y)
     stacked = y.numpy()
     if not all(np.array_equal(stacked[c], single) for c in range(COPIES)):
         raise RuntimeError("stacked GEMV differs from the single GEMV")
 
-    # single launches at the exact shape, each bracketed by events
-    views = [(xq.view((M, K), offset_bytes=c * M * K), xs.view((M,), offset_bytes=c * M * 4),
-              q.view((N, K), offset_bytes=c * N * K), ws.view((N,), offset_bytes=c * N * 4)) for c in range(COPIES)]
     out1 = DeviceArray((M, N), np.float32)
-    args_single = [[out1, v[0], v[1], v[2], v[3], None, None] for v in views]
+    args_single = [[out1, xq.ptr + c * M * K, xs.ptr + c * M * 4, q.ptr + c * N * K, ws.ptr + c * N * 4]
+                   for c in range(COPIES)]
     for a in args_single[:8]:
         hip.call("nc_matmul_i8_token", a, [M, N, K, 0])
     hip.sync()
-    starts = [Event() for _ in range(COPIES)]
-    stops = [Event() for _ in range(COPIES)]
+    starts, stops = [Event() for _ in range(COPIES)], [Event() for _ in range(COPIES)]
     for c in range(COPIES):
         starts[c].record()
         hip.call("nc_matmul_i8_token", args_single[c], [M, N, K, 0])
@@ -96,111 +95,197 @@ def gpu_gemv(steps: int, warmup: int, seed: int = 0) -> dict:
     hip.sync()
     single_us = statistics.median(starts[c].elapsed_ms(stops[c]) * 1e3 for c in range(COPIES))
 
-    # the stacked launch: warmup, then exactly `steps`, each bracketed by events
     stacked_args = [y, xq, xs, q, ws]
     for _ in range(warmup):
         hip.call("nc_matmul_i8_token_stacked", stacked_args, [COPIES, M, N, K, 0])
     hip.sync()
     ev = [(Event(), Event()) for _ in range(steps)]
-    t0 = time.perf_counter()
     for a, b in ev:
         a.record()
         hip.call("nc_matmul_i8_token_stacked", stacked_args, [COPIES, M, N, K, 0])
         b.record()
     hip.sync()
-    wall = time.perf_counter() - t0
     launch_ms = [a.elapsed_ms(b) for a, b in ev]
     mean_ms = statistics.fmean(launch_ms)
     per_launch_bytes = gemv_bytes(M, N, K) * COPIES
-    return {
-        "info": info,
-        "stacked_ms": mean_ms,
-        "stacked_ms_median": statistics.median(launch_ms),
-        "stacked_gbps": per_launch_bytes / (mean_ms * 1e-3) / 1e9,
-        "single_us": single_us,
-        "single_gbps": gemv_bytes(M, N, K) / (single_us * 1e-6) / 1e9,
-        "wall_s": wall,
-        "per_launch_bytes": per_launch_bytes,
-    }
+    return {"stacked_ms": mean_ms, "stacked_gbps": per_launch_bytes / (mean_ms * 1e-3) / 1e9,
+            "single_us": single_us, "single_gbps": gemv_bytes(M, N, K) / (single_us * 1e-6) / 1e9,
+            "per_launch_bytes": per_launch_bytes}
 
 
-# -- the CPU leg (the oracle's host C path, timed as the baseline) --------------
-
-
-def cpu_gemv(seconds: float = 12.0, seed: int = 0) -> dict:
+def cpu_gemv(seconds: float = 6.0, seed: int = 0) -> dict:
     from oracle import build, host
-
     if not build.LIBRARY.exists():
         build.build()
     rng = np.random.default_rng(seed)
     cores = os.cpu_count() or 1
-    copies = 240                                   # 1.05 GB: past twice any host LLC in sight
+    copies = 240
     q = rng.integers(-127, 128, (copies, N, K), dtype=np.int8)
     ws = (rng.random((copies, N)) * 1e-3).astype(np.float32)
     xq = rng.integers(-127, 128, (M, K), dtype=np.int8)
     xs = np.ones(M, np.float32)
-    counts = sorted({1, 2, 4, 8, 16, 32, 64, min(cores, 128)} & set(range(1, min(cores, 128) + 1)))
-    per = seconds / max(1, len(counts))
+    counts = sorted({1, 4, 8, 16, min(cores, 64)} & set(range(1, min(cores, 64) + 1)))
     results = {}
     for t in counts:
         host.set_threads(t)
-        s1 = host.time_matmul_i8_token(xq, xs, q, ws, 1)         # one pass: calibrate
-        reps = max(1, int(per / max(s1, 1e-6)))
+        s1 = host.time_matmul_i8_token(xq, xs, q, ws, 1)
+        reps = max(1, int(seconds / len(counts) / max(s1, 1e-6)))
         s = host.time_matmul_i8_token(xq, xs, q, ws, reps)
         results[t] = gemv_bytes(M, N, K) * copies * reps / s / 1e9
     best = max(results, key=results.get)
-    return {"gbps_by_threads": {str(k): round(v, 2) for k, v in results.items()}, "best_threads": best,
-            "best_gbps": results[best], "all_threads": counts[-1], "all_gbps": results[counts[-1]],
-            "isa": host.isa(), "cores": cores, "sample": f"{copies} rotated weight copies, thread sweep {counts}"}
+    return {"gbps": results[best], "threads": best, "by_threads": {str(k): round(v, 2) for k, v in results.items()},
+            "isa": host.isa(), "cores": cores}
+
+
+# -- config 5: the whole model, greedy decode ----------------------------------------
+
+
+def decode(steps: int, warmup: int, cpu: bool, seed: int = 0) -> dict:
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import Event
+    from nanocompile_amd.models.config import QWEN25_05B
+    from nanocompile_amd.models.config import random_weights
+    from nanocompile_amd.models.qwen2 import Qwen2
+
+    config = QWEN25_05B
+    new_tokens = steps + 1
+    t0 = time.perf_counter()
+    weights = random_weights(config, seed=seed)
+    prompt = [int(t) for t in np.random.default_rng(seed + 1).integers(0, config.vocab_size, PROMPT)]
+    log(f"decode: weights drawn in {time.perf_counter() - t0:.1f} s")
+    t0 = time.perf_counter()
+    model = Qwen2(config, weights, max_tokens=PROMPT)
+    log(f"decode: model uploaded and quantized on the GPU in {time.perf_counter() - t0:.1f} s")
+
+    for _ in range(warmup):
+        model.generate(prompt, min(16, new_tokens))
+    start, stop = Event(), Event()
+
+    def timer(what: str) -> None:
+        (start if what == "start" else stop).record()
+
+    t0 = time.perf_counter()
+    tokens = model.generate(prompt, new_tokens, timer=timer)
+    wall = time.perf_counter() - t0
+    decode_ms = start.elapsed_ms(stop)
+    result = {"tokens": tokens, "decode_ms": decode_ms, "steps": steps, "wall_s": wall,
+              "tok_s": steps / (decode_ms * 1e-3)}
+
+    # the dominant kernel, timed alone on the library stream: the float32 LM head
+    H, V = config.hidden_size, config.vocab_size
+    reps = 20
+    evs = [(Event(), Event()) for _ in range(reps)]
+    for a, b in evs:
+        a.record()
+        hip.call("nc_lm_head", [None, model.best, model.normed, model.head], [1, V, H])
+        b.record()
+    hip.sync()
+    lm_ms = statistics.fmean(a.elapsed_ms(b) for a, b in evs)
+    lm_bytes = 4 * V * H + 4 * H + 8
+    result.update({"lm_head_us": lm_ms * 1e3, "lm_head_gbps": lm_bytes / (lm_ms * 1e-3) / 1e9, "lm_bytes": lm_bytes})
+    step_bytes = 904_503_808 + 24_576 * (PROMPT + new_tokens // 2)
+    result["step_bytes_mid"] = step_bytes
+
+    if cpu:
+        from oracle import host
+        from oracle.host_model import HostQwen2
+        cores = os.cpu_count() or 1
+        threads = min(cores, 64)
+        host.set_threads(threads)
+        t0 = time.perf_counter()
+        ref = HostQwen2(config, weights, capacity=PROMPT + new_tokens)
+        log(f"decode: host model built in {time.perf_counter() - t0:.1f} s")
+        t0 = time.perf_counter()
+        _, first = ref.forward(prompt)
+        prefill_s = time.perf_counter() - t0
+        cpu_tokens = [first]
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            _, tok = ref.forward([cpu_tokens[-1]])
+            cpu_tokens.append(tok)
+        cpu_s = time.perf_counter() - t0
+        result["cpu"] = {"tok_s": steps / cpu_s, "prefill_s": prefill_s, "threads": threads, "cores": cores,
+                         "isa": host.isa()}
+        result["tokens_identical"] = cpu_tokens == tokens
+        if cpu_tokens != tokens:
+            first_diff = next(i for i, (a, b) in enumerate(zip(cpu_tokens, tokens)) if a != b)
+            log(f"decode: TOKENS DIFFER from the host C model at position {first_diff}")
+    return result
 
 
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=20)
-    parser.add_argument("--warmup", type=int, default=3)
-    parser.add_argument("--workload", choices=("gemv",), default="gemv")
-    parser.add_argument("--cpu-seconds", type=float, default=12.0)
+    parser.add_argument("--steps", type=int, default=NEW_TOKENS - 1)
+    parser.add_argument("--warmup", type=int, default=1)
+    parser.add_argument("--workload", choices=("decode", "gemv"), default="decode")
     parser.add_argument("--no-cpu", action="store_true")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)
         return 2
+    from nanocompile_amd import hip
+    hip.init(0)
+    info = hip.device_info()
 
-    log(f"gemv: {COPIES} copies of [{N},{K}] int8, {args.warmup} warmup + {args.steps} steps")
-    g = gpu_gemv(args.steps, args.warmup)
-    log(f"gpu: stacked {g['stacked_gbps']:.0f} GB/s ({g['stacked_ms']:.3f} ms), "
-        f"single {g['single_us']:.2f} us = {g['single_gbps']:.0f} GB/s")
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_gemv(args.cpu_seconds)
-        log(f"cpu: {cpu['best_gbps']:.1f} GB/s at {cpu['best_threads']} threads ({cpu['isa']})")
+    g = gpu_gemv(20 if args.workload == "decode" else args.steps, 3)
+    log(f"gemv: stacked {g['stacked_gbps']:.0f} GB/s, single {g['single_us']:.2f} us")
+    gemv_record = {"stacked_gbps": round(g["stacked_gbps"], 1), "frac": round(g["stacked_gbps"] / HBM_PEAK_GBPS, 4),
+                   "stacked_ms": round(g["stacked_ms"], 4), "single_launch_us": round(g["single_us"], 3),
+                   "single_launch_gbps": round(g["single_gbps"], 1), "copies_per_launch": COPIES,
+                   "kernel": "gemv_i8_token<896,8,1,1,false,true> (stacked)"}
+    if args.workload == "gemv":
+        cpu = None if args.no_cpu else cpu_gemv()
+        record = {
+            "metric": "int8 GEMV HBM GB/s (decode projection [1,896]x[4864,896]^T)", "value": round(g["stacked_gbps"], 1),
+            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": 3, "ms_per_step": round(g["stacked_ms"], 4),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+            "data": "synthetic (seeded N(0,0.02) weights, N(0,1) activations)",
+            "config": {"workload": "config 1: decode GEMV, per-token int8 x per-row int8", "device": info["arch"]},
+            "roofline": {"bound": "hbm", "achieved": round(g["stacked_gbps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": round(g["stacked_gbps"] / HBM_PEAK_GBPS, 4), "traffic": None,
+                         "kernel": gemv_record["kernel"], "bytes_per_launch": g["per_launch_bytes"]},
+            "cpu_baseline": None if cpu is None else {
+                "value": round(cpu["gbps"], 2), "unit": "GB/s", "cores": cpu["threads"], "kind": "port",
+                "sample": "240 rotated weight copies", "isa": cpu["isa"], "by_threads": cpu["by_threads"]},
+        }
+        print(json.dumps(record), flush=True)
+        return 0
+
+    d = decode(args.steps, args.warmup, cpu=not args.no_cpu)
+    log(f"decode: {d['tok_s']:.1f} tok/s on the GPU; LM head {d['lm_head_us']:.1f} us = {d['lm_head_gbps']:.0f} GB/s")
+    cpu = d.get("cpu")
     record = {
-        "metric": "int8 GEMV HBM GB/s (decode projection, Qwen2-0.5B gate/up shape)",
-        "value": round(g["stacked_gbps"], 1),
-        "unit": "GB/s",
+        "metric": "decode tok/s, Qwen2-0.5B-shape int8 on 1 MI355X",
+        "value": round(d["tok_s"], 2),
+        "unit": "tok/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(g["stacked_ms"], 4),
+        "ms_per_step": round(d["decode_ms"] / args.steps, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (seeded N(0,0.02) weights, N(0,1) activations)",
-        "config": {"workload": "config 1: decode GEMV [1,896] x [4864,896]^T, per-token int8 x per-row int8",
-                   "copies_per_launch": COPIES, "single_launch_us": round(g["single_us"], 3),
-                   "single_launch_gbps": round(g["single_gbps"], 1), "device": g["info"]["arch"],
-                   "compute_units": g["info"]["compute_units"]},
-        "roofline": {"bound": "hbm", "achieved": round(g["stacked_gbps"], 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(g["stacked_gbps"] / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel": "gemv_i8_token<896,8,1,1,false,true> (stacked)",
-                     "bytes_per_launch": g["per_launch_bytes"]},
+        "data": "synthetic (random-init weights N(0,0.02), uniform-random 128-token prompt)",
+        "config": {"workload": "config 5: Qwen2.5-0.5B-shaped, int8 projections with per-token int8 activations, "
+                               "fp32 tied LM head; 128-token prompt then greedy decode",
+                   "prompt_tokens": PROMPT, "new_tokens": args.steps + 1, "device": info["arch"],
+                   "compute_units": info["compute_units"],
+                   "tokens_identical_to_host_c": d.get("tokens_identical"),
+                   "decode_ms_total": round(d["decode_ms"], 3), "gemv": gemv_record},
+        "roofline": {"bound": "hbm", "achieved": round(d["lm_head_gbps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(d["lm_head_gbps"] / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "lm_head<4> (fp32 tied LM head, 60% of a decode step's bytes)",
+                     "bytes_per_launch": d["lm_bytes"], "launch_us": round(d["lm_head_us"], 3),
+                     "step_bytes": d["step_bytes_mid"],
+                     "step_gbps": round(d["step_bytes_mid"] * d["tok_s"] / 1e9, 1)},
         "cpu_baseline": None if cpu is None else {
-            "value": round(cpu["best_gbps"], 2), "unit": "GB/s", "cores": cpu["best_threads"], "kind": "port",
-            "sample": cpu["sample"], "isa": cpu["isa"], "host_cores": cpu["cores"],
-            "all_threads_gbps": round(cpu["all_gbps"], 2), "by_threads": cpu["gbps_by_threads"]},
+            "value": round(cpu["tok_s"], 2), "unit": "tok/s", "cores": cpu["threads"], "kind": "port",
+            "sample": f"the same prompt and {args.steps} greedy decode steps on the host C int8 model "
+                      f"(oracle/nc_model.c), {cpu['isa']}",
+            "host_cores": cpu["cores"], "prefill_s": round(cpu["prefill_s"], 3)},
     }
     print(json.dumps(record), flush=True)
     return 0

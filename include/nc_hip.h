@@ -30,6 +30,7 @@ extern "C" {
 #define NC_FAIL_INDEX 1
 #define NC_BAD_ARGS 2
 #define NC_LAUNCH_FAILED 3
+#define NC_FAIL_CAPACITY 4   /* a position read from the device ran past the cache */
 
 /* -- runtime ------------------------------------------------------------------
  * Replaces the reference's library loading and executor binding
@@ -185,6 +186,16 @@ int32_t nc_argmax_clear(void **p, const int64_t *s);
 
 /* p: [index i64[n], best u64[n]];  s: [n]  (argmax keys to token ids) */
 int32_t nc_argmax_index(void **p, const int64_t *s);
+
+/* Greedy decoding's bookkeeping on the device (models/qwen2.py:362-367 does it
+ * on the host): token = argmax of the step just run; tokens[pos + 1] = token;
+ * ids[0] = token; pos += 1; the argmax key cleared. A captured decode step
+ * ends with it, so steps chain with no host round trip. Records
+ * NC_FAIL_CAPACITY when pos + 1 reaches the capacity.
+ * p: [ids i64[1], tokens i64[capacity], best u64[1], pos i64[1]];  s: [capacity]
+ * nc_rope_append and nc_attention take pos as an optional p[4], read on the
+ * device in place of s[4] (past). */
+int32_t nc_decode_advance(void **p, const int64_t *s);
 
 #ifdef __cplusplus
 }

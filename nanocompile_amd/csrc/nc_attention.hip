@@ -72,6 +72,20 @@ __device__ void softmax_lds(float *e, int T, float *scratch) {
     __syncthreads();
 }
 
+// A position read from the device (a captured decode step): past = *pos_ptr,
+// which must leave room for the m new tokens. Every thread of every block
+// reads the same word and takes the same branch.
+__device__ __forceinline__ bool position_fits(const int64_t *pos_ptr, int m, int capacity, int32_t *error,
+                                              int &past) {
+    const int64_t p = *pos_ptr;
+    if (p < 0 || p + m > capacity) {
+        if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) atomicCAS(error, 0, NC_FAIL_CAPACITY);
+        return false;
+    }
+    past = (int)p;
+    return true;
+}
+
 __device__ __forceinline__ void rope_pair(float x0, float x1, float c, float s, float &y0, float &y1) {
     // y[j] = x[j] * c + (-x[j + h]) * s;  y[j + h] = x[j + h] * c + x[j] * s
     y0 = __fadd_rn(__fmul_rn(x0, c), __fmul_rn(-x1, s));
@@ -83,7 +97,9 @@ __device__ __forceinline__ void rope_pair(float x0, float x1, float c, float s, 
 __global__ __launch_bounds__(kThreads) void rope_append(float *__restrict__ qkv, float *__restrict__ kcache,
                                                         float *__restrict__ vcache,
                                                         const float *__restrict__ inv_freq, int heads, int kv_heads,
-                                                        int D, int past, int capacity) {
+                                                        int D, int past, int capacity,
+                                                        const int64_t *__restrict__ pos_ptr, int32_t *__restrict__ error) {
+    if (pos_ptr && !position_fits(pos_ptr, (int)gridDim.x, capacity, error, past)) return;
     const int i = blockIdx.x;
     const int half = D / 2;
     const int width = (heads + 2 * kv_heads) * D;
@@ -120,7 +136,9 @@ __global__ __launch_bounds__(kThreads) void attention_rows(float *__restrict__ c
                                                            const float *__restrict__ kcache,
                                                            const float *__restrict__ vcache, int heads,
                                                            int kv_heads, int D, int past, int capacity,
-                                                           float scale) {
+                                                           float scale, const int64_t *__restrict__ pos_ptr,
+                                                           int32_t *__restrict__ error) {
+    if (pos_ptr && !position_fits(pos_ptr, (int)gridDim.y, capacity, error, past)) return;
     extern __shared__ float e[];
     __shared__ float q[64];
     __shared__ float part[4][64];
@@ -201,33 +219,38 @@ float bits_to_float(int64_t bits) {
 }  // namespace
 
 // p: [qkv f32[M, (H + 2*KV*D)] (q rotated in place), kcache f32[KV, C, D], vcache f32[KV, C, D],
-//     inv_freq f32[D/2]];  s: [M, heads, kv_heads, D, past, capacity]
+//     inv_freq f32[D/2], pos i64[1] | NULL];  s: [M, heads, kv_heads, D, past, capacity]
+// With pos, past is read from the device when the kernel runs (s[4] is ignored).
 NC_EXPORT int32_t nc_rope_append(void **p, const int64_t *s) {
     NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3], "nc_rope_append: null operand");
     const int64_t M = s[0], heads = s[1], kv = s[2], D = s[3], past = s[4], cap = s[5];
-    NC_REQUIRE(M >= 0 && heads > 0 && kv > 0 && heads % kv == 0 && D > 0 && D % 2 == 0 && D <= 64 && past >= 0 &&
-                   past + M <= cap && cap < (1 << 24) && M < (1 << 24),
+    const int64_t *pos = (const int64_t *)p[4];
+    NC_REQUIRE(M >= 0 && heads > 0 && kv > 0 && heads % kv == 0 && D > 0 && D % 2 == 0 && D <= 64 &&
+                   (pos || (past >= 0 && past + M <= cap)) && M <= cap && cap < (1 << 24) && M < (1 << 24),
                "nc_rope_append: bad shape or the cache is full");
     if (M == 0) return NC_OK;
     hipLaunchKernelGGL(rope_append, dim3((unsigned)M), dim3(kThreads), 0, nc::stream(), (float *)p[0],
-                       (float *)p[1], (float *)p[2], (const float *)p[3], (int)heads, (int)kv, (int)D, (int)past,
-                       (int)cap);
+                       (float *)p[1], (float *)p[2], (const float *)p[3], (int)heads, (int)kv, (int)D,
+                       pos ? 0 : (int)past, (int)cap, pos, nc::error_word());
     return nc::launched("rope_append");
 }
 
-// p: [ctx f32[M, heads*D], qkv f32[M, (H + 2*KV*D)] (q rotated), kcache, vcache];
+// p: [ctx f32[M, heads*D], qkv f32[M, (H + 2*KV*D)] (q rotated), kcache, vcache, pos i64[1] | NULL];
 // s: [M, heads, kv_heads, D, past, capacity, scale as float32 bits]
+// With pos, past is read from the device when the kernel runs (s[4] is ignored).
 NC_EXPORT int32_t nc_attention(void **p, const int64_t *s) {
     NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3], "nc_attention: null operand");
     const int64_t M = s[0], heads = s[1], kv = s[2], D = s[3], past = s[4], cap = s[5];
-    NC_REQUIRE(M >= 0 && heads > 0 && kv > 0 && heads % kv == 0 && D > 0 && D <= 64 && past >= 0 &&
-                   past + M <= cap && past + M <= kMaxKeys && M < 65536 && heads < 65536,
+    const int64_t *pos = (const int64_t *)p[4];
+    NC_REQUIRE(M >= 0 && heads > 0 && kv > 0 && heads % kv == 0 && D > 0 && D <= 64 &&
+                   (pos ? cap <= kMaxKeys : (past >= 0 && past + M <= cap && past + M <= kMaxKeys)) &&
+                   M <= cap && M < 65536 && heads < 65536,
                "nc_attention: bad shape");
     if (M == 0) return NC_OK;
-    const size_t lds = (size_t)(past + M) * sizeof(float);
+    const size_t lds = (size_t)(pos ? cap : past + M) * sizeof(float);
     hipLaunchKernelGGL(attention_rows, dim3((unsigned)heads, (unsigned)M), dim3(kThreads), lds, nc::stream(),
                        (float *)p[0], (const float *)p[1], (const float *)p[2], (const float *)p[3], (int)heads,
-                       (int)kv, (int)D, (int)past, (int)cap, bits_to_float(s[6]));
+                       (int)kv, (int)D, pos ? 0 : (int)past, (int)cap, bits_to_float(s[6]), pos, nc::error_word());
     return nc::launched("attention_rows");
 }
 

@@ -21,6 +21,7 @@
 #define NC_FAIL_INDEX 1      // a gather index out of range (loopir.Fail code 1)
 #define NC_BAD_ARGS 2        // the host launcher rejected a shape or pointer
 #define NC_LAUNCH_FAILED 3   // the HIP runtime refused the launch
+#define NC_FAIL_CAPACITY 4   // a device-side position ran past the KV cache's capacity
 
 namespace nc {
 

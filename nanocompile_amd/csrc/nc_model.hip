@@ -152,3 +152,35 @@ NC_EXPORT int32_t nc_argmax_index(void **p, const int64_t *s) {
                        (int64_t *)p[0], (const unsigned long long *)p[1], (int)s[0]);
     return nc::launched("argmax_decode");
 }
+
+namespace {
+// One greedy step's bookkeeping on the device: the argmax of the step just run
+// becomes the next input token and is appended to the history at position
+// pos + 1; pos advances; the argmax key is cleared for the next step.
+__global__ void decode_advance(int64_t *__restrict__ ids, int64_t *__restrict__ tokens,
+                               unsigned long long *__restrict__ best, int64_t *__restrict__ pos, int64_t capacity,
+                               int32_t *__restrict__ error) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    const int64_t p = *pos;
+    const int64_t token = (int64_t)(0xFFFFFFFFu - (uint32_t)(best[0] & 0xFFFFFFFFull));
+    if (p < -1 || p + 1 >= capacity) {
+        atomicCAS(error, 0, NC_FAIL_CAPACITY);
+        return;
+    }
+    tokens[p + 1] = token;
+    ids[0] = token;
+    *pos = p + 1;
+    best[0] = 0ull;
+}
+}  // namespace
+
+// The greedy loop's step on the device (models/qwen2.py:362-367 does it on
+// the host: argmax, append, feed back), so a captured decode step needs no
+// host round trip.
+// p: [ids i64[1], tokens i64[capacity], best u64[1], pos i64[1]];  s: [capacity]
+NC_EXPORT int32_t nc_decode_advance(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3] && s[0] > 0, "nc_decode_advance: bad operand");
+    hipLaunchKernelGGL(decode_advance, dim3(1), dim3(64), 0, nc::stream(), (int64_t *)p[0], (int64_t *)p[1],
+                       (unsigned long long *)p[2], (int64_t *)p[3], s[0], nc::error_word());
+    return nc::launched("decode_advance");
+}

@@ -120,11 +120,19 @@ def kernel(name: str):
     return fn
 
 
+PAD = 16   # entries every p[] and s[] array carries: optional trailing operands read NULL / 0
+
+
 def call(name: str, pointers, sizes) -> None:
-    """Enqueue kernel ``name`` on the library stream; raises on a rejected launch."""
+    """Enqueue kernel ``name`` on the library stream; raises on a rejected launch.
+
+    The arrays are padded with NULL pointers and zero sizes to ``PAD``
+    entries, so an entry point's optional trailing operands (a position read
+    from the device, say) are NULL unless the caller gives them.
+    """
     init()
-    p = (ctypes.c_void_p * max(1, len(pointers)))(*[_address(x) for x in pointers])
-    s = (ctypes.c_int64 * max(1, len(sizes)))(*[int(v) for v in sizes])
+    p = (ctypes.c_void_p * max(PAD, len(pointers)))(*[_address(x) for x in pointers])
+    s = (ctypes.c_int64 * max(PAD, len(sizes)))(*[int(v) for v in sizes])
     status = kernel(name)(p, s)
     if status != NC_OK:
         raise KernelError(f"{name} failed with {status}: {last_error()}")

@@ -190,8 +190,12 @@ class Qwen2:
     def new_cache(self, capacity: int = 256) -> KVCache:
         return KVCache(self.config, capacity)
 
-    def _layers(self, m: int, past: int, cache: KVCache) -> None:
-        """The decoder layers over m new tokens at positions past .. past + m - 1."""
+    def _layers(self, m: int, past: int, cache: KVCache, pos: DeviceArray | None = None) -> None:
+        """The decoder layers over m new tokens at positions past .. past + m - 1.
+
+        With ``pos`` (a device int64), the position is read on the device when
+        the kernels run, so the launches can be captured once and replayed.
+        """
         c = self.config
         H, I, D = c.hidden_size, c.intermediate_size, c.head_dim
         heads, kv, W = c.num_attention_heads, c.num_key_value_heads, self.width
@@ -202,8 +206,9 @@ class Qwen2:
             hip.call("nc_rms_norm_quant", [None, self.xq, self.xs, self.x, w["g1"]], [m, H, eps])
             q, s = w["qkv"]
             hip.call("nc_matmul_i8_token", [self.qkv, self.xq, self.xs, q, s, w["qkv_b"], None], [m, W, H, 0])
-            hip.call("nc_rope_append", [self.qkv, kc, vc, self.inv_freq], [m, heads, kv, D, past, cache.capacity])
-            hip.call("nc_attention", [self.ctx, self.qkv, kc, vc],
+            hip.call("nc_rope_append", [self.qkv, kc, vc, self.inv_freq, pos],
+                     [m, heads, kv, D, past, cache.capacity])
+            hip.call("nc_attention", [self.ctx, self.qkv, kc, vc, pos],
                      [m, heads, kv, D, past, cache.capacity, float_bits(self.scale)])
             hip.call("nc_quantize_token_i8", [self.xq, self.xs, self.ctx], [m, Q])
             q, s = w["o"]
@@ -267,6 +272,66 @@ class Qwen2:
         hip.sync()
         cache.length = past + m
         return int(out[0])
+
+
+    # -- greedy decoding on the device -------------------------------------------------
+
+    def _head_argmax(self, row_ptr: int) -> None:
+        """Final rms_norm of one row, the LM head, and its argmax key into ``best``."""
+        c = self.config
+        H, V = c.hidden_size, c.vocab_size
+        hip.call("nc_rms_norm_quant", [self.normed, self.xq, self.xs, row_ptr, self.norm],
+                 [1, H, float_bits(c.rms_norm_eps)])
+        hip.call("nc_lm_head", [None, self.best, self.normed, self.head], [1, V, H])
+
+    def generate(self, prompt_ids: Sequence[int], max_new_tokens: int, timer=None) -> list[int]:
+        """Greedy decoding with the whole loop on the device; the same tokens as :func:`greedy`.
+
+        The prompt runs as one forward; each following token is one replay of
+        a HIP graph holding a whole decode step (embedding, every layer, the
+        LM head, the argmax and the bookkeeping that feeds the token back),
+        with the position read on the device. ``timer``, if given, is called
+        as ``timer("start")`` and ``timer("stop")`` around the replays.
+        """
+        prompt = np.asarray(prompt_ids, dtype=np.int64)
+        m = int(prompt.size)
+        if m == 0 or max_new_tokens <= 0:
+            raise ValueError("need a non-empty prompt and at least one new token")
+        if m > self.max_tokens:
+            raise ValueError(f"a {m}-token prompt; this model was made for at most {self.max_tokens}")
+        c = self.config
+        H, V = c.hidden_size, c.vocab_size
+        capacity = m + max_new_tokens
+        cache = self.new_cache(capacity)
+        tokens = DeviceArray((capacity,), np.int64)
+        pos = DeviceArray((1,), np.int64)
+        one_id = self.acts.base.view((1,), np.int64, offset_bytes=self.ids.ptr - self.acts.base.ptr)
+
+        self.ids.view((m,)).upload(prompt)
+        hip.call("nc_embed", [self.x, self.embed, self.ids], [m, H, V])
+        self._layers(m, 0, cache)
+        hip.call("nc_argmax_clear", [self.best], [1])
+        self._head_argmax(self.x.ptr + (m - 1) * H * 4)
+        pos.upload(np.array([m - 1], np.int64))
+        hip.call("nc_decode_advance", [one_id, tokens, self.best, pos], [capacity])
+
+        def step() -> None:
+            hip.call("nc_embed", [self.x, self.embed, one_id], [1, H, V])
+            self._layers(1, 0, cache, pos=pos)
+            self._head_argmax(self.x.ptr)
+            hip.call("nc_decode_advance", [one_id, tokens, self.best, pos], [capacity])
+
+        hip.sync()
+        graph = hip.Graph.capture(step)
+        if timer:
+            timer("start")
+        for _ in range(max_new_tokens - 1):
+            graph.launch()
+        if timer:
+            timer("stop")
+        hip.sync()
+        cache.length = capacity - 1
+        return [int(t) for t in tokens.numpy()[m:capacity]]
 
 
 def greedy(model: Qwen2, prompt_ids: Sequence[int], max_new_tokens: int, use_cache: bool = True) -> list[int]:

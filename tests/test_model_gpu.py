@@ -208,3 +208,14 @@ def test_full_width_model_matches_the_oracle(gpu, host):
     oracle_model.reset()
     logits, _ = oracle_model.forward(prompt)
     assert np.array_equal(bits(model.forward(prompt, last_only=True)), bits(logits))
+
+
+def test_device_greedy_loop_is_greedy(tiny):
+    """generate(): the whole decode loop on the device, one graph replay per token."""
+    from nanocompile_amd.models.qwen2 import greedy
+    model, oracle_model = tiny
+    for prompt in PROMPTS:
+        expected = oracle_model.greedy(prompt, 20)
+        assert model.generate(prompt, 20) == expected
+        assert greedy(model, prompt, 20) == expected
+    assert model.generate([9], 1) == oracle_model.greedy([9], 1)
