@@ -140,7 +140,7 @@ def cpu_gemv(seconds: float = 6.0, seed: int = 0) -> dict:
 # -- config 5: the whole model, greedy decode ----------------------------------------
 
 
-def decode(steps: int, warmup: int, cpu: bool, seed: int = 0) -> dict:
+def decode(steps: int, warmup: int, cpu: bool, seed: int = 0, graph: bool = True) -> dict:
     from nanocompile_amd import hip
     from nanocompile_amd.hip import Event
     from nanocompile_amd.models.config import QWEN25_05B
@@ -158,14 +158,14 @@ def decode(steps: int, warmup: int, cpu: bool, seed: int = 0) -> dict:
     log(f"decode: model uploaded and quantized on the GPU in {time.perf_counter() - t0:.1f} s")
 
     for _ in range(warmup):
-        model.generate(prompt, min(16, new_tokens))
+        model.generate(prompt, min(16, new_tokens), graph=graph)
     start, stop = Event(), Event()
 
     def timer(what: str) -> None:
         (start if what == "start" else stop).record()
 
     t0 = time.perf_counter()
-    tokens = model.generate(prompt, new_tokens, timer=timer)
+    tokens = model.generate(prompt, new_tokens, timer=timer, graph=graph)
     wall = time.perf_counter() - t0
     decode_ms = start.elapsed_ms(stop)
     result = {"tokens": tokens, "decode_ms": decode_ms, "steps": steps, "wall_s": wall,
@@ -220,6 +220,9 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=1)
     parser.add_argument("--workload", choices=("decode", "gemv"), default="decode")
     parser.add_argument("--no-cpu", action="store_true")
+    parser.add_argument("--no-graph", action="store_true",
+                        help="launch each decode step's kernels directly instead of replaying a HIP graph "
+                             "(for profilers that cannot follow graph launches)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus})",
@@ -253,7 +256,7 @@ def main() -> int:
         print(json.dumps(record), flush=True)
         return 0
 
-    d = decode(args.steps, args.warmup, cpu=not args.no_cpu)
+    d = decode(args.steps, args.warmup, cpu=not args.no_cpu, graph=not args.no_graph)
     log(f"decode: {d['tok_s']:.1f} tok/s on the GPU; LM head {d['lm_head_us']:.1f} us = {d['lm_head_gbps']:.0f} GB/s")
     cpu = d.get("cpu")
     record = {

@@ -48,14 +48,39 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int64_t n) {
     return ((unsigned long long)ord << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)n);
 }
 
+// With gamma, x is first rms-normed (nn.py:34-38) in the row kernels' order:
+// thread t sums x[t]^2, x[t+256]^2, ... in order; butterfly per wave;
+// (w0 + w1) + (w2 + w3). The workgroup is 256 threads, so thread t is virtual
+// thread t of that order.
+__device__ float sum4(float v, float *scratch) {
+    v = nc::wave_sum_f32(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    return __fadd_rn(__fadd_rn(scratch[0], scratch[1]), __fadd_rn(scratch[2], scratch[3]));
+}
+
 template <int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void lm_head(float *__restrict__ logits, unsigned long long *__restrict__ best,
                                                       const float *__restrict__ x, const float4 *__restrict__ packed,
-                                                      int64_t V, int H) {
+                                                      int64_t V, int H, const float *__restrict__ gamma, float eps) {
     extern __shared__ float sxh[];
+    __shared__ float scratch[4];
     const int m = blockIdx.y;
-    for (int i = threadIdx.x; i < H; i += 64 * WAVES) sxh[i] = x[(size_t)m * H + i];
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < H; i += 64 * WAVES) {
+        const float v = x[(size_t)m * H + i];
+        sxh[i] = v;
+        ss = __fadd_rn(ss, __fmul_rn(v, v));
+    }
     __syncthreads();
+    if (gamma) {
+        static_assert(WAVES == 4, "the row-sum order needs 256 threads");
+        const float total = sum4(ss, scratch);
+        const float rcp = nc::div_rn(1.0f, nc::sqrt_rn(__fadd_rn(nc::div_rn(total, (float)H), eps)));
+        for (int i = threadIdx.x; i < H; i += 64 * WAVES) sxh[i] = __fmul_rn(__fmul_rn(sxh[i], rcp), gamma[i]);
+        __syncthreads();
+    }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t blk = (int64_t)blockIdx.x * WAVES + wave;
     const int64_t n = blk * 64 + lane;
@@ -84,6 +109,12 @@ __global__ __launch_bounds__(64 * WAVES) void lm_head(float *__restrict__ logits
         }
         if (lane == 0) atomicMax(best + m, key);
     }
+}
+
+float bits_to_float(int64_t bits) {
+    union { uint32_t u; float f; } c;
+    c.u = (uint32_t)bits;
+    return c.f;
 }
 
 __global__ void fill_u64(unsigned long long *p, int n) {
@@ -120,7 +151,9 @@ NC_EXPORT int32_t nc_pack_rows64(void **p, const int64_t *s) {
 
 // logits[m, n] = sum_k x[m, k] * table[n, k] in k order, and best[m] the
 // argmax key of row m (atomic maximum: clear it first with nc_argmax_clear).
-// p: [logits f32[M,V] | NULL, best u64[M] | NULL, x f32[M,H], packed table];  s: [M, V, H]
+// With gamma (p[4]), x is rms-normed first with eps = s[3] (as float32 bits).
+// p: [logits f32[M,V] | NULL, best u64[M] | NULL, x f32[M,H], packed table, gamma f32[H] | NULL];
+// s: [M, V, H, eps bits]
 NC_EXPORT int32_t nc_lm_head(void **p, const int64_t *s) {
     NC_REQUIRE(p && s && p[2] && p[3] && (p[0] || p[1]), "nc_lm_head: null operand");
     NC_REQUIRE(s[0] >= 0 && s[0] < 65536 && s[1] > 0 && s[1] < (1LL << 31) && s[2] > 0 && s[2] % 4 == 0 &&
@@ -131,7 +164,8 @@ NC_EXPORT int32_t nc_lm_head(void **p, const int64_t *s) {
     const int64_t blocks = (s[1] + 63) / 64;
     hipLaunchKernelGGL((lm_head<W>), dim3((unsigned)((blocks + W - 1) / W), (unsigned)s[0]), dim3(64 * W),
                        (size_t)s[2] * sizeof(float), nc::stream(), (float *)p[0], (unsigned long long *)p[1],
-                       (const float *)p[2], (const float4 *)p[3], s[1], (int)s[2]);
+                       (const float *)p[2], (const float4 *)p[3], s[1], (int)s[2], (const float *)p[4],
+                       bits_to_float(s[3]));
     return nc::launched("lm_head");
 }
 

@@ -170,6 +170,8 @@ class Qwen2:
         self.inv_freq = self.weights.take((D // 2,), np.float32)
         self.inv_freq.upload(inverse_frequencies(D, c.rope_theta))
         self.scale = float(np.float32(D ** -0.5))
+        # the fused one-token kernels exist for these widths (nc_decode.hip)
+        self.fused_decode = (H, I, D) in ((896, 4864, 64), (128, 256, 32)) and Q == H
         hip.sync()
         del stage
 
@@ -201,6 +203,22 @@ class Qwen2:
         heads, kv, W = c.num_attention_heads, c.num_key_value_heads, self.width
         Q = heads * D
         eps = float_bits(c.rms_norm_eps)
+        if m == 1 and self.fused_decode:
+            # five kernels a layer: each projection computes its own activation
+            # prologue, attention does RoPE and the cache append (nc_decode.hip)
+            for i, w in enumerate(self.layers):
+                kc, vc = cache.layer(i)
+                q, s = w["qkv"]
+                hip.call("nc_decode_projection", [self.qkv, self.x, w["g1"], q, s, w["qkv_b"]], [W, H, 0, eps])
+                hip.call("nc_attention_decode", [self.ctx, self.qkv, kc, vc, self.inv_freq, pos],
+                         [heads, kv, D, past, cache.capacity, float_bits(self.scale)])
+                q, s = w["o"]
+                hip.call("nc_decode_projection", [self.x, self.ctx, None, q, s], [H, Q, 1, eps])
+                (qg, sg), (qu, su) = w["gate"], w["up"]
+                hip.call("nc_decode_projection", [self.h, self.x, w["g2"], qg, sg, None, qu, su], [I, H, 2, eps])
+                q, s = w["down"]
+                hip.call("nc_decode_projection", [self.x, self.h, None, q, s], [H, I, 1, eps])
+            return
         for i, w in enumerate(self.layers):
             kc, vc = cache.layer(i)
             hip.call("nc_rms_norm_quant", [None, self.xq, self.xs, self.x, w["g1"]], [m, H, eps])
@@ -277,14 +295,13 @@ class Qwen2:
     # -- greedy decoding on the device -------------------------------------------------
 
     def _head_argmax(self, row_ptr: int) -> None:
-        """Final rms_norm of one row, the LM head, and its argmax key into ``best``."""
+        """Final rms_norm of one row and the LM head (one kernel), its argmax key into ``best``."""
         c = self.config
         H, V = c.hidden_size, c.vocab_size
-        hip.call("nc_rms_norm_quant", [self.normed, self.xq, self.xs, row_ptr, self.norm],
-                 [1, H, float_bits(c.rms_norm_eps)])
-        hip.call("nc_lm_head", [None, self.best, self.normed, self.head], [1, V, H])
+        hip.call("nc_lm_head", [None, self.best, row_ptr, self.head, self.norm],
+                 [1, V, H, float_bits(c.rms_norm_eps)])
 
-    def generate(self, prompt_ids: Sequence[int], max_new_tokens: int, timer=None) -> list[int]:
+    def generate(self, prompt_ids: Sequence[int], max_new_tokens: int, timer=None, graph: bool = True) -> list[int]:
         """Greedy decoding with the whole loop on the device; the same tokens as :func:`greedy`.
 
         The prompt runs as one forward; each following token is one replay of
@@ -322,11 +339,11 @@ class Qwen2:
             hip.call("nc_decode_advance", [one_id, tokens, self.best, pos], [capacity])
 
         hip.sync()
-        graph = hip.Graph.capture(step)
+        replay = hip.Graph.capture(step).launch if graph else step
         if timer:
             timer("start")
         for _ in range(max_new_tokens - 1):
-            graph.launch()
+            replay()
         if timer:
             timer("stop")
         hip.sync()

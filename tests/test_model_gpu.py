@@ -210,6 +210,29 @@ def test_full_width_model_matches_the_oracle(gpu, host):
     assert np.array_equal(bits(model.forward(prompt, last_only=True)), bits(logits))
 
 
+@pytest.mark.parametrize("full", [False, True])
+def test_fused_decode_step_is_the_unfused_step(gpu, tiny, full):
+    """The one-token kernels (prologues and RoPE fused in) compute the unfused kernels' bits."""
+    from nanocompile_amd.models.qwen2 import Qwen2
+    if full:
+        config = replace(QWEN25_05B, num_hidden_layers=2)
+        model = Qwen2(config, random_weights(config, seed=13), max_tokens=32)
+    else:
+        model, _ = tiny
+    assert model.fused_decode
+    prompt = [int(t) for t in np.random.default_rng(3).integers(0, model.config.vocab_size, 9)]
+    rows = {}
+    for fused in (True, False):
+        model.fused_decode = fused
+        cache = model.new_cache(16)
+        out = [model.forward(prompt, cache=cache, last_only=True)]
+        for t in (5, 17, 3):
+            out.append(model.forward([t], cache=cache, last_only=True))
+        rows[fused] = np.concatenate(out)
+    model.fused_decode = True
+    assert np.array_equal(bits(rows[True]), bits(rows[False]))
+
+
 def test_device_greedy_loop_is_greedy(tiny):
     """generate(): the whole decode loop on the device, one graph replay per token."""
     from nanocompile_amd.models.qwen2 import greedy
