@@ -82,21 +82,30 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 }
 
 template <int K>
-__device__ __forceinline__ int32_t row_dot(const int8_t *__restrict__ row, const int8_t *__restrict__ sxq, int sub) {
-    constexpr int STEP = kL * 16;
-    constexpr int ITERS = K / STEP;
+struct RowChunks {
+    static constexpr int STEP = kL * 16;
+    static constexpr int ITERS = K / STEP;
     static_assert(K % STEP == 0, "K must be a multiple of 128");
     i8x16 w[ITERS];
+
+    // The lane's 16-byte chunks of its weight row, loads issued back to back.
+    __device__ __forceinline__ void load(const int8_t *__restrict__ row, int sub) {
 #pragma unroll
-    for (int it = 0; it < ITERS; ++it) w[it] = nc::load16_stream(row + it * STEP + sub * 16);
-    int32_t acc = 0;
+        for (int it = 0; it < ITERS; ++it) w[it] = nc::load16_stream(row + it * STEP + sub * 16);
+    }
+
+    __device__ __forceinline__ int32_t dot(const int8_t *__restrict__ sxq, int sub) const {
+        int32_t acc = 0;
 #pragma unroll
-    for (int it = 0; it < ITERS; ++it)
-        acc = nc::dot16(w[it], *reinterpret_cast<const i8x16 *>(sxq + it * STEP + sub * 16), acc);
-    return acc;
-}
+        for (int it = 0; it < ITERS; ++it)
+            acc = nc::dot16(w[it], *reinterpret_cast<const i8x16 *>(sxq + it * STEP + sub * 16), acc);
+        return acc;
+    }
+};
 
 // One decode projection: workgroup = one wave = 8 rows (8 row pairs for SwiGLU).
+// The weight loads are issued first, so they are in flight while the
+// workgroup computes its activation prologue.
 template <int K, int PRO, int EPI>
 __global__ __launch_bounds__(64) void gemv_decode(float *__restrict__ out, const float *__restrict__ x,
                                                   const float *__restrict__ gamma, float eps,
@@ -104,14 +113,17 @@ __global__ __launch_bounds__(64) void gemv_decode(float *__restrict__ out, const
                                                   const float *__restrict__ bias, const int8_t *__restrict__ q2,
                                                   const float *__restrict__ ws2, int N) {
     __shared__ __align__(16) int8_t sxq[K];
-    const float xs = activation_prologue<K, PRO>(sxq, x, gamma, eps);
     const int lane = threadIdx.x, sub = lane & (kL - 1);
     const int n = blockIdx.x * kRows + lane / kL;
     const bool valid = n < N;
     const int nr = valid ? n : 0;
-    int32_t acc = row_dot<K>(q + (size_t)nr * K, sxq, sub);
+    RowChunks<K> w1, w2;
+    w1.load(q + (size_t)nr * K, sub);
+    if constexpr (EPI == kSwiglu) w2.load(q2 + (size_t)nr * K, sub);
+    const float xs = activation_prologue<K, PRO>(sxq, x, gamma, eps);
+    int32_t acc = w1.dot(sxq, sub);
     int32_t acc2 = 0;
-    if constexpr (EPI == kSwiglu) acc2 = row_dot<K>(q2 + (size_t)nr * K, sxq, sub);
+    if constexpr (EPI == kSwiglu) acc2 = w2.dot(sxq, sub);
     acc = nc::group_sum_i32<kL>(acc);
     if constexpr (EPI == kSwiglu) acc2 = nc::group_sum_i32<kL>(acc2);
     if (sub != 0 || !valid) return;
@@ -245,15 +257,19 @@ __global__ __launch_bounds__(kT) void attention_decode(float *__restrict__ ctx, 
     const int t0 = wave * S, t1 = min(T, t0 + S);
     float acc = 0.0f;
     if (lane < D) {
-        int t = t0;
-        for (; t + 8 <= t1; t += 8) {
-            float vv[8];
+        // tiles of 32 positions: the 32 loads go out together, then the adds in order
+        constexpr int TILE = 32;
+        for (int t = t0; t < t1; t += TILE) {
+            float vv[TILE];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) vv[j] = (t + j == past) ? vnew[lane] : V[(size_t)(t + j) * D + lane];
+            for (int j = 0; j < TILE; ++j) {
+                const int tj = t + j;
+                vv[j] = tj < t1 ? (tj == past ? vnew[lane] : V[(size_t)tj * D + lane]) : 0.0f;
+            }
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc = __fadd_rn(acc, __fmul_rn(e[t + j], vv[j]));
+            for (int j = 0; j < TILE; ++j)
+                if (t + j < t1) acc = __fadd_rn(acc, __fmul_rn(e[t + j], vv[j]));
         }
-        for (; t < t1; ++t) acc = __fadd_rn(acc, __fmul_rn(e[t], t == past ? vnew[lane] : V[(size_t)t * D + lane]));
         part[wave][lane] = acc;
     }
     __syncthreads();

@@ -88,7 +88,7 @@ __global__ __launch_bounds__(64 * WAVES) void lm_head(float *__restrict__ logits
     const int k4n = H / 4;
     const float4 *e = packed + blk * k4n * 64 + lane;
     float acc = 0.0f;
-#pragma unroll 8
+#pragma unroll 16
     for (int k4 = 0; k4 < k4n; ++k4) {
         typedef float f32x4 __attribute__((ext_vector_type(4)));
         const f32x4 w = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(e + (size_t)k4 * 64));
