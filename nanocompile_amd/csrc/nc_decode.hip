@@ -199,6 +199,35 @@ __global__ __launch_bounds__(kT) void attention_decode(float *__restrict__ ctx, 
     const float *krow = qkv + heads * D + g * D;
     const float *vrow = qkv + (heads + kv_heads) * D + g * D;
     const float fpos = (float)past;
+    const int T = past + 1;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int S = (T + 3) / 4;
+    const int t0 = wave * S, t1 = min(T, t0 + S);
+    float *K = kcache + (size_t)g * capacity * D;
+    float *V = vcache + (size_t)g * capacity * D;
+
+    // Cache reads go out first, all at once, so their latency overlaps the RoPE
+    // and each other: the key rows this thread scores (positions tid and
+    // tid + 256) and the first VP values of its wave's chunk for P.V.
+    constexpr int KP = 2, VP = 64;
+    float4 kreg[KP][D / 4];
+#pragma unroll
+    for (int r = 0; r < KP; ++r) {
+        const int t = tid + r * kT;
+        const bool load = t < past;                    // position past is the new key, in LDS
+        const float4 *k = reinterpret_cast<const float4 *>(K + (size_t)(load ? t : 0) * D);
+#pragma unroll
+        for (int d4 = 0; d4 < D / 4; ++d4) kreg[r][d4] = load ? k[d4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float vreg[VP];
+#pragma unroll
+    for (int j = 0; j < VP; ++j) {
+        const int t = t0 + j;
+        const bool load = lane < D && t < t1 && t < past;
+        const float v = V[(size_t)(load ? t : 0) * D + (lane < D ? lane : 0)];   // always in bounds
+        vreg[j] = load ? v : 0.0f;
+    }
+
     if (tid < half) {
         const float ang = __fmul_rn(fpos, inv_freq[tid]);
         const float c = nc_cosf(ang), s = nc_sinf(ang);
@@ -217,16 +246,12 @@ __global__ __launch_bounds__(kT) void attention_decode(float *__restrict__ ctx, 
         vnew[d] = vrow[d];
     }
     __syncthreads();
-    float *K = kcache + (size_t)g * capacity * D;
-    float *V = vcache + (size_t)g * capacity * D;
     if (h % group == 0 && tid < D) {
         K[(size_t)past * D + tid] = knew[tid];
         V[(size_t)past * D + tid] = vnew[tid];
     }
 
-    const int T = past + 1;
-    for (int t = tid; t < T; t += kT) {
-        const float4 *k = reinterpret_cast<const float4 *>(t == past ? knew : K + (size_t)t * D);
+    auto score = [&](const float4 *k) {
         float acc = 0.0f;
 #pragma unroll
         for (int d4 = 0; d4 < D / 4; ++d4) {
@@ -236,8 +261,15 @@ __global__ __launch_bounds__(kT) void attention_decode(float *__restrict__ ctx, 
             acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 2], kv4.z));
             acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 3], kv4.w));
         }
-        e[t] = __fadd_rn(__fmul_rn(acc, scale), 0.0f);
+        return __fadd_rn(__fmul_rn(acc, scale), 0.0f);
+    };
+#pragma unroll
+    for (int r = 0; r < KP; ++r) {
+        const int t = tid + r * kT;
+        if (t < T) e[t] = score(t == past ? reinterpret_cast<const float4 *>(knew) : kreg[r]);
     }
+    for (int t = tid + KP * kT; t < T; t += kT)
+        e[t] = score(t == past ? reinterpret_cast<const float4 *>(knew) : reinterpret_cast<const float4 *>(K + (size_t)t * D));
     __syncthreads();
     float m = -__builtin_inff();
     for (int t = tid; t < T; t += kT) m = nan_max(m, e[t]);
@@ -252,14 +284,17 @@ __global__ __launch_bounds__(kT) void attention_decode(float *__restrict__ ctx, 
     for (int t = tid; t < T; t += kT) e[t] = nc::div_rn(e[t], sum);
     __syncthreads();
 
-    const int lane = tid & 63, wave = tid >> 6;
-    const int S = (T + 3) / 4;
-    const int t0 = wave * S, t1 = min(T, t0 + S);
     float acc = 0.0f;
     if (lane < D) {
-        // tiles of 32 positions: the 32 loads go out together, then the adds in order
+        // the prefetched first VP positions of the chunk, then tiles of 32
+        // whose 32 loads go out together; the adds always in position order
+#pragma unroll
+        for (int j = 0; j < VP; ++j) {
+            const int t = t0 + j;
+            if (t < t1) acc = __fadd_rn(acc, __fmul_rn(e[t], t == past ? vnew[lane] : vreg[j]));
+        }
         constexpr int TILE = 32;
-        for (int t = t0; t < t1; t += TILE) {
+        for (int t = t0 + VP; t < t1; t += TILE) {
             float vv[TILE];
 #pragma unroll
             for (int j = 0; j < TILE; ++j) {
