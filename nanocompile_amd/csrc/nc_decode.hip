@@ -206,26 +206,26 @@ __global__ __launch_bounds__(kT) void attention_decode(float *__restrict__ ctx, 
     float *K = kcache + (size_t)g * capacity * D;
     float *V = vcache + (size_t)g * capacity * D;
 
-    // Cache reads go out first, all at once, so their latency overlaps the RoPE
-    // and each other: the key rows this thread scores (positions tid and
-    // tid + 256) and the first VP values of its wave's chunk for P.V.
+    // Cache reads go out first, all at once and without branches, so their
+    // latency overlaps the RoPE and each other: the key rows this thread scores
+    // (positions tid and tid + 256) and the first VP values of its wave's chunk
+    // for P.V. Addresses are clamped into the cache and unused values replaced
+    // by selection, never by guarding a load.
     constexpr int KP = 2, VP = 64;
     float4 kreg[KP][D / 4];
 #pragma unroll
     for (int r = 0; r < KP; ++r) {
         const int t = tid + r * kT;
-        const bool load = t < past;                    // position past is the new key, in LDS
-        const float4 *k = reinterpret_cast<const float4 *>(K + (size_t)(load ? t : 0) * D);
+        const float4 *k = reinterpret_cast<const float4 *>(K + (size_t)(t < past ? t : 0) * D);
 #pragma unroll
-        for (int d4 = 0; d4 < D / 4; ++d4) kreg[r][d4] = load ? k[d4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int d4 = 0; d4 < D / 4; ++d4) kreg[r][d4] = k[d4];
     }
+    const int dl = lane < D ? lane : 0;
     float vreg[VP];
 #pragma unroll
     for (int j = 0; j < VP; ++j) {
         const int t = t0 + j;
-        const bool load = lane < D && t < t1 && t < past;
-        const float v = V[(size_t)(load ? t : 0) * D + (lane < D ? lane : 0)];   // always in bounds
-        vreg[j] = load ? v : 0.0f;
+        vreg[j] = V[(size_t)(t < past ? t : 0) * D + dl];
     }
 
     if (tid < half) {
@@ -251,25 +251,35 @@ __global__ __launch_bounds__(kT) void attention_decode(float *__restrict__ ctx, 
         V[(size_t)past * D + tid] = vnew[tid];
     }
 
-    auto score = [&](const float4 *k) {
+    // scores: q . k in order of d (the new key, at position past, from LDS)
+    auto score = [&](const float4 (&k)[D / 4]) {
         float acc = 0.0f;
 #pragma unroll
         for (int d4 = 0; d4 < D / 4; ++d4) {
-            const float4 kv4 = k[d4];
-            acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 0], kv4.x));
-            acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 1], kv4.y));
-            acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 2], kv4.z));
-            acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 3], kv4.w));
+            acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 0], k[d4].x));
+            acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 1], k[d4].y));
+            acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 2], k[d4].z));
+            acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 3], k[d4].w));
         }
         return __fadd_rn(__fmul_rn(acc, scale), 0.0f);
     };
+    const float4 *knew4 = reinterpret_cast<const float4 *>(knew);
 #pragma unroll
     for (int r = 0; r < KP; ++r) {
         const int t = tid + r * kT;
-        if (t < T) e[t] = score(t == past ? reinterpret_cast<const float4 *>(knew) : kreg[r]);
+        const bool fresh = t == past;
+#pragma unroll
+        for (int d4 = 0; d4 < D / 4; ++d4) kreg[r][d4] = fresh ? knew4[d4] : kreg[r][d4];
+        const float z = score(kreg[r]);
+        if (t < T) e[t] = z;
     }
-    for (int t = tid + KP * kT; t < T; t += kT)
-        e[t] = score(t == past ? reinterpret_cast<const float4 *>(knew) : reinterpret_cast<const float4 *>(K + (size_t)t * D));
+    for (int t = tid + KP * kT; t < T; t += kT) {          // contexts beyond 512 keys
+        float4 k[D / 4];
+        const float4 *src = reinterpret_cast<const float4 *>(K + (size_t)(t < past ? t : 0) * D);
+#pragma unroll
+        for (int d4 = 0; d4 < D / 4; ++d4) k[d4] = t == past ? knew4[d4] : src[d4];
+        e[t] = score(k);
+    }
     __syncthreads();
     float m = -__builtin_inff();
     for (int t = tid; t < T; t += kT) m = nan_max(m, e[t]);
@@ -284,29 +294,37 @@ __global__ __launch_bounds__(kT) void attention_decode(float *__restrict__ ctx, 
     for (int t = tid; t < T; t += kT) e[t] = nc::div_rn(e[t], sum);
     __syncthreads();
 
+    // P.V over the wave's chunk in position order. A position past the chunk
+    // contributes 0 * 0 = +0, and the accumulator (from +0, adding products)
+    // is never -0, so that addition is exact and changes nothing.
+    const float vfresh = vnew[dl];
     float acc = 0.0f;
-    if (lane < D) {
-        // the prefetched first VP positions of the chunk, then tiles of 32
-        // whose 32 loads go out together; the adds always in position order
 #pragma unroll
-        for (int j = 0; j < VP; ++j) {
-            const int t = t0 + j;
-            if (t < t1) acc = __fadd_rn(acc, __fmul_rn(e[t], t == past ? vnew[lane] : vreg[j]));
-        }
-        constexpr int TILE = 32;
-        for (int t = t0 + VP; t < t1; t += TILE) {
-            float vv[TILE];
-#pragma unroll
-            for (int j = 0; j < TILE; ++j) {
-                const int tj = t + j;
-                vv[j] = tj < t1 ? (tj == past ? vnew[lane] : V[(size_t)tj * D + lane]) : 0.0f;
-            }
-#pragma unroll
-            for (int j = 0; j < TILE; ++j)
-                if (t + j < t1) acc = __fadd_rn(acc, __fmul_rn(e[t + j], vv[j]));
-        }
-        part[wave][lane] = acc;
+    for (int j = 0; j < VP; ++j) {
+        const int t = t0 + j;
+        const bool in = t < t1;
+        const float p = in ? e[in ? t : 0] : 0.0f;
+        const float v = in ? (t == past ? vfresh : vreg[j]) : 0.0f;
+        acc = __fadd_rn(acc, __fmul_rn(p, v));
     }
+    constexpr int TILE = 32;
+    for (int t = t0 + VP; t < t1; t += TILE) {
+        float vv[TILE];
+#pragma unroll
+        for (int j = 0; j < TILE; ++j) {
+            const int tj = t + j;
+            vv[j] = V[(size_t)(tj < past ? tj : 0) * D + dl];
+        }
+#pragma unroll
+        for (int j = 0; j < TILE; ++j) {
+            const int tj = t + j;
+            const bool in = tj < t1;
+            const float p = in ? e[in ? tj : 0] : 0.0f;
+            const float v = in ? (tj == past ? vfresh : vv[j]) : 0.0f;
+            acc = __fadd_rn(acc, __fmul_rn(p, v));
+        }
+    }
+    if (lane < D) part[wave][lane] = acc;
     __syncthreads();
     if (tid < D) ctx[h * D + tid] = __fadd_rn(__fadd_rn(part[0][tid], part[1][tid]), __fadd_rn(part[2][tid], part[3][tid]));
 }
