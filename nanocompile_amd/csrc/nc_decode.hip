@@ -167,6 +167,31 @@ __device__ float block_max(float v, float *scratch) {
     return r;
 }
 
+// One key row held in registers: D/4 float4, dotted with q in order of d.
+template <int D>
+struct KeyRow {
+    float4 v[D / 4];
+    __device__ __forceinline__ void load(const float *__restrict__ row) {
+#pragma unroll
+        for (int d4 = 0; d4 < D / 4; ++d4) v[d4] = reinterpret_cast<const float4 *>(row)[d4];
+    }
+    __device__ __forceinline__ void load_lds(const float *row) {
+#pragma unroll
+        for (int d4 = 0; d4 < D / 4; ++d4) v[d4] = reinterpret_cast<const float4 *>(row)[d4];
+    }
+    __device__ __forceinline__ float score(const float *q, float scale) const {
+        float acc = 0.0f;
+#pragma unroll
+        for (int d4 = 0; d4 < D / 4; ++d4) {
+            acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 0], v[d4].x));
+            acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 1], v[d4].y));
+            acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 2], v[d4].z));
+            acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 3], v[d4].w));
+        }
+        return __fadd_rn(__fmul_rn(acc, scale), 0.0f);
+    }
+};
+
 // Head h of the new token at position past (read from pos_ptr when given).
 // q and the new k are rotated here (the same nc_cosf/nc_sinf of
 // f32(past) * inv_freq[j] as nc_rope_append); the first query head of each KV
@@ -211,15 +236,9 @@ __global__ __launch_bounds__(kT) void attention_decode(float *__restrict__ ctx, 
     // (positions tid and tid + 256) and the first VP values of its wave's chunk
     // for P.V. Addresses are clamped into the cache and unused values replaced
     // by selection, never by guarding a load.
-    constexpr int KP = 2, VP = 64;
-    float4 kreg[KP][D / 4];
-#pragma unroll
-    for (int r = 0; r < KP; ++r) {
-        const int t = tid + r * kT;
-        const float4 *k = reinterpret_cast<const float4 *>(K + (size_t)(t < past ? t : 0) * D);
-#pragma unroll
-        for (int d4 = 0; d4 < D / 4; ++d4) kreg[r][d4] = k[d4];
-    }
+    constexpr int VP = 32;
+    KeyRow<D> kreg;
+    kreg.load(K + (size_t)(tid < past ? tid : 0) * D);
     const int dl = lane < D ? lane : 0;
     float vreg[VP];
 #pragma unroll
@@ -251,34 +270,14 @@ __global__ __launch_bounds__(kT) void attention_decode(float *__restrict__ ctx, 
         V[(size_t)past * D + tid] = vnew[tid];
     }
 
-    // scores: q . k in order of d (the new key, at position past, from LDS)
-    auto score = [&](const float4 (&k)[D / 4]) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int d4 = 0; d4 < D / 4; ++d4) {
-            acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 0], k[d4].x));
-            acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 1], k[d4].y));
-            acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 2], k[d4].z));
-            acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 3], k[d4].w));
-        }
-        return __fadd_rn(__fmul_rn(acc, scale), 0.0f);
-    };
-    const float4 *knew4 = reinterpret_cast<const float4 *>(knew);
-#pragma unroll
-    for (int r = 0; r < KP; ++r) {
-        const int t = tid + r * kT;
-        const bool fresh = t == past;
-#pragma unroll
-        for (int d4 = 0; d4 < D / 4; ++d4) kreg[r][d4] = fresh ? knew4[d4] : kreg[r][d4];
-        const float z = score(kreg[r]);
-        if (t < T) e[t] = z;
-    }
-    for (int t = tid + KP * kT; t < T; t += kT) {          // contexts beyond 512 keys
-        float4 k[D / 4];
-        const float4 *src = reinterpret_cast<const float4 *>(K + (size_t)(t < past ? t : 0) * D);
-#pragma unroll
-        for (int d4 = 0; d4 < D / 4; ++d4) k[d4] = t == past ? knew4[d4] : src[d4];
-        e[t] = score(k);
+    // scores: q . k in order of d; the new key (position past) from LDS
+    if (tid == past) kreg.load_lds(knew);
+    if (tid < T) e[tid] = kreg.score(q, scale);
+    for (int t = tid + kT; t < T; t += kT) {              // contexts beyond 256 keys
+        KeyRow<D> k;
+        if (t == past) k.load_lds(knew);
+        else k.load(K + (size_t)t * D);
+        e[t] = k.score(q, scale);
     }
     __syncthreads();
     float m = -__builtin_inff();
