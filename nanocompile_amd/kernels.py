@@ -132,3 +132,94 @@ def matmul_i8_token_stacked(xq, xs, q, scales, out: DeviceArray | None = None, s
         out = DeviceArray((b, m, n), F32)
     hip.call("nc_matmul_i8_token_stacked", [out, xq, xs, q, scales], [b, m, n, k, schedule])
     return out
+
+
+# -- the reference's two int8 modes (matmul_i8, matmul_i8_vnni) ----------------------
+
+
+def pack_chains(q: np.ndarray) -> np.ndarray:
+    """matmul_i8's weight layout: per row, per group of 4 whole 32-blocks, lane l's 16 bytes
+    are [block][c] = w[32*k0 + 8c + l] (zeros past the last block)."""
+    q = np.ascontiguousarray(q, np.int8)
+    n, k = q.shape
+    blocks = k // 32
+    quads = -(-blocks // 4)
+    wide = np.zeros((n, quads * 4, 4, 8), np.int8)                      # (n, k0, c, l)
+    wide[:, :blocks] = q[:, :blocks * 32].reshape(n, blocks, 4, 8)
+    return np.ascontiguousarray(wide.reshape(n, quads, 4, 4, 8).transpose(0, 1, 4, 2, 3))   # (n, j, l, kk, c)
+
+
+def pack_chains_vnni(q: np.ndarray) -> np.ndarray:
+    """matmul_i8_vnni's weight layout: per row, per 128-block, lane l's 16 bytes are the
+    four dwords w[128*k0 + 32c + 4l .. + 3], c = 0..3."""
+    q = np.ascontiguousarray(q, np.int8)
+    n, k = q.shape
+    strides = k // 128
+    wide = q[:, :strides * 128].reshape(n, strides, 4, 8, 4)             # (n, k0, c, l, j)
+    return np.ascontiguousarray(wide.transpose(0, 1, 3, 2, 4))            # (n, k0, l, c, j)
+
+
+def _epilogue_operands(op, n, m, bias, residual):
+    if bias is not None:
+        bias = _device(bias, F32)
+        if bias.shape != (n,):
+            raise ShapeError(f"{op}: bias must be f32[{n}]")
+    if residual is not None:
+        residual = _device(residual, F32)
+        if residual.shape != (m, n):
+            raise ShapeError(f"{op}: residual must be f32[{m}, {n}]")
+    return bias, residual
+
+
+def matmul_i8(x, q, scales, packed=None, bias=None, residual=None) -> DeviceArray:
+    """The reference's matmul_i8 (ir.py:392-406): float activations, per-row int8 weights,
+    the 32-chain FMA order of lower.py:294-356, bit for bit."""
+    x, scales = _device(x, F32), _device(scales, F32)
+    if len(x.shape) != 2:
+        raise ShapeError(f"matmul_i8: activations must be f32[M, K], got {list(x.shape)}")
+    m, k = x.shape
+    host_q = q.numpy() if isinstance(q, DeviceArray) else np.asarray(q)
+    q = _device(q, I8)
+    n = _int8_weight("matmul_i8", q, scales, k)
+    packed = _device(pack_chains(host_q) if packed is None else packed, I8)
+    bias, residual = _epilogue_operands("matmul_i8", n, m, bias, residual)
+    y = DeviceArray((m, n), F32)
+    hip.call("nc_matmul_i8", [y, x, packed, q, scales, bias, residual], [m, n, k])
+    return y
+
+
+def quantize_blocks(x, block: int = 32) -> tuple[DeviceArray, DeviceArray, DeviceArray]:
+    """Block activation quantization (quantize.py:102-124): (xq i8[M,K], xs f32[M,K/block], offset f32[M])."""
+    x = _device(x, F32)
+    if len(x.shape) != 2:
+        raise ShapeError(f"quantize_blocks: activations must be f32[M, K], got {list(x.shape)}")
+    m, k = x.shape
+    if k % block:
+        raise ValueError(f"width {k} is not a whole number of blocks of {block}")
+    xq, xs, offset = DeviceArray((m, k), I8), DeviceArray((m, k // block), F32), DeviceArray((m,), F32)
+    if m:
+        hip.call("nc_quantize_blocks", [xq, xs, offset, x], [m, k, block])
+    return xq, xs, offset
+
+
+def matmul_i8_vnni(xq, xs, offset, q, scales, block: int = 32, packed=None, bias=None,
+                   residual=None) -> DeviceArray:
+    """The reference's matmul_i8_vnni (ir.py:409-439) in the order of lower.py:359-397, bit for bit."""
+    if not (isinstance(block, int) and block >= 32 and block & (block - 1) == 0):
+        raise ShapeError(f"matmul_i8_vnni: block must be a power of two >= 32, got {block!r}")
+    xq, xs, offset, scales = _device(xq, I8), _device(xs, F32), _device(offset, F32), _device(scales, F32)
+    if len(xq.shape) != 2:
+        raise ShapeError(f"matmul_i8_vnni: activations must be i8[M, K], got {list(xq.shape)}")
+    m, k = xq.shape
+    if k % block:
+        raise ShapeError(f"matmul_i8_vnni: width {k} is not a whole number of blocks of {block}")
+    if xs.shape != (m, k // block) or offset.shape not in ((m,), (m, 1)):
+        raise ShapeError("matmul_i8_vnni: expected f32[M, K/block] scales and f32[M, 1] offsets")
+    host_q = q.numpy() if isinstance(q, DeviceArray) else np.asarray(q)
+    q = _device(q, I8)
+    n = _int8_weight("matmul_i8_vnni", q, scales, k)
+    packed = _device(pack_chains_vnni(host_q) if packed is None else packed, I8)
+    bias, residual = _epilogue_operands("matmul_i8_vnni", n, m, bias, residual)
+    y = DeviceArray((m, n), F32)
+    hip.call("nc_matmul_i8_vnni", [y, xq, xs, offset, packed, q, scales, bias, residual], [m, n, k, block])
+    return y

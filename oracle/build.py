@@ -24,7 +24,7 @@ def build(verbose: bool = False) -> Path:
     cc = os.environ.get("CC") or shutil.which("gcc") or "cc"
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     scratch = LIBRARY.with_suffix(".so.tmp")
-    cmd = [cc, *CFLAGS, "-o", str(scratch), str(HERE / "nc_host.c"), str(HERE / "nc_model.c"), "-lm"]
+    cmd = [cc, *CFLAGS, "-o", str(scratch), str(HERE / "nc_host.c"), str(HERE / "nc_model.c"), str(HERE / "nc_modes.c"), "-lm"]
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
         raise RuntimeError(f"gcc failed on nc_host.c:\n{result.stderr[-6000:]}")

@@ -156,3 +156,22 @@ def matmul_i8_token_swiglu(xq, xs, qg, sg, qu, su) -> np.ndarray:
     args = [np.ascontiguousarray(a) for a in (xq, xs, qg, sg, qu, su)]
     _sig("nc_host_matmul_i8_token_swiglu", 7, 3)(_ptr(h), *[_ptr(a) for a in args], m, n, k)
     return h
+
+
+def matmul_i8_f32(x, q, scales) -> np.ndarray:
+    """The reference's matmul_i8 (float activations) in its 32-chain FMA order (lower.py:294-356)."""
+    x, q, scales = (np.ascontiguousarray(a) for a in (x, q, scales))
+    m, k = x.shape
+    y = np.empty((m, q.shape[0]), np.float32)
+    _sig("nc_host_matmul_i8_f32", 4, 3)(_ptr(y), _ptr(x), _ptr(q), _ptr(scales), m, q.shape[0], k)
+    return y
+
+
+def matmul_i8_vnni(xq, xs, offset, q, scales, block: int = 32) -> np.ndarray:
+    """The reference's matmul_i8_vnni in its Dp4 / block-scale order (lower.py:359-397)."""
+    xq, xs, offset, q, scales = (np.ascontiguousarray(a) for a in (xq, xs, offset, q, scales))
+    m, k = xq.shape
+    y = np.empty((m, q.shape[0]), np.float32)
+    _sig("nc_host_matmul_i8_vnni", 6, 4)(_ptr(y), _ptr(xq), _ptr(xs), _ptr(offset), _ptr(q), _ptr(scales), m,
+                                         q.shape[0], k, block)
+    return y

@@ -118,3 +118,40 @@ def test_nc_math_against_the_c_library(host):
     assert e[0] == 1 and e[1] == 1 and e[2] == np.inf and e[3] == 0 and np.isnan(e[4]) and e[6] == 0
     s = host.math("nc_sin", special)
     assert s[0] == 0 and np.signbit(s[1]) and np.isnan(s[2]) and np.isnan(s[3]) and s[7] == np.float32(1e-30)
+
+
+WIDTHS = [(896, 72), (4864, 24), (77, 40), (40, 16), (160, 40), (96, 24)]
+
+
+def golden_matmul_inputs(k, n, tokens):
+    from tests.golden.make_golden import matmul_inputs
+    w, x = matmul_inputs(k, n, tokens, seed=k + tokens)
+    return w, x
+
+
+@pytest.mark.parametrize("k,n", WIDTHS)
+def test_g2_matmul_i8_order_is_the_references(golden, meta, host, k, n):
+    """The host restatement of the 32-chain FMA order, bitwise against the reference's generated C."""
+    for tokens in (1, 3, 7):
+        w, x = golden_matmul_inputs(k, n, tokens)
+        key = f"g2_{k}_{n}_{tokens}"
+        assert sha(w) == meta[key]["w_sha"] and sha(x) == meta[key]["x_sha"]
+        q, s = R.quantize_int8(w)
+        assert np.array_equal(bits(host.matmul_i8_f32(x, q, s)), bits(golden[key]))
+
+
+@pytest.mark.parametrize("k,n", [(k, n) for k, n in WIDTHS if k % 32 == 0])
+def test_g3_matmul_i8_vnni_order_is_the_references(golden, meta, host, k, n):
+    for tokens in (1, 3, 7):
+        w, x = golden_matmul_inputs(k, n, tokens)
+        key = f"g3_{k}_{n}_{tokens}"
+        q, s = R.quantize_int8(w)
+        xq, xs, off = R.quantize_blocks(x, 32)
+        assert np.array_equal(bits(host.matmul_i8_vnni(xq, xs, off, q, s)), bits(golden[key]))
+
+
+def test_the_interpreter_meanings_agree_with_the_orders_to_rounding(golden):
+    """The reference's interpreter (simulated int8, f64 block combine) vs its C, as it documents."""
+    for key in [k for k in golden.files if (k.startswith("g2_") or k.startswith("g3_")) and not k.endswith("_interp")
+                and not k.startswith("g3_quant")]:
+        np.testing.assert_allclose(golden[key], golden[key + "_interp"], rtol=1e-4, atol=1e-3)

@@ -1,0 +1,91 @@
+"""The reference's int8 modes on the GPU, bit for bit against the reference's generated C.
+
+tests/golden G2 and G3 hold what the reference's own compiled kernels produce
+for matmul_i8 and matmul_i8_vnni at its test widths (test_int8.py:146) and
+1, 3, 7 tokens, from inputs regenerated here from the recorded seeds.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import reference as R
+from tests.conftest import bits
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden" / "golden.npz"
+WIDTHS = [(896, 72), (4864, 24), (77, 40), (40, 16), (160, 40), (96, 24)]
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(GOLDEN, allow_pickle=False)
+
+
+def inputs(k, n, tokens):
+    from tests.golden.make_golden import matmul_inputs
+    return matmul_inputs(k, n, tokens, seed=k + tokens)
+
+
+@pytest.mark.parametrize("k,n", WIDTHS)
+def test_matmul_i8_is_the_references_generated_c(gpu, golden, k, n):
+    from nanocompile_amd import kernels
+    print(f"matmul_i8 k={k} n={n}", flush=True)
+    for tokens in (1, 3, 7):
+        w, x = inputs(k, n, tokens)
+        q, s = R.quantize_int8(w)
+        got = kernels.matmul_i8(x, q, s).numpy()
+        assert np.array_equal(bits(got), bits(golden[f"g2_{k}_{n}_{tokens}"])), tokens
+
+
+@pytest.mark.parametrize("k,n", [(k, n) for k, n in WIDTHS if k % 32 == 0])
+def test_matmul_i8_vnni_is_the_references_generated_c(gpu, golden, k, n):
+    from nanocompile_amd import kernels
+    print(f"matmul_i8_vnni k={k} n={n}", flush=True)
+    for tokens in (1, 3, 7):
+        w, x = inputs(k, n, tokens)
+        q, s = R.quantize_int8(w)
+        xq, xs, off = kernels.quantize_blocks(x, 32)
+        exq, exs, eoff = R.quantize_blocks(x, 32)
+        assert np.array_equal(xq.numpy(), exq) and np.array_equal(bits(xs.numpy()), bits(exs))
+        assert np.array_equal(bits(off.numpy()), bits(eoff[:, 0]))
+        got = kernels.matmul_i8_vnni(xq, xs, off, q, s, 32).numpy()
+        assert np.array_equal(bits(got), bits(golden[f"g3_{k}_{n}_{tokens}"])), tokens
+
+
+def test_block_quantizer_is_the_references(gpu, golden):
+    from nanocompile_amd import kernels
+    _, x = inputs(96, 1, 5)
+    xq, xs, off = kernels.quantize_blocks(x, 32)
+    assert np.array_equal(xq.numpy(), golden["g3_quant_xq"])
+    assert np.array_equal(bits(xs.numpy()), bits(golden["g3_quant_xs"]))
+    assert np.array_equal(bits(off.numpy()), bits(golden["g3_quant_offset"][:, 0]))
+
+
+@pytest.mark.parametrize("k,n,m", [(896, 896, 1), (4864, 896, 2), (896, 4864, 5), (128, 40, 3), (64, 8, 2)])
+def test_modes_at_model_shapes_match_the_host_restatement(gpu, host, k, n, m):
+    """Model widths the golden set does not cover, with bias and residual epilogues."""
+    from nanocompile_amd import kernels
+    rng = np.random.default_rng(k + n + m)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[rng.random(x.shape) < 0.01] *= 20
+    b, r = rng.standard_normal(n).astype(np.float32), rng.standard_normal((m, n)).astype(np.float32)
+    q, s = R.quantize_int8(w)
+    y = kernels.matmul_i8(x, q, s, bias=b, residual=r).numpy()
+    expected = (r + (host.matmul_i8_f32(x, q, s) + b).astype(np.float32)).astype(np.float32)
+    assert np.array_equal(bits(y), bits(expected))
+    xq, xs, off = R.quantize_blocks(x, 32)
+    y = kernels.matmul_i8_vnni(xq, xs, off[:, 0], q, s, 32).numpy()
+    assert np.array_equal(bits(y), bits(host.matmul_i8_vnni(xq, xs, off, q, s)))
+
+
+def test_vnni_rejects_blocks_that_are_not_powers_of_two(gpu):
+    from nanocompile_amd import kernels
+    xq = np.zeros((1, 96), np.int8)
+    with pytest.raises(kernels.ShapeError, match="power of two"):
+        kernels.matmul_i8_vnni(xq, np.ones((1, 2), np.float32), np.zeros(1, np.float32),
+                               np.zeros((4, 96), np.int8), np.ones(4, np.float32), block=48)
