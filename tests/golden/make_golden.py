@@ -50,6 +50,7 @@ from nanocompile.models.qwen2 import Qwen2, Qwen2Config, greedy  # noqa: E402
 from nanocompile.runtime import CBackend, CompiledGraph  # noqa: E402
 
 from nanocompile_amd.models import config as ours  # noqa: E402  (the seeded weight generator)
+from tests.golden.inputs import matmul_inputs, special_rows  # noqa: E402
 
 
 def sha(a: np.ndarray) -> str:
@@ -65,15 +66,6 @@ def put(name: str, a) -> None:
 
 
 # -- G1: the weight quantizer ------------------------------------------------------
-
-
-def special_rows() -> np.ndarray:
-    rng = np.random.default_rng(0)
-    w = (rng.standard_normal((37, 70)) * 0.04).astype(np.float32)
-    w[3] = 0.0
-    w[5, :4] = [0.5, -0.5, 1.5, -2.5]
-    w[5, 4] = 127.0 / 64
-    return w
 
 
 def g1() -> None:
@@ -97,15 +89,6 @@ def projection(k: int, n: int):
     b = GraphBuilder("projection")
     x = b.input("x", dtypes.f32, (b.symbol("seq"), k))
     return b.build({"y": nn.linear(x, b.weight("w", (n, k)))})
-
-
-def matmul_inputs(k: int, n: int, tokens: int, seed: int):
-    """The reference test's inputs (test_int8.py:150-155): weights N(0, 0.05), x N(0, 4), outliers."""
-    rng = np.random.default_rng(seed)
-    w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
-    x = (rng.standard_normal((tokens, k)) * 2).astype(np.float32)
-    x[:, ::13] *= 40.0
-    return w, x
 
 
 def g2_g3() -> None:

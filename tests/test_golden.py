@@ -47,7 +47,7 @@ def test_g1_quantize_int8_is_the_references(golden, meta):
 
 
 def test_g3_block_quantizer_is_the_references(golden, meta):
-    from tests.golden.make_golden import matmul_inputs
+    from tests.golden.inputs import matmul_inputs
     _, x = matmul_inputs(96, 1, 5, seed=101)
     assert sha(x) == meta["g3_quant"]["x_sha"]
     xq, xs, offset = R.quantize_blocks(x, 32)
@@ -124,7 +124,7 @@ WIDTHS = [(896, 72), (4864, 24), (77, 40), (40, 16), (160, 40), (96, 24)]
 
 
 def golden_matmul_inputs(k, n, tokens):
-    from tests.golden.make_golden import matmul_inputs
+    from tests.golden.inputs import matmul_inputs
     w, x = matmul_inputs(k, n, tokens, seed=k + tokens)
     return w, x
 

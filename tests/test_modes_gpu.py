@@ -26,7 +26,7 @@ def golden():
 
 
 def inputs(k, n, tokens):
-    from tests.golden.make_golden import matmul_inputs
+    from tests.golden.inputs import matmul_inputs
     return matmul_inputs(k, n, tokens, seed=k + tokens)
 
 
