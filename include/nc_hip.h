@@ -132,6 +132,54 @@ int32_t nc_matmul_i8_token_stacked(void **p, const int64_t *s);
  * s: [M, N, K] (K a multiple of 16, at most 8192) */
 int32_t nc_matmul_i8_token_swiglu(void **p, const int64_t *s);
 
+/* -- the reference's own int8 modes, bit for bit ------------------------------ */
+
+/* matmul_i8: y = x @ (q * scales).T with f32 activations times int8 weights,
+ * each dot summed in the reference's 32 interleaved chains then its tree
+ * (lower.py:298-360, kernel at lower.py:400-417), then + bias, then
+ * residual + y. The packed operand is q reordered chain-major once per weight
+ * (nanocompile_amd.kernels.pack_chains) so the chains load coalesced.
+ * p: [y f32[M,N], x f32[M,K], packed i8, q i8[N,K], scales f32[N],
+ *     bias f32[N] or NULL, residual f32[M,N] or NULL];  s: [M, N, K] (K <= 16384) */
+int32_t nc_matmul_i8(void **p, const int64_t *s);
+
+/* matmul_i8_vnni: per-block int8 activations (xq, xs, offset from
+ * nc_quantize_blocks) times int8 weights, each block's byte dots in the
+ * reference's Dp4 order with its +128 offset (lower.py:363-397), the block
+ * sums scaled by xs and added in order, minus offset, times scales[n].
+ * p: [y f32[M,N], xq i8[M,K], xs f32[M,K/block], offset f32[M], packed i8
+ *     (pack_chains_vnni), q i8[N,K], scales f32[N], bias or NULL, residual or NULL];
+ * s: [M, N, K, block] (block a power of two >= 32 dividing K) */
+int32_t nc_matmul_i8_vnni(void **p, const int64_t *s);
+
+/* The block activation quantizer of matmul_i8_vnni (quantize.py:102-124):
+ * per block of K, xs = max|x| / 127 (1 for an all-zero block), xq = round(x / xs),
+ * offset = 128 * sum_b xs[b] * sum_{k in b} xq[k].
+ * p: [xq i8[M,K], xs f32[M,K/block], offset f32[M], x f32[M,K]];  s: [M, K, block] */
+int32_t nc_quantize_blocks(void **p, const int64_t *s);
+
+/* -- one decode token, fused ---------------------------------------------------- */
+
+/* One projection of a single token with its activation prologue fused
+ * (the reference's fused rms_norm row kernel and matmul epilogues,
+ * fusion.py:631-711, for M = 1): kind 0 = rms_norm + per-token quantize +
+ * bias (q, k, v); 1 = per-token quantize + residual added into out (o, down);
+ * 2 = rms_norm + quantize + SwiGLU pair (gate, up). Same arithmetic, bit for
+ * bit, as nc_rms_norm_quant followed by nc_matmul_i8_token(_swiglu).
+ * p: [out f32[N] (holds the residual for kind 1), x f32[K], gamma f32[K] or NULL,
+ *     q i8[N,K], scales f32[N], bias f32[N] or NULL, q2 i8[N,K] or NULL, scales2 f32[N] or NULL];
+ * s: [N, K, kind, eps as float32 bits]; K in {896, 4864} (and the test model's 128, 256);
+ * other widths take the unfused kernels. */
+int32_t nc_decode_projection(void **p, const int64_t *s);
+
+/* Attention of one new token (models/qwen2.py:113-155 at seq = 1) with RoPE of
+ * its q and k heads and the cache append fused in: the same arithmetic, bit for
+ * bit, as nc_rope_append followed by nc_attention.
+ * p: [ctx f32[heads*D], qkv f32[(heads+2*kv)*D] (unrotated), kcache f32[kv,C,D],
+ *     vcache f32[kv,C,D], inv_freq f32[D/2], pos i64[1] or NULL (read in place of s[3])];
+ * s: [heads, kv, D, past, C, scale as float32 bits] (D 64 or 32, C <= 16384) */
+int32_t nc_attention_decode(void **p, const int64_t *s);
+
 /* -- fused groups around the projections (nn.py, models/qwen2.py) ------------ */
 
 /* y = silu(g) * u elementwise: p = 0 <= g, e = exp(p ? -g : g),
