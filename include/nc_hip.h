@@ -43,6 +43,10 @@ int32_t nc_device_count(void);
 int32_t nc_init(int32_t device);
 int32_t nc_device_info(char *arch, int64_t arch_len, int64_t *compute_units, int64_t *lds_bytes,
                        int64_t *hbm_bytes, int64_t *clock_khz);
+/* HIP runtime and driver versions: with the arch and CU count, the machine
+ * key of the tuning cache (the reference keys on compiler, CPU and threads,
+ * autotune.py:481-484). */
+int32_t nc_runtime_version(int64_t *runtime, int64_t *driver);
 
 /* Device memory: the reference's one 64-byte-aligned arena (runtime.py:39,
  * 239-243) becomes one hipMalloc arena the Python runtime carves up. */
@@ -110,8 +114,21 @@ int32_t nc_probe_fp32_ops(void **p, const int64_t *s);
  * the reference lacks.
  * p: [y f32[M,N], xq i8[M,K], xs f32[M], q i8[N,K], scales f32[N],
  *     bias f32[N] or NULL, residual f32[M,N] or NULL];
- * s: [M, N, K, schedule] (schedule 0 is the default) */
+ * s: [M, N, K, schedule]. Schedules (the reference's schedule knobs,
+ * schedules.py:96-110, become GPU launch shapes): 0 = the library's choice
+ * (the GEMV below 16 tokens, else an MFMA tile chosen by shape);
+ * 1..7 = the decode GEMV (lanes per row x waves per workgroup);
+ * 16..24 = the MFMA GEMM on v_mfma_i32_16x16x64_i8 with LDS-staged tiles
+ * (tile m x n, k stage, wave tile, register stages in flight), K a multiple of 16.
+ * nc_schedule_info describes each. Every schedule computes the same bits. */
 int32_t nc_matmul_i8_token(void **p, const int64_t *s);
+
+/* A schedule's launch shape, for the tuner (no device call): out[0] = 0 for
+ * the GEMV, then [lanes per row, waves, bytes per load]; out[0] = 1 for the
+ * MFMA GEMM, then [tile m, tile n, k stage, wave m, wave n, register stages,
+ * threads, LDS bytes]. NC_BAD_ARGS for 0 or an unknown index. The
+ * reference's schedule space is schedules.SPACES (schedules.py:96). */
+int32_t nc_schedule_info(int32_t schedule, int64_t *out);
 
 /* The raw int32 accumulators of matmul_i8_token, for bit-exact checking.
  * p: [acc i32[M,N], xq i8[M,K], q i8[N,K]];  s: [M, N, K, schedule] */
@@ -129,7 +146,8 @@ int32_t nc_matmul_i8_token_stacked(void **p, const int64_t *s);
  * (fusion.py:677-711 shares their k loop), then h = silu(gate) * up
  * (nn.py:41-54) in the epilogue; each projection's epilogue as above.
  * p: [h f32[M,N], xq i8[M,K], xs f32[M], qg i8[N,K], sg f32[N], qu i8[N,K], su f32[N]];
- * s: [M, N, K] (K a multiple of 16, at most 8192) */
+ * s: [M, N, K, schedule] (K a multiple of 16, at most 8192; schedule 0, the
+ * GEMV 7, or an MFMA tile 16..24) */
 int32_t nc_matmul_i8_token_swiglu(void **p, const int64_t *s);
 
 /* -- the reference's own int8 modes, bit for bit ------------------------------ */

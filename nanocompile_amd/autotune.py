@@ -1,0 +1,304 @@
+"""GPU autotuning of the int8 projections: each shape's schedule chosen by measurement.
+
+The reference tunes each generated C kernel over a space of CPU schedules
+(autotune.py:1-53): candidates timed in alternation, medians over rounds,
+weights rotated so they stream, every candidate checked bit for bit against
+the unscheduled kernel, a margin before a tuned schedule replaces the
+hand-written one, and a JSON cache keyed by machine and kernel. This module
+keeps those rules for the GPU library:
+
+* **The space** is the library's own schedule table, read with
+  ``nc_schedule_info`` (so the tuner searches exactly what the library runs):
+  GEMV launch shapes (lanes per row, waves per workgroup, 16-byte loads) and
+  MFMA tiles (tile m x n, k stage, wave tile, register stages in flight,
+  LDS bytes). Schedule 0, the library's own choice, is the incumbent.
+* **Cost** is HIP-event time per call, on the library stream, of a captured
+  graph of ``reps`` launches cycling over weight copies that together exceed
+  the 256 MB Infinity Cache, so weights stream from HBM as a decode step's do.
+  Candidates run in alternation, each round starting from a different one;
+  the cost is the median over rounds.
+* **Correctness**: each candidate runs once on random operands before it is
+  timed, and its output must equal schedule 0's bit for bit.
+* **Choice**: every legal candidate is measured (the space is small); the best
+  then runs against the incumbent with twice the rounds and replaces it only
+  if faster by more than ``margin``.
+* **Dispatch**: a GPU kernel's schedule is chosen per call, so the tuner picks
+  per token count M (decode and each prefill length) rather than one schedule
+  scored over a mix of workloads (the reference's DECODE/PREFILL weights,
+  autotune.py:65-69, exist because its C is compiled once for all seq).
+* **The cache** is JSON keyed by machine (arch, HIP runtime and driver
+  versions, CU count) and by problem (op, M, N, K, the space).
+"""
+
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+import statistics
+import tempfile
+import time
+from dataclasses import dataclass, field
+from pathlib import Path
+
+import numpy as np
+
+from nanocompile_amd import hip, kernels
+from nanocompile_amd.hip import DeviceArray, Event, Graph
+
+OPS = ("matmul_i8_token", "matmul_i8_token_swiglu")
+STREAM_BYTES = 512 * 2**20      # weight bytes one sample cycles through: past the 256 MB Infinity Cache
+MAX_COPIES = 64
+CACHE_VERSION = 1
+
+
+class TuningError(RuntimeError):
+    """A candidate failed its bit-for-bit check or could not be measured."""
+
+
+# -- the space ---------------------------------------------------------------------------
+
+
+def legal_space(op: str, m: int, n: int, k: int) -> list[dict]:
+    """Schedule 0 (the library's choice) first, then every schedule that applies to this problem."""
+    if op not in OPS:
+        raise ValueError(f"no tuning space for {op!r}")
+    out = [{"schedule": 0, "kernel": "default"}]
+    gemv = list(kernels.GEMV_SCHEDULES) if op == "matmul_i8_token" else [7]
+    for s in gemv:
+        out.append(hip.schedule_info(s))
+    if k % 16 == 0 and (op == "matmul_i8_token" or k <= 8192):
+        for s in kernels.GEMM_SCHEDULES:
+            out.append(hip.schedule_info(s))
+    return out
+
+
+# -- the problem on the device -------------------------------------------------------------
+
+
+class Problem:
+    """Device operands for one projection shape, with its weights in rotating copies."""
+
+    def __init__(self, op: str, m: int, n: int, k: int, seed: int = 0,
+                 stream_bytes: int = STREAM_BYTES) -> None:
+        self.op, self.m, self.n, self.k = op, m, n, k
+        rng = np.random.default_rng(seed)
+        per_copy = n * k * (2 if op == "matmul_i8_token_swiglu" else 1)
+        self.copies = int(min(MAX_COPIES, max(2, -(-stream_bytes // max(per_copy, 1)))))
+        self.xq = DeviceArray.from_host(rng.integers(-127, 128, (m, k)).astype(np.int8))
+        self.xs = DeviceArray.from_host((rng.random(m) * 0.05 + 1e-3).astype(np.float32))
+        matrices = 2 if op == "matmul_i8_token_swiglu" else 1
+        host = [rng.integers(-127, 128, (n, k)).astype(np.int8) for _ in range(matrices)]
+        self.q = [[DeviceArray.from_host(w) for w in host] for _ in range(self.copies)]
+        self.scales = [DeviceArray.from_host((rng.random(n) * 1e-3).astype(np.float32)) for _ in range(matrices)]
+        self.bias = DeviceArray.from_host(rng.standard_normal(n).astype(np.float32))
+        self.y = DeviceArray((m, n), np.float32)
+
+    def launch(self, schedule: int, copy: int = 0) -> None:
+        q = self.q[copy % self.copies]
+        if self.op == "matmul_i8_token":
+            hip.call("nc_matmul_i8_token", [self.y, self.xq, self.xs, q[0], self.scales[0], self.bias, None],
+                     [self.m, self.n, self.k, schedule])
+        else:
+            hip.call("nc_matmul_i8_token_swiglu",
+                     [self.y, self.xq, self.xs, q[0], self.scales[0], q[1], self.scales[1]],
+                     [self.m, self.n, self.k, schedule])
+
+    def output(self, schedule: int) -> np.ndarray:
+        self.launch(schedule, 0)
+        hip.sync()
+        return self.y.numpy().view(np.uint32).copy()
+
+
+def measure(problem: Problem, schedules: list[int], rounds: int, reps: int) -> list[float]:
+    """Median seconds per call of each schedule, the candidates alternating round by round."""
+    graphs = {}
+    for s in schedules:
+        graphs[s] = Graph.capture(lambda s=s: [problem.launch(s, i) for i in range(reps)])
+        graphs[s].launch()                      # warm: code objects loaded, caches in steady state
+    hip.sync()
+    start, stop = Event(), Event()
+    samples: dict[int, list[float]] = {s: [] for s in schedules}
+    for r in range(rounds):
+        order = schedules[r % len(schedules):] + schedules[:r % len(schedules)]
+        for s in order:
+            start.record()
+            graphs[s].launch()
+            stop.record()
+            hip.sync()
+            samples[s].append(start.elapsed_ms(stop) * 1e-3 / reps)
+    return [statistics.median(samples[s]) for s in schedules]
+
+
+# -- records and the cache ----------------------------------------------------------------------
+
+
+@dataclass
+class Evaluation:
+    stage: str
+    schedules: list[int]
+    costs: list[float]
+
+
+@dataclass
+class TuneRecord:
+    key: str
+    op: str
+    shape: tuple[int, int, int]
+    space_size: int
+    winner: int = 0
+    default_cost: float | None = None
+    winner_cost: float | None = None
+    evaluations: list[Evaluation] = field(default_factory=list)
+    seconds: float = 0.0
+    cached: bool = False
+
+    @property
+    def speedup(self) -> float | None:
+        if not self.default_cost or not self.winner_cost:
+            return None
+        return self.default_cost / self.winner_cost
+
+    def as_json(self) -> dict:
+        return {"key": self.key, "op": self.op, "shape": list(self.shape), "space": self.space_size,
+                "winner": self.winner, "default_cost": self.default_cost, "winner_cost": self.winner_cost,
+                "speedup": self.speedup, "seconds": round(self.seconds, 3), "cached": self.cached,
+                "evaluations": [{"stage": e.stage, "schedules": e.schedules, "costs": e.costs}
+                                for e in self.evaluations]}
+
+
+def choose(space: list[int], cost, margin: float) -> tuple[int, list[Evaluation], float, float]:
+    """Measure every candidate, then the best against the incumbent (space[0]) with more rounds.
+
+    ``cost(stage, schedules)`` returns seconds per call. The best replaces the
+    incumbent only if it is faster by more than ``margin``; returns (winner,
+    evaluations, incumbent's cost, winner's cost).
+    """
+    incumbent = space[0]
+    log = []
+    costs = cost("sample", list(space))
+    log.append(Evaluation("sample", list(space), costs))
+    best = space[int(np.argmin(costs))]
+    if best == incumbent:
+        return incumbent, log, costs[0], costs[0]
+    confirm = cost("confirm", [incumbent, best])
+    log.append(Evaluation("confirm", [incumbent, best], confirm))
+    if confirm[1] < confirm[0] * (1.0 - margin):
+        return best, log, confirm[0], confirm[1]
+    return incumbent, log, confirm[0], confirm[0]
+
+
+def machine_key() -> str:
+    """Arch, HIP runtime and driver, CU count: a schedule tuned on one need not suit another."""
+    info = hip.device_info()
+    runtime, driver = hip.runtime_version()
+    material = f"{info['arch']}|{runtime}|{driver}|{info['compute_units']}"
+    return hashlib.sha256(material.encode()).hexdigest()[:16]
+
+
+class TuningCache:
+    """Winning schedules on disk: ``{"machines": {machine: {problem: entry}}}``, in JSON."""
+
+    def __init__(self, path: Path | str | None = None) -> None:
+        if path is None:
+            path = os.environ.get("NANOCOMPILE_AMD_TUNING") or (
+                Path.home() / ".cache" / "nanocompile_amd" / "tuning.json")
+        self.path = Path(path)
+
+    def _load(self) -> dict:
+        try:
+            data = json.loads(self.path.read_text(encoding="utf-8"))
+        except (FileNotFoundError, json.JSONDecodeError):
+            return {"version": CACHE_VERSION, "machines": {}}
+        if data.get("version") != CACHE_VERSION:
+            return {"version": CACHE_VERSION, "machines": {}}
+        return data
+
+    def get(self, machine: str, key: str) -> dict | None:
+        return self._load()["machines"].get(machine, {}).get(key)
+
+    def put(self, machine: str, key: str, entry: dict) -> None:
+        data = self._load()
+        data["machines"].setdefault(machine, {})[key] = entry
+        self.path.parent.mkdir(parents=True, exist_ok=True)
+        fd, scratch = tempfile.mkstemp(dir=self.path.parent, suffix=".tmp")
+        with os.fdopen(fd, "w", encoding="utf-8") as f:
+            json.dump(data, f, indent=1, sort_keys=True)
+        os.replace(scratch, self.path)        # whole file or nothing
+
+
+# -- the tuner --------------------------------------------------------------------------------
+
+
+class Autotuner:
+    """Chooses the schedule of each projection problem (op, M, N, K) on this GPU.
+
+    ``cache`` is a TuningCache, a path, True for the default file, or None to
+    measure every time. ``records`` holds what each tuning did.
+    """
+
+    def __init__(self, rounds: int = 7, reps: int = 32, margin: float = 0.03, seed: int = 0,
+                 cache: TuningCache | Path | str | bool | None = True, verbose: bool = False,
+                 stream_bytes: int = STREAM_BYTES) -> None:
+        self.rounds, self.reps, self.margin, self.seed = rounds, reps, margin, seed
+        if cache is True:
+            cache = TuningCache()
+        elif cache not in (None, False) and not isinstance(cache, TuningCache):
+            cache = TuningCache(cache)
+        self.cache: TuningCache | None = cache or None
+        self.verbose = verbose
+        self.stream_bytes = stream_bytes
+        self.records: list[TuneRecord] = []
+        self._chosen: dict[tuple, int] = {}
+
+    @staticmethod
+    def problem_key(op: str, m: int, n: int, k: int, space: list[dict]) -> str:
+        material = json.dumps({"op": op, "m": m, "n": n, "k": k, "space": space}, sort_keys=True)
+        return hashlib.sha256(material.encode()).hexdigest()[:20]
+
+    def schedule(self, op: str, m: int, n: int, k: int) -> int:
+        """The schedule to launch ``op`` with on an [m, k] x [n, k]^T problem (tuned once, then remembered)."""
+        at = (op, m, n, k)
+        if at not in self._chosen:
+            self._chosen[at] = self.tune(op, m, n, k).winner
+        return self._chosen[at]
+
+    def tune(self, op: str, m: int, n: int, k: int) -> TuneRecord:
+        started = time.perf_counter()
+        space = legal_space(op, m, n, k)
+        key = self.problem_key(op, m, n, k, space)
+        record = TuneRecord(key, op, (m, n, k), len(space))
+        machine = machine_key()
+        if self.cache is not None:
+            entry = self.cache.get(machine, key)
+            if entry is not None and isinstance(entry.get("winner"), int):
+                record.winner, record.cached = entry["winner"], True
+                record.default_cost, record.winner_cost = entry.get("default_cost"), entry.get("winner_cost")
+                record.seconds = time.perf_counter() - started
+                self.records.append(record)
+                return record
+
+        problem = Problem(op, m, n, k, self.seed, self.stream_bytes)
+        schedules = [c["schedule"] for c in space]
+        reference = problem.output(0)
+        for s in schedules[1:]:
+            if not np.array_equal(problem.output(s), reference):
+                raise TuningError(f"{op} schedule {s} on {(m, n, k)} differs from the default's bits")
+
+        def cost(stage: str, candidates: list[int]) -> list[float]:
+            rounds = self.rounds * 2 if stage == "confirm" else self.rounds
+            return measure(problem, candidates, rounds, self.reps)
+
+        winner, log, default_cost, winner_cost = choose(schedules, cost, self.margin)
+        record.winner, record.evaluations = winner, log
+        record.default_cost, record.winner_cost = default_cost, winner_cost
+        record.seconds = time.perf_counter() - started
+        self.records.append(record)
+        if self.cache is not None:
+            self.cache.put(machine, key, {"winner": winner, "default_cost": default_cost,
+                                          "winner_cost": winner_cost, "op": op, "shape": [m, n, k]})
+        if self.verbose:
+            print(f"tuned {op} {(m, n, k)}: {len(space)} schedules in {record.seconds:.1f} s, "
+                  f"schedule {winner} at {winner_cost * 1e6:.2f} us ({record.speedup:.2f}x the default)",
+                  flush=True)
+        return record

@@ -115,6 +115,15 @@ int32_t *error_word();
 // NC_OK, or NC_LAUNCH_FAILED with the message recorded for nc_last_error().
 int32_t launched(const char *what);
 void set_message(const char *text);
+
+// The MFMA GEMM (nc_gemm.hip): tile index 0..8, epilogue 0 = dequantize
+// (+ bias, + residual), 1 = raw int32 accumulators, 2 = SwiGLU pair (q2, ws2).
+// K must be a multiple of 16.
+int32_t gemm_i8_token(int tile, int epi, void *out, const int8_t *xq, const float *xs, const int8_t *q,
+                      const float *ws, const float *bias, const float *residual, const int8_t *q2,
+                      const float *ws2, int M, int N, int K);
+// A tile's primitives: [BM, BN, BK, WM, WN, NS, threads, LDS bytes]; NC_BAD_ARGS past the table.
+int32_t gemm_tile_info(int tile, int64_t *out);
 }  // namespace nc
 
 // A launcher's argument checks: on failure, record why and return NC_BAD_ARGS.

@@ -19,7 +19,7 @@
 // fused step computes the same bits as the unfused one, and the host oracle
 // covers both.
 #include "nc_common.h"
-#include "nc_math.h"
+#include "nc_epilogue.h"
 
 namespace {
 
@@ -72,13 +72,6 @@ __device__ float activation_prologue(int8_t *__restrict__ sxq, const float *__re
     }
     __syncthreads();
     return scale;
-}
-
-__device__ __forceinline__ float silu_mul(float g, float u) {
-    const bool p = 0.0f <= g;
-    const float e = nc_expf(p ? -g : g);
-    const float sig = nc::div_rn(p ? 1.0f : e, __fadd_rn(e, 1.0f));
-    return __fmul_rn(__fmul_rn(g, sig), u);
 }
 
 template <int K>
@@ -134,7 +127,7 @@ __global__ __launch_bounds__(64) void gemv_decode(float *__restrict__ out, const
         out[n] = __fadd_rn(out[n], y);                     // out is the residual stream, updated in place
     } else {
         const float u = __fmul_rn(__fmul_rn((float)acc2, xs), ws2[n]);
-        out[n] = silu_mul(y, u);
+        out[n] = nc::silu_mul(y, u);
     }
 }
 

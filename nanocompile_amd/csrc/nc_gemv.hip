@@ -18,7 +18,7 @@
 // partial sums are added with lane shuffles, exact in int32, and lane 0 of
 // the group applies the epilogue.
 #include "nc_common.h"
-#include "nc_math.h"
+#include "nc_epilogue.h"
 
 namespace {
 
@@ -94,15 +94,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_i8_token(
     }
 }
 
-// silu(g) * u in the reference's float32 order (nn.py:41-54):
-// p = 0 <= g; e = exp(p ? -g : g); sigmoid = (p ? 1 : e) / (e + 1); (g * sigmoid) * u.
-__device__ __forceinline__ float silu_mul(float g, float u) {
-    const bool p = 0.0f <= g;
-    const float e = nc_expf(p ? -g : g);
-    const float sig = nc::div_rn(p ? 1.0f : e, __fadd_rn(e, 1.0f));
-    return __fmul_rn(__fmul_rn(g, sig), u);
-}
-
 // The SwiGLU pair: gate row n and up row n read by the same lane group, sharing
 // the activation chunks (the reference's gate and up share one k loop,
 // fusion.py:677-711), then h[m, n] = silu(gate) * up with each projection's
@@ -161,7 +152,7 @@ __global__ __launch_bounds__(64) void gemv_i8_token_swiglu(
             const float x = xs[m0 + m];
             const float g = __fmul_rn(__fmul_rn((float)ag[m], x), wsg[n]);
             const float u = __fmul_rn(__fmul_rn((float)au[m], x), wsu[n]);
-            h[(size_t)(m0 + m) * N + n] = silu_mul(g, u);
+            h[(size_t)(m0 + m) * N + n] = nc::silu_mul(g, u);
         }
     }
 }
@@ -226,20 +217,41 @@ int32_t launch_bytes(const Args &a) {
     return nc::launched("gemv_i8_token_bytes");
 }
 
-// The schedule space of the decode GEMV: lanes per row L and waves per
-// workgroup. Index 0 is the default. The token tile MT follows M.
+// The schedule space of the projection (one index space for the GEMV and
+// the MFMA GEMM):
+//   0            the default: gemv_schedule_default below for few tokens,
+//                else the MFMA tile auto_tile picks;
+//   1..7         the GEMV with lanes per row L and waves per workgroup
+//                (7 is the default GEMV, L = 8, one wave); the token tile MT follows M;
+//   16..16+8     the MFMA GEMM's tiles (nc_gemm.hip), K a multiple of 16.
+// (index, lanes per row L, waves per workgroup)
+#define NC_GEMV_SCHEDULES(X) X(1, 4, 1) X(2, 16, 1) X(3, 8, 2) X(4, 8, 4) X(5, 4, 2) X(6, 16, 2) X(7, 8, 1)
+constexpr int kGemmFirst = 16;
+constexpr int kGemmTiles = 9;
+constexpr int kGemmMinTokens = 16;
+
+// The MFMA tile for a shape when the caller asks for the default (measured on
+// MI355X at M = 512): 64 x 64 tiles once they give every CU two workgroups,
+// 32 x 64 with 8 stages in flight for long k loops, 32 x 64 while there are
+// still most of a workgroup per CU, else 32 x 32.
+int auto_tile(int M, int N, int K) {
+    auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+    if (tiles(64, 64) >= 512) return 5;
+    if (K >= 2048) return 4;
+    if (tiles(32, 64) >= 192) return 1;
+    return 2;
+}
+
 template <int KS, int MT, bool ACC_OUT>
 int32_t dispatch_schedule(const Args &a, int schedule) {
+#define NC_GEMV_CASE(I, L, W) \
+    case I: return launch<KS, L, W, MT, ACC_OUT>(a);
     switch (schedule) {
         case 0: return launch<KS, 8, 1, MT, ACC_OUT>(a);
-        case 1: return launch<KS, 4, 1, MT, ACC_OUT>(a);
-        case 2: return launch<KS, 16, 1, MT, ACC_OUT>(a);
-        case 3: return launch<KS, 8, 2, MT, ACC_OUT>(a);
-        case 4: return launch<KS, 8, 4, MT, ACC_OUT>(a);
-        case 5: return launch<KS, 4, 2, MT, ACC_OUT>(a);
-        case 6: return launch<KS, 16, 2, MT, ACC_OUT>(a);
+        NC_GEMV_SCHEDULES(NC_GEMV_CASE)
         default: nc::set_message("gemv_i8_token: no such schedule"); return NC_BAD_ARGS;
     }
+#undef NC_GEMV_CASE
 }
 
 template <int KS, bool ACC_OUT>
@@ -253,6 +265,19 @@ int32_t dispatch_tokens(const Args &a, int schedule) {
 template <bool ACC_OUT>
 int32_t run(const Args &a, int schedule) {
     if (a.M == 0 || a.N == 0) return NC_OK;
+    if (schedule < 0 || (schedule > 7 && schedule < kGemmFirst) || schedule >= kGemmFirst + kGemmTiles) {
+        nc::set_message("matmul_i8_token: no such schedule");
+        return NC_BAD_ARGS;
+    }
+    const bool gemm_ok = a.batch == 1 && a.K % 16 == 0;
+    if (schedule >= kGemmFirst && !gemm_ok) {
+        nc::set_message("matmul_i8_token: the MFMA schedules need K a multiple of 16 and one problem");
+        return NC_BAD_ARGS;
+    }
+    if (schedule == 0 && gemm_ok && a.M >= kGemmMinTokens) schedule = kGemmFirst + auto_tile(a.M, a.N, a.K);
+    if (schedule >= kGemmFirst)
+        return nc::gemm_i8_token(schedule - kGemmFirst, ACC_OUT ? 1 : 0, a.out, a.xq, a.xs, a.q, a.ws, a.bias,
+                                 a.residual, nullptr, nullptr, a.M, a.N, a.K);
     if (a.K % 16 != 0 || (size_t)8 * a.K > 65536) {
         if (a.batch != 1) { nc::set_message("stacked GEMV needs K a multiple of 16"); return NC_BAD_ARGS; }
         return launch_bytes<ACC_OUT>(a);
@@ -263,6 +288,30 @@ int32_t run(const Args &a, int schedule) {
 }
 
 }  // namespace
+
+// What schedule index `schedule` of the projection is, for the tuner; a
+// table lookup, no device call.
+// out[0] = 0 (GEMV): out[1..3] = [lanes per row, waves per workgroup, bytes per lane load];
+// out[0] = 1 (MFMA GEMM): out[1..8] = [BM, BN, BK, WM, WN, NS, threads, LDS bytes].
+// Schedule 0 (the default) reports NC_BAD_ARGS: it is a choice, not a schedule.
+NC_EXPORT int32_t nc_schedule_info(int32_t schedule, int64_t *out) {
+    if (!out) return NC_BAD_ARGS;
+#define NC_GEMV_INFO(I, L, W) \
+    if (schedule == I) {      \
+        out[0] = 0;           \
+        out[1] = L;           \
+        out[2] = W;           \
+        out[3] = 16;          \
+        return NC_OK;         \
+    }
+    NC_GEMV_SCHEDULES(NC_GEMV_INFO)
+#undef NC_GEMV_INFO
+    if (schedule >= kGemmFirst && schedule < kGemmFirst + kGemmTiles) {
+        out[0] = 1;
+        return nc::gemm_tile_info(schedule - kGemmFirst, out + 1);
+    }
+    return NC_BAD_ARGS;
+}
 
 // p: [y f32[M,N], xq i8[M,K], xs f32[M], q i8[N,K], scales f32[N], bias f32[N] | NULL,
 //     residual f32[M,N] | NULL];  s: [M, N, K, schedule]
@@ -329,6 +378,9 @@ NC_EXPORT int32_t nc_matmul_i8_token_swiglu(void **p, const int64_t *s) {
                    s[1] < (1 << 24),
                "nc_matmul_i8_token_swiglu: bad shape (K must be a multiple of 16, at most 8192)");
     const int M = (int)s[0], N = (int)s[1], K = (int)s[2];
+    int schedule = (int)s[3];
+    NC_REQUIRE(schedule == 0 || schedule == 7 || (schedule >= kGemmFirst && schedule < kGemmFirst + kGemmTiles),
+               "nc_matmul_i8_token_swiglu: no such schedule (0, 7 or an MFMA tile)");
     if (M == 0 || N == 0) return NC_OK;
     float *h = (float *)p[0];
     auto xq = (const int8_t *)p[1];
@@ -337,6 +389,9 @@ NC_EXPORT int32_t nc_matmul_i8_token_swiglu(void **p, const int64_t *s) {
     auto sg = (const float *)p[4];
     auto qu = (const int8_t *)p[5];
     auto su = (const float *)p[6];
+    if (schedule == 0 && M >= kGemmMinTokens) schedule = kGemmFirst + auto_tile(M, N, K);
+    if (schedule >= kGemmFirst)
+        return nc::gemm_i8_token(schedule - kGemmFirst, 2, h, xq, xs, qg, sg, nullptr, nullptr, qu, su, M, N, K);
     if (K == 896) return swiglu_tokens<896>(h, xq, xs, qg, sg, qu, su, M, N, K);
     return swiglu_tokens<0>(h, xq, xs, qg, sg, qu, su, M, N, K);
 }
@@ -345,7 +400,7 @@ namespace {
 __global__ void silu_mul_rows(float *__restrict__ y, const float *__restrict__ g, const float *__restrict__ u,
                               int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) y[i] = silu_mul(g[i], u[i]);
+    if (i < n) y[i] = nc::silu_mul(g[i], u[i]);
 }
 }  // namespace
 

@@ -74,6 +74,19 @@ NC_EXPORT int32_t nc_device_info(char *name, int64_t name_len, int64_t *compute_
     return NC_OK;
 }
 
+// The HIP runtime and driver versions (hipRuntimeGetVersion, hipDriverGetVersion):
+// part of the key under which tuned schedules are cached.
+NC_EXPORT int32_t nc_runtime_version(int64_t *runtime, int64_t *driver) {
+    int r = 0, d = 0;
+    int32_t rc = record(hipRuntimeGetVersion(&r), "hipRuntimeGetVersion");
+    if (rc) return rc;
+    rc = record(hipDriverGetVersion(&d), "hipDriverGetVersion");
+    if (rc) return rc;
+    if (runtime) *runtime = r;
+    if (driver) *driver = d;
+    return NC_OK;
+}
+
 NC_EXPORT void *nc_malloc(int64_t bytes) {
     void *p = nullptr;
     if (bytes <= 0) bytes = 1;

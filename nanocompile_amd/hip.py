@@ -44,6 +44,8 @@ _RUNTIME = {
     "nc_device_count": (ctypes.c_int32, []),
     "nc_init": (ctypes.c_int32, [ctypes.c_int32]),
     "nc_device_info": (ctypes.c_int32, [ctypes.c_char_p, ctypes.c_int64] + [ctypes.POINTER(ctypes.c_int64)] * 4),
+    "nc_runtime_version": (ctypes.c_int32, [ctypes.POINTER(ctypes.c_int64)] * 2),
+    "nc_schedule_info": (ctypes.c_int32, [ctypes.c_int32, ctypes.POINTER(ctypes.c_int64)]),
     "nc_malloc": (ctypes.c_void_p, [ctypes.c_int64]),
     "nc_free": (ctypes.c_int32, [ctypes.c_void_p]),
     "nc_host_malloc": (ctypes.c_void_p, [ctypes.c_int64]),
@@ -111,6 +113,26 @@ def device_info() -> dict:
                                  ctypes.byref(clock)), "nc_device_info")
     return {"arch": name.value.decode(), "compute_units": cus.value, "lds_bytes": lds.value,
             "hbm_bytes": hbm.value, "clock_khz": clock.value}
+
+
+def runtime_version() -> tuple[int, int]:
+    """(HIP runtime version, driver version)."""
+    init()
+    runtime, driver = ctypes.c_int64(), ctypes.c_int64()
+    _check(load().nc_runtime_version(ctypes.byref(runtime), ctypes.byref(driver)), "nc_runtime_version")
+    return runtime.value, driver.value
+
+
+def schedule_info(schedule: int) -> dict | None:
+    """The launch shape of projection schedule ``schedule`` (a table lookup; no GPU needed)."""
+    out = (ctypes.c_int64 * 16)()
+    if load().nc_schedule_info(int(schedule), out) != NC_OK:
+        return None
+    if out[0] == 0:
+        return {"schedule": int(schedule), "kernel": "gemv", "lanes_per_row": out[1], "waves": out[2],
+                "load_bytes": out[3]}
+    return {"schedule": int(schedule), "kernel": "mfma", "tile_m": out[1], "tile_n": out[2], "k_stage": out[3],
+            "wave_m": out[4], "wave_n": out[5], "stages": out[6], "threads": out[7], "lds_bytes": out[8]}
 
 
 def kernel(name: str):

@@ -108,6 +108,25 @@ def matmul_i8_token(xq, xs, q, scales, bias=None, residual=None, schedule: int =
     return y
 
 
+GEMV_SCHEDULES = range(1, 8)      # lanes per row x waves; 7 is the default GEMV
+GEMM_SCHEDULES = range(16, 25)    # the MFMA GEMM's tiles; K a multiple of 16
+
+
+def matmul_i8_token_swiglu(xq, xs, qg, sg, qu, su, schedule: int = 0) -> DeviceArray:
+    """``silu(gate) * up`` with gate and up each ``(f32(xq @ q.T) * xs) * scales``, one kernel."""
+    xq, xs = _device(xq, I8), _device(xs, F32)
+    if len(xq.shape) != 2 or xs.shape != (xq.shape[0],):
+        raise ShapeError(f"matmul_i8_token_swiglu: activations i8[M, K] and f32[M], got {list(xq.shape)}")
+    m, k = xq.shape
+    qg, sg, qu, su = _device(qg, I8), _device(sg, F32), _device(qu, I8), _device(su, F32)
+    n = _int8_weight("matmul_i8_token_swiglu", qg, sg, k)
+    if _int8_weight("matmul_i8_token_swiglu", qu, su, k) != n:
+        raise ShapeError("matmul_i8_token_swiglu: gate and up must have the same rows")
+    h = DeviceArray((m, n), F32)
+    hip.call("nc_matmul_i8_token_swiglu", [h, xq, xs, qg, sg, qu, su], [m, n, k, schedule])
+    return h
+
+
 def matmul_i8_token_acc(xq, q, schedule: int = 0) -> DeviceArray:
     """The int32 accumulators ``xq @ q.T`` alone, for checking them bit for bit."""
     xq, q = _device(xq, I8), _device(q, I8)

@@ -98,11 +98,18 @@ class Qwen2:
     """The model's front door on the GPU: token ids in, logits out (models/qwen2.py:278-345)."""
 
     def __init__(self, config: Qwen2Config, weights: Mapping[str, np.ndarray], quantization: str = "int8-token",
-                 max_tokens: int = 512, device: int = 0) -> None:
+                 max_tokens: int = 512, device: int = 0, schedule="default") -> None:
+        """``schedule`` picks the projections' launch shapes, as the reference's
+        ``CompiledGraph(schedule=...)`` does (runtime.py:167-222): "default" (or
+        None) for the library's choice, or an ``autotune.Autotuner``, which
+        measures each projection shape on first use and caches the winner."""
         if quantization not in QUANTIZATIONS:
             raise ValueError(f"quantization must be one of {QUANTIZATIONS}")
+        if schedule not in ("default", None) and not hasattr(schedule, "schedule"):
+            raise ValueError("schedule must be 'default', None or an autotune.Autotuner")
         hip.init(device)
         self.config, self.quantization, self.max_tokens = config, quantization, max_tokens
+        self.tuner = None if schedule in ("default", None) else schedule
         c = config
         H, I, D = c.hidden_size, c.intermediate_size, c.head_dim
         Q, KVW = c.num_attention_heads * D, c.num_key_value_heads * D
@@ -219,24 +226,37 @@ class Qwen2:
                 q, s = w["down"]
                 hip.call("nc_decode_projection", [self.x, self.h, None, q, s], [H, I, 1, eps])
             return
+        s_qkv, s_o, s_mlp, s_down = self._projection_schedules(m)
         for i, w in enumerate(self.layers):
             kc, vc = cache.layer(i)
             hip.call("nc_rms_norm_quant", [None, self.xq, self.xs, self.x, w["g1"]], [m, H, eps])
             q, s = w["qkv"]
-            hip.call("nc_matmul_i8_token", [self.qkv, self.xq, self.xs, q, s, w["qkv_b"], None], [m, W, H, 0])
+            hip.call("nc_matmul_i8_token", [self.qkv, self.xq, self.xs, q, s, w["qkv_b"], None], [m, W, H, s_qkv])
             hip.call("nc_rope_append", [self.qkv, kc, vc, self.inv_freq, pos],
                      [m, heads, kv, D, past, cache.capacity])
             hip.call("nc_attention", [self.ctx, self.qkv, kc, vc, pos],
                      [m, heads, kv, D, past, cache.capacity, float_bits(self.scale)])
             hip.call("nc_quantize_token_i8", [self.xq, self.xs, self.ctx], [m, Q])
             q, s = w["o"]
-            hip.call("nc_matmul_i8_token", [self.x, self.xq, self.xs, q, s, None, self.x], [m, H, Q, 0])
+            hip.call("nc_matmul_i8_token", [self.x, self.xq, self.xs, q, s, None, self.x], [m, H, Q, s_o])
             hip.call("nc_rms_norm_quant", [None, self.xq, self.xs, self.x, w["g2"]], [m, H, eps])
             (qg, sg), (qu, su) = w["gate"], w["up"]
-            hip.call("nc_matmul_i8_token_swiglu", [self.h, self.xq, self.xs, qg, sg, qu, su], [m, I, H])
+            hip.call("nc_matmul_i8_token_swiglu", [self.h, self.xq, self.xs, qg, sg, qu, su], [m, I, H, s_mlp])
             hip.call("nc_quantize_token_i8", [self.xq, self.xs, self.h], [m, I])
             q, s = w["down"]
-            hip.call("nc_matmul_i8_token", [self.x, self.xq, self.xs, q, s, None, self.x], [m, H, I, 0])
+            hip.call("nc_matmul_i8_token", [self.x, self.xq, self.xs, q, s, None, self.x], [m, H, I, s_down])
+
+    def _projection_schedules(self, m: int) -> tuple[int, int, int, int]:
+        """Schedules of the qkv, o, gate/up and down projections over m tokens:
+        0 (the library's choice), or the tuner's (measured on first use, so
+        never call this first inside a graph capture)."""
+        if self.tuner is None:
+            return 0, 0, 0, 0
+        c = self.config
+        H, I, Q = c.hidden_size, c.intermediate_size, c.num_attention_heads * c.head_dim
+        t = self.tuner.schedule
+        return (t("matmul_i8_token", m, self.width, H), t("matmul_i8_token", m, H, Q),
+                t("matmul_i8_token_swiglu", m, I, H), t("matmul_i8_token", m, H, I))
 
     def forward(self, token_ids: Sequence[int] | np.ndarray, cache: KVCache | None = None,
                 last_only: bool = False) -> np.ndarray:
@@ -338,6 +358,8 @@ class Qwen2:
             self._head_argmax(self.x.ptr)
             hip.call("nc_decode_advance", [one_id, tokens, self.best, pos], [capacity])
 
+        if not self.fused_decode:
+            self._projection_schedules(1)          # any tuning happens now, not under capture
         hip.sync()
         replay = hip.Graph.capture(step).launch if graph else step
         if timer:
