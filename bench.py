@@ -19,9 +19,21 @@ its decode rate is the CPU baseline.
 weights rotated through 128 device copies (560 MB, past the 256 MB Infinity
 Cache); also measured in the default run and reported under "gemv".
 
+The default run also measures, on the same model's weights, and reports under
+``config.blocks``: config 2 (the fused rms_norm -> int8 row kernel at 1, 64
+and 512 rows), config 3 (one decoder block's decode step at past 512, per
+block over all 24) and config 4 (one block's prefill of 512 tokens, per
+block, and its four MFMA GEMM shapes alone, with MFMA utilisation against the
+5.0 POP/s dense int8 peak).
+
 Roofline numerators are algorithmic bytes:
   GEMV:    N*K + 4N + M*K + 4M + 4MN = 4,397,956 B per [1,896]x[4864,896]^T.
   LM head: 4*V*H (float32 table) + 4*H (x) + 8 (argmax key) = 544,542,216 B per step.
+  Block decode (past 512): 15,507,456 B.  GEMM: M*K + N*K + 4MN + 4M + 4N.
+
+Before anything else the run copies 256 MiB device to device once
+(``__amd_rocclr_copyBuffer``): a copy of known size whose FETCH_SIZE and
+WRITE_SIZE calibrate the profiler's byte counters.
 """
 
 from __future__ import annotations
@@ -39,6 +51,7 @@ HBM_PEAK_GBPS = 8000.0
 N, K, M = 4864, 896, 1
 COPIES = 128
 PROMPT, NEW_TOKENS = 128, 256
+CALIBRATION_BYTES = 256 * 2**20
 
 
 def gemv_bytes(m: int, n: int, k: int) -> int:
@@ -137,10 +150,135 @@ def cpu_gemv(seconds: float = 6.0, seed: int = 0) -> dict:
             "isa": host.isa(), "cores": cores}
 
 
+# -- configs 2-4: the fused row kernel, one block's decode step, one block's prefill ----------
+
+MFMA_I8_PEAK_TOPS = 5000.0          # MI355X dense int8 MFMA, 5.0 POP/s
+BLOCK_DECODE_BYTES = 15_507_456     # int8 W + scales + biases + gammas + KV read (past 512) + KV write + ~10 KB
+PREFILL_SHAPES = {"q/o (896,896)": (896, 896), "k/v (128,896)": (128, 896),
+                  "gate/up (4864,896)": (4864, 896), "down (896,4864)": (896, 4864)}
+
+
+def gemm_bytes(m: int, n: int, k: int) -> int:
+    """int8 A and B, f32 output, both scale vectors."""
+    return m * k + n * k + 4 * m * n + 4 * m + 4 * n
+
+
+def rms_row_bytes(m: int, k: int = 896) -> int:
+    """Read x, write normed, int8 row and scale per row; gamma once."""
+    return m * (4 * k + 4 * k + k + 4) + 4 * k
+
+
+USE_GRAPHS = True     # False under profilers that cannot follow graph launches (--no-graph)
+
+
+def graph_us(fn, reps: int, rounds: int = 5) -> float:
+    """Median over rounds of one captured graph of ``reps`` calls, per call, in microseconds."""
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import Event, Graph
+    run = lambda: [fn(i) for i in range(reps)]
+    launch = Graph.capture(run).launch if USE_GRAPHS else run
+    launch()
+    hip.sync()
+    a, b = Event(), Event()
+    samples = []
+    for _ in range(rounds):
+        a.record()
+        launch()
+        b.record()
+        hip.sync()
+        samples.append(a.elapsed_ms(b) * 1e3 / reps)
+    return statistics.median(samples)
+
+
+def block_measurements(model, seed: int = 7) -> dict:
+    """Configs 2, 3 and 4 on the decode model's own weights (24 layers, so weights stream as in the model)."""
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import DeviceArray, Graph, Event
+    from nanocompile_amd.kernels import float_bits
+
+    c = model.config
+    H, I, D, L = c.hidden_size, c.intermediate_size, c.head_dim, c.num_hidden_layers
+    heads, kv = c.num_attention_heads, c.num_key_value_heads
+    eps = float_bits(c.rms_norm_eps)
+    rng = np.random.default_rng(seed)
+    out: dict = {}
+
+    # config 2: rms_norm -> per-token int8 at M in {1, 64, 512}, one kernel
+    gamma = DeviceArray.from_host((1 + 0.1 * rng.standard_normal(H)).astype(np.float32))
+    rows = {}
+    for m in (1, 64, 512):
+        x = rng.standard_normal((m, H)).astype(np.float32)
+        x[rng.random(x.shape) < 0.01] *= 20
+        xd = DeviceArray.from_host(x)
+        normed, xq, xs = DeviceArray((m, H), np.float32), DeviceArray((m, H), np.int8), DeviceArray((m,), np.float32)
+        us = graph_us(lambda i: hip.call("nc_rms_norm_quant", [normed, xq, xs, xd, gamma], [m, H, eps]), 32)
+        rows[str(m)] = {"us": round(us, 3), "bytes": rms_row_bytes(m, H),
+                        "gbps": round(rms_row_bytes(m, H) / (us * 1e-6) / 1e9, 1)}
+    out["rms_norm_quant"] = {"kernel": "rms_norm_quant (one pass: normed f32, int8 row, scale)", "rows": rows}
+
+    # config 3: one decoder block's decode step at past = 512 (all 24 blocks replayed, per block)
+    past = 512
+    cache = model.new_cache(past + 8)
+    kvals = rng.standard_normal((L, kv, past + 8, D)).astype(np.float32)
+    cache.keys.upload(kvals)
+    cache.values.upload(rng.standard_normal(kvals.shape).astype(np.float32))
+    x0 = DeviceArray.from_host(rng.standard_normal((1, H)).astype(np.float32))
+    lib = hip.load()
+
+    def decode_layers(_):
+        lib.nc_memcpy_d2d(model.x.ptr, x0.ptr, H * 4)      # same residual input every replay
+        model._layers(1, past, cache)
+
+    us = graph_us(decode_layers, 1, rounds=9)
+    per_block = us / L
+    out["block_decode"] = {"past": past, "block_us": round(per_block, 3), "layers_us": round(us, 2),
+                           "bytes_per_block": BLOCK_DECODE_BYTES,
+                           "gbps": round(BLOCK_DECODE_BYTES / (per_block * 1e-6) / 1e9, 1),
+                           "frac": round(BLOCK_DECODE_BYTES / (per_block * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+                           "kernels_per_block": 5}
+
+    # config 4: one block's prefill at seq = 512, past = 0 (all 24 blocks, per block), and its GEMMs alone
+    m = 512
+    if model.max_tokens >= m:
+        pcache = model.new_cache(m)
+        ids = DeviceArray.from_host(rng.integers(0, c.vocab_size, m).astype(np.int64))
+
+        def prefill_layers(_):
+            hip.call("nc_embed", [model.x, model.embed, ids], [m, H, c.vocab_size])
+            model._layers(m, 0, pcache)
+
+        us = graph_us(prefill_layers, 1, rounds=5)
+        gemms = {}
+        for name, (n, k) in PREFILL_SHAPES.items():
+            xq = DeviceArray.from_host(rng.integers(-127, 128, (m, k)).astype(np.int8))
+            xs = DeviceArray.from_host((rng.random(m) * 0.05).astype(np.float32))
+            y = DeviceArray((m, n), np.float32)
+            key = {"q/o (896,896)": "o", "k/v (128,896)": "qkv", "gate/up (4864,896)": "gate",
+                   "down (896,4864)": "down"}[name]
+            offset = 896 * k if key == "qkv" else 0           # the k rows of the fused qkv matrix
+            weights = [(model.layers[i][key][0].ptr + offset, model.layers[i][key][1].ptr + offset // k * 4)
+                       for i in range(L)]
+
+            def gemm(i, n=n, k=k, xq=xq, xs=xs, y=y, weights=weights):
+                q, s = weights[i % L]
+                hip.call("nc_matmul_i8_token", [y, xq, xs, q, s, None, None], [m, n, k, 0])
+
+            t = graph_us(gemm, 2 * L)
+            ops = 2 * m * n * k
+            gemms[name] = {"us": round(t, 3), "tops": round(ops / (t * 1e-6) / 1e12, 1),
+                           "mfma_frac": round(ops / (t * 1e-6) / 1e12 / MFMA_I8_PEAK_TOPS, 4),
+                           "bytes": gemm_bytes(m, n, k),
+                           "hbm_frac": round(gemm_bytes(m, n, k) / (t * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+        out["prefill"] = {"seq": m, "block_us": round(us / L, 2), "layers_us": round(us, 1),
+                          "tok_s": round(m / (us * 1e-6), 1), "gemm": gemms,
+                          "gemm_kernel": "gemm_i8_mfma (v_mfma_i32_16x16x64_i8, LDS-staged tiles)"}
+    return out
+
+
 # -- config 5: the whole model, greedy decode ----------------------------------------
 
 
-def decode(steps: int, warmup: int, cpu: bool, seed: int = 0, graph: bool = True) -> dict:
+def decode(steps: int, warmup: int, cpu: bool, seed: int = 0, graph: bool = True, blocks: bool = True) -> dict:
     from nanocompile_amd import hip
     from nanocompile_amd.hip import Event
     from nanocompile_amd.models.config import QWEN25_05B
@@ -154,7 +292,7 @@ def decode(steps: int, warmup: int, cpu: bool, seed: int = 0, graph: bool = True
     prompt = [int(t) for t in np.random.default_rng(seed + 1).integers(0, config.vocab_size, PROMPT)]
     log(f"decode: weights drawn in {time.perf_counter() - t0:.1f} s")
     t0 = time.perf_counter()
-    model = Qwen2(config, weights, max_tokens=PROMPT)
+    model = Qwen2(config, weights, max_tokens=512)        # 512: config 4's prefill length
     log(f"decode: model uploaded and quantized on the GPU in {time.perf_counter() - t0:.1f} s")
 
     for _ in range(warmup):
@@ -185,6 +323,10 @@ def decode(steps: int, warmup: int, cpu: bool, seed: int = 0, graph: bool = True
     result.update({"lm_head_us": lm_ms * 1e3, "lm_head_gbps": lm_bytes / (lm_ms * 1e-3) / 1e9, "lm_bytes": lm_bytes})
     step_bytes = 904_503_808 + 24_576 * (PROMPT + new_tokens // 2)
     result["step_bytes_mid"] = step_bytes
+    if blocks:
+        t0 = time.perf_counter()
+        result["blocks"] = block_measurements(model)
+        log(f"blocks: configs 2-4 measured in {time.perf_counter() - t0:.1f} s")
 
     if cpu:
         from oracle import host
@@ -220,6 +362,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=1)
     parser.add_argument("--workload", choices=("decode", "gemv"), default="decode")
     parser.add_argument("--no-cpu", action="store_true")
+    parser.add_argument("--no-blocks", action="store_true", help="skip the per-block measurements (configs 2-4)")
     parser.add_argument("--no-graph", action="store_true",
                         help="launch each decode step's kernels directly instead of replaying a HIP graph "
                              "(for profilers that cannot follow graph launches)")
@@ -229,8 +372,14 @@ def main() -> int:
               file=sys.stderr)
         return 2
     from nanocompile_amd import hip
+    from nanocompile_amd.hip import DeviceArray
     hip.init(0)
     info = hip.device_info()
+    calibration = CALIBRATION_BYTES
+    src, dst = DeviceArray((calibration,), np.uint8), DeviceArray((calibration,), np.uint8)
+    hip.load().nc_memcpy_d2d(dst.ptr, src.ptr, calibration)
+    hip.sync()
+    del src, dst
 
     g = gpu_gemv(20 if args.workload == "decode" else args.steps, 3)
     log(f"gemv: stacked {g['stacked_gbps']:.0f} GB/s, single {g['single_us']:.2f} us")
@@ -256,7 +405,9 @@ def main() -> int:
         print(json.dumps(record), flush=True)
         return 0
 
-    d = decode(args.steps, args.warmup, cpu=not args.no_cpu, graph=not args.no_graph)
+    global USE_GRAPHS
+    USE_GRAPHS = not args.no_graph
+    d = decode(args.steps, args.warmup, cpu=not args.no_cpu, graph=not args.no_graph, blocks=not args.no_blocks)
     log(f"decode: {d['tok_s']:.1f} tok/s on the GPU; LM head {d['lm_head_us']:.1f} us = {d['lm_head_gbps']:.0f} GB/s")
     cpu = d.get("cpu")
     record = {
@@ -277,7 +428,8 @@ def main() -> int:
                    "prompt_tokens": PROMPT, "new_tokens": args.steps + 1, "device": info["arch"],
                    "compute_units": info["compute_units"],
                    "tokens_identical_to_host_c": d.get("tokens_identical"),
-                   "decode_ms_total": round(d["decode_ms"], 3), "gemv": gemv_record},
+                   "decode_ms_total": round(d["decode_ms"], 3), "gemv": gemv_record,
+                   "blocks": d.get("blocks")},
         "roofline": {"bound": "hbm", "achieved": round(d["lm_head_gbps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(d["lm_head_gbps"] / HBM_PEAK_GBPS, 4), "traffic": None,
                      "kernel": "lm_head<4> (fp32 tied LM head, 60% of a decode step's bytes)",
