@@ -192,11 +192,19 @@ int32_t nc_decode_projection(void **p, const int64_t *s);
 
 /* Attention of one new token (models/qwen2.py:113-155 at seq = 1) with RoPE of
  * its q and k heads and the cache append fused in: the same arithmetic, bit for
- * bit, as nc_rope_append followed by nc_attention.
+ * bit, as nc_rope_append followed by nc_attention (the 64-key chunked order
+ * both share). One workgroup per query head, its waves taking the chunks.
  * p: [ctx f32[heads*D], qkv f32[(heads+2*kv)*D] (unrotated), kcache f32[kv,C,D],
- *     vcache f32[kv,C,D], inv_freq f32[D/2], pos i64[1] or NULL (read in place of s[3])];
+ *     vcache f32[kv,C,D], inv_freq f32[D/2], pos i64[1] or NULL (read in place of s[3]),
+ *     rope table f32[2,C,D/2] from nc_rope_table or NULL (then cos and sin are computed)];
  * s: [heads, kv, D, past, C, scale as float32 bits] (D 64 or 32, C <= 16384) */
 int32_t nc_attention_decode(void **p, const int64_t *s);
+
+/* RoPE's cos and sin for every position of a cache, computed once with the
+ * kernels' own nc_cosf / nc_sinf of f32(position) * inv_freq[i] (the reference
+ * builds the same angles as rope_tables, nn.py:78-94).
+ * p: [table f32[2,C,D/2] (cos, then sin), inv_freq f32[D/2]];  s: [C, D] */
+int32_t nc_rope_table(void **p, const int64_t *s);
 
 /* -- fused groups around the projections (nn.py, models/qwen2.py) ------------ */
 
@@ -223,9 +231,11 @@ int32_t nc_rope_append(void **p, const int64_t *s);
 
 /* Grouped-query attention of each new row over the cache, causal
  * (models/qwen2.py:113-155; query head h reads KV head h / (heads / kv), the
- * reference's repeat_kv as index arithmetic, nn.py:109-120).
- * p: [ctx f32[M,heads*D], qkv (q rotated), kcache, vcache];
- * s: [M, heads, kv, D, past, C, scale as float32 bits] (D <= 64) */
+ * reference's repeat_kv as index arithmetic, nn.py:109-120). The softmax and
+ * the context are computed in 64-key chunks combined afterwards, the order
+ * nc_attention_decode shares, so prefill and decode agree bit for bit.
+ * p: [ctx f32[M,heads*D], qkv (q rotated), kcache, vcache, pos i64[1] or NULL];
+ * s: [M, heads, kv, D, past, C, scale as float32 bits] (D 16, 32 or 64; at most 16384 keys) */
 int32_t nc_attention(void **p, const int64_t *s);
 
 /* -- the model's ends ---------------------------------------------------------- */

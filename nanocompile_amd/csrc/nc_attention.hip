@@ -8,19 +8,19 @@
 //    the host as the reference does, nn.py:69-75); y = x * cos + rot * sin
 //    with rot = [-x[d/2:], x[:d/2]] (nn.py:97-106); cos and sin are
 //    nc_cosf / nc_sinf (nc_math.h).
-//  * scores: s_t = sum over d of q[d] * k_t[d], in order of d, from 0
-//    (the reference's matmul kernel, lower.py:255-269); z_t = s_t * scale + 0
-//    (the mask adds 0 where a key is visible; masked keys contribute exactly
-//    nothing and are skipped).
-//  * softmax: m = max z (NaN-propagating, as fusion.py:603-609);
-//    e_t = nc_expf(z_t - m); the sum of e_t in the row-sum order of the row
-//    kernels (256 virtual threads, thread v adding t = v, v + 256, ... in order;
-//    xor butterfly within each 64; (w0 + w1) + (w2 + w3)); p_t = e_t / sum.
-//  * context: four contiguous chunks of keys, chunk c = [c*S, (c+1)*S) with
-//    S = ceil(T / 4); c_c[d] = sum over its t of p_t * v_t[d] in order;
-//    ctx[d] = (c_0 + c_1) + (c_2 + c_3).
+//  * softmax (nc_softmax_causal): m = max z (NaN-propagating, as
+//    fusion.py:603-609); e_t = nc_expf(z_t - m); the sum of e_t in the row-sum
+//    order of the row kernels (256 virtual threads, thread v adding
+//    t = v, v + 256, ... in order; xor butterfly within each 64;
+//    (w0 + w1) + (w2 + w3)); p_t = e_t / sum. Masked entries are 0.
+//  * attention (nc_attention): scores s_t = sum over d of q[d] * k_t[d] in
+//    order of d (the reference's matmul kernel, lower.py:255-269), times
+//    scale, + 0 (the mask adds 0 where a key is visible; masked keys are
+//    skipped); then the softmax and the context in 64-key chunks combined
+//    after, the order nc_attend.h states (shared with the decode kernel).
 // The host oracle (oracle/nc_model.c) replays exactly these orders.
 #include "nc_common.h"
+#include "nc_attend.h"
 #include "nc_math.h"
 
 namespace {
@@ -131,48 +131,46 @@ __global__ __launch_bounds__(kThreads) void rope_append(float *__restrict__ qkv,
 }
 
 // One query row of one head: grid (heads, M). Query row i sits at position
-// past + i and sees keys 0 .. past + i of its KV head (h / group).
+// past + i and sees keys 0 .. past + i of its KV head (h / group). The four
+// waves take the 64-key chunks in turn (nc_attend.h gives the order), leave
+// their partials in LDS, and wave 0 combines them: the same bits as the
+// decode kernel's split over workgroups.
+template <int D>
 __global__ __launch_bounds__(kThreads) void attention_rows(float *__restrict__ ctx, const float *__restrict__ qkv,
                                                            const float *__restrict__ kcache,
                                                            const float *__restrict__ vcache, int heads,
-                                                           int kv_heads, int D, int past, int capacity,
-                                                           float scale, const int64_t *__restrict__ pos_ptr,
+                                                           int kv_heads, int past, int capacity, float scale,
+                                                           const int64_t *__restrict__ pos_ptr,
                                                            int32_t *__restrict__ error) {
     if (pos_ptr && !position_fits(pos_ptr, (int)gridDim.y, capacity, error, past)) return;
-    extern __shared__ float e[];
-    __shared__ float q[64];
-    __shared__ float part[4][64];
-    __shared__ float scratch[4];
+    extern __shared__ float part[];               // [J][D + 2]: m_j, l_j, o_j[D]
+    __shared__ __align__(16) float q[D];
     const int h = blockIdx.x, i = blockIdx.y;
     const int g = h / (heads / kv_heads);
     const int width = (heads + 2 * kv_heads) * D;
-    const int T = past + i + 1;
+    const int T = past + i + 1, J = (T + nc::kChunk - 1) / nc::kChunk;
     if (threadIdx.x < D) q[threadIdx.x] = qkv[(size_t)i * width + h * D + threadIdx.x];
     __syncthreads();
 
     const float *K = kcache + (size_t)g * capacity * D;
     const float *V = vcache + (size_t)g * capacity * D;
-    for (int t = threadIdx.x; t < T; t += kThreads) {
-        const float *k = K + (size_t)t * D;
-        float acc = 0.0f;
-        for (int d = 0; d < D; ++d) acc = __fadd_rn(acc, __fmul_rn(q[d], k[d]));
-        e[t] = __fadd_rn(__fmul_rn(acc, scale), 0.0f);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int j = wave; j < J; j += kThreads / 64) {
+        const int t0 = j * nc::kChunk;
+        nc::Chunk<D, false> chunk(K, V, t0, min(nc::kChunk, T - t0), -1);
+        const nc::ChunkResult r = chunk.attend(q, nullptr, nullptr, scale);
+        float *pj = part + j * (D + 2);
+        if (lane == 0) {
+            pj[0] = r.m;
+            pj[1] = r.l;
+        }
+        if (lane < D) pj[2 + lane] = r.o;
     }
     __syncthreads();
-    softmax_lds(e, T, scratch);
-
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int S = (T + 3) / 4;
-    const int t0 = wave * S, t1 = min(T, t0 + S);
-    float acc = 0.0f;
-    if (lane < D)
-        for (int t = t0; t < t1; ++t) acc = __fadd_rn(acc, __fmul_rn(e[t], V[(size_t)t * D + lane]));
-    part[wave][lane] = acc;
-    __syncthreads();
-    if (threadIdx.x < D) {
-        const int d = threadIdx.x;
-        ctx[(size_t)i * heads * D + h * D + d] =
-            __fadd_rn(__fadd_rn(part[0][d], part[1][d]), __fadd_rn(part[2][d], part[3][d]));
+    if (wave == 0) {
+        const float out = nc::combine_chunks(J, lane < D ? lane : 0,
+                                             [&](int c, int k) { return part[c * (D + 2) + k]; });
+        if (lane < D) ctx[(size_t)i * heads * D + h * D + lane] = out;
     }
 }
 
@@ -235,24 +233,50 @@ NC_EXPORT int32_t nc_rope_append(void **p, const int64_t *s) {
     return nc::launched("rope_append");
 }
 
+namespace {
+
+template <int D>
+int32_t launch_rows(void **p, int64_t M, int64_t heads, int64_t kv, int64_t past, int64_t cap, float scale,
+                    const int64_t *pos) {
+    // partials of every chunk in LDS: up to 256 chunks x 66 floats = 67.6 KB
+    // at 16384 keys, past the 64 KB a launch gets without asking
+    static bool raised = false;
+    if (!raised) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&attention_rows<D>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) != hipSuccess) {
+            nc::set_message("nc_attention: could not raise the LDS limit");
+            return NC_LAUNCH_FAILED;
+        }
+        raised = true;
+    }
+    const int64_t keys = pos ? cap : past + M;
+    const size_t lds = (size_t)((keys + nc::kChunk - 1) / nc::kChunk) * (D + 2) * sizeof(float);
+    hipLaunchKernelGGL(attention_rows<D>, dim3((unsigned)heads, (unsigned)M), dim3(kThreads), lds, nc::stream(),
+                       (float *)p[0], (const float *)p[1], (const float *)p[2], (const float *)p[3], (int)heads,
+                       (int)kv, pos ? 0 : (int)past, (int)cap, scale, pos, nc::error_word());
+    return nc::launched("attention_rows");
+}
+
+}  // namespace
+
 // p: [ctx f32[M, heads*D], qkv f32[M, (H + 2*KV*D)] (q rotated), kcache, vcache, pos i64[1] | NULL];
-// s: [M, heads, kv_heads, D, past, capacity, scale as float32 bits]
+// s: [M, heads, kv_heads, D, past, capacity, scale as float32 bits]  (D 16, 32 or 64)
 // With pos, past is read from the device when the kernel runs (s[4] is ignored).
 NC_EXPORT int32_t nc_attention(void **p, const int64_t *s) {
     NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3], "nc_attention: null operand");
     const int64_t M = s[0], heads = s[1], kv = s[2], D = s[3], past = s[4], cap = s[5];
     const int64_t *pos = (const int64_t *)p[4];
-    NC_REQUIRE(M >= 0 && heads > 0 && kv > 0 && heads % kv == 0 && D > 0 && D <= 64 &&
+    NC_REQUIRE(M >= 0 && heads > 0 && kv > 0 && heads % kv == 0 && (D == 16 || D == 32 || D == 64) &&
                    (pos ? cap <= kMaxKeys : (past >= 0 && past + M <= cap && past + M <= kMaxKeys)) &&
                    M <= cap && M < 65536 && heads < 65536,
-               "nc_attention: bad shape");
+               "nc_attention: bad shape (head_dim 16, 32 or 64; at most 16384 keys)");
     if (M == 0) return NC_OK;
-    const size_t lds = (size_t)(pos ? cap : past + M) * sizeof(float);
-    hipLaunchKernelGGL(attention_rows, dim3((unsigned)heads, (unsigned)M), dim3(kThreads), lds, nc::stream(),
-                       (float *)p[0], (const float *)p[1], (const float *)p[2], (const float *)p[3], (int)heads,
-                       (int)kv, (int)D, pos ? 0 : (int)past, (int)cap, bits_to_float(s[6]), pos, nc::error_word());
-    return nc::launched("attention_rows");
+    const float scale = bits_to_float(s[6]);
+    if (D == 64) return launch_rows<64>(p, M, heads, kv, past, cap, scale, pos);
+    if (D == 32) return launch_rows<32>(p, M, heads, kv, past, cap, scale, pos);
+    return launch_rows<16>(p, M, heads, kv, past, cap, scale, pos);
 }
+
 
 // p: [y f32[heads, seq, past+seq], s f32[heads, seq, past+seq]];  s: [heads, seq, past]
 NC_EXPORT int32_t nc_softmax_causal(void **p, const int64_t *s) {
@@ -276,4 +300,32 @@ NC_EXPORT int32_t nc_rope(void **p, const int64_t *s) {
     hipLaunchKernelGGL(rope_rows, dim3((unsigned)(s[0] * s[1])), dim3(kThreads), 0, nc::stream(), (float *)p[0],
                        (const float *)p[1], (const float *)p[2], (int)s[1], (int)s[2], (int)s[3]);
     return nc::launched("rope_rows");
+}
+
+namespace {
+// cos and sin of f32(position) * inv_freq[i] for every position of a cache:
+// RoPE's angles (nn.py:78-94, the reference's rope_tables) computed once with
+// the same nc_cosf / nc_sinf the kernels use, so a table lookup gives the same
+// bits as computing them in place.
+__global__ __launch_bounds__(kThreads) void rope_table(float *__restrict__ table, const float *__restrict__ inv_freq,
+                                                       int capacity, int half) {
+    const int64_t n = (int64_t)capacity * half;
+    const int64_t u = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (u >= n) return;
+    const int pos = (int)(u / half), i = (int)(u - (int64_t)pos * half);
+    const float ang = __fmul_rn((float)pos, inv_freq[i]);
+    table[u] = nc_cosf(ang);
+    table[n + u] = nc_sinf(ang);
+}
+}  // namespace
+
+// p: [table f32[2, C, D/2] (cos, then sin), inv_freq f32[D/2]];  s: [C, D]
+NC_EXPORT int32_t nc_rope_table(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1], "nc_rope_table: null operand");
+    NC_REQUIRE(s[0] > 0 && s[0] < (1 << 24) && s[1] > 0 && s[1] % 2 == 0 && s[1] <= 1024,
+               "nc_rope_table: bad shape");
+    const int64_t n = s[0] * (s[1] / 2);
+    hipLaunchKernelGGL(rope_table, dim3((unsigned)((n + kThreads - 1) / kThreads)), dim3(kThreads), 0, nc::stream(),
+                       (float *)p[0], (const float *)p[1], (int)s[0], (int)(s[1] / 2));
+    return nc::launched("rope_table");
 }

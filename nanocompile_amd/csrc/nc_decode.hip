@@ -19,6 +19,7 @@
 // fused step computes the same bits as the unfused one, and the host oracle
 // covers both.
 #include "nc_common.h"
+#include "nc_attend.h"
 #include "nc_epilogue.h"
 
 namespace {
@@ -132,70 +133,23 @@ __global__ __launch_bounds__(64) void gemv_decode(float *__restrict__ out, const
 }
 
 // -- attention for one new token, RoPE and the cache append fused in ---------------
+//
+// One workgroup per query head, kWaves wavefronts: wave w attends the head to
+// the 64-key chunks w, w + kWaves, ... (nc_attend.h gives the order), leaves
+// each chunk's partial result in LDS, and wave 0 combines them. Up to
+// 64 * kWaves keys every chunk is in flight at once; the chunk loads go out
+// before RoPE, which overlaps their latency. The same order as
+// nc_attention's prefill kernel, so a decode step and a prefill agree bit for
+// bit. (Splitting a head over several workgroups instead costs device-scope
+// fences or a second launch to combine, more than the keys take to read at
+// these lengths.)
+constexpr int kWaves = 4;
 
-constexpr int kT = 256;
-
-__device__ __forceinline__ float nan_max(float a, float b) { return (a < b || b != b) ? b : a; }
-
-__device__ float block_sum(float v, float *scratch) {
-    v = nc::wave_sum_f32(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();
-    if (lane == 0) scratch[wave] = v;
-    __syncthreads();
-    const float r = __fadd_rn(__fadd_rn(scratch[0], scratch[1]), __fadd_rn(scratch[2], scratch[3]));
-    __syncthreads();
-    return r;
-}
-
-__device__ float block_max(float v, float *scratch) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = nan_max(v, __shfl_xor(v, off, 64));
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();
-    if (lane == 0) scratch[wave] = v;
-    __syncthreads();
-    const float r = nan_max(nan_max(scratch[0], scratch[1]), nan_max(scratch[2], scratch[3]));
-    __syncthreads();
-    return r;
-}
-
-// One key row held in registers: D/4 float4, dotted with q in order of d.
-template <int D>
-struct KeyRow {
-    float4 v[D / 4];
-    __device__ __forceinline__ void load(const float *__restrict__ row) {
-#pragma unroll
-        for (int d4 = 0; d4 < D / 4; ++d4) v[d4] = reinterpret_cast<const float4 *>(row)[d4];
-    }
-    __device__ __forceinline__ void load_lds(const float *row) {
-#pragma unroll
-        for (int d4 = 0; d4 < D / 4; ++d4) v[d4] = reinterpret_cast<const float4 *>(row)[d4];
-    }
-    __device__ __forceinline__ float score(const float *q, float scale) const {
-        float acc = 0.0f;
-#pragma unroll
-        for (int d4 = 0; d4 < D / 4; ++d4) {
-            acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 0], v[d4].x));
-            acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 1], v[d4].y));
-            acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 2], v[d4].z));
-            acc = __fadd_rn(acc, __fmul_rn(q[4 * d4 + 3], v[d4].w));
-        }
-        return __fadd_rn(__fmul_rn(acc, scale), 0.0f);
-    }
-};
-
-// Head h of the new token at position past (read from pos_ptr when given).
-// q and the new k are rotated here (the same nc_cosf/nc_sinf of
-// f32(past) * inv_freq[j] as nc_rope_append); the first query head of each KV
-// group writes the new k and v into the cache; every head reads the new key
-// and value from its own LDS copy, so no head waits on another's write.
-template <int D>
-__global__ __launch_bounds__(kT) void attention_decode(float *__restrict__ ctx, const float *__restrict__ qkv,
-                                                       float *__restrict__ kcache, float *__restrict__ vcache,
-                                                       const float *__restrict__ inv_freq, int heads, int kv_heads,
-                                                       int past, int capacity, float scale,
-                                                       const int64_t *__restrict__ pos_ptr, int32_t *__restrict__ error) {
+template <int D, bool TABLE>
+__global__ __launch_bounds__(64 * kWaves) void attention_decode(
+    float *__restrict__ ctx, const float *__restrict__ qkv, float *__restrict__ kcache, float *__restrict__ vcache,
+    const float *__restrict__ inv_freq, int heads, int kv_heads, int past, int capacity, float scale,
+    const int64_t *__restrict__ pos_ptr, int32_t *__restrict__ error, const float *__restrict__ table) {
     if (pos_ptr) {
         const int64_t p = *pos_ptr;
         if (p < 0 || p + 1 > capacity) {
@@ -204,58 +158,46 @@ __global__ __launch_bounds__(kT) void attention_decode(float *__restrict__ ctx, 
         }
         past = (int)p;
     }
-    extern __shared__ float e[];
+    extern __shared__ float part[];               // [J][D + 2]: m_j, l_j, o_j[D]
     __shared__ __align__(16) float q[D];
     __shared__ __align__(16) float knew[D];
     __shared__ __align__(16) float vnew[D];
-    __shared__ float part[4][D];
-    __shared__ float scratch[4];
     constexpr int half = D / 2;
     const int h = blockIdx.x, group = heads / kv_heads, g = h / group;
-    const int tid = threadIdx.x;
-    const float *qrow = qkv + h * D;
-    const float *krow = qkv + heads * D + g * D;
-    const float *vrow = qkv + (heads + kv_heads) * D + g * D;
-    const float fpos = (float)past;
-    const int T = past + 1;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int S = (T + 3) / 4;
-    const int t0 = wave * S, t1 = min(T, t0 + S);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int T = past + 1, J = (T + nc::kChunk - 1) / nc::kChunk;
     float *K = kcache + (size_t)g * capacity * D;
     float *V = vcache + (size_t)g * capacity * D;
 
-    // Cache reads go out first, all at once and without branches, so their
-    // latency overlaps the RoPE and each other: the key rows this thread scores
-    // (positions tid and tid + 256) and the first VP values of its wave's chunk
-    // for P.V. Addresses are clamped into the cache and unused values replaced
-    // by selection, never by guarding a load.
-    constexpr int VP = 32;
-    KeyRow<D> kreg;
-    kreg.load(K + (size_t)(tid < past ? tid : 0) * D);
-    const int dl = lane < D ? lane : 0;
-    float vreg[VP];
-#pragma unroll
-    for (int j = 0; j < VP; ++j) {
-        const int t = t0 + j;
-        vreg[j] = V[(size_t)(t < past ? t : 0) * D + dl];
-    }
+    // every wave's first chunk (clamped to the last for waves past J) loads now
+    const int j0 = min(wave, J - 1), t0 = j0 * nc::kChunk;
+    nc::Chunk<D, true> chunk(K, V, t0, min(nc::kChunk, T - t0), past);
 
-    if (tid < half) {
-        const float ang = __fmul_rn(fpos, inv_freq[tid]);
-        const float c = nc_cosf(ang), s = nc_sinf(ang);
-        const float x0 = qrow[tid], x1 = qrow[tid + half];
-        q[tid] = __fadd_rn(__fmul_rn(x0, c), __fmul_rn(-x1, s));
-        q[tid + half] = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(x0, s));
-    } else if (tid < 2 * half) {
-        const int j = tid - half;
-        const float ang = __fmul_rn(fpos, inv_freq[j]);
-        const float c = nc_cosf(ang), s = nc_sinf(ang);
-        const float x0 = krow[j], x1 = krow[j + half];
-        knew[j] = __fadd_rn(__fmul_rn(x0, c), __fmul_rn(-x1, s));
-        knew[j + half] = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(x0, s));
-    } else if (tid < 2 * D) {
-        const int d = tid - D;
-        vnew[d] = vrow[d];
+    // q rotated by lanes 0 .. half - 1 of wave 0, the new key by lanes
+    // half .. D - 1: cos and sin of f32(past) * inv_freq[i] from the cache's
+    // table (nc_rope_table) when given, else computed here, the same
+    // nc_cosf / nc_sinf either way; the first head of each KV group writes the
+    // cache row
+    if (tid < D) {
+        const float *qrow = qkv + h * D;
+        const float *krow = qkv + heads * D + g * D;
+        const float *vrow = qkv + (heads + kv_heads) * D + g * D;
+        const int i = tid < half ? tid : tid - half;
+        const float *x = tid < half ? qrow : krow;
+        float *y = tid < half ? q : knew;
+        float c, s;
+        if constexpr (TABLE) {
+            c = table[(size_t)past * half + i];
+            s = table[((size_t)capacity + past) * half + i];
+        } else {
+            const float ang = __fmul_rn((float)past, inv_freq[i]);
+            c = nc_cosf(ang);
+            s = nc_sinf(ang);
+        }
+        const float x0 = x[i], x1 = x[i + half];
+        y[i] = __fadd_rn(__fmul_rn(x0, c), __fmul_rn(-x1, s));
+        y[i + half] = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(x0, s));
+        vnew[tid] = vrow[tid];
     }
     __syncthreads();
     if (h % group == 0 && tid < D) {
@@ -263,62 +205,26 @@ __global__ __launch_bounds__(kT) void attention_decode(float *__restrict__ ctx, 
         V[(size_t)past * D + tid] = vnew[tid];
     }
 
-    // scores: q . k in order of d; the new key (position past) from LDS
-    if (tid == past) kreg.load_lds(knew);
-    if (tid < T) e[tid] = kreg.score(q, scale);
-    for (int t = tid + kT; t < T; t += kT) {              // contexts beyond 256 keys
-        KeyRow<D> k;
-        if (t == past) k.load_lds(knew);
-        else k.load(K + (size_t)t * D);
-        e[t] = k.score(q, scale);
-    }
-    __syncthreads();
-    float m = -__builtin_inff();
-    for (int t = tid; t < T; t += kT) m = nan_max(m, e[t]);
-    m = block_max(m, scratch);
-    float partial = 0.0f;
-    for (int t = tid; t < T; t += kT) {
-        const float v = nc_expf(__fsub_rn(e[t], m));
-        e[t] = v;
-        partial = __fadd_rn(partial, v);
-    }
-    const float sum = block_sum(partial, scratch);
-    for (int t = tid; t < T; t += kT) e[t] = nc::div_rn(e[t], sum);
-    __syncthreads();
-
-    // P.V over the wave's chunk in position order. A position past the chunk
-    // contributes 0 * 0 = +0, and the accumulator (from +0, adding products)
-    // is never -0, so that addition is exact and changes nothing.
-    const float vfresh = vnew[dl];
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < VP; ++j) {
-        const int t = t0 + j;
-        const bool in = t < t1;
-        const float p = in ? e[in ? t : 0] : 0.0f;
-        const float v = in ? (t == past ? vfresh : vreg[j]) : 0.0f;
-        acc = __fadd_rn(acc, __fmul_rn(p, v));
-    }
-    constexpr int TILE = 32;
-    for (int t = t0 + VP; t < t1; t += TILE) {
-        float vv[TILE];
-#pragma unroll
-        for (int j = 0; j < TILE; ++j) {
-            const int tj = t + j;
-            vv[j] = V[(size_t)(tj < past ? tj : 0) * D + dl];
+    auto keep = [&](int j, const nc::ChunkResult &r) {
+        float *pj = part + j * (D + 2);
+        if (lane == 0) {
+            pj[0] = r.m;
+            pj[1] = r.l;
         }
-#pragma unroll
-        for (int j = 0; j < TILE; ++j) {
-            const int tj = t + j;
-            const bool in = tj < t1;
-            const float p = in ? e[in ? tj : 0] : 0.0f;
-            const float v = in ? (tj == past ? vfresh : vv[j]) : 0.0f;
-            acc = __fadd_rn(acc, __fmul_rn(p, v));
-        }
+        if (lane < D) pj[2 + lane] = r.o;
+    };
+    if (wave < J) keep(wave, chunk.attend(q, knew, vnew, scale));
+    for (int j = wave + kWaves; j < J; j += kWaves) {      // contexts past 64 * kWaves keys
+        const int tj = j * nc::kChunk;
+        nc::Chunk<D, true> more(K, V, tj, min(nc::kChunk, T - tj), past);
+        keep(j, more.attend(q, knew, vnew, scale));
     }
-    if (lane < D) part[wave][lane] = acc;
     __syncthreads();
-    if (tid < D) ctx[h * D + tid] = __fadd_rn(__fadd_rn(part[0][tid], part[1][tid]), __fadd_rn(part[2][tid], part[3][tid]));
+    if (wave == 0) {
+        const float out = nc::combine_chunks(J, lane < D ? lane : 0,
+                                             [&](int c, int k) { return part[c * (D + 2) + k]; });
+        if (lane < D) ctx[h * D + lane] = out;
+    }
 }
 
 float bits_to_float(int64_t bits) {
@@ -364,10 +270,34 @@ NC_EXPORT int32_t nc_decode_projection(void **p, const int64_t *s) {
     return NC_BAD_ARGS;
 }
 
+namespace {
+
+template <int D, bool TABLE>
+int32_t launch_attention_decode(void **p, const int64_t *s, const int64_t *pos) {
+    static bool raised = false;                          // partials of 256 chunks: 67.6 KB of LDS
+    if (!raised) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&attention_decode<D, TABLE>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) != hipSuccess) {
+            nc::set_message("nc_attention_decode: could not raise the LDS limit");
+            return NC_LAUNCH_FAILED;
+        }
+        raised = true;
+    }
+    const int64_t cap = s[4];
+    const size_t lds = (size_t)((cap + nc::kChunk - 1) / nc::kChunk) * (D + 2) * sizeof(float);
+    hipLaunchKernelGGL((attention_decode<D, TABLE>), dim3((unsigned)s[0]), dim3(64 * kWaves), lds, nc::stream(),
+                       (float *)p[0], (const float *)p[1], (float *)p[2], (float *)p[3], (const float *)p[4],
+                       (int)s[0], (int)s[1], pos ? 0 : (int)s[3], (int)cap, bits_to_float(s[5]), pos,
+                       nc::error_word(), (const float *)p[6]);
+    return nc::launched("attention_decode");
+}
+
+}  // namespace
+
 // Attention of one new token with RoPE and the cache append fused in.
 // p: [ctx f32[heads*D], qkv f32[(heads+2*kv)*D] (unrotated, with bias), kcache f32[kv,C,D],
-//     vcache f32[kv,C,D], inv_freq f32[D/2], pos i64[1] | NULL];
-// s: [heads, kv, D, past, C, scale as float32 bits]  (D = 64; past read from pos when given)
+//     vcache f32[kv,C,D], inv_freq f32[D/2], pos i64[1] | NULL, rope table f32[2,C,D/2] | NULL];
+// s: [heads, kv, D, past, C, scale as float32 bits]  (D 64 or 32, C <= 16384; past read from pos when given)
 NC_EXPORT int32_t nc_attention_decode(void **p, const int64_t *s) {
     NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3] && p[4], "nc_attention_decode: null operand");
     const int64_t heads = s[0], kv = s[1], D = s[2], past = s[3], cap = s[4];
@@ -375,10 +305,8 @@ NC_EXPORT int32_t nc_attention_decode(void **p, const int64_t *s) {
     NC_REQUIRE(heads > 0 && kv > 0 && heads % kv == 0 && heads < 65536 && (D == 64 || D == 32) && cap > 0 &&
                    cap <= 16384 && (pos || (past >= 0 && past + 1 <= cap)),
                "nc_attention_decode: bad shape (head_dim 64 or 32, capacity at most 16384)");
-    auto kernel = D == 64 ? attention_decode<64> : attention_decode<32>;
-    hipLaunchKernelGGL(kernel, dim3((unsigned)heads), dim3(kT), (size_t)cap * sizeof(float), nc::stream(),
-                       (float *)p[0], (const float *)p[1], (float *)p[2], (float *)p[3], (const float *)p[4],
-                       (int)heads, (int)kv, pos ? 0 : (int)past, (int)cap, bits_to_float(s[5]), pos,
-                       nc::error_word());
-    return nc::launched("attention_decode");
+    if (p[6]) return D == 64 ? launch_attention_decode<64, true>(p, s, pos) : launch_attention_decode<32, true>(p, s, pos);
+    return D == 64 ? launch_attention_decode<64, false>(p, s, pos) : launch_attention_decode<32, false>(p, s, pos);
 }
+
+

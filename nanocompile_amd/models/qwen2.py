@@ -85,6 +85,13 @@ class KVCache:
         shape = (config.num_hidden_layers, config.num_key_value_heads, capacity, config.head_dim)
         self.keys, self.values = DeviceArray(shape, np.float32), DeviceArray(shape, np.float32)
         self._layer = config.num_key_value_heads * capacity * config.head_dim * 4
+        # cos and sin of every position's RoPE angles (nc_rope_table), for the
+        # decode attention kernel: the same bits it would compute, one lookup
+        D = config.head_dim
+        self.rope = DeviceArray((2, capacity, D // 2), np.float32)
+        inv = DeviceArray.from_host(inverse_frequencies(D, config.rope_theta))
+        hip.call("nc_rope_table", [self.rope, inv], [capacity, D])
+        hip.sync()
 
     def layer(self, index: int) -> tuple[int, int]:
         return self.keys.ptr + index * self._layer, self.values.ptr + index * self._layer
@@ -217,7 +224,7 @@ class Qwen2:
                 kc, vc = cache.layer(i)
                 q, s = w["qkv"]
                 hip.call("nc_decode_projection", [self.qkv, self.x, w["g1"], q, s, w["qkv_b"]], [W, H, 0, eps])
-                hip.call("nc_attention_decode", [self.ctx, self.qkv, kc, vc, self.inv_freq, pos],
+                hip.call("nc_attention_decode", [self.ctx, self.qkv, kc, vc, self.inv_freq, pos, cache.rope],
                          [heads, kv, D, past, cache.capacity, float_bits(self.scale)])
                 q, s = w["o"]
                 hip.call("nc_decode_projection", [self.x, self.ctx, None, q, s], [H, Q, 1, eps])

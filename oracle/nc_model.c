@@ -151,32 +151,71 @@ typedef struct {
     float scale;
 } attn_ctx;
 
+/* Attention of one query row in the chunked order of the GPU kernels
+ * (nanocompile_amd/csrc/nc_attend.h): per chunk of 64 keys the scores in
+ * order of d, the chunk max, p = exp(s - max), the chunk sum as the
+ * wavefront butterfly over 64 lanes (0 past the chunk), o in key order; then
+ * the chunks combined in order: m = max m_j, w_j = exp(m_j - m),
+ * L = sum l_j w_j, O = sum o_j w_j, out = O / L. */
+#define CHUNK 64
+
+static float butterfly64(float *v /* [64], destroyed */) {
+    float t[64];
+    for (int off = 32; off > 0; off >>= 1) {
+        for (int i = 0; i < 64; ++i) t[i] = v[i] + v[i ^ off];
+        memcpy(v, t, sizeof t);
+    }
+    return v[0];
+}
+
+static void attend_row(float *out, const float *q, const float *K, const float *V, int64_t T, int64_t d,
+                       float scale) {
+    const int64_t J = (T + CHUNK - 1) / CHUNK;
+    float *part = (float *)malloc(sizeof(float) * (size_t)(J * (d + 2)));
+    for (int64_t j = 0; j < J; ++j) {
+        const int64_t t0 = j * CHUNK, n = T - t0 < CHUNK ? T - t0 : CHUNK;
+        float s[CHUNK], p[CHUNK];
+        float m = -INFINITY;
+        for (int64_t i = 0; i < n; ++i) {
+            float acc = 0.0f;
+            for (int64_t k = 0; k < d; ++k) acc = acc + q[k] * K[(t0 + i) * d + k];
+            s[i] = (acc * scale) + 0.0f;
+            m = nan_max(m, s[i]);
+        }
+        for (int64_t i = 0; i < CHUNK; ++i) p[i] = i < n ? nc_expf(s[i] - m) : 0.0f;
+        float lanes[64];
+        memcpy(lanes, p, sizeof lanes);
+        float *pj = part + j * (d + 2);
+        pj[0] = m;
+        pj[1] = butterfly64(lanes);
+        for (int64_t k = 0; k < d; ++k) {
+            float o = 0.0f;
+            for (int64_t i = 0; i < n; ++i) o = o + p[i] * V[(t0 + i) * d + k];
+            pj[2 + k] = o;
+        }
+    }
+    float m = -INFINITY;
+    for (int64_t j = 0; j < J; ++j) m = nan_max(m, part[j * (d + 2)]);
+    for (int64_t k = 0; k < d; ++k) {
+        float L = 0.0f, O = 0.0f;
+        for (int64_t j = 0; j < J; ++j) {
+            const float *pj = part + j * (d + 2);
+            const float w = nc_expf(pj[0] - m);
+            L = L + pj[1] * w;
+            O = O + pj[2 + k] * w;
+        }
+        out[k] = O / L;
+    }
+    free(part);
+}
+
 static void attention_task(void *arg, int64_t job) {
     const attn_ctx *a = (const attn_ctx *)arg;
     const int64_t h = job % a->heads, i = job / a->heads, d = a->d;
     const int64_t g = h / (a->heads / a->kv), width = (a->heads + 2 * a->kv) * d;
-    const int64_t T = a->past + i + 1;
     const float *q = a->qkv + i * width + h * d;
     const float *K = a->kcache + g * a->capacity * d, *V = a->vcache + g * a->capacity * d;
-    float *e = (float *)malloc(sizeof(float) * (size_t)T);
-    for (int64_t t = 0; t < T; ++t) {
-        float acc = 0.0f;
-        for (int64_t j = 0; j < d; ++j) acc = acc + q[j] * K[t * d + j];
-        e[t] = (acc * a->scale) + 0.0f;
-    }
-    softmax_row(e, T);
-    const int64_t S = (T + 3) / 4;
-    for (int64_t j = 0; j < d; ++j) {
-        float part[4];
-        for (int c = 0; c < 4; ++c) {
-            float acc = 0.0f;
-            const int64_t t0 = c * S, t1 = t0 + S < T ? t0 + S : T;
-            for (int64_t t = t0; t < t1; ++t) acc = acc + e[t] * V[t * d + j];
-            part[c] = acc;
-        }
-        a->ctx[i * a->heads * d + h * d + j] = (part[0] + part[1]) + (part[2] + part[3]);
-    }
-    free(e);
+    attend_row(a->ctx + i * a->heads * d + h * d, q, K, V, a->past + i + 1, d, a->scale);
 }
 
 EXPORT void nc_host_attention(float *ctx, const float *qkv, const float *kcache, const float *vcache, int64_t m,

@@ -1,0 +1,154 @@
+"""Attention on the GPU, bit for bit against the host oracle's chunked order.
+
+The decode kernel gives each head one workgroup whose waves take the 64-key
+chunks and combine them in LDS; these tests cover both sides of every chunk
+edge, contexts longer than one pass of the waves, both head widths, the
+position read from the device, back-to-back calls, and a captured graph
+replayed at advancing positions.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle.host_model import inverse_frequencies
+from tests.conftest import bits
+
+pytestmark = pytest.mark.gpu
+
+
+def setup(rng, heads, kv, d, cap, m=1):
+    width = (heads + 2 * kv) * d
+    qkv = rng.standard_normal((m, width)).astype(np.float32)
+    kc = rng.standard_normal((kv, cap, d)).astype(np.float32)
+    vc = rng.standard_normal((kv, cap, d)).astype(np.float32)
+    return qkv, kc, vc
+
+
+@pytest.mark.parametrize("d,heads,kv", [(64, 14, 2), (32, 4, 2)])
+@pytest.mark.parametrize("past", [0, 1, 63, 64, 65, 127, 128, 200, 511, 512, 1000, 3000])
+def test_decode_attention_is_the_oracle(gpu, host, d, heads, kv, past):
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import DeviceArray
+    from nanocompile_amd.kernels import float_bits
+    print(f"attention_decode d={d} past={past}", flush=True)
+    rng = np.random.default_rng(past + d)
+    cap = past + 5
+    qkv, kc, vc = setup(rng, heads, kv, d, cap)
+    inv = inverse_frequencies(d, 1e6)
+    scale = float(np.float32(d ** -0.5))
+    hq, hk, hv = qkv.copy(), kc.copy(), vc.copy()
+    expected = host.rope_append_attention(hq, hk, hv, inv, heads, kv, d, past, scale)
+
+    dq, dk, dv = DeviceArray.from_host(qkv), DeviceArray.from_host(kc), DeviceArray.from_host(vc)
+    dinv, ctx = DeviceArray.from_host(inv), DeviceArray((1, heads * d), np.float32)
+    pos = DeviceArray.from_host(np.array([past], np.int64))
+    for use_pos in (False, True, True):
+        hip.call("nc_attention_decode", [ctx, dq, dk, dv, dinv, pos if use_pos else None],
+                 [heads, kv, d, 0 if use_pos else past, cap, float_bits(scale)])
+        assert np.array_equal(bits(ctx.numpy()), bits(expected)), use_pos
+    assert np.array_equal(bits(dk.numpy()), bits(hk)) and np.array_equal(bits(dv.numpy()), bits(hv))
+
+
+@pytest.mark.parametrize("d", [64, 32])
+def test_prefill_and_decode_attention_agree(gpu, host, d):
+    """A prompt's last row through nc_attention equals a decode step at the same position."""
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import DeviceArray
+    from nanocompile_amd.kernels import float_bits
+    rng = np.random.default_rng(d)
+    heads, kv, m, past = 4, 2, 130, 70
+    cap = past + m
+    qkv, kc, vc = setup(rng, heads, kv, d, cap, m)
+    inv = inverse_frequencies(d, 1e6)
+    scale = float(np.float32(d ** -0.5))
+    hq, hk, hv = qkv.copy(), kc.copy(), vc.copy()
+    expected = host.rope_append_attention(hq, hk, hv, inv, heads, kv, d, past, scale)
+    dq, dk, dv = DeviceArray.from_host(qkv), DeviceArray.from_host(kc), DeviceArray.from_host(vc)
+    dinv, ctx = DeviceArray.from_host(inv), DeviceArray((m, heads * d), np.float32)
+    hip.call("nc_rope_append", [dq, dk, dv, dinv], [m, heads, kv, d, past, cap])
+    hip.call("nc_attention", [ctx, dq, dk, dv], [m, heads, kv, d, past, cap, float_bits(scale)])
+    prefill = ctx.numpy()
+    assert np.array_equal(bits(prefill), bits(expected))
+    # the last row again (unrotated) as a decode step at its position, over the
+    # cache the prefill filled (the step rewrites its own key with the same bits)
+    dq2 = DeviceArray.from_host(qkv[-1:])
+    one = DeviceArray((1, heads * d), np.float32)
+    hip.call("nc_attention_decode", [one, dq2, dk, dv, dinv, None],
+             [heads, kv, d, past + m - 1, cap, float_bits(scale)])
+    assert np.array_equal(bits(one.numpy()[0]), bits(prefill[-1]))
+    assert np.array_equal(bits(dk.numpy()), bits(hk))
+
+
+def test_decode_attention_in_a_graph_at_advancing_positions(gpu, host):
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import DeviceArray, Graph
+    from nanocompile_amd.kernels import float_bits
+    rng = np.random.default_rng(9)
+    heads, kv, d, cap = 14, 2, 64, 300
+    qkv, kc, vc = setup(rng, heads, kv, d, cap)
+    inv = inverse_frequencies(d, 1e6)
+    scale = float(np.float32(0.125))
+    dq, dk, dv = DeviceArray.from_host(qkv), DeviceArray.from_host(kc), DeviceArray.from_host(vc)
+    dinv, ctx = DeviceArray.from_host(inv), DeviceArray((1, heads * d), np.float32)
+    pos = DeviceArray.from_host(np.array([0], np.int64))
+    graph = Graph.capture(lambda: hip.call("nc_attention_decode", [ctx, dq, dk, dv, dinv, pos],
+                                           [heads, kv, d, 0, cap, float_bits(scale)]))
+    hk, hv = kc.copy(), vc.copy()
+    for past in (10, 63, 64, 150, 299):
+        print(f"graph replay at past={past}", flush=True)
+        pos.upload(np.array([past], np.int64))
+        graph.launch()
+        hip.sync()
+        expected = host.rope_append_attention(qkv.copy(), hk, hv, inv, heads, kv, d, past, scale)
+        assert np.array_equal(bits(ctx.numpy()), bits(expected)), past
+
+
+def test_decode_attention_rejects_bad_shapes(gpu):
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import DeviceArray
+    x = DeviceArray((4096,), np.float32)
+    with pytest.raises(hip.KernelError, match="bad shape"):
+        hip.call("nc_attention_decode", [x, x, x, x, x], [4, 2, 48, 3, 8, 0])      # head_dim 48
+    with pytest.raises(hip.KernelError, match="bad shape"):
+        hip.call("nc_attention_decode", [x, x, x, x, x], [4, 2, 64, 8, 8, 0])      # past + 1 > capacity
+    with pytest.raises(hip.KernelError, match="null operand"):
+        hip.call("nc_attention_decode", [x, x, None, x, x], [4, 2, 64, 3, 8, 0])
+
+
+@pytest.mark.parametrize("d", [64, 32])
+def test_rope_table_is_nc_cosf_and_nc_sinf(gpu, host, d):
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import DeviceArray
+    cap = 3000
+    inv = inverse_frequencies(d, 1e6)
+    table = DeviceArray((2, cap, d // 2), np.float32)
+    hip.call("nc_rope_table", [table, DeviceArray.from_host(inv)], [cap, d])
+    got = table.numpy()
+    ang = (np.arange(cap, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float32)
+    assert np.array_equal(bits(got[0]), bits(host.math("nc_cos", ang)))
+    assert np.array_equal(bits(got[1]), bits(host.math("nc_sin", ang)))
+
+
+@pytest.mark.parametrize("past", [0, 100, 300, 700])
+def test_decode_attention_with_the_rope_table(gpu, host, past):
+    """The table path (what the model runs) and the computing path give the oracle's bits."""
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import DeviceArray
+    from nanocompile_amd.kernels import float_bits
+    rng = np.random.default_rng(past + 1)
+    heads, kv, d = 14, 2, 64
+    cap = past + 9
+    qkv, kc, vc = setup(rng, heads, kv, d, cap)
+    inv = inverse_frequencies(d, 1e6)
+    scale = float(np.float32(0.125))
+    expected = host.rope_append_attention(qkv.copy(), kc.copy(), vc.copy(), inv, heads, kv, d, past, scale)
+    dinv = DeviceArray.from_host(inv)
+    table = DeviceArray((2, cap, d // 2), np.float32)
+    hip.call("nc_rope_table", [table, dinv], [cap, d])
+    for tab in (table, None):
+        dq, dk, dv = DeviceArray.from_host(qkv), DeviceArray.from_host(kc), DeviceArray.from_host(vc)
+        ctx = DeviceArray((1, heads * d), np.float32)
+        hip.call("nc_attention_decode", [ctx, dq, dk, dv, dinv, None, tab], [heads, kv, d, past, cap, float_bits(scale)])
+        assert np.array_equal(bits(ctx.numpy()), bits(expected)), tab is None
