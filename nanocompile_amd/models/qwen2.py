@@ -20,7 +20,10 @@ driver only uploads token ids and downloads what the caller asks for:
 then the final rms_norm, the float32 tied LM head (the reference keeps it
 float32, quantize.py:24-28) and the argmax. ``quantization="int8-token"`` is
 the north star's mode: per-row int8 weights, per-token int8 activations,
-exact int32 accumulation.
+exact int32 accumulation. ``"int8"`` and ``"int8-vnni"`` are the reference's
+own modes (quantize.py:127-164): float32 activations times int8 weights in
+its 32-chain order, or 32-wide int8 activation blocks in its VNNI order, each
+bit for bit with its generated C (nc_matmul_i8, nc_matmul_i8_vnni).
 
 Memory: the weights go into one device arena, made once; activations for up
 to ``max_tokens`` new tokens into a second, also made once; the KV cache is a
@@ -36,11 +39,19 @@ import numpy as np
 
 from nanocompile_amd import hip
 from nanocompile_amd.hip import DeviceArray
-from nanocompile_amd.kernels import float_bits
+from nanocompile_amd.kernels import float_bits, pack_chains, pack_chains_vnni
 from nanocompile_amd.models.config import Qwen2Config
 
-QUANTIZATIONS = ("int8-token",)
+QUANTIZATIONS = ("int8-token", "int8", "int8-vnni")
+BLOCK = 32          # matmul_i8_vnni's activation block (quantize.py:44)
 ALIGN = 256
+
+
+def _packed_bytes(quantization: str, n: int, k: int) -> int:
+    """Bytes of pack_chains (int8) or pack_chains_vnni (int8-vnni) of an [n, k] weight."""
+    if quantization == "int8":
+        return n * -(-(k // 32) // 4) * 128
+    return n * (k // 128) * 128
 
 
 def inverse_frequencies(head_dim: int, theta: float) -> np.ndarray:
@@ -130,6 +141,9 @@ class Qwen2:
         per_layer = [((H,), np.float32), ((H,), np.float32), ((W, H), np.int8), ((W,), np.float32),
                      ((W,), np.float32), ((H, Q), np.int8), ((H,), np.float32), ((I, H), np.int8),
                      ((I,), np.float32), ((I, H), np.int8), ((I,), np.float32), ((H, I), np.int8), ((H,), np.float32)]
+        if quantization != "int8-token":       # the reference modes' packed copies (pack_chains*)
+            per_layer += [((_packed_bytes(quantization, n, k),), np.int8)
+                          for n, k in ((W, H), (H, Q), (I, H), (I, H), (H, I))]
         shapes = per_layer * L + [((V, H), np.float32), ((vblocks, H), np.float32), ((H,), np.float32),
                                   ((D // 2,), np.float32)]
         self.weights = Arena(Arena.size(shapes))
@@ -139,8 +153,9 @@ class Qwen2:
             into.upload(np.ascontiguousarray(weights[name], np.float32))
             return into
 
-        def quantized(names: Sequence[str], rows: int, k: int) -> tuple[DeviceArray, DeviceArray]:
-            """Per-row int8 of the named matrices stacked row-wise (quantize.py:55-70, on the device)."""
+        def quantized(names: Sequence[str], rows: int, k: int) -> tuple:
+            """Per-row int8 of the named matrices stacked row-wise (quantize.py:55-70, on the device),
+            plus, for the reference's modes, the packed copy their kernels read (made once)."""
             q, s = self.weights.take((rows, k), np.int8), self.weights.take((rows,), np.float32)
             at = 0
             for name in names:
@@ -155,7 +170,13 @@ class Qwen2:
                 at += n
             if at != rows:
                 raise ValueError(f"{names} have {at} rows, expected {rows}")
-            return q, s
+            if quantization == "int8-token":
+                return q, s
+            host_q = q.numpy()
+            pack = pack_chains(host_q) if quantization == "int8" else pack_chains_vnni(host_q)
+            packed = self.weights.take((pack.size,), np.int8)
+            packed.upload(pack.reshape(-1))
+            return q, s, packed
 
         self.layers = []
         for i in range(L):
@@ -185,14 +206,16 @@ class Qwen2:
         self.inv_freq.upload(inverse_frequencies(D, c.rope_theta))
         self.scale = float(np.float32(D ** -0.5))
         # the fused one-token kernels exist for these widths (nc_decode.hip)
-        self.fused_decode = (H, I, D) in ((896, 4864, 64), (128, 256, 32)) and Q == H
+        self.fused_decode = (H, I, D) in ((896, 4864, 64), (128, 256, 32)) and Q == H \
+            and quantization == "int8-token"
         hip.sync()
         del stage
 
         M = max_tokens
         act = [((M, H), np.float32), ((M, W), np.float32), ((M, Q), np.float32), ((M, I), np.float32),
                ((M, max(I, H, Q)), np.int8), ((M,), np.float32), ((M, H), np.float32), ((M,), np.int64),
-               ((M,), np.uint64), ((1, V), np.float32), ((M,), np.int64)]
+               ((M,), np.uint64), ((1, V), np.float32), ((M,), np.int64), ((M, I), np.float32),
+               ((M, I), np.float32), ((M, -(-max(I, H, Q) // BLOCK)), np.float32), ((M,), np.float32)]
         self.acts = Arena(Arena.size(act))
         self.x, self.qkv = self.acts.take((M, H), np.float32), self.acts.take((M, W), np.float32)
         self.ctx, self.h = self.acts.take((M, Q), np.float32), self.acts.take((M, I), np.float32)
@@ -200,6 +223,10 @@ class Qwen2:
         self.normed, self.ids = self.acts.take((M, H), np.float32), self.acts.take((M,), np.int64)
         self.best, self.logits_row = self.acts.take((M,), np.uint64), self.acts.take((1, V), np.float32)
         self.argmax = self.acts.take((M,), np.int64)
+        # the reference modes: gate and up apart, and the block quantizer's scales and offsets
+        self.gate, self.up = self.acts.take((M, I), np.float32), self.acts.take((M, I), np.float32)
+        self.xsb = self.acts.take((M, -(-max(I, H, Q) // BLOCK)), np.float32)
+        self.xoff = self.acts.take((M,), np.float32)
 
     # -- running ---------------------------------------------------------------------
 
@@ -233,6 +260,9 @@ class Qwen2:
                 q, s = w["down"]
                 hip.call("nc_decode_projection", [self.x, self.h, None, q, s], [H, I, 1, eps])
             return
+        if self.quantization != "int8-token":
+            self._layers_reference_modes(m, past, cache, pos)
+            return
         s_qkv, s_o, s_mlp, s_down = self._projection_schedules(m)
         for i, w in enumerate(self.layers):
             kc, vc = cache.layer(i)
@@ -252,6 +282,39 @@ class Qwen2:
             hip.call("nc_quantize_token_i8", [self.xq, self.xs, self.h], [m, I])
             q, s = w["down"]
             hip.call("nc_matmul_i8_token", [self.x, self.xq, self.xs, q, s, None, self.x], [m, H, I, s_down])
+
+    def _layers_reference_modes(self, m: int, past: int, cache: KVCache, pos: DeviceArray | None) -> None:
+        """The layers with the reference's own int8 modes (quantize.py:127-164): float32 activations
+        into matmul_i8 ("int8"), or 32-wide int8 blocks into matmul_i8_vnni ("int8-vnni"), each in the
+        reference's k order; rms_norm, RoPE, attention and the LM head as in "int8-token"."""
+        c = self.config
+        H, I, D = c.hidden_size, c.intermediate_size, c.head_dim
+        heads, kv, W = c.num_attention_heads, c.num_key_value_heads, self.width
+        Q = heads * D
+        eps = float_bits(c.rms_norm_eps)
+        for i, w in enumerate(self.layers):
+            kc, vc = cache.layer(i)
+            hip.call("nc_rms_norm_quant", [self.normed, self.xq, self.xs, self.x, w["g1"]], [m, H, eps])
+            self._project(w["qkv"], self.normed, self.qkv, m, W, H, bias=w["qkv_b"])
+            hip.call("nc_rope_append", [self.qkv, kc, vc, self.inv_freq, pos],
+                     [m, heads, kv, D, past, cache.capacity])
+            hip.call("nc_attention", [self.ctx, self.qkv, kc, vc, pos],
+                     [m, heads, kv, D, past, cache.capacity, float_bits(self.scale)])
+            self._project(w["o"], self.ctx, self.x, m, H, Q, residual=self.x)
+            hip.call("nc_rms_norm_quant", [self.normed, self.xq, self.xs, self.x, w["g2"]], [m, H, eps])
+            self._project(w["gate"], self.normed, self.gate, m, I, H)
+            self._project(w["up"], self.normed, self.up, m, I, H)
+            hip.call("nc_silu_mul", [self.h, self.gate, self.up], [m * I])
+            self._project(w["down"], self.h, self.x, m, H, I, residual=self.x)
+
+    def _project(self, weight, x, y, m: int, n: int, k: int, bias=None, residual=None) -> None:
+        q, s, packed = weight
+        if self.quantization == "int8":
+            hip.call("nc_matmul_i8", [y, x, packed, q, s, bias, residual], [m, n, k])
+        else:
+            hip.call("nc_quantize_blocks", [self.xq, self.xsb, self.xoff, x], [m, k, BLOCK])
+            hip.call("nc_matmul_i8_vnni", [y, self.xq, self.xsb, self.xoff, packed, q, s, bias, residual],
+                     [m, n, k, BLOCK])
 
     def _projection_schedules(self, m: int) -> tuple[int, int, int, int]:
         """Schedules of the qkv, o, gate/up and down projections over m tokens:
