@@ -62,6 +62,19 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+TRAFFIC = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+
+
+def measured_traffic(kernel: str) -> int | None:
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    passes (profiles/traffic.json, counters calibrated on a copy of known size), or None."""
+    try:
+        with open(TRAFFIC, encoding="utf-8") as f:
+            return int(json.load(f)["kernels"][kernel]["traffic_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 # -- config 1: the decode GEMV -----------------------------------------------------
 
 
@@ -396,7 +409,9 @@ def main() -> int:
             "data": "synthetic (seeded N(0,0.02) weights, N(0,1) activations)",
             "config": {"workload": "config 1: decode GEMV, per-token int8 x per-row int8", "device": info["arch"]},
             "roofline": {"bound": "hbm", "achieved": round(g["stacked_gbps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                         "frac": round(g["stacked_gbps"] / HBM_PEAK_GBPS, 4), "traffic": None,
+                         "frac": round(g["stacked_gbps"] / HBM_PEAK_GBPS, 4),
+                         "traffic": measured_traffic("gemv_i8_token stacked (128 copies)"),
+                         "traffic_source": "profiles/traffic.json (rocprofv3 PMC, calibrated)",
                          "kernel": gemv_record["kernel"], "bytes_per_launch": g["per_launch_bytes"]},
             "cpu_baseline": None if cpu is None else {
                 "value": round(cpu["gbps"], 2), "unit": "GB/s", "cores": cpu["threads"], "kind": "port",
@@ -431,7 +446,8 @@ def main() -> int:
                    "decode_ms_total": round(d["decode_ms"], 3), "gemv": gemv_record,
                    "blocks": d.get("blocks")},
         "roofline": {"bound": "hbm", "achieved": round(d["lm_head_gbps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(d["lm_head_gbps"] / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(d["lm_head_gbps"] / HBM_PEAK_GBPS, 4), "traffic": measured_traffic("lm_head<4>"),
+                     "traffic_source": "profiles/traffic.json (rocprofv3 PMC, calibrated)",
                      "kernel": "lm_head<4> (fp32 tied LM head, 60% of a decode step's bytes)",
                      "bytes_per_launch": d["lm_bytes"], "launch_us": round(d["lm_head_us"], 3),
                      "step_bytes": d["step_bytes_mid"],
