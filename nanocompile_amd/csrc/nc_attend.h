@@ -1,8 +1,7 @@
 // Attention of one query over a chunk of at most 64 keys, by one wavefront:
-// the unit that both the decode kernel (one workgroup per chunk, so a long
-// context spreads over many CUs) and the prefill kernel (a workgroup's four
-// waves taking turns through the chunks) are built from, so both compute the
-// same bits, and the host oracle replays the same order.
+// the unit that both the decode kernel (a workgroup's waves taking a head's
+// chunks) and the prefill kernel (the same, per query row) are built from, so
+// both compute the same bits, and the host oracle replays the same order.
 //
 // The order (models/qwen2.py:113-155 computes softmax(q K^T * scale) V; this
 // is the split form of that softmax, each chunk normalised by its own max and
@@ -36,63 +35,76 @@ __device__ __forceinline__ float lane_value(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+// LDS floats one wave needs to turn its chunk's key rows around (rows padded
+// by 4 floats, so 16-byte reads of consecutive rows hit distinct banks).
+template <int D>
+constexpr int chunk_stage_floats() { return kChunk * (D + 4); }
+
 struct ChunkResult {
     float m, l, o;    // the chunk's max and sum (every lane), and o[d] in lane d
 };
 
-// One chunk's keys and values in registers: lane l holds key row t0 + l and,
-// for each of the chunk's keys i, value v[t0 + i][d] for its d = l. Loads
-// are issued in the constructor, from addresses clamped into the chunk (rows
-// past it, and the row `fresh`, are read at t0 and never used), so a caller
-// can start them early and overlap their latency with other work. With
-// FRESH, key `fresh` (when in the chunk) is taken from knew / vnew instead of
-// the cache: the decode kernel's new key, whose cache row another workgroup
-// may be writing.
+// One chunk's keys and values: the key rows loaded coalesced (D / 4 lanes
+// per row, 16 bytes each) and turned around through LDS so lane l holds key
+// row t0 + l; for each key i, value v[t0 + i][d] for the lane's d = l. Loads
+// are issued in the constructor, rows clamped to the cache's last row (rows
+// past the chunk are never used), so a caller can start them early. With
+// FRESH, key `fresh` (the last key of the context, when in this chunk) comes
+// from knew / vnew instead of the cache: the decode kernel's new key, whose
+// cache row another workgroup may be writing.
 template <int D, bool FRESH>
 struct Chunk {
-    static_assert(D % 4 == 0 && D <= 64, "head_dim");
-    float4 k[D / 4];
+    static_assert(D % 4 == 0 && D <= 64 && 256 % D == 0, "head_dim");
+    static constexpr int kLanesPerRow = D / 4;
+    static constexpr int kRowsPerLoad = 64 / kLanesPerRow;
+    float4 kc[D / 4];          // coalesced: load r holds row r * kRowsPerLoad + lane / kLanesPerRow
     float v[kChunk];
     int t0, n, fresh;
 
     __device__ __forceinline__ Chunk(const float *__restrict__ K, const float *__restrict__ V, int t0_, int n_,
-                                     int fresh_)
+                                     int fresh_, int last_row)
         : t0(t0_), n(n_), fresh(FRESH ? fresh_ : -1) {
         const int lane = threadIdx.x & 63;
         const int dl = lane < D ? lane : 0;
-        const int t = t0 + lane;
-        const float *krow = K + (size_t)(lane < n && t != fresh ? t : t0) * D;
+        const int col = (lane % kLanesPerRow) * 4;
 #pragma unroll
-        for (int i = 0; i < D / 4; ++i) k[i] = reinterpret_cast<const float4 *>(krow)[i];
-#pragma unroll
-        for (int i = 0; i < kChunk; ++i) {
-            const int ti = t0 + i;
-            v[i] = V[(size_t)(i < n && ti != fresh ? ti : t0) * D + dl];
+        for (int r = 0; r < D / 4; ++r) {
+            const int row = min(t0 + r * kRowsPerLoad + lane / kLanesPerRow, last_row);
+            kc[r] = *reinterpret_cast<const float4 *>(K + (size_t)row * D + col);
         }
+#pragma unroll
+        for (int i = 0; i < kChunk; ++i) v[i] = V[(size_t)min(t0 + i, last_row) * D + dl];
     }
 
-    // Attend q (rotated, D floats readable by every lane, e.g. in LDS). The
+    // Attend q (rotated, D floats readable by every lane, e.g. in LDS), using
+    // `stage` (chunk_stage_floats<D>() floats of LDS owned by this wave). The
     // whole wavefront must call this together.
-    __device__ __forceinline__ ChunkResult attend(const float *q, const float *knew, const float *vnew,
-                                                  float scale) const {
+    __device__ __forceinline__ ChunkResult attend(const float *q, const float *knew, const float *vnew, float scale,
+                                                  float *stage) const {
         const int lane = threadIdx.x & 63;
         const int dl = lane < D ? lane : 0;
-        const bool mine = t0 + lane == fresh;
+        constexpr int P = D + 4;
+#pragma unroll
+        for (int r = 0; r < D / 4; ++r) {
+            const int row = r * kRowsPerLoad + lane / kLanesPerRow;
+            *reinterpret_cast<float4 *>(stage + row * P + (lane % kLanesPerRow) * 4) = kc[r];
+        }
+        // (the wave's own LDS writes complete before its reads: in order, no barrier)
         float acc = 0.0f;
 #pragma unroll
         for (int i = 0; i < D / 4; ++i) {
-            float4 kk = k[i];
-            if constexpr (FRESH) {      // per component: a select of whole float4s goes through scratch
-                const float4 f = reinterpret_cast<const float4 *>(knew)[i];
-                kk.x = mine ? f.x : kk.x;
-                kk.y = mine ? f.y : kk.y;
-                kk.z = mine ? f.z : kk.z;
-                kk.w = mine ? f.w : kk.w;
-            }
-            acc = __fadd_rn(acc, __fmul_rn(q[4 * i + 0], kk.x));
-            acc = __fadd_rn(acc, __fmul_rn(q[4 * i + 1], kk.y));
-            acc = __fadd_rn(acc, __fmul_rn(q[4 * i + 2], kk.z));
-            acc = __fadd_rn(acc, __fmul_rn(q[4 * i + 3], kk.w));
+            const float4 k = *reinterpret_cast<const float4 *>(stage + lane * P + 4 * i);
+            acc = __fadd_rn(acc, __fmul_rn(q[4 * i + 0], k.x));
+            acc = __fadd_rn(acc, __fmul_rn(q[4 * i + 1], k.y));
+            acc = __fadd_rn(acc, __fmul_rn(q[4 * i + 2], k.z));
+            acc = __fadd_rn(acc, __fmul_rn(q[4 * i + 3], k.w));
+        }
+        const bool has_fresh = FRESH && fresh >= t0 && fresh < t0 + n;   // uniform; then fresh = t0 + n - 1
+        if (has_fresh) {
+            float f = 0.0f;
+#pragma unroll
+            for (int d = 0; d < D; ++d) f = __fadd_rn(f, __fmul_rn(q[d], knew[d]));
+            acc = lane == fresh - t0 ? f : acc;
         }
         const float s = lane < n ? __fadd_rn(__fmul_rn(acc, scale), 0.0f) : -__builtin_inff();
         float m = s;
@@ -102,34 +114,40 @@ struct Chunk {
         const float p = nc_expf(__fsub_rn(s, m));        // exp(-inf) = 0 for lanes past the chunk
         const float l = wave_sum_f32(p);
 
-        // o[d] in key order. A key past the chunk adds 0 * 0 = +0 to an
-        // accumulator that starts at +0 and is never -0: exact, no change.
-        float vf = 0.0f;
-        if constexpr (FRESH) vf = vnew[dl];
+        // o[d] in key order, the new key (the chunk's last) added last. A key
+        // past the loop's range adds 0 * 0 = +0 to an accumulator that starts
+        // at +0 and is never -0: exact, no change.
+        const int looped = has_fresh ? n - 1 : n;
         float o = 0.0f;
 #pragma unroll
         for (int i = 0; i < kChunk; ++i) {
-            const bool in = i < n;
+            const bool in = i < looped;
             const float pi = lane_value(p, i);
-            float vi = v[i];
-            if constexpr (FRESH) vi = t0 + i == fresh ? vf : vi;
-            o = __fadd_rn(o, __fmul_rn(in ? pi : 0.0f, in ? vi : 0.0f));
+            o = __fadd_rn(o, __fmul_rn(in ? pi : 0.0f, in ? v[i] : 0.0f));
         }
+        if (has_fresh) o = __fadd_rn(o, __fmul_rn(lane_value(p, n - 1), vnew[dl]));
         return {m, l, o};
     }
 };
 
 // The combine over chunks 0 .. J - 1 for lane d: partial j is m_j = at(j, 0),
-// l_j = at(j, 1), o_j[d] = at(j, 2 + d).
+// l_j = at(j, 1), o_j[d] = at(j, 2 + d). The weights w_j are computed 64 at a
+// time, one per lane, then the sums run in order of j. The whole wavefront
+// must call this together.
 template <typename At>
 __device__ __forceinline__ float combine_chunks(int J, int dl, At at) {
+    const int lane = threadIdx.x & 63;
     float m = -__builtin_inff();
     for (int j = 0; j < J; ++j) m = nan_max(m, at(j, 0));
     float L = 0.0f, O = 0.0f;
-    for (int j = 0; j < J; ++j) {
-        const float w = nc_expf(__fsub_rn(at(j, 0), m));
-        L = __fadd_rn(L, __fmul_rn(at(j, 1), w));
-        O = __fadd_rn(O, __fmul_rn(at(j, 2 + dl), w));
+    for (int j0 = 0; j0 < J; j0 += 64) {
+        const float w = j0 + lane < J ? nc_expf(__fsub_rn(at(j0 + lane, 0), m)) : 0.0f;
+        const int end = min(64, J - j0);
+        for (int j = 0; j < end; ++j) {
+            const float wj = lane_value(w, j);
+            L = __fadd_rn(L, __fmul_rn(at(j0 + j, 1), wj));
+            O = __fadd_rn(O, __fmul_rn(at(j0 + j, 2 + dl), wj));
+        }
     }
     return div_rn(O, L);
 }

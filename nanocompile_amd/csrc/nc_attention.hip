@@ -143,7 +143,9 @@ __global__ __launch_bounds__(kThreads) void attention_rows(float *__restrict__ c
                                                            const int64_t *__restrict__ pos_ptr,
                                                            int32_t *__restrict__ error) {
     if (pos_ptr && !position_fits(pos_ptr, (int)gridDim.y, capacity, error, past)) return;
-    extern __shared__ float part[];               // [J][D + 2]: m_j, l_j, o_j[D]
+    extern __shared__ __align__(16) float lds[];  // [4 waves][chunk stage], then [J][D + 2]: m_j, l_j, o_j[D]
+    float *stage = lds + (threadIdx.x >> 6) * nc::chunk_stage_floats<D>();
+    float *part = lds + (kThreads / 64) * nc::chunk_stage_floats<D>();
     __shared__ __align__(16) float q[D];
     const int h = blockIdx.x, i = blockIdx.y;
     const int g = h / (heads / kv_heads);
@@ -157,8 +159,8 @@ __global__ __launch_bounds__(kThreads) void attention_rows(float *__restrict__ c
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (int j = wave; j < J; j += kThreads / 64) {
         const int t0 = j * nc::kChunk;
-        nc::Chunk<D, false> chunk(K, V, t0, min(nc::kChunk, T - t0), -1);
-        const nc::ChunkResult r = chunk.attend(q, nullptr, nullptr, scale);
+        nc::Chunk<D, false> chunk(K, V, t0, min(nc::kChunk, T - t0), -1, capacity - 1);
+        const nc::ChunkResult r = chunk.attend(q, nullptr, nullptr, scale, stage);
         float *pj = part + j * (D + 2);
         if (lane == 0) {
             pj[0] = r.m;
@@ -238,19 +240,21 @@ namespace {
 template <int D>
 int32_t launch_rows(void **p, int64_t M, int64_t heads, int64_t kv, int64_t past, int64_t cap, float scale,
                     const int64_t *pos) {
-    // partials of every chunk in LDS: up to 256 chunks x 66 floats = 67.6 KB
-    // at 16384 keys, past the 64 KB a launch gets without asking
+    // the waves' chunk stages (70 KB) and the partials of every chunk (up to
+    // 256 chunks x 66 floats = 67.6 KB at 16384 keys): past the 64 KB a
+    // launch gets without asking
     static bool raised = false;
     if (!raised) {
         if (hipFuncSetAttribute(reinterpret_cast<const void *>(&attention_rows<D>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) != hipSuccess) {
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024) != hipSuccess) {
             nc::set_message("nc_attention: could not raise the LDS limit");
             return NC_LAUNCH_FAILED;
         }
         raised = true;
     }
     const int64_t keys = pos ? cap : past + M;
-    const size_t lds = (size_t)((keys + nc::kChunk - 1) / nc::kChunk) * (D + 2) * sizeof(float);
+    const size_t lds = ((size_t)(kThreads / 64) * nc::chunk_stage_floats<D>() +
+                        (size_t)((keys + nc::kChunk - 1) / nc::kChunk) * (D + 2)) * sizeof(float);
     hipLaunchKernelGGL(attention_rows<D>, dim3((unsigned)heads, (unsigned)M), dim3(kThreads), lds, nc::stream(),
                        (float *)p[0], (const float *)p[1], (const float *)p[2], (const float *)p[3], (int)heads,
                        (int)kv, pos ? 0 : (int)past, (int)cap, scale, pos, nc::error_word());

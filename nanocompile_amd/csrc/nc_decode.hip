@@ -26,7 +26,6 @@ namespace {
 
 using nc::i8x16;
 constexpr int kL = 8;                  // lanes per weight row: 8 x 16 B = one 128-byte line per load
-constexpr int kRows = 64 / kL;         // weight rows per one-wave workgroup
 
 enum Prologue { kNorm = 0, kQuant = 1 };
 enum Epilogue { kBias = 0, kResidual = 1, kSwiglu = 2 };
@@ -75,11 +74,11 @@ __device__ float activation_prologue(int8_t *__restrict__ sxq, const float *__re
     return scale;
 }
 
-template <int K>
+template <int K, int L>
 struct RowChunks {
-    static constexpr int STEP = kL * 16;
+    static constexpr int STEP = L * 16;
     static constexpr int ITERS = K / STEP;
-    static_assert(K % STEP == 0, "K must be a multiple of 128");
+    static_assert(K % STEP == 0, "K must be a multiple of 16 L");
     i8x16 w[ITERS];
 
     // The lane's 16-byte chunks of its weight row, loads issued back to back.
@@ -97,29 +96,29 @@ struct RowChunks {
     }
 };
 
-// One decode projection: workgroup = one wave = 8 rows (8 row pairs for SwiGLU).
-// The weight loads are issued first, so they are in flight while the
-// workgroup computes its activation prologue.
-template <int K, int PRO, int EPI>
+// One decode projection: workgroup = one wave = 64 / L rows (row pairs for
+// SwiGLU), L lanes per row. The weight loads are issued first, so they are in
+// flight while the workgroup computes its activation prologue.
+template <int K, int PRO, int EPI, int L>
 __global__ __launch_bounds__(64) void gemv_decode(float *__restrict__ out, const float *__restrict__ x,
                                                   const float *__restrict__ gamma, float eps,
                                                   const int8_t *__restrict__ q, const float *__restrict__ ws,
                                                   const float *__restrict__ bias, const int8_t *__restrict__ q2,
                                                   const float *__restrict__ ws2, int N) {
     __shared__ __align__(16) int8_t sxq[K];
-    const int lane = threadIdx.x, sub = lane & (kL - 1);
-    const int n = blockIdx.x * kRows + lane / kL;
+    const int lane = threadIdx.x, sub = lane & (L - 1);
+    const int n = blockIdx.x * (64 / L) + lane / L;
     const bool valid = n < N;
     const int nr = valid ? n : 0;
-    RowChunks<K> w1, w2;
+    RowChunks<K, L> w1, w2;
     w1.load(q + (size_t)nr * K, sub);
     if constexpr (EPI == kSwiglu) w2.load(q2 + (size_t)nr * K, sub);
     const float xs = activation_prologue<K, PRO>(sxq, x, gamma, eps);
     int32_t acc = w1.dot(sxq, sub);
     int32_t acc2 = 0;
     if constexpr (EPI == kSwiglu) acc2 = w2.dot(sxq, sub);
-    acc = nc::group_sum_i32<kL>(acc);
-    if constexpr (EPI == kSwiglu) acc2 = nc::group_sum_i32<kL>(acc2);
+    acc = nc::group_sum_i32<L>(acc);
+    if constexpr (EPI == kSwiglu) acc2 = nc::group_sum_i32<L>(acc2);
     if (sub != 0 || !valid) return;
     const float y = __fmul_rn(__fmul_rn((float)acc, xs), ws[n]);
     if constexpr (EPI == kBias) {
@@ -158,33 +157,35 @@ __global__ __launch_bounds__(64 * kWaves) void attention_decode(
         }
         past = (int)p;
     }
-    extern __shared__ float part[];               // [J][D + 2]: m_j, l_j, o_j[D]
-    __shared__ __align__(16) float q[D];
-    __shared__ __align__(16) float knew[D];
-    __shared__ __align__(16) float vnew[D];
+    extern __shared__ __align__(16) float lds[];  // [kWaves][chunk stage], then [J][D + 2]: m_j, l_j, o_j[D]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float *stage = lds + wave * nc::chunk_stage_floats<D>();
+    float *part = lds + kWaves * nc::chunk_stage_floats<D>();
+    __shared__ __align__(16) float rotated[kWaves][3 * D];     // per wave: q, the new key, the new value
+    float *q = rotated[wave], *knew = q + D, *vnew = q + 2 * D;
     constexpr int half = D / 2;
     const int h = blockIdx.x, group = heads / kv_heads, g = h / group;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int T = past + 1, J = (T + nc::kChunk - 1) / nc::kChunk;
     float *K = kcache + (size_t)g * capacity * D;
     float *V = vcache + (size_t)g * capacity * D;
 
     // every wave's first chunk (clamped to the last for waves past J) loads now
     const int j0 = min(wave, J - 1), t0 = j0 * nc::kChunk;
-    nc::Chunk<D, true> chunk(K, V, t0, min(nc::kChunk, T - t0), past);
+    nc::Chunk<D, true> chunk(K, V, t0, min(nc::kChunk, T - t0), past, capacity - 1);
 
-    // q rotated by lanes 0 .. half - 1 of wave 0, the new key by lanes
-    // half .. D - 1: cos and sin of f32(past) * inv_freq[i] from the cache's
-    // table (nc_rope_table) when given, else computed here, the same
-    // nc_cosf / nc_sinf either way; the first head of each KV group writes the
-    // cache row
-    if (tid < D) {
+    // Each wave rotates its own copy of q (lanes 0 .. half - 1) and of the new
+    // key (lanes half .. D - 1), so no workgroup barrier separates the loads
+    // above from their use: cos and sin of f32(past) * inv_freq[i] from the
+    // cache's table (nc_rope_table) when given, else computed here, the same
+    // nc_cosf / nc_sinf either way. A wave's LDS writes complete before its
+    // own later reads.
+    if (lane < D) {
         const float *qrow = qkv + h * D;
         const float *krow = qkv + heads * D + g * D;
         const float *vrow = qkv + (heads + kv_heads) * D + g * D;
-        const int i = tid < half ? tid : tid - half;
-        const float *x = tid < half ? qrow : krow;
-        float *y = tid < half ? q : knew;
+        const int i = lane < half ? lane : lane - half;
+        const float *x = lane < half ? qrow : krow;
+        float *y = lane < half ? q : knew;
         float c, s;
         if constexpr (TABLE) {
             c = table[(size_t)past * half + i];
@@ -197,14 +198,8 @@ __global__ __launch_bounds__(64 * kWaves) void attention_decode(
         const float x0 = x[i], x1 = x[i + half];
         y[i] = __fadd_rn(__fmul_rn(x0, c), __fmul_rn(-x1, s));
         y[i + half] = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(x0, s));
-        vnew[tid] = vrow[tid];
+        vnew[lane] = vrow[lane];
     }
-    __syncthreads();
-    if (h % group == 0 && tid < D) {
-        K[(size_t)past * D + tid] = knew[tid];
-        V[(size_t)past * D + tid] = vnew[tid];
-    }
-
     auto keep = [&](int j, const nc::ChunkResult &r) {
         float *pj = part + j * (D + 2);
         if (lane == 0) {
@@ -213,11 +208,20 @@ __global__ __launch_bounds__(64 * kWaves) void attention_decode(
         }
         if (lane < D) pj[2 + lane] = r.o;
     };
-    if (wave < J) keep(wave, chunk.attend(q, knew, vnew, scale));
+    if (wave < J) keep(wave, chunk.attend(q, knew, vnew, scale, stage));
     for (int j = wave + kWaves; j < J; j += kWaves) {      // contexts past 64 * kWaves keys
         const int tj = j * nc::kChunk;
-        nc::Chunk<D, true> more(K, V, tj, min(nc::kChunk, T - tj), past);
-        keep(j, more.attend(q, knew, vnew, scale));
+        nc::Chunk<D, true> more(K, V, tj, min(nc::kChunk, T - tj), past, capacity - 1);
+        keep(j, more.attend(q, knew, vnew, scale, stage));
+    }
+    // The cache row of the new key, written after the chunks are read: no
+    // workgroup reads it (the chunk holding it takes knew / vnew), and a
+    // store through the cache pointer before the reads would make the
+    // compiler keep the chunk's registers in scratch (a generic pointer may
+    // alias them).
+    if (wave == 0 && h % group == 0 && lane < D) {
+        K[(size_t)past * D + lane] = knew[lane];
+        V[(size_t)past * D + lane] = vnew[lane];
     }
     __syncthreads();
     if (wave == 0) {
@@ -233,9 +237,12 @@ float bits_to_float(int64_t bits) {
     return c.f;
 }
 
-template <int K, int PRO, int EPI>
+// Lanes per row: 8 (one 128-byte line per load, 8 rows a workgroup), or 16
+// for the long down projection (twice the workgroups, half the loads each).
+template <int K, int PRO, int EPI, int L = (K >= 4096 ? 16 : kL)>
 int32_t launch_decode(void **p, int N, float eps) {
-    hipLaunchKernelGGL((gemv_decode<K, PRO, EPI>), dim3((N + kRows - 1) / kRows), dim3(64), 0, nc::stream(),
+    constexpr int ROWS = 64 / L;
+    hipLaunchKernelGGL((gemv_decode<K, PRO, EPI, L>), dim3((N + ROWS - 1) / ROWS), dim3(64), 0, nc::stream(),
                        (float *)p[0], (const float *)p[1], (const float *)p[2], eps, (const int8_t *)p[3],
                        (const float *)p[4], (const float *)p[5], (const int8_t *)p[6], (const float *)p[7], N);
     return nc::launched("gemv_decode");
@@ -274,17 +281,18 @@ namespace {
 
 template <int D, bool TABLE>
 int32_t launch_attention_decode(void **p, const int64_t *s, const int64_t *pos) {
-    static bool raised = false;                          // partials of 256 chunks: 67.6 KB of LDS
+    static bool raised = false;          // chunk stages (70 KB) + partials of 256 chunks (67.6 KB)
     if (!raised) {
         if (hipFuncSetAttribute(reinterpret_cast<const void *>(&attention_decode<D, TABLE>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) != hipSuccess) {
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024) != hipSuccess) {
             nc::set_message("nc_attention_decode: could not raise the LDS limit");
             return NC_LAUNCH_FAILED;
         }
         raised = true;
     }
     const int64_t cap = s[4];
-    const size_t lds = (size_t)((cap + nc::kChunk - 1) / nc::kChunk) * (D + 2) * sizeof(float);
+    const size_t lds = ((size_t)kWaves * nc::chunk_stage_floats<D>() +
+                        (size_t)((cap + nc::kChunk - 1) / nc::kChunk) * (D + 2)) * sizeof(float);
     hipLaunchKernelGGL((attention_decode<D, TABLE>), dim3((unsigned)s[0]), dim3(64 * kWaves), lds, nc::stream(),
                        (float *)p[0], (const float *)p[1], (float *)p[2], (float *)p[3], (const float *)p[4],
                        (int)s[0], (int)s[1], pos ? 0 : (int)s[3], (int)cap, bits_to_float(s[5]), pos,
