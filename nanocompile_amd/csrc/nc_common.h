@@ -92,7 +92,7 @@ __device__ __forceinline__ float round_half_away(float v) { return __builtin_rou
 
 // Per-token activation quantization of one value (the reference's
 // quantize_activations with one block spanning the row, quantize.py:116-121):
-// clamp(round(x / scale), -127, 127).
+// clamp(round(x / scale), -127, 127), the division correctly rounded.
 __device__ __forceinline__ int8_t quantize_value(float x, float scale) {
     float r = round_half_away(div_rn(x, scale));
     r = r <= 127.0f ? r : 127.0f;

@@ -31,44 +31,71 @@ enum Prologue { kNorm = 0, kQuant = 1 };
 enum Epilogue { kBias = 0, kResidual = 1, kSwiglu = 2 };
 
 // The activation row x[K] (f32) to int8 in LDS; returns its scale. NORM
-// applies rms_norm first (rms_norm(x) * gamma, eps).
-template <int K, int PRO>
+// applies rms_norm first (rms_norm(x) * gamma, eps). The workgroup's W waves
+// share the work: thread t of 64 W holds elements t, t + 64 W, ... With W = 4
+// the threads are the row-sum order's 256 virtual threads themselves; with
+// W = 1 lane l holds virtual threads l, l + 64, l + 128, l + 192. Either way
+// the sum of squares is the row kernels' (nc_quant.hip) bit for bit.
+template <int K, int PRO, int W>
 __device__ float activation_prologue(int8_t *__restrict__ sxq, const float *__restrict__ x,
-                                     const float *__restrict__ gamma, float eps) {
-    constexpr int PER = (K + 63) / 64;
-    const int lane = threadIdx.x;
+                                     const float *__restrict__ gamma, float eps, float *scratch) {
+    static_assert(W == 1 || W == 4, "one wave, or the row order's 256 threads");
+    constexpr int T = 64 * W;
+    constexpr int PER = (K + T - 1) / T;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float v[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-        const int k = lane + 64 * i;
-        v[i] = (K % 64 == 0 || k < K) ? x[k] : 0.0f;
+        const int k = tid + T * i;
+        v[i] = (K % T == 0 || k < K) ? x[k] : 0.0f;
     }
     if constexpr (PRO == kNorm) {
-        float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};      // virtual threads lane + 64 g, g = 0..3
+        float ss;
+        if constexpr (W == 1) {
+            float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};      // virtual threads lane + 64 g, g = 0..3
 #pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int k = lane + 64 * i;
-            if (K % 64 == 0 || k < K) s[i & 3] = __fadd_rn(s[i & 3], __fmul_rn(v[i], v[i]));
+            for (int i = 0; i < PER; ++i) {
+                const int k = lane + 64 * i;
+                if (K % 64 == 0 || k < K) s[i & 3] = __fadd_rn(s[i & 3], __fmul_rn(v[i], v[i]));
+            }
+            float w[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) w[g] = nc::wave_sum_f32(s[g]);
+            ss = __fadd_rn(__fadd_rn(w[0], w[1]), __fadd_rn(w[2], w[3]));
+        } else {
+            float s = 0.0f;                             // virtual thread tid
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int k = tid + T * i;
+                if (K % T == 0 || k < K) s = __fadd_rn(s, __fmul_rn(v[i], v[i]));
+            }
+            s = nc::wave_sum_f32(s);
+            if (lane == 0) scratch[wave] = s;
+            __syncthreads();
+            ss = __fadd_rn(__fadd_rn(scratch[0], scratch[1]), __fadd_rn(scratch[2], scratch[3]));
+            __syncthreads();
         }
-        float w[4];
-#pragma unroll
-        for (int g = 0; g < 4; ++g) w[g] = nc::wave_sum_f32(s[g]);
-        const float ss = __fadd_rn(__fadd_rn(w[0], w[1]), __fadd_rn(w[2], w[3]));
         const float rcp = nc::div_rn(1.0f, nc::sqrt_rn(__fadd_rn(nc::div_rn(ss, (float)K), eps)));
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const int k = lane + 64 * i;
-            if (K % 64 == 0 || k < K) v[i] = __fmul_rn(__fmul_rn(v[i], rcp), gamma[k]);
+            const int k = tid + T * i;
+            if (K % T == 0 || k < K) v[i] = __fmul_rn(__fmul_rn(v[i], rcp), gamma[k]);
         }
     }
     float mag = 0.0f;
 #pragma unroll
     for (int i = 0; i < PER; ++i) mag = fmaxf(mag, fabsf(v[i]));
-    const float scale = nc::token_scale(nc::wave_max_f32(mag));
+    mag = nc::wave_max_f32(mag);
+    if constexpr (W > 1) {
+        if (lane == 0) scratch[4 + wave] = mag;
+        __syncthreads();
+        mag = fmaxf(fmaxf(scratch[4], scratch[5]), fmaxf(scratch[6], scratch[7]));
+    }
+    const float scale = nc::token_scale(mag);
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-        const int k = lane + 64 * i;
-        if (K % 64 == 0 || k < K) sxq[k] = nc::quantize_value(v[i], scale);
+        const int k = tid + T * i;
+        if (K % T == 0 || k < K) sxq[k] = nc::quantize_value(v[i], scale);
     }
     __syncthreads();
     return scale;
@@ -96,24 +123,26 @@ struct RowChunks {
     }
 };
 
-// One decode projection: workgroup = one wave = 64 / L rows (row pairs for
-// SwiGLU), L lanes per row. The weight loads are issued first, so they are in
-// flight while the workgroup computes its activation prologue.
-template <int K, int PRO, int EPI, int L>
-__global__ __launch_bounds__(64) void gemv_decode(float *__restrict__ out, const float *__restrict__ x,
-                                                  const float *__restrict__ gamma, float eps,
-                                                  const int8_t *__restrict__ q, const float *__restrict__ ws,
-                                                  const float *__restrict__ bias, const int8_t *__restrict__ q2,
-                                                  const float *__restrict__ ws2, int N) {
+// One decode projection: W waves a workgroup, 64 / L rows a wave (row pairs
+// for SwiGLU), L lanes per row. The weight loads are issued first, so they
+// are in flight while the workgroup computes its activation prologue, which
+// its W waves share.
+template <int K, int PRO, int EPI, int L, int W>
+__global__ __launch_bounds__(64 * W) void gemv_decode(float *__restrict__ out, const float *__restrict__ x,
+                                                      const float *__restrict__ gamma, float eps,
+                                                      const int8_t *__restrict__ q, const float *__restrict__ ws,
+                                                      const float *__restrict__ bias, const int8_t *__restrict__ q2,
+                                                      const float *__restrict__ ws2, int N) {
     __shared__ __align__(16) int8_t sxq[K];
-    const int lane = threadIdx.x, sub = lane & (L - 1);
-    const int n = blockIdx.x * (64 / L) + lane / L;
+    __shared__ float scratch[8];
+    const int lane = threadIdx.x & 63, sub = lane & (L - 1);
+    const int n = blockIdx.x * (W * 64 / L) + (threadIdx.x >> 6) * (64 / L) + lane / L;
     const bool valid = n < N;
     const int nr = valid ? n : 0;
     RowChunks<K, L> w1, w2;
     w1.load(q + (size_t)nr * K, sub);
     if constexpr (EPI == kSwiglu) w2.load(q2 + (size_t)nr * K, sub);
-    const float xs = activation_prologue<K, PRO>(sxq, x, gamma, eps);
+    const float xs = activation_prologue<K, PRO, W>(sxq, x, gamma, eps, scratch);
     int32_t acc = w1.dot(sxq, sub);
     int32_t acc2 = 0;
     if constexpr (EPI == kSwiglu) acc2 = w2.dot(sxq, sub);
@@ -237,12 +266,15 @@ float bits_to_float(int64_t bits) {
     return c.f;
 }
 
-// Lanes per row: 8 (one 128-byte line per load, 8 rows a workgroup), or 16
-// for the long down projection (twice the workgroups, half the loads each).
-template <int K, int PRO, int EPI, int L = (K >= 4096 ? 16 : kL)>
+// Lanes per row: 8 (one 128-byte line per load), or 16 for the long down
+// projection (half the loads each). Waves per workgroup: 1, or 4 for the long
+// down projection, whose 4864-wide prologue would otherwise cost each lane 76
+// correctly rounded divisions (measured on MI355X: 7.3 us with one wave,
+// 5.4 us with four; the 896-wide projections are faster with one).
+template <int K, int PRO, int EPI, int L = (K >= 4096 ? 16 : kL), int W = (K >= 4096 ? 4 : 1)>
 int32_t launch_decode(void **p, int N, float eps) {
-    constexpr int ROWS = 64 / L;
-    hipLaunchKernelGGL((gemv_decode<K, PRO, EPI, L>), dim3((N + ROWS - 1) / ROWS), dim3(64), 0, nc::stream(),
+    constexpr int ROWS = W * 64 / L;
+    hipLaunchKernelGGL((gemv_decode<K, PRO, EPI, L, W>), dim3((N + ROWS - 1) / ROWS), dim3(64 * W), 0, nc::stream(),
                        (float *)p[0], (const float *)p[1], (const float *)p[2], eps, (const int8_t *)p[3],
                        (const float *)p[4], (const float *)p[5], (const int8_t *)p[6], (const float *)p[7], N);
     return nc::launched("gemv_decode");

@@ -169,3 +169,30 @@ def test_device_division_sqrt_and_round_are_correctly_rounded(gpu):
     assert np.array_equal(bits(quotient), bits((a / b).astype(np.float32)))
     assert np.array_equal(bits(root), bits(np.sqrt(np.abs(a)).astype(np.float32)))
     assert np.array_equal(bits(rounded), bits(R.round_half_away(a)))
+
+
+def test_token_quantizer_at_half_integers(gpu):
+    """Values placed at, and a few ulps to 2^-12 around, every k + 1/2 of their row's scale:
+    where round(x / scale) depends on the division's last bit, the quantizer must still give
+    the correctly rounded quotient's rounding, as the oracle does."""
+    from nanocompile_amd import kernels
+    rng = np.random.default_rng(17)
+    rows = []
+    for _ in range(64):
+        mag = np.float32(rng.uniform(0.01, 100.0))
+        scale = np.float32(mag / np.float32(127.0))
+        k = rng.integers(-127, 127, 895).astype(np.float32) + np.float32(0.5)
+        base = (k * scale).astype(np.float32)
+        nudges = rng.choice([0, 1, -1, 2, -2], size=895)
+        x = base.copy()
+        toward = np.where(nudges > 0, np.float32(np.inf), np.float32(-np.inf))
+        for step in (1, 2):
+            x = np.where(np.abs(nudges) >= step, np.nextafter(x, toward).astype(np.float32), x)
+        spread = rng.choice([0.0, 2.0 ** -20, -(2.0 ** -20), 2.0 ** -14, -(2.0 ** -14), 2.0 ** -12], size=895)
+        x = np.where(spread != 0, ((k + spread) * scale).astype(np.float32), x)
+        x = np.clip(x, -mag, mag).astype(np.float32)
+        rows.append(np.concatenate([[mag], x]).astype(np.float32))
+    x = np.stack(rows)
+    xq, xs = kernels.quantize_token(x)
+    eq, es = R.quantize_token(x)
+    assert np.array_equal(xq.numpy(), eq) and np.array_equal(bits(xs.numpy()), bits(es))
