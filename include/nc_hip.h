@@ -193,11 +193,14 @@ int32_t nc_decode_projection(void **p, const int64_t *s);
 /* Attention of one new token (models/qwen2.py:113-155 at seq = 1) with RoPE of
  * its q and k heads and the cache append fused in: the same arithmetic, bit for
  * bit, as nc_rope_append followed by nc_attention (the 64-key chunked order
- * both share). One workgroup per query head, its waves taking the chunks.
+ * both share). One workgroup per (64-key chunk, KV head) attends all the
+ * group's query heads to its chunk; a second launch combines the chunks.
  * p: [ctx f32[heads*D], qkv f32[(heads+2*kv)*D] (unrotated), kcache f32[kv,C,D],
  *     vcache f32[kv,C,D], inv_freq f32[D/2], pos i64[1] or NULL (read in place of s[3]),
- *     rope table f32[2,C,D/2] from nc_rope_table or NULL (then cos and sin are computed)];
- * s: [heads, kv, D, past, C, scale as float32 bits] (D 64 or 32, C <= 16384) */
+ *     rope table f32[2,C,D/2] from nc_rope_table or NULL (then cos and sin are computed),
+ *     work f32 (the chunk results: heads * ceil(keys / 64) * (D + 2) floats, keys = C
+ *     with pos, else past + 1)];
+ * s: [heads, kv, D, past, C, scale as float32 bits, work bytes] (D 16, 32 or 64, C <= 16384) */
 int32_t nc_attention_decode(void **p, const int64_t *s);
 
 /* RoPE's cos and sin for every position of a cache, computed once with the
@@ -233,9 +236,16 @@ int32_t nc_rope_append(void **p, const int64_t *s);
  * (models/qwen2.py:113-155; query head h reads KV head h / (heads / kv), the
  * reference's repeat_kv as index arithmetic, nn.py:109-120). The softmax and
  * the context are computed in 64-key chunks combined afterwards, the order
- * nc_attention_decode shares, so prefill and decode agree bit for bit.
- * p: [ctx f32[M,heads*D], qkv (q rotated), kcache, vcache, pos i64[1] or NULL];
- * s: [M, heads, kv, D, past, C, scale as float32 bits] (D 16, 32 or 64; at most 16384 keys) */
+ * nc_attention_decode shares, so prefill and decode agree bit for bit. One
+ * workgroup per (64-key chunk, KV head, 8 query rows) attends the rows' query
+ * heads of the group to its chunk; a second launch combines the chunks. The
+ * reference materializes the [heads, M, keys] scores instead (README.md:317).
+ * p: [ctx f32[M,heads*D], qkv (q rotated), kcache, vcache, pos i64[1] or NULL,
+ *     work f32 (the chunk results: heads * ceil(keys / 64) * (D + 2) floats per query
+ *     row, keys = C with pos, else past + M; fewer than M rows' worth takes the rows
+ *     in slabs)];
+ * s: [M, heads, kv, D, past, C, scale as float32 bits, work bytes] (D 16, 32 or 64;
+ *    at most 16384 keys) */
 int32_t nc_attention(void **p, const int64_t *s);
 
 /* -- the model's ends ---------------------------------------------------------- */

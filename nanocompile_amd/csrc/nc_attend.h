@@ -1,7 +1,9 @@
 // Attention of one query over a chunk of at most 64 keys, by one wavefront:
-// the unit that both the decode kernel (a workgroup's waves taking a head's
-// chunks) and the prefill kernel (the same, per query row) are built from, so
-// both compute the same bits, and the host oracle replays the same order.
+// the unit that both the decode kernel and the prefill kernel are built from
+// (a workgroup stages a chunk's keys and values in LDS once, and its waves
+// attend every query head of the KV group, and every query row it holds, to
+// it), so both compute the same bits, and the host oracle replays the same
+// order.
 //
 // The order (models/qwen2.py:113-155 computes softmax(q K^T * scale) V; this
 // is the split form of that softmax, each chunk normalised by its own max and
@@ -20,6 +22,8 @@
 //     out  = O / L
 //
 // Every multiply and add rounds once (-ffp-contract=off); exp is nc_expf.
+// The chunk results (m_j, l_j, o_j) of a query travel between the two
+// kernels as D + 2 floats: m_j, l_j, o_j[0 .. D - 1].
 #pragma once
 
 #include "nc_common.h"
@@ -35,100 +39,121 @@ __device__ __forceinline__ float lane_value(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
-// LDS floats one wave needs to turn its chunk's key rows around (rows padded
-// by 4 floats, so 16-byte reads of consecutive rows hit distinct banks).
+// A chunk staged in LDS: key rows padded to D + 4 floats (so 16-byte reads of
+// consecutive rows hit distinct banks), then value rows of D floats.
 template <int D>
-constexpr int chunk_stage_floats() { return kChunk * (D + 4); }
+struct Staged {
+    static constexpr int kKeyStride = D + 4;
+    static constexpr int kFloats = kChunk * (D + 4) + kChunk * D;
+    float *keys, *values;
+    __device__ __forceinline__ explicit Staged(float *lds) : keys(lds), values(lds + kChunk * (D + 4)) {}
+};
+
+// Keys and values t0 .. t0 + 63 of one KV head (rows clamped to last_row),
+// loaded by the workgroup's NT threads, coalesced, 16 bytes a thread a load.
+// issue() starts the loads, so a caller can overlap them with other work;
+// store() writes them to LDS, rows from `valid` on as zeros (the rows past the
+// context: whatever the cache holds there must not reach a product) and row
+// `skip` (-1: none) left for the caller.
+template <int D, int NT>
+struct ChunkLoad {
+    static constexpr int kRow4 = D / 4;                     // float4 per row
+    static constexpr int kTotal = kChunk * kRow4;
+    static constexpr int kIters = (kTotal + NT - 1) / NT;
+    float4 k[kIters], v[kIters];
+
+    __device__ __forceinline__ void issue(const float *__restrict__ K, const float *__restrict__ V, int t0,
+                                          int last_row) {
+#pragma unroll
+        for (int it = 0; it < kIters; ++it) {
+            const int u = threadIdx.x + it * NT;
+            const int row = u / kRow4, col = (u % kRow4) * 4;
+            const size_t at = (size_t)min(t0 + row, last_row) * D + col;
+            if (kTotal % NT == 0 || u < kTotal) {
+                k[it] = *reinterpret_cast<const float4 *>(K + at);
+                v[it] = *reinterpret_cast<const float4 *>(V + at);
+            }
+        }
+    }
+
+    // (selects per component: a float4-wide select is lowered through scratch)
+    static __device__ __forceinline__ float4 keep_if(bool in, const float4 &x) {
+        return make_float4(in ? x.x : 0.0f, in ? x.y : 0.0f, in ? x.z : 0.0f, in ? x.w : 0.0f);
+    }
+
+    __device__ __forceinline__ void store(const Staged<D> &st, int skip, int valid) const {
+#pragma unroll
+        for (int it = 0; it < kIters; ++it) {
+            const int u = threadIdx.x + it * NT;
+            const int row = u / kRow4, col = (u % kRow4) * 4;
+            if ((kTotal % NT == 0 || u < kTotal) && row != skip) {
+                const bool in = row < valid;
+                *reinterpret_cast<float4 *>(st.keys + row * Staged<D>::kKeyStride + col) = keep_if(in, k[it]);
+                *reinterpret_cast<float4 *>(st.values + row * D + col) = keep_if(in, v[it]);
+            }
+        }
+    }
+};
 
 struct ChunkResult {
     float m, l, o;    // the chunk's max and sum (every lane), and o[d] in lane d
 };
 
-// One chunk's keys and values: the key rows loaded coalesced (D / 4 lanes
-// per row, 16 bytes each) and turned around through LDS so lane l holds key
-// row t0 + l; for each key i, value v[t0 + i][d] for the lane's d = l. Loads
-// are issued in the constructor, rows clamped to the cache's last row (rows
-// past the chunk are never used), so a caller can start them early. With
-// FRESH, key `fresh` (the last key of the context, when in this chunk) comes
-// from knew / vnew instead of the cache: the decode kernel's new key, whose
-// cache row another workgroup may be writing.
-template <int D, bool FRESH>
-struct Chunk {
-    static_assert(D % 4 == 0 && D <= 64 && 256 % D == 0, "head_dim");
-    static constexpr int kLanesPerRow = D / 4;
-    static constexpr int kRowsPerLoad = 64 / kLanesPerRow;
-    float4 kc[D / 4];          // coalesced: load r holds row r * kRowsPerLoad + lane / kLanesPerRow
-    float v[kChunk];
-    int t0, n, fresh;
-
-    __device__ __forceinline__ Chunk(const float *__restrict__ K, const float *__restrict__ V, int t0_, int n_,
-                                     int fresh_, int last_row)
-        : t0(t0_), n(n_), fresh(FRESH ? fresh_ : -1) {
-        const int lane = threadIdx.x & 63;
-        const int dl = lane < D ? lane : 0;
-        const int col = (lane % kLanesPerRow) * 4;
+// Attend q (D floats in LDS, read by every lane) to the first n keys of a
+// staged chunk whose rows past the context are zeros; `pbuf` is 64 floats of
+// LDS owned by the calling wave. The whole wavefront must call this together;
+// the chunk must be staged (and a barrier passed) before.
+template <int D>
+__device__ __forceinline__ ChunkResult attend_staged(const float *q, const Staged<D> &st, int n, float scale,
+                                                     float *pbuf) {
+    const int lane = threadIdx.x & 63;
+    const int dl = lane < D ? lane : 0;
+    float acc = 0.0f;
+    const float *krow = st.keys + lane * Staged<D>::kKeyStride;
 #pragma unroll
-        for (int r = 0; r < D / 4; ++r) {
-            const int row = min(t0 + r * kRowsPerLoad + lane / kLanesPerRow, last_row);
-            kc[r] = *reinterpret_cast<const float4 *>(K + (size_t)row * D + col);
-        }
-#pragma unroll
-        for (int i = 0; i < kChunk; ++i) v[i] = V[(size_t)min(t0 + i, last_row) * D + dl];
+    for (int i = 0; i < D / 4; ++i) {
+        const float4 k = *reinterpret_cast<const float4 *>(krow + 4 * i);
+        const float4 qi = *reinterpret_cast<const float4 *>(q + 4 * i);
+        acc = __fadd_rn(acc, __fmul_rn(qi.x, k.x));
+        acc = __fadd_rn(acc, __fmul_rn(qi.y, k.y));
+        acc = __fadd_rn(acc, __fmul_rn(qi.z, k.z));
+        acc = __fadd_rn(acc, __fmul_rn(qi.w, k.w));
     }
+    const float s = lane < n ? __fadd_rn(__fmul_rn(acc, scale), 0.0f) : -__builtin_inff();
+    float m = s;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = nan_max(m, __shfl_xor(m, off, 64));
+    m = lane_value(m, 0);
+    const float p = nc_expf(__fsub_rn(s, m));        // exp(-inf) = 0 for lanes past the chunk
+    const float l = wave_sum_f32(p);
 
-    // Attend q (rotated, D floats readable by every lane, e.g. in LDS), using
-    // `stage` (chunk_stage_floats<D>() floats of LDS owned by this wave). The
-    // whole wavefront must call this together.
-    __device__ __forceinline__ ChunkResult attend(const float *q, const float *knew, const float *vnew, float scale,
-                                                  float *stage) const {
-        const int lane = threadIdx.x & 63;
-        const int dl = lane < D ? lane : 0;
-        constexpr int P = D + 4;
+    // o[d] in key order, p read back from LDS four at a time (the wave's own
+    // write lands before its reads). A key past n adds 0 * v = +-0 (v a real
+    // key, masked, or a zero row) to an accumulator that starts at +0 and is
+    // never -0: exact, no change.
+    pbuf[lane] = p;
+    float o = 0.0f;
 #pragma unroll
-        for (int r = 0; r < D / 4; ++r) {
-            const int row = r * kRowsPerLoad + lane / kLanesPerRow;
-            *reinterpret_cast<float4 *>(stage + row * P + (lane % kLanesPerRow) * 4) = kc[r];
-        }
-        // (the wave's own LDS writes complete before its reads: in order, no barrier)
-        float acc = 0.0f;
-#pragma unroll
-        for (int i = 0; i < D / 4; ++i) {
-            const float4 k = *reinterpret_cast<const float4 *>(stage + lane * P + 4 * i);
-            acc = __fadd_rn(acc, __fmul_rn(q[4 * i + 0], k.x));
-            acc = __fadd_rn(acc, __fmul_rn(q[4 * i + 1], k.y));
-            acc = __fadd_rn(acc, __fmul_rn(q[4 * i + 2], k.z));
-            acc = __fadd_rn(acc, __fmul_rn(q[4 * i + 3], k.w));
-        }
-        const bool has_fresh = FRESH && fresh >= t0 && fresh < t0 + n;   // uniform; then fresh = t0 + n - 1
-        if (has_fresh) {
-            float f = 0.0f;
-#pragma unroll
-            for (int d = 0; d < D; ++d) f = __fadd_rn(f, __fmul_rn(q[d], knew[d]));
-            acc = lane == fresh - t0 ? f : acc;
-        }
-        const float s = lane < n ? __fadd_rn(__fmul_rn(acc, scale), 0.0f) : -__builtin_inff();
-        float m = s;
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) m = nan_max(m, __shfl_xor(m, off, 64));
-        m = lane_value(m, 0);
-        const float p = nc_expf(__fsub_rn(s, m));        // exp(-inf) = 0 for lanes past the chunk
-        const float l = wave_sum_f32(p);
-
-        // o[d] in key order, the new key (the chunk's last) added last. A key
-        // past the loop's range adds 0 * 0 = +0 to an accumulator that starts
-        // at +0 and is never -0: exact, no change.
-        const int looped = has_fresh ? n - 1 : n;
-        float o = 0.0f;
-#pragma unroll
-        for (int i = 0; i < kChunk; ++i) {
-            const bool in = i < looped;
-            const float pi = lane_value(p, i);
-            o = __fadd_rn(o, __fmul_rn(in ? pi : 0.0f, in ? v[i] : 0.0f));
-        }
-        if (has_fresh) o = __fadd_rn(o, __fmul_rn(lane_value(p, n - 1), vnew[dl]));
-        return {m, l, o};
+    for (int i = 0; i < kChunk / 4; ++i) {
+        const float4 pi = *reinterpret_cast<const float4 *>(pbuf + 4 * i);
+        o = __fadd_rn(o, __fmul_rn(pi.x, st.values[(4 * i + 0) * D + dl]));
+        o = __fadd_rn(o, __fmul_rn(pi.y, st.values[(4 * i + 1) * D + dl]));
+        o = __fadd_rn(o, __fmul_rn(pi.z, st.values[(4 * i + 2) * D + dl]));
+        o = __fadd_rn(o, __fmul_rn(pi.w, st.values[(4 * i + 3) * D + dl]));
     }
-};
+    return {m, l, o};
+}
+
+// Store a chunk result at part[0 .. D + 1] (m_j, l_j, o_j).
+template <int D>
+__device__ __forceinline__ void keep_result(float *part, const ChunkResult &r) {
+    const int lane = threadIdx.x & 63;
+    if (lane == 0) {
+        part[0] = r.m;
+        part[1] = r.l;
+    }
+    if (lane < D) part[2 + lane] = r.o;
+}
 
 // The combine over chunks 0 .. J - 1 for lane d: partial j is m_j = at(j, 0),
 // l_j = at(j, 1), o_j[d] = at(j, 2 + d). The weights w_j are computed 64 at a

@@ -19,6 +19,8 @@
 //    skipped); then the softmax and the context in 64-key chunks combined
 //    after, the order nc_attend.h states (shared with the decode kernel).
 // The host oracle (oracle/nc_model.c) replays exactly these orders.
+#include <algorithm>
+
 #include "nc_common.h"
 #include "nc_attend.h"
 #include "nc_math.h"
@@ -130,49 +132,211 @@ __global__ __launch_bounds__(kThreads) void rope_append(float *__restrict__ qkv,
     }
 }
 
-// One query row of one head: grid (heads, M). Query row i sits at position
-// past + i and sees keys 0 .. past + i of its KV head (h / group). The four
-// waves take the 64-key chunks in turn (nc_attend.h gives the order), leave
-// their partials in LDS, and wave 0 combines them: the same bits as the
-// decode kernel's split over workgroups.
-template <int D>
-__global__ __launch_bounds__(kThreads) void attention_rows(float *__restrict__ ctx, const float *__restrict__ qkv,
-                                                           const float *__restrict__ kcache,
-                                                           const float *__restrict__ vcache, int heads,
-                                                           int kv_heads, int past, int capacity, float scale,
-                                                           const int64_t *__restrict__ pos_ptr,
-                                                           int32_t *__restrict__ error) {
-    if (pos_ptr && !position_fits(pos_ptr, (int)gridDim.y, capacity, error, past)) return;
-    extern __shared__ __align__(16) float lds[];  // [4 waves][chunk stage], then [J][D + 2]: m_j, l_j, o_j[D]
-    float *stage = lds + (threadIdx.x >> 6) * nc::chunk_stage_floats<D>();
-    float *part = lds + (kThreads / 64) * nc::chunk_stage_floats<D>();
-    __shared__ __align__(16) float q[D];
-    const int h = blockIdx.x, i = blockIdx.y;
-    const int g = h / (heads / kv_heads);
-    const int width = (heads + 2 * kv_heads) * D;
-    const int T = past + i + 1, J = (T + nc::kChunk - 1) / nc::kChunk;
-    if (threadIdx.x < D) q[threadIdx.x] = qkv[(size_t)i * width + h * D + threadIdx.x];
-    __syncthreads();
+// -- attention over a chunked context --------------------------------------------
+//
+// Two kernels a call. The first takes a grid of (64-key chunk, KV head[, block
+// of query rows]): each workgroup stages its chunk's keys and values in LDS
+// once and attends every query of the block to it, one wave per query row,
+// for every query head of the KV group (h / group), writing each query's
+// chunk result (m_j, l_j, o_j) to a workspace. The second combines a query's
+// chunk results in order of j. The order is nc_attend.h's, shared by the
+// prefill and the decode kernels and the host oracle, so a prompt's rows and a
+// decode step at the same position agree bit for bit. Splitting at a kernel
+// boundary (rather than combining inside one workgroup per head) puts one
+// workgroup on every chunk: at 384 keys a decode step uses 12 workgroups that
+// each read 32 KB instead of 14 that each read 196 KB.
+//
+// Workspace layout, floats: part[((h * rows + r) * jstride + j) * (D + 2) + e],
+// e = 0 (m_j), 1 (l_j), 2 + d (o_j[d]); jstride = the chunks of the longest
+// context of the call.
+constexpr int kWaves = 8;              // waves of a chunk workgroup
+constexpr int kRowsPerBlock = kWaves;  // prefill: one query row per wave
 
-    const float *K = kcache + (size_t)g * capacity * D;
-    const float *V = vcache + (size_t)g * capacity * D;
+template <typename F>
+__device__ __forceinline__ F *chunk_result(F *part, int h, int rows, int r, int jstride, int j, int D) {
+    return part + (((size_t)h * rows + r) * jstride + j) * (D + 2);
+}
+
+// Prefill: grid (chunks, kv_heads, ceil(rows / 8)) over the slab of query rows
+// i0 .. i0 + rows - 1 of a call of M rows; row i sits at position past + i and
+// sees keys 0 .. past + i (the cache already holds them, nc_rope_append).
+template <int D>
+__global__ __launch_bounds__(64 * kWaves) void attention_rows_chunks(
+    float *__restrict__ part, const float *__restrict__ qkv, const float *__restrict__ kcache,
+    const float *__restrict__ vcache, int heads, int kv_heads, int past, int capacity, float scale, int i0, int rows,
+    int M, int jstride, const int64_t *__restrict__ pos_ptr, int32_t *__restrict__ error) {
+    if (pos_ptr && !position_fits(pos_ptr, M, capacity, error, past)) return;
+    const int j = blockIdx.x, g = blockIdx.y, t0 = j * nc::kChunk;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int j = wave; j < J; j += kThreads / 64) {
-        const int t0 = j * nc::kChunk;
-        nc::Chunk<D, false> chunk(K, V, t0, min(nc::kChunk, T - t0), -1, capacity - 1);
-        const nc::ChunkResult r = chunk.attend(q, nullptr, nullptr, scale, stage);
-        float *pj = part + j * (D + 2);
-        if (lane == 0) {
-            pj[0] = r.m;
-            pj[1] = r.l;
+    const int r_last = min((int)blockIdx.z * kRowsPerBlock + kRowsPerBlock, rows) - 1;
+    if (past + i0 + r_last + 1 <= t0) return;             // no row of the block sees this chunk
+    __shared__ __align__(16) float lds[nc::Staged<D>::kFloats];
+    __shared__ __align__(16) float qs[kWaves][kWaves][D];   // per wave: up to 8 query heads of its row
+    __shared__ __align__(16) float pbuf[kWaves][nc::kChunk];
+    const nc::Staged<D> st(lds);
+    const int group = heads / kv_heads, width = (heads + 2 * kv_heads) * D;
+    nc::ChunkLoad<D, 64 * kWaves> load;
+    load.issue(kcache + (size_t)g * capacity * D, vcache + (size_t)g * capacity * D, t0, capacity - 1);
+    const int r = blockIdx.z * kRowsPerBlock + wave, i = i0 + r;
+    const bool valid = r < rows && past + i + 1 > t0;
+    const float *qrow = qkv + (size_t)(valid ? i : 0) * width + (size_t)g * group * D;
+    float qv[kWaves];
+#pragma unroll
+    for (int u = 0; u < kWaves; ++u) qv[u] = (valid && u < group && lane < D) ? qrow[u * D + lane] : 0.0f;
+    load.store(st, -1, past + M - t0);                    // keys past + M and on: not yet in the cache
+#pragma unroll
+    for (int u = 0; u < kWaves; ++u)
+        if (u < group && lane < D) qs[wave][u][lane] = qv[u];
+    __syncthreads();
+    if (!valid) return;
+    const int n = min(nc::kChunk, past + i + 1 - t0);
+    for (int hh = 0; hh < group; ++hh) {
+        if (hh >= kWaves && hh % kWaves == 0) {             // groups of more than 8 heads, 8 at a time (wave-local)
+#pragma unroll
+            for (int u = 0; u < kWaves; ++u) qv[u] = (hh + u < group && lane < D) ? qrow[(hh + u) * D + lane] : 0.0f;
+#pragma unroll
+            for (int u = 0; u < kWaves; ++u)
+                if (lane < D) qs[wave][u][lane] = qv[u];
         }
-        if (lane < D) pj[2 + lane] = r.o;
+        const nc::ChunkResult res = nc::attend_staged<D>(qs[wave][hh % kWaves], st, n, scale, pbuf[wave]);
+        nc::keep_result<D>(chunk_result(part, g * group + hh, rows, r, jstride, j, D), res);
+    }
+}
+
+// The combine of one query's chunk results: grid (heads, rows), one wave.
+// Row r of the slab is query row i0 + r at position past + i0 + r. The first
+// 512 floats of the row's results (every chunk up to 7 chunks at D = 64) are
+// loaded before the position is read.
+template <int D>
+__global__ __launch_bounds__(64) void attention_combine(float *__restrict__ ctx, const float *__restrict__ part,
+                                                        int heads, int past, int capacity, int i0, int rows, int M,
+                                                        int jstride, const int64_t *__restrict__ pos_ptr) {
+    extern __shared__ __align__(16) float results[];     // [J][D + 2]
+    constexpr int kBatch = 8;                            // independent loads a lane keeps in flight
+    const int h = blockIdx.x, r = blockIdx.y, lane = threadIdx.x;
+    const float *src = chunk_result(part, h, rows, r, jstride, 0, D);
+    const int all = jstride * (D + 2);
+    float v[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+        const int at = lane + 64 * u;
+        v[u] = at < all ? src[at] : 0.0f;
+    }
+    if (pos_ptr) {
+        const int64_t p = *pos_ptr;
+        if (p < 0 || p + M > capacity) return;            // the chunk kernel reported it
+        past = (int)p;
+    }
+    const int J = (past + i0 + r + 1 + nc::kChunk - 1) / nc::kChunk;
+    const int total = J * (D + 2);
+    for (int base = 0; base < total; base += 64 * kBatch) {
+        if (base > 0) {
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const int at = base + lane + 64 * u;
+                v[u] = at < total ? src[at] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int at = base + lane + 64 * u;
+            if (at < total) results[at] = v[u];
+        }
+    }
+    // (a wave's LDS writes complete before its own later reads: no barrier)
+    const float out = nc::combine_chunks(J, lane < D ? lane : 0,
+                                         [&](int c, int k) { return results[c * (D + 2) + k]; });
+    if (lane < D) ctx[(size_t)(i0 + r) * heads * D + h * D + lane] = out;
+}
+
+// Decode: one new token at position past. Grid (chunks, kv_heads). Wave w
+// attends query head g * group + w (then + 8, ... for larger groups), each
+// wave rotating its own head's query; wave 0 of the chunk holding the new key
+// rotates it, puts it and the new value in the staged chunk, and appends both
+// to the cache (no workgroup loads that row: the others' chunks end before
+// it). cos and sin of f32(past) * inv_freq[i] come from the cache's table
+// (nc_rope_table) when given, else are computed here, the same nc_cosf /
+// nc_sinf either way. The loads that do not depend on the position (the
+// first kEarlyChunks chunks' keys and values, the q, k, v rows) go out before
+// the position is read, so the two memory round trips overlap.
+constexpr int kEarlyChunks = 16;
+
+template <int D, bool TABLE>
+__global__ __launch_bounds__(64 * kWaves) void attention_decode_chunks(
+    float *__restrict__ part, const float *__restrict__ qkv, float *__restrict__ kcache, float *__restrict__ vcache,
+    const float *__restrict__ inv_freq, const float *__restrict__ table, int heads, int kv_heads, int past,
+    int capacity, float scale, int jstride, const int64_t *__restrict__ pos_ptr, int32_t *__restrict__ error) {
+    const int j = blockIdx.x, g = blockIdx.y, t0 = j * nc::kChunk;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int group = heads / kv_heads;
+    constexpr int half = D / 2;
+    float *K = kcache + (size_t)g * capacity * D;
+    float *V = vcache + (size_t)g * capacity * D;
+    nc::ChunkLoad<D, 64 * kWaves> load;
+    const bool early = j < kEarlyChunks;
+    if (early) load.issue(K, V, t0, capacity - 1);
+
+    // RoPE operands: lane i < half of wave w, pair i of its head's query;
+    // lanes half .. D - 1 of wave 0, pair lane - half of the new key.
+    const int pi = lane < half ? lane : lane - half;
+    const bool holds = lane < D && (lane < half ? wave < group : wave == 0);
+    float x0 = 0.0f, x1 = 0.0f;
+    if (holds) {
+        const float *x = qkv + (size_t)(lane < half ? g * group + wave : heads + g) * D;
+        x0 = x[pi];
+        x1 = x[pi + half];
+    }
+    const float vnew = (wave == 0 && lane < D) ? qkv[(size_t)(heads + kv_heads + g) * D + lane] : 0.0f;
+
+    if (pos_ptr && !position_fits(pos_ptr, 1, capacity, error, past)) return;
+    const int T = past + 1, J = (T + nc::kChunk - 1) / nc::kChunk;
+    if (j >= J) return;
+    if (!early) load.issue(K, V, t0, capacity - 1);
+    __shared__ __align__(16) float lds[nc::Staged<D>::kFloats];
+    __shared__ __align__(16) float qs[kWaves][D];
+    __shared__ __align__(16) float pbuf[kWaves][nc::kChunk];
+    const nc::Staged<D> st(lds);
+    const int n = min(nc::kChunk, T - t0);
+    const bool fresh = j == J - 1;                       // the new key is row past - t0 of this chunk
+    const bool rotates = holds && (lane < half || fresh);
+    float c = 0.0f, s = 0.0f;
+    if (holds) {
+        if constexpr (TABLE) {
+            c = table[(size_t)past * half + pi];
+            s = table[((size_t)capacity + past) * half + pi];
+        } else {
+            const float ang = __fmul_rn((float)past, inv_freq[pi]);
+            c = nc_cosf(ang);
+            s = nc_sinf(ang);
+        }
+    }
+    load.store(st, fresh ? past - t0 : -1, n);
+    if (rotates) {
+        float y0, y1;
+        rope_pair(x0, x1, c, s, y0, y1);
+        float *y = lane < half ? qs[wave] : st.keys + (past - t0) * nc::Staged<D>::kKeyStride;
+        y[pi] = y0;
+        y[pi + half] = y1;
+        if (lane >= half) {
+            K[(size_t)past * D + pi] = y0;
+            K[(size_t)past * D + pi + half] = y1;
+        }
+    }
+    if (fresh && wave == 0 && lane < D) {
+        st.values[(past - t0) * D + lane] = vnew;
+        V[(size_t)past * D + lane] = vnew;
     }
     __syncthreads();
-    if (wave == 0) {
-        const float out = nc::combine_chunks(J, lane < D ? lane : 0,
-                                             [&](int c, int k) { return part[c * (D + 2) + k]; });
-        if (lane < D) ctx[(size_t)i * heads * D + h * D + lane] = out;
+    for (int hh = wave; hh < group; hh += kWaves) {
+        if (hh != wave && lane < half) {                  // groups of more than 8 heads (wave-local)
+            const float *x = qkv + (size_t)(g * group + hh) * D;
+            float y0, y1;
+            rope_pair(x[pi], x[pi + half], c, s, y0, y1);
+            qs[wave][pi] = y0;
+            qs[wave][pi + half] = y1;
+        }
+        const nc::ChunkResult res = nc::attend_staged<D>(qs[wave], st, n, scale, pbuf[wave]);
+        nc::keep_result<D>(chunk_result(part, g * group + hh, 1, 0, jstride, j, D), res);
     }
 }
 
@@ -237,48 +401,111 @@ NC_EXPORT int32_t nc_rope_append(void **p, const int64_t *s) {
 
 namespace {
 
+// LDS of a combine: J chunk results of D + 2 floats, 67.6 KB at 16384 keys and
+// D = 64, past the 64 KB a launch gets without asking.
 template <int D>
-int32_t launch_rows(void **p, int64_t M, int64_t heads, int64_t kv, int64_t past, int64_t cap, float scale,
-                    const int64_t *pos) {
-    // the waves' chunk stages (70 KB) and the partials of every chunk (up to
-    // 256 chunks x 66 floats = 67.6 KB at 16384 keys): past the 64 KB a
-    // launch gets without asking
+int32_t launch_combine(float *ctx, const float *part, int64_t heads, int64_t past, int64_t cap, int64_t i0,
+                       int64_t rows, int64_t M, int64_t jstride, const int64_t *pos) {
     static bool raised = false;
     if (!raised) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&attention_rows<D>),
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&attention_combine<D>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024) != hipSuccess) {
-            nc::set_message("nc_attention: could not raise the LDS limit");
+            nc::set_message("attention: could not raise the LDS limit of the combine");
             return NC_LAUNCH_FAILED;
         }
         raised = true;
     }
-    const int64_t keys = pos ? cap : past + M;
-    const size_t lds = ((size_t)(kThreads / 64) * nc::chunk_stage_floats<D>() +
-                        (size_t)((keys + nc::kChunk - 1) / nc::kChunk) * (D + 2)) * sizeof(float);
-    hipLaunchKernelGGL(attention_rows<D>, dim3((unsigned)heads, (unsigned)M), dim3(kThreads), lds, nc::stream(),
-                       (float *)p[0], (const float *)p[1], (const float *)p[2], (const float *)p[3], (int)heads,
-                       (int)kv, pos ? 0 : (int)past, (int)cap, scale, pos, nc::error_word());
-    return nc::launched("attention_rows");
+    const size_t lds = (size_t)jstride * (D + 2) * sizeof(float);
+    hipLaunchKernelGGL(attention_combine<D>, dim3((unsigned)heads, (unsigned)rows), dim3(64), lds, nc::stream(), ctx,
+                       part, (int)heads, (int)past, (int)cap, (int)i0, (int)rows, (int)M, (int)jstride, pos);
+    return nc::launched("attention_combine");
+}
+
+// Query rows in slabs whose chunk results fit the workspace; each slab is a
+// chunk launch and a combine launch.
+template <int D>
+int32_t launch_prefill(void **p, int64_t M, int64_t heads, int64_t kv, int64_t past, int64_t cap, float scale,
+                       const int64_t *pos, float *work, int64_t work_bytes) {
+    const int64_t jstride = ((pos ? cap : past + M) + nc::kChunk - 1) / nc::kChunk;
+    const int64_t row_bytes = heads * jstride * (D + 2) * (int64_t)sizeof(float);
+    int64_t slab = std::min<int64_t>(M, work_bytes / row_bytes);
+    NC_REQUIRE(slab >= 1, "nc_attention: the workspace is smaller than one query row's chunk results "
+                          "(heads * ceil(keys / 64) * (head_dim + 2) floats)");
+    if (slab < M && slab >= kRowsPerBlock) slab -= slab % kRowsPerBlock;
+    const int64_t host_past = pos ? 0 : past;
+    for (int64_t i0 = 0; i0 < M; i0 += slab) {
+        const int64_t rows = std::min(slab, M - i0);
+        const int64_t chunks = pos ? jstride : (past + i0 + rows + nc::kChunk - 1) / nc::kChunk;
+        hipLaunchKernelGGL(attention_rows_chunks<D>,
+                           dim3((unsigned)chunks, (unsigned)kv, (unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock)),
+                           dim3(64 * kWaves), 0, nc::stream(), work, (const float *)p[1], (const float *)p[2],
+                           (const float *)p[3], (int)heads, (int)kv, (int)host_past, (int)cap, scale, (int)i0,
+                           (int)rows, (int)M, (int)jstride, pos, nc::error_word());
+        int32_t rc = nc::launched("attention_rows_chunks");
+        if (rc == NC_OK) rc = launch_combine<D>((float *)p[0], work, heads, host_past, cap, i0, rows, M, jstride, pos);
+        if (rc != NC_OK) return rc;
+    }
+    return NC_OK;
+}
+
+template <int D, bool TABLE>
+int32_t launch_decode(void **p, const int64_t *s, const int64_t *pos, float *work, int64_t work_bytes) {
+    const int64_t heads = s[0], kv = s[1], past = s[3], cap = s[4];
+    const int64_t jstride = ((pos ? cap : past + 1) + nc::kChunk - 1) / nc::kChunk;
+    NC_REQUIRE(heads * jstride * (D + 2) * (int64_t)sizeof(float) <= work_bytes,
+               "nc_attention_decode: the workspace is smaller than heads * ceil(keys / 64) * (head_dim + 2) floats");
+    const int64_t host_past = pos ? 0 : past;
+    hipLaunchKernelGGL((attention_decode_chunks<D, TABLE>), dim3((unsigned)jstride, (unsigned)kv), dim3(64 * kWaves), 0,
+                       nc::stream(), work, (const float *)p[1], (float *)p[2], (float *)p[3], (const float *)p[4],
+                       (const float *)p[6], (int)heads, (int)kv, (int)host_past, (int)cap, bits_to_float(s[5]),
+                       (int)jstride, pos, nc::error_word());
+    const int32_t rc = nc::launched("attention_decode_chunks");
+    if (rc != NC_OK) return rc;
+    return launch_combine<D>((float *)p[0], work, heads, host_past, cap, 0, 1, 1, jstride, pos);
 }
 
 }  // namespace
 
-// p: [ctx f32[M, heads*D], qkv f32[M, (H + 2*KV*D)] (q rotated), kcache, vcache, pos i64[1] | NULL];
-// s: [M, heads, kv_heads, D, past, capacity, scale as float32 bits]  (D 16, 32 or 64)
-// With pos, past is read from the device when the kernel runs (s[4] is ignored).
+// p: [ctx f32[M, heads*D], qkv f32[M, (H + 2*KV*D)] (q rotated), kcache, vcache, pos i64[1] | NULL,
+//     work f32[...]];
+// s: [M, heads, kv_heads, D, past, capacity, scale as float32 bits, work bytes]  (D 16, 32 or 64)
+// With pos, past is read from the device when the kernels run (s[4] is ignored). The workspace
+// holds the chunk results; one query row needs heads * ceil(keys / 64) * (D + 2) floats, keys =
+// past + M (capacity with pos), and a smaller workspace than M rows' takes the rows in slabs.
 NC_EXPORT int32_t nc_attention(void **p, const int64_t *s) {
-    NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3], "nc_attention: null operand");
-    const int64_t M = s[0], heads = s[1], kv = s[2], D = s[3], past = s[4], cap = s[5];
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3] && p[5], "nc_attention: null operand");
+    const int64_t M = s[0], heads = s[1], kv = s[2], D = s[3], past = s[4], cap = s[5], work_bytes = s[7];
     const int64_t *pos = (const int64_t *)p[4];
     NC_REQUIRE(M >= 0 && heads > 0 && kv > 0 && heads % kv == 0 && (D == 16 || D == 32 || D == 64) &&
                    (pos ? cap <= kMaxKeys : (past >= 0 && past + M <= cap && past + M <= kMaxKeys)) &&
-                   M <= cap && M < 65536 && heads < 65536,
+                   M <= cap && M < 65536 && heads < 65536 && work_bytes >= 0,
                "nc_attention: bad shape (head_dim 16, 32 or 64; at most 16384 keys)");
     if (M == 0) return NC_OK;
     const float scale = bits_to_float(s[6]);
-    if (D == 64) return launch_rows<64>(p, M, heads, kv, past, cap, scale, pos);
-    if (D == 32) return launch_rows<32>(p, M, heads, kv, past, cap, scale, pos);
-    return launch_rows<16>(p, M, heads, kv, past, cap, scale, pos);
+    float *work = (float *)p[5];
+    if (D == 64) return launch_prefill<64>(p, M, heads, kv, past, cap, scale, pos, work, work_bytes);
+    if (D == 32) return launch_prefill<32>(p, M, heads, kv, past, cap, scale, pos, work, work_bytes);
+    return launch_prefill<16>(p, M, heads, kv, past, cap, scale, pos, work, work_bytes);
+}
+
+// Attention of one new token with RoPE and the cache append fused in.
+// p: [ctx f32[heads*D], qkv f32[(heads+2*kv)*D] (unrotated, with bias), kcache f32[kv,C,D],
+//     vcache f32[kv,C,D], inv_freq f32[D/2], pos i64[1] | NULL, rope table f32[2,C,D/2] | NULL,
+//     work f32[heads * ceil(keys / 64) * (D + 2)]];
+// s: [heads, kv, D, past, C, scale as float32 bits, work bytes]  (D 16, 32 or 64, C <= 16384; past
+//    read from pos when given, and then keys = C, else past + 1)
+NC_EXPORT int32_t nc_attention_decode(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3] && p[4] && p[7], "nc_attention_decode: null operand");
+    const int64_t heads = s[0], kv = s[1], D = s[2], past = s[3], cap = s[4];
+    const int64_t *pos = (const int64_t *)p[5];
+    NC_REQUIRE(heads > 0 && kv > 0 && heads % kv == 0 && heads < 65536 && (D == 64 || D == 32 || D == 16) &&
+                   cap > 0 && cap <= kMaxKeys && (pos || (past >= 0 && past + 1 <= cap)),
+               "nc_attention_decode: bad shape (head_dim 16, 32 or 64, capacity at most 16384)");
+    float *work = (float *)p[7];
+    const bool table = p[6] != nullptr;
+    if (D == 64) return table ? launch_decode<64, true>(p, s, pos, work, s[6]) : launch_decode<64, false>(p, s, pos, work, s[6]);
+    if (D == 32) return table ? launch_decode<32, true>(p, s, pos, work, s[6]) : launch_decode<32, false>(p, s, pos, work, s[6]);
+    return table ? launch_decode<16, true>(p, s, pos, work, s[6]) : launch_decode<16, false>(p, s, pos, work, s[6]);
 }
 
 

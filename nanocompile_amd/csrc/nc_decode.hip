@@ -1,5 +1,6 @@
-// Decode-step kernels (one new token): each projection with its activation
-// prologue fused in, and attention with RoPE and the cache append fused in.
+// Decode-step projections (one new token), each with its activation prologue
+// fused in. (Attention with RoPE and the cache append fused in is
+// nc_attention_decode, nc_attention.hip.)
 //
 // A decode step is latency-bound: each projection streams 0.1-4.4 MB, a few
 // microseconds at HBM speed, so every separate small kernel (an rms_norm, a
@@ -19,7 +20,6 @@
 // fused step computes the same bits as the unfused one, and the host oracle
 // covers both.
 #include "nc_common.h"
-#include "nc_attend.h"
 #include "nc_epilogue.h"
 
 namespace {
@@ -160,106 +160,6 @@ __global__ __launch_bounds__(64 * W) void gemv_decode(float *__restrict__ out, c
     }
 }
 
-// -- attention for one new token, RoPE and the cache append fused in ---------------
-//
-// One workgroup per query head, kWaves wavefronts: wave w attends the head to
-// the 64-key chunks w, w + kWaves, ... (nc_attend.h gives the order), leaves
-// each chunk's partial result in LDS, and wave 0 combines them. Up to
-// 64 * kWaves keys every chunk is in flight at once; the chunk loads go out
-// before RoPE, which overlaps their latency. The same order as
-// nc_attention's prefill kernel, so a decode step and a prefill agree bit for
-// bit. (Splitting a head over several workgroups instead costs device-scope
-// fences or a second launch to combine, more than the keys take to read at
-// these lengths.)
-constexpr int kWaves = 4;
-
-template <int D, bool TABLE>
-__global__ __launch_bounds__(64 * kWaves) void attention_decode(
-    float *__restrict__ ctx, const float *__restrict__ qkv, float *__restrict__ kcache, float *__restrict__ vcache,
-    const float *__restrict__ inv_freq, int heads, int kv_heads, int past, int capacity, float scale,
-    const int64_t *__restrict__ pos_ptr, int32_t *__restrict__ error, const float *__restrict__ table) {
-    if (pos_ptr) {
-        const int64_t p = *pos_ptr;
-        if (p < 0 || p + 1 > capacity) {
-            if (blockIdx.x == 0 && threadIdx.x == 0) atomicCAS(error, 0, NC_FAIL_CAPACITY);
-            return;
-        }
-        past = (int)p;
-    }
-    extern __shared__ __align__(16) float lds[];  // [kWaves][chunk stage], then [J][D + 2]: m_j, l_j, o_j[D]
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    float *stage = lds + wave * nc::chunk_stage_floats<D>();
-    float *part = lds + kWaves * nc::chunk_stage_floats<D>();
-    __shared__ __align__(16) float rotated[kWaves][3 * D];     // per wave: q, the new key, the new value
-    float *q = rotated[wave], *knew = q + D, *vnew = q + 2 * D;
-    constexpr int half = D / 2;
-    const int h = blockIdx.x, group = heads / kv_heads, g = h / group;
-    const int T = past + 1, J = (T + nc::kChunk - 1) / nc::kChunk;
-    float *K = kcache + (size_t)g * capacity * D;
-    float *V = vcache + (size_t)g * capacity * D;
-
-    // every wave's first chunk (clamped to the last for waves past J) loads now
-    const int j0 = min(wave, J - 1), t0 = j0 * nc::kChunk;
-    nc::Chunk<D, true> chunk(K, V, t0, min(nc::kChunk, T - t0), past, capacity - 1);
-
-    // Each wave rotates its own copy of q (lanes 0 .. half - 1) and of the new
-    // key (lanes half .. D - 1), so no workgroup barrier separates the loads
-    // above from their use: cos and sin of f32(past) * inv_freq[i] from the
-    // cache's table (nc_rope_table) when given, else computed here, the same
-    // nc_cosf / nc_sinf either way. A wave's LDS writes complete before its
-    // own later reads.
-    if (lane < D) {
-        const float *qrow = qkv + h * D;
-        const float *krow = qkv + heads * D + g * D;
-        const float *vrow = qkv + (heads + kv_heads) * D + g * D;
-        const int i = lane < half ? lane : lane - half;
-        const float *x = lane < half ? qrow : krow;
-        float *y = lane < half ? q : knew;
-        float c, s;
-        if constexpr (TABLE) {
-            c = table[(size_t)past * half + i];
-            s = table[((size_t)capacity + past) * half + i];
-        } else {
-            const float ang = __fmul_rn((float)past, inv_freq[i]);
-            c = nc_cosf(ang);
-            s = nc_sinf(ang);
-        }
-        const float x0 = x[i], x1 = x[i + half];
-        y[i] = __fadd_rn(__fmul_rn(x0, c), __fmul_rn(-x1, s));
-        y[i + half] = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(x0, s));
-        vnew[lane] = vrow[lane];
-    }
-    auto keep = [&](int j, const nc::ChunkResult &r) {
-        float *pj = part + j * (D + 2);
-        if (lane == 0) {
-            pj[0] = r.m;
-            pj[1] = r.l;
-        }
-        if (lane < D) pj[2 + lane] = r.o;
-    };
-    if (wave < J) keep(wave, chunk.attend(q, knew, vnew, scale, stage));
-    for (int j = wave + kWaves; j < J; j += kWaves) {      // contexts past 64 * kWaves keys
-        const int tj = j * nc::kChunk;
-        nc::Chunk<D, true> more(K, V, tj, min(nc::kChunk, T - tj), past, capacity - 1);
-        keep(j, more.attend(q, knew, vnew, scale, stage));
-    }
-    // The cache row of the new key, written after the chunks are read: no
-    // workgroup reads it (the chunk holding it takes knew / vnew), and a
-    // store through the cache pointer before the reads would make the
-    // compiler keep the chunk's registers in scratch (a generic pointer may
-    // alias them).
-    if (wave == 0 && h % group == 0 && lane < D) {
-        K[(size_t)past * D + lane] = knew[lane];
-        V[(size_t)past * D + lane] = vnew[lane];
-    }
-    __syncthreads();
-    if (wave == 0) {
-        const float out = nc::combine_chunks(J, lane < D ? lane : 0,
-                                             [&](int c, int k) { return part[c * (D + 2) + k]; });
-        if (lane < D) ctx[h * D + lane] = out;
-    }
-}
-
 float bits_to_float(int64_t bits) {
     union { uint32_t u; float f; } c;
     c.u = (uint32_t)bits;
@@ -308,45 +208,3 @@ NC_EXPORT int32_t nc_decode_projection(void **p, const int64_t *s) {
     nc::set_message("nc_decode_projection: no fused kernel for this width and kind");
     return NC_BAD_ARGS;
 }
-
-namespace {
-
-template <int D, bool TABLE>
-int32_t launch_attention_decode(void **p, const int64_t *s, const int64_t *pos) {
-    static bool raised = false;          // chunk stages (70 KB) + partials of 256 chunks (67.6 KB)
-    if (!raised) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&attention_decode<D, TABLE>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024) != hipSuccess) {
-            nc::set_message("nc_attention_decode: could not raise the LDS limit");
-            return NC_LAUNCH_FAILED;
-        }
-        raised = true;
-    }
-    const int64_t cap = s[4];
-    const size_t lds = ((size_t)kWaves * nc::chunk_stage_floats<D>() +
-                        (size_t)((cap + nc::kChunk - 1) / nc::kChunk) * (D + 2)) * sizeof(float);
-    hipLaunchKernelGGL((attention_decode<D, TABLE>), dim3((unsigned)s[0]), dim3(64 * kWaves), lds, nc::stream(),
-                       (float *)p[0], (const float *)p[1], (float *)p[2], (float *)p[3], (const float *)p[4],
-                       (int)s[0], (int)s[1], pos ? 0 : (int)s[3], (int)cap, bits_to_float(s[5]), pos,
-                       nc::error_word(), (const float *)p[6]);
-    return nc::launched("attention_decode");
-}
-
-}  // namespace
-
-// Attention of one new token with RoPE and the cache append fused in.
-// p: [ctx f32[heads*D], qkv f32[(heads+2*kv)*D] (unrotated, with bias), kcache f32[kv,C,D],
-//     vcache f32[kv,C,D], inv_freq f32[D/2], pos i64[1] | NULL, rope table f32[2,C,D/2] | NULL];
-// s: [heads, kv, D, past, C, scale as float32 bits]  (D 64 or 32, C <= 16384; past read from pos when given)
-NC_EXPORT int32_t nc_attention_decode(void **p, const int64_t *s) {
-    NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3] && p[4], "nc_attention_decode: null operand");
-    const int64_t heads = s[0], kv = s[1], D = s[2], past = s[3], cap = s[4];
-    const int64_t *pos = (const int64_t *)p[5];
-    NC_REQUIRE(heads > 0 && kv > 0 && heads % kv == 0 && heads < 65536 && (D == 64 || D == 32) && cap > 0 &&
-                   cap <= 16384 && (pos || (past >= 0 && past + 1 <= cap)),
-               "nc_attention_decode: bad shape (head_dim 64 or 32, capacity at most 16384)");
-    if (p[6]) return D == 64 ? launch_attention_decode<64, true>(p, s, pos) : launch_attention_decode<32, true>(p, s, pos);
-    return D == 64 ? launch_attention_decode<64, false>(p, s, pos) : launch_attention_decode<32, false>(p, s, pos);
-}
-
-

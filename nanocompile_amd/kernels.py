@@ -37,6 +37,12 @@ def float_bits(value: float) -> int:
     return int(np.array(value, dtype=np.float32).view(np.uint32))
 
 
+def attention_workspace_bytes(heads: int, head_dim: int, rows: int, keys: int) -> int:
+    """Bytes of the chunk results nc_attention / nc_attention_decode keep for ``rows``
+    query rows over ``keys`` keys: (m, l, o[head_dim]) per head, row and 64-key chunk."""
+    return heads * rows * -(-keys // 64) * (head_dim + 2) * 4
+
+
 def _int8_weight(op: str, q: DeviceArray, scales: DeviceArray, k: int) -> int:
     """Check ``q: i8[N, K]`` and ``scales: f32[N]`` against width ``k``; return N (ir.py:381-389)."""
     if q.dtype != I8 or len(q.shape) != 2:

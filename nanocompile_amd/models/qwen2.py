@@ -39,7 +39,7 @@ import numpy as np
 
 from nanocompile_amd import hip
 from nanocompile_amd.hip import DeviceArray
-from nanocompile_amd.kernels import float_bits, pack_chains, pack_chains_vnni
+from nanocompile_amd.kernels import attention_workspace_bytes, float_bits, pack_chains, pack_chains_vnni
 from nanocompile_amd.models.config import Qwen2Config
 
 QUANTIZATIONS = ("int8-token", "int8", "int8-vnni")
@@ -52,6 +52,9 @@ def _packed_bytes(quantization: str, n: int, k: int) -> int:
     if quantization == "int8":
         return n * -(-(k // 32) // 4) * 128
     return n * (k // 128) * 128
+
+
+WORKSPACE_BYTES = 64 << 20     # attention chunk results held at once (longer prompts go in slabs)
 
 
 def inverse_frequencies(head_dim: int, theta: float) -> np.ndarray:
@@ -102,6 +105,11 @@ class KVCache:
         self.rope = DeviceArray((2, capacity, D // 2), np.float32)
         inv = DeviceArray.from_host(inverse_frequencies(D, config.rope_theta))
         hip.call("nc_rope_table", [self.rope, inv], [capacity, D])
+        # attention's chunk results (nc_attention, nc_attention_decode): every
+        # query row of a prompt up to 64 MiB, longer prompts in slabs
+        per_row = attention_workspace_bytes(config.num_attention_heads, D, 1, capacity)
+        self.work_bytes = per_row * max(1, min(capacity, WORKSPACE_BYTES // per_row))
+        self.work = DeviceArray((self.work_bytes // 4,), np.float32)
         hip.sync()
 
     def layer(self, index: int) -> tuple[int, int]:
@@ -246,13 +254,13 @@ class Qwen2:
         eps = float_bits(c.rms_norm_eps)
         if m == 1 and self.fused_decode:
             # five kernels a layer: each projection computes its own activation
-            # prologue, attention does RoPE and the cache append (nc_decode.hip)
+            # prologue (nc_decode.hip), attention does RoPE and the cache append
             for i, w in enumerate(self.layers):
                 kc, vc = cache.layer(i)
                 q, s = w["qkv"]
                 hip.call("nc_decode_projection", [self.qkv, self.x, w["g1"], q, s, w["qkv_b"]], [W, H, 0, eps])
-                hip.call("nc_attention_decode", [self.ctx, self.qkv, kc, vc, self.inv_freq, pos, cache.rope],
-                         [heads, kv, D, past, cache.capacity, float_bits(self.scale)])
+                hip.call("nc_attention_decode", [self.ctx, self.qkv, kc, vc, self.inv_freq, pos, cache.rope, cache.work],
+                         [heads, kv, D, past, cache.capacity, float_bits(self.scale), cache.work_bytes])
                 q, s = w["o"]
                 hip.call("nc_decode_projection", [self.x, self.ctx, None, q, s], [H, Q, 1, eps])
                 (qg, sg), (qu, su) = w["gate"], w["up"]
@@ -271,8 +279,8 @@ class Qwen2:
             hip.call("nc_matmul_i8_token", [self.qkv, self.xq, self.xs, q, s, w["qkv_b"], None], [m, W, H, s_qkv])
             hip.call("nc_rope_append", [self.qkv, kc, vc, self.inv_freq, pos],
                      [m, heads, kv, D, past, cache.capacity])
-            hip.call("nc_attention", [self.ctx, self.qkv, kc, vc, pos],
-                     [m, heads, kv, D, past, cache.capacity, float_bits(self.scale)])
+            hip.call("nc_attention", [self.ctx, self.qkv, kc, vc, pos, cache.work],
+                     [m, heads, kv, D, past, cache.capacity, float_bits(self.scale), cache.work_bytes])
             hip.call("nc_quantize_token_i8", [self.xq, self.xs, self.ctx], [m, Q])
             q, s = w["o"]
             hip.call("nc_matmul_i8_token", [self.x, self.xq, self.xs, q, s, None, self.x], [m, H, Q, s_o])
@@ -298,8 +306,8 @@ class Qwen2:
             self._project(w["qkv"], self.normed, self.qkv, m, W, H, bias=w["qkv_b"])
             hip.call("nc_rope_append", [self.qkv, kc, vc, self.inv_freq, pos],
                      [m, heads, kv, D, past, cache.capacity])
-            hip.call("nc_attention", [self.ctx, self.qkv, kc, vc, pos],
-                     [m, heads, kv, D, past, cache.capacity, float_bits(self.scale)])
+            hip.call("nc_attention", [self.ctx, self.qkv, kc, vc, pos, cache.work],
+                     [m, heads, kv, D, past, cache.capacity, float_bits(self.scale), cache.work_bytes])
             self._project(w["o"], self.ctx, self.x, m, H, Q, residual=self.x)
             hip.call("nc_rms_norm_quant", [self.normed, self.xq, self.xs, self.x, w["g2"]], [m, H, eps])
             self._project(w["gate"], self.normed, self.gate, m, I, H)

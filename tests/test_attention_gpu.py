@@ -1,8 +1,10 @@
 """Attention on the GPU, bit for bit against the host oracle's chunked order.
 
-The decode kernel gives each head one workgroup whose waves take the 64-key
-chunks and combine them in LDS; these tests cover both sides of every chunk
-edge, contexts longer than one pass of the waves, both head widths, the
+Both kernels stage each 64-key chunk in LDS once per KV head (and, in a
+prompt, per block of 8 query rows), attend every query head of the group to
+it, and combine the chunk results in a second launch; these tests cover both
+sides of every chunk edge, long contexts, every head width, groups of more
+than 8 query heads, prompts taken in slabs when the workspace is small, the
 position read from the device, back-to-back calls, and a captured graph
 replayed at advancing positions.
 """
@@ -18,6 +20,13 @@ from tests.conftest import bits
 pytestmark = pytest.mark.gpu
 
 
+def workspace(heads, d, rows, keys):
+    from nanocompile_amd.hip import DeviceArray
+    from nanocompile_amd.kernels import attention_workspace_bytes
+    n = attention_workspace_bytes(heads, d, rows, keys)
+    return DeviceArray((n // 4,), np.float32), n
+
+
 def setup(rng, heads, kv, d, cap, m=1):
     width = (heads + 2 * kv) * d
     qkv = rng.standard_normal((m, width)).astype(np.float32)
@@ -26,7 +35,7 @@ def setup(rng, heads, kv, d, cap, m=1):
     return qkv, kc, vc
 
 
-@pytest.mark.parametrize("d,heads,kv", [(64, 14, 2), (32, 4, 2)])
+@pytest.mark.parametrize("d,heads,kv", [(64, 14, 2), (32, 4, 2), (16, 4, 1), (64, 18, 2)])
 @pytest.mark.parametrize("past", [0, 1, 63, 64, 65, 127, 128, 200, 511, 512, 1000, 3000])
 def test_decode_attention_is_the_oracle(gpu, host, d, heads, kv, past):
     from nanocompile_amd import hip
@@ -44,21 +53,25 @@ def test_decode_attention_is_the_oracle(gpu, host, d, heads, kv, past):
     dq, dk, dv = DeviceArray.from_host(qkv), DeviceArray.from_host(kc), DeviceArray.from_host(vc)
     dinv, ctx = DeviceArray.from_host(inv), DeviceArray((1, heads * d), np.float32)
     pos = DeviceArray.from_host(np.array([past], np.int64))
+    work, nbytes = workspace(heads, d, 1, cap)
     for use_pos in (False, True, True):
-        hip.call("nc_attention_decode", [ctx, dq, dk, dv, dinv, pos if use_pos else None],
-                 [heads, kv, d, 0 if use_pos else past, cap, float_bits(scale)])
+        hip.call("nc_attention_decode", [ctx, dq, dk, dv, dinv, pos if use_pos else None, None, work],
+                 [heads, kv, d, 0 if use_pos else past, cap, float_bits(scale), nbytes])
         assert np.array_equal(bits(ctx.numpy()), bits(expected)), use_pos
     assert np.array_equal(bits(dk.numpy()), bits(hk)) and np.array_equal(bits(dv.numpy()), bits(hv))
 
 
-@pytest.mark.parametrize("d", [64, 32])
-def test_prefill_and_decode_attention_agree(gpu, host, d):
-    """A prompt's last row through nc_attention equals a decode step at the same position."""
+@pytest.mark.parametrize("d,heads,kv", [(64, 4, 2), (32, 4, 2), (16, 2, 2), (64, 18, 2)])
+@pytest.mark.parametrize("slab", [None, 8, 13, 1])
+def test_prefill_and_decode_attention_agree(gpu, host, d, heads, kv, slab):
+    """A prompt through nc_attention is the oracle, in one pass or in slabs of rows when the
+    workspace is smaller; its last row equals a decode step at the same position."""
     from nanocompile_amd import hip
     from nanocompile_amd.hip import DeviceArray
     from nanocompile_amd.kernels import float_bits
-    rng = np.random.default_rng(d)
-    heads, kv, m, past = 4, 2, 130, 70
+    print(f"attention prefill d={d} heads={heads} slab={slab}", flush=True)
+    rng = np.random.default_rng(d + heads)
+    m, past = 130, 70
     cap = past + m
     qkv, kc, vc = setup(rng, heads, kv, d, cap, m)
     inv = inverse_frequencies(d, 1e6)
@@ -68,15 +81,17 @@ def test_prefill_and_decode_attention_agree(gpu, host, d):
     dq, dk, dv = DeviceArray.from_host(qkv), DeviceArray.from_host(kc), DeviceArray.from_host(vc)
     dinv, ctx = DeviceArray.from_host(inv), DeviceArray((m, heads * d), np.float32)
     hip.call("nc_rope_append", [dq, dk, dv, dinv], [m, heads, kv, d, past, cap])
-    hip.call("nc_attention", [ctx, dq, dk, dv], [m, heads, kv, d, past, cap, float_bits(scale)])
+    work, nbytes = workspace(heads, d, slab or m, past + m)
+    hip.call("nc_attention", [ctx, dq, dk, dv, None, work], [m, heads, kv, d, past, cap, float_bits(scale), nbytes])
     prefill = ctx.numpy()
     assert np.array_equal(bits(prefill), bits(expected))
     # the last row again (unrotated) as a decode step at its position, over the
     # cache the prefill filled (the step rewrites its own key with the same bits)
     dq2 = DeviceArray.from_host(qkv[-1:])
     one = DeviceArray((1, heads * d), np.float32)
-    hip.call("nc_attention_decode", [one, dq2, dk, dv, dinv, None],
-             [heads, kv, d, past + m - 1, cap, float_bits(scale)])
+    work, nbytes = workspace(heads, d, 1, cap)
+    hip.call("nc_attention_decode", [one, dq2, dk, dv, dinv, None, None, work],
+             [heads, kv, d, past + m - 1, cap, float_bits(scale), nbytes])
     assert np.array_equal(bits(one.numpy()[0]), bits(prefill[-1]))
     assert np.array_equal(bits(dk.numpy()), bits(hk))
 
@@ -93,8 +108,9 @@ def test_decode_attention_in_a_graph_at_advancing_positions(gpu, host):
     dq, dk, dv = DeviceArray.from_host(qkv), DeviceArray.from_host(kc), DeviceArray.from_host(vc)
     dinv, ctx = DeviceArray.from_host(inv), DeviceArray((1, heads * d), np.float32)
     pos = DeviceArray.from_host(np.array([0], np.int64))
-    graph = Graph.capture(lambda: hip.call("nc_attention_decode", [ctx, dq, dk, dv, dinv, pos],
-                                           [heads, kv, d, 0, cap, float_bits(scale)]))
+    work, nbytes = workspace(heads, d, 1, cap)
+    graph = Graph.capture(lambda: hip.call("nc_attention_decode", [ctx, dq, dk, dv, dinv, pos, None, work],
+                                           [heads, kv, d, 0, cap, float_bits(scale), nbytes]))
     hk, hv = kc.copy(), vc.copy()
     for past in (10, 63, 64, 150, 299):
         print(f"graph replay at past={past}", flush=True)
@@ -110,11 +126,17 @@ def test_decode_attention_rejects_bad_shapes(gpu):
     from nanocompile_amd.hip import DeviceArray
     x = DeviceArray((4096,), np.float32)
     with pytest.raises(hip.KernelError, match="bad shape"):
-        hip.call("nc_attention_decode", [x, x, x, x, x], [4, 2, 48, 3, 8, 0])      # head_dim 48
+        hip.call("nc_attention_decode", [x, x, x, x, x, None, None, x], [4, 2, 48, 3, 8, 0, 1 << 14])   # head_dim 48
     with pytest.raises(hip.KernelError, match="bad shape"):
-        hip.call("nc_attention_decode", [x, x, x, x, x], [4, 2, 64, 8, 8, 0])      # past + 1 > capacity
+        hip.call("nc_attention_decode", [x, x, x, x, x, None, None, x], [4, 2, 64, 8, 8, 0, 1 << 14])   # past + 1 > capacity
     with pytest.raises(hip.KernelError, match="null operand"):
-        hip.call("nc_attention_decode", [x, x, None, x, x], [4, 2, 64, 3, 8, 0])
+        hip.call("nc_attention_decode", [x, x, None, x, x, None, None, x], [4, 2, 64, 3, 8, 0, 1 << 14])
+    with pytest.raises(hip.KernelError, match="null operand"):
+        hip.call("nc_attention_decode", [x, x, x, x, x, None, None, None], [4, 2, 64, 3, 8, 0, 1 << 14])
+    with pytest.raises(hip.KernelError, match="workspace"):        # 4 heads x 1 chunk x 66 floats
+        hip.call("nc_attention_decode", [x, x, x, x, x, None, None, x], [4, 2, 64, 3, 8, 0, 4 * 66 * 4 - 4])
+    with pytest.raises(hip.KernelError, match="workspace"):
+        hip.call("nc_attention", [x, x, x, x, None, x], [2, 4, 2, 64, 3, 8, 0, 4 * 66 * 4 - 4])
 
 
 @pytest.mark.parametrize("d", [64, 32])
@@ -147,8 +169,11 @@ def test_decode_attention_with_the_rope_table(gpu, host, past):
     dinv = DeviceArray.from_host(inv)
     table = DeviceArray((2, cap, d // 2), np.float32)
     hip.call("nc_rope_table", [table, dinv], [cap, d])
+    work, nbytes = workspace(heads, d, 1, cap)
     for tab in (table, None):
         dq, dk, dv = DeviceArray.from_host(qkv), DeviceArray.from_host(kc), DeviceArray.from_host(vc)
         ctx = DeviceArray((1, heads * d), np.float32)
-        hip.call("nc_attention_decode", [ctx, dq, dk, dv, dinv, None, tab], [heads, kv, d, past, cap, float_bits(scale)])
+        hip.call("nc_attention_decode", [ctx, dq, dk, dv, dinv, None, tab, work],
+                 [heads, kv, d, past, cap, float_bits(scale), nbytes])
         assert np.array_equal(bits(ctx.numpy()), bits(expected)), tab is None
+

@@ -92,7 +92,10 @@ def test_rope_append_and_attention(gpu, host, m, past):
     dq, dk, dv = DeviceArray.from_host(qkv), DeviceArray.from_host(kc), DeviceArray.from_host(vc)
     ctx = DeviceArray((m, heads * d), np.float32)
     hip.call("nc_rope_append", [dq, dk, dv, DeviceArray.from_host(inv)], [m, heads, kv, d, past, cap])
-    hip.call("nc_attention", [ctx, dq, dk, dv], [m, heads, kv, d, past, cap, float_bits(scale)])
+    from nanocompile_amd.kernels import attention_workspace_bytes
+    nbytes = attention_workspace_bytes(heads, d, m, past + m)
+    work = DeviceArray((nbytes // 4,), np.float32)
+    hip.call("nc_attention", [ctx, dq, dk, dv, None, work], [m, heads, kv, d, past, cap, float_bits(scale), nbytes])
     hip.sync()
     hq, hk, hv = qkv.copy(), kc.copy(), vc.copy()
     expected = host.rope_append_attention(hq, hk, hv, inv, heads, kv, d, past, scale)
