@@ -120,9 +120,8 @@ __device__ __forceinline__ ChunkResult attend_staged(const float *q, const Stage
         acc = __fadd_rn(acc, __fmul_rn(qi.w, k.w));
     }
     const float s = lane < n ? __fadd_rn(__fmul_rn(acc, scale), 0.0f) : -__builtin_inff();
-    float m = s;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = nan_max(m, __shfl_xor(m, off, 64));
+    // (scores are never -0, so nan_max commutes up to which NaN propagates)
+    float m = butterfly<64>(s, [](float a, float b) { return nan_max(a, b); });
     m = lane_value(m, 0);
     const float p = nc_expf(__fsub_rn(s, m));        // exp(-inf) = 0 for lanes past the chunk
     const float l = wave_sum_f32(p);

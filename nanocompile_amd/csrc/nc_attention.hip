@@ -47,8 +47,7 @@ __device__ float row_sum(float v, float *scratch) {
 }
 
 __device__ float row_max(float v, float *scratch) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = nan_max(v, __shfl_xor(v, off, 64));
+    v = nc::butterfly<64>(v, [](float a, float b) { return nan_max(a, b); });
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     __syncthreads();
     if (lane == 0) scratch[wave] = v;

@@ -56,27 +56,76 @@ __device__ __forceinline__ i8x16 load16_stream(const int8_t *p) {
     return v;
 }
 
+// Lane exchanges without an LDS round trip (__shfl_xor compiles to
+// ds_bpermute, ~100 cycles of latency a step). For a commutative f, one
+// gfx950 lane swap gives every lane f(v[i], v[i ^ 32]) (v_permlane32_swap)
+// or f(v[i], v[i ^ 16]) (v_permlane16_swap): swapping v with itself leaves
+// v[i] in one result and v[i ^ off] in the other, in an order that differs
+// between the two halves, which commutativity makes immaterial. The partners
+// i ^ 8, 4, 2, 1 come from DPP within rows of 16 lanes: row_ror:8 is xor 8;
+// xor 4 takes row_ror:4 into the banks of lanes with bit 2 set (source
+// lane - 4) and row_ror:12 into the others (source lane + 4); xor 2 and xor 1
+// are quad permutations.
+template <int CTRL, int BANKS>
+__device__ __forceinline__ int32_t dpp_mov(int32_t old, int32_t v) {
+    return __builtin_amdgcn_update_dpp(old, v, CTRL, 0xF, BANKS, false);
+}
+
+template <int OFF>
+__device__ __forceinline__ int32_t xor_partner(int32_t v) {
+    static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8, "DPP partners within a row of 16");
+    if constexpr (OFF == 1) return dpp_mov<0xB1, 0xF>(v, v);          // quad_perm [1, 0, 3, 2]
+    else if constexpr (OFF == 2) return dpp_mov<0x4E, 0xF>(v, v);     // quad_perm [2, 3, 0, 1]
+    else if constexpr (OFF == 4) return dpp_mov<0x12C, 0x5>(dpp_mov<0x124, 0xA>(v, v), v);
+    else return dpp_mov<0x128, 0xF>(v, v);                            // row_ror:8
+}
+
+template <int OFF>
+__device__ __forceinline__ float xor_partner(float v) {
+    return __int_as_float(xor_partner<OFF>(__float_as_int(v)));
+}
+
+// f(v[i], v[i ^ OFF]) in every lane, OFF a power of two <= 32, f commutative.
+template <int OFF, typename T, typename F>
+__device__ __forceinline__ T butterfly_step(T v, F f) {
+    if constexpr (OFF >= 16) {
+        const uint32_t u = __builtin_bit_cast(uint32_t, v);
+        const auto r = OFF == 32 ? __builtin_amdgcn_permlane32_swap(u, u, false, false)
+                                 : __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        return f(__builtin_bit_cast(T, (uint32_t)r[0]), __builtin_bit_cast(T, (uint32_t)r[1]));
+    } else {
+        return f(v, xor_partner<OFF>(v));
+    }
+}
+
+// The xor butterfly over aligned groups of G lanes (G a power of two <= 64):
+// steps G / 2, ..., 2, 1, each lane combining with lane i ^ step.
+template <int G, typename T, typename F>
+__device__ __forceinline__ T butterfly(T v, F f) {
+    if constexpr (G >= 64) v = butterfly_step<32>(v, f);
+    if constexpr (G >= 32) v = butterfly_step<16>(v, f);
+    if constexpr (G >= 16) v = butterfly_step<8>(v, f);
+    if constexpr (G >= 8) v = butterfly_step<4>(v, f);
+    if constexpr (G >= 4) v = butterfly_step<2>(v, f);
+    if constexpr (G >= 2) v = butterfly_step<1>(v, f);
+    return v;
+}
+
 // Sum over the L lanes of an aligned group (L a power of two <= 64). Integer
 // addition is exact, so the order is immaterial.
 template <int L>
 __device__ __forceinline__ int32_t group_sum_i32(int32_t v) {
-#pragma unroll
-    for (int off = L / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+    return butterfly<L>(v, [](int32_t a, int32_t b) { return a + b; });
 }
 
 // Sum over a whole wavefront, the butterfly (v[i] + v[i ^ off]) for
 // off = 32, 16, 8, 4, 2, 1. Addition commutes, so all lanes agree bitwise.
 __device__ __forceinline__ float wave_sum_f32(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = v + __shfl_xor(v, off, 64);
-    return v;
+    return butterfly<64>(v, [](float a, float b) { return __fadd_rn(a, b); });
 }
 
 __device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
+    return butterfly<64>(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
 // Correctly rounded float32 square root. Not __fsqrt_rn: without
