@@ -54,6 +54,9 @@ PROMPT, NEW_TOKENS = 128, 256
 CALIBRATION_BYTES = 256 * 2**20
 
 
+LM_HEAD_KERNEL = "lm_head_ring<4, 896, 24>"     # nc_lm_head at the model's width (nc_model.hip)
+
+
 def gemv_bytes(m: int, n: int, k: int) -> int:
     return n * k + 4 * n + m * k + 4 * m + 4 * m * n
 
@@ -446,9 +449,9 @@ def main() -> int:
                    "decode_ms_total": round(d["decode_ms"], 3), "gemv": gemv_record,
                    "blocks": d.get("blocks")},
         "roofline": {"bound": "hbm", "achieved": round(d["lm_head_gbps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(d["lm_head_gbps"] / HBM_PEAK_GBPS, 4), "traffic": measured_traffic("lm_head<4>"),
+                     "frac": round(d["lm_head_gbps"] / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(LM_HEAD_KERNEL),
                      "traffic_source": "profiles/traffic.json (rocprofv3 PMC, calibrated)",
-                     "kernel": "lm_head<4> (fp32 tied LM head, 60% of a decode step's bytes)",
+                     "kernel": f"{LM_HEAD_KERNEL} (fp32 tied LM head, 60% of a decode step's bytes)",
                      "bytes_per_launch": d["lm_bytes"], "launch_us": round(d["lm_head_us"], 3),
                      "step_bytes": d["step_bytes_mid"],
                      "step_gbps": round(d["step_bytes_mid"] * d["tok_s"] / 1e9, 1)},

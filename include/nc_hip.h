@@ -277,8 +277,11 @@ int32_t nc_argmax_index(void **p, const int64_t *s);
  * on the host): token = argmax of the step just run; tokens[pos + 1] = token;
  * ids[0] = token; pos += 1; the argmax key cleared. A captured decode step
  * ends with it, so steps chain with no host round trip. Records
- * NC_FAIL_CAPACITY when pos + 1 reaches the capacity.
- * p: [ids i64[1], tokens i64[capacity], best u64[1], pos i64[1]];  s: [capacity]
+ * NC_FAIL_CAPACITY when pos + 1 reaches the capacity. With x, the token's
+ * embedding row is gathered into x as well (nc_embed's gather and Fail code 1),
+ * so the next step needs no separate embedding launch.
+ * p: [ids i64[1], tokens i64[capacity], best u64[1], pos i64[1], x f32[H] or NULL,
+ *     table f32[V,H] or NULL];  s: [capacity, H, V] (H, V read only with x)
  * nc_rope_append and nc_attention take pos as an optional p[4], read on the
  * device in place of s[4] (past). */
 int32_t nc_decode_advance(void **p, const int64_t *s);

@@ -111,6 +111,72 @@ __global__ __launch_bounds__(64 * WAVES) void lm_head(float *__restrict__ logits
     }
 }
 
+// The same head for a width known at compile time, its loads kept in flight
+// continuously: a ring of R 1-KB loads per wave, each refilled as soon as it is
+// consumed (the loop is unrolled whole, so the compiler's waits count only the
+// loads issued since), the first R issued before the x prologue. A loop that
+// issues a batch of loads and then consumes it lets the batch drain to zero
+// at every iteration, half its loads in flight on average.
+template <int WAVES, int H, int R>
+__global__ __launch_bounds__(64 * WAVES) void lm_head_ring(float *__restrict__ logits,
+                                                           unsigned long long *__restrict__ best,
+                                                           const float *__restrict__ x,
+                                                           const float4 *__restrict__ packed, int64_t V,
+                                                           const float *__restrict__ gamma, float eps) {
+    static_assert(H % 4 == 0 && R <= H / 4, "ring of at most H / 4 loads");
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    constexpr int K4 = H / 4;
+    __shared__ __align__(16) float sxh[H];
+    __shared__ float scratch[4];
+    const int m = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t blk = (int64_t)blockIdx.x * WAVES + wave;
+    const bool live = blk * 64 < V;
+    const f32x4 *e = reinterpret_cast<const f32x4 *>(packed) + (live ? blk : 0) * K4 * 64 + lane;
+    f32x4 ring[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) ring[i] = __builtin_nontemporal_load(e + (size_t)i * 64);
+
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < H; i += 64 * WAVES) {
+        const float v = x[(size_t)m * H + i];
+        sxh[i] = v;
+        ss = __fadd_rn(ss, __fmul_rn(v, v));
+    }
+    __syncthreads();
+    if (gamma) {
+        static_assert(WAVES == 4, "the row-sum order needs 256 threads");
+        const float total = sum4(ss, scratch);
+        const float rcp = nc::div_rn(1.0f, nc::sqrt_rn(__fadd_rn(nc::div_rn(total, (float)H), eps)));
+        for (int i = threadIdx.x; i < H; i += 64 * WAVES) sxh[i] = __fmul_rn(__fmul_rn(sxh[i], rcp), gamma[i]);
+        __syncthreads();
+    }
+    if (!live) return;
+    float acc = 0.0f;
+#pragma unroll
+    for (int k4 = 0; k4 < K4; ++k4) {
+        const f32x4 w = ring[k4 % R];
+        if (k4 + R < K4) ring[k4 % R] = __builtin_nontemporal_load(e + (size_t)(k4 + R) * 64);
+        const float4 xv = *reinterpret_cast<const float4 *>(sxh + 4 * k4);
+        acc = __fadd_rn(acc, __fmul_rn(xv.x, w.x));
+        acc = __fadd_rn(acc, __fmul_rn(xv.y, w.y));
+        acc = __fadd_rn(acc, __fmul_rn(xv.z, w.z));
+        acc = __fadd_rn(acc, __fmul_rn(xv.w, w.w));
+    }
+    const int64_t n = blk * 64 + lane;
+    const bool valid = n < V;
+    if (logits && valid) logits[(size_t)m * V + n] = acc;
+    if (best) {
+        unsigned long long key = valid ? argmax_key(acc, n) : 0ull;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const unsigned long long other = __shfl_xor(key, off, 64);
+            key = other > key ? other : key;
+        }
+        if (lane == 0) atomicMax(best + m, key);
+    }
+}
+
 float bits_to_float(int64_t bits) {
     union { uint32_t u; float f; } c;
     c.u = (uint32_t)bits;
@@ -162,6 +228,13 @@ NC_EXPORT int32_t nc_lm_head(void **p, const int64_t *s) {
     if (s[0] == 0) return NC_OK;
     constexpr int W = 4;
     const int64_t blocks = (s[1] + 63) / 64;
+    const dim3 grid((unsigned)((blocks + W - 1) / W), (unsigned)s[0]);
+    if (s[2] == 896) {       // the model's width: the ring kernel, 24 loads (24 KB) in flight per wave
+        hipLaunchKernelGGL((lm_head_ring<W, 896, 24>), grid, dim3(64 * W), 0, nc::stream(), (float *)p[0],
+                           (unsigned long long *)p[1], (const float *)p[2], (const float4 *)p[3], s[1],
+                           (const float *)p[4], bits_to_float(s[3]));
+        return nc::launched("lm_head_ring");
+    }
     hipLaunchKernelGGL((lm_head<W>), dim3((unsigned)((blocks + W - 1) / W), (unsigned)s[0]), dim3(64 * W),
                        (size_t)s[2] * sizeof(float), nc::stream(), (float *)p[0], (unsigned long long *)p[1],
                        (const float *)p[2], (const float4 *)p[3], s[1], (int)s[2], (const float *)p[4],
@@ -190,17 +263,28 @@ NC_EXPORT int32_t nc_argmax_index(void **p, const int64_t *s) {
 namespace {
 // One greedy step's bookkeeping on the device: the argmax of the step just run
 // becomes the next input token and is appended to the history at position
-// pos + 1; pos advances; the argmax key is cleared for the next step.
-__global__ void decode_advance(int64_t *__restrict__ ids, int64_t *__restrict__ tokens,
-                               unsigned long long *__restrict__ best, int64_t *__restrict__ pos, int64_t capacity,
-                               int32_t *__restrict__ error) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+// pos + 1; pos advances; the argmax key is cleared for the next step. With x,
+// the token's embedding row is gathered into x too (the next step's input, as
+// nc_embed would: an id outside 0..V-1 records Fail code 1 and leaves x zero).
+__global__ __launch_bounds__(256) void decode_advance(int64_t *__restrict__ ids, int64_t *__restrict__ tokens,
+                                                      unsigned long long *__restrict__ best,
+                                                      int64_t *__restrict__ pos, int64_t capacity,
+                                                      float *__restrict__ x, const float *__restrict__ table, int H,
+                                                      int64_t V, int32_t *__restrict__ error) {
     const int64_t p = *pos;
     const int64_t token = (int64_t)(0xFFFFFFFFu - (uint32_t)(best[0] & 0xFFFFFFFFull));
     if (p < -1 || p + 1 >= capacity) {
-        atomicCAS(error, 0, NC_FAIL_CAPACITY);
+        if (threadIdx.x == 0) atomicCAS(error, 0, NC_FAIL_CAPACITY);
         return;
     }
+    if (x) {
+        const bool bad = token < 0 || token >= V;
+        if (bad && threadIdx.x == 0) atomicCAS(error, 0, NC_FAIL_INDEX);
+        const float *row = table + (bad ? 0 : token) * (int64_t)H;
+        for (int k = threadIdx.x; k < H; k += 256) x[k] = bad ? 0.0f : row[k];
+    }
+    __syncthreads();                              // every thread has read best before it is cleared
+    if (threadIdx.x != 0) return;
     tokens[p + 1] = token;
     ids[0] = token;
     *pos = p + 1;
@@ -211,10 +295,13 @@ __global__ void decode_advance(int64_t *__restrict__ ids, int64_t *__restrict__ 
 // The greedy loop's step on the device (models/qwen2.py:362-367 does it on
 // the host: argmax, append, feed back), so a captured decode step needs no
 // host round trip.
-// p: [ids i64[1], tokens i64[capacity], best u64[1], pos i64[1]];  s: [capacity]
+// p: [ids i64[1], tokens i64[capacity], best u64[1], pos i64[1], x f32[H] | NULL, table f32[V,H] | NULL];
+// s: [capacity, H, V] (H and V read only with x)
 NC_EXPORT int32_t nc_decode_advance(void **p, const int64_t *s) {
     NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3] && s[0] > 0, "nc_decode_advance: bad operand");
-    hipLaunchKernelGGL(decode_advance, dim3(1), dim3(64), 0, nc::stream(), (int64_t *)p[0], (int64_t *)p[1],
-                       (unsigned long long *)p[2], (int64_t *)p[3], s[0], nc::error_word());
+    NC_REQUIRE(!p[4] || (p[5] && s[1] > 0 && s[1] < (1 << 24) && s[2] > 0), "nc_decode_advance: x needs the table");
+    hipLaunchKernelGGL(decode_advance, dim3(1), dim3(256), 0, nc::stream(), (int64_t *)p[0], (int64_t *)p[1],
+                       (unsigned long long *)p[2], (int64_t *)p[3], s[0], (float *)p[4], (const float *)p[5],
+                       p[4] ? (int)s[1] : 0, p[4] ? s[2] : 0, nc::error_word());
     return nc::launched("decode_advance");
 }

@@ -428,13 +428,14 @@ class Qwen2:
         hip.call("nc_argmax_clear", [self.best], [1])
         self._head_argmax(self.x.ptr + (m - 1) * H * 4)
         pos.upload(np.array([m - 1], np.int64))
-        hip.call("nc_decode_advance", [one_id, tokens, self.best, pos], [capacity])
+        # the advance also gathers the next token's embedding row into x
+        advance = ("nc_decode_advance", [one_id, tokens, self.best, pos, self.x, self.embed], [capacity, H, V])
+        hip.call(*advance)
 
         def step() -> None:
-            hip.call("nc_embed", [self.x, self.embed, one_id], [1, H, V])
             self._layers(1, 0, cache, pos=pos)
             self._head_argmax(self.x.ptr)
-            hip.call("nc_decode_advance", [one_id, tokens, self.best, pos], [capacity])
+            hip.call(*advance)
 
         if not self.fused_decode:
             self._projection_schedules(1)          # any tuning happens now, not under capture

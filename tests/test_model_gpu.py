@@ -245,3 +245,27 @@ def test_device_greedy_loop_is_greedy(tiny):
         assert model.generate(prompt, 20) == expected
         assert greedy(model, prompt, 20) == expected
     assert model.generate([9], 1) == oracle_model.greedy([9], 1)
+
+
+def test_decode_advance_gathers_the_next_row(gpu):
+    """nc_decode_advance with x: the argmax's token appended, pos advanced, the key cleared, and
+    the token's embedding row in x; an argmax key that names no row is Fail code 1 and x zero."""
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import DeviceArray, KernelError
+    rng = np.random.default_rng(3)
+    V, H, cap = 50, 40, 8
+    table = rng.standard_normal((V, H)).astype(np.float32)
+    dt, x = DeviceArray.from_host(table), DeviceArray((H,), np.float32)
+    ids, tokens = DeviceArray((1,), np.int64), DeviceArray.from_host(np.zeros(cap, np.int64))
+    pos = DeviceArray.from_host(np.array([2], np.int64))
+    token = 17
+    best = DeviceArray.from_host(np.array([(123 << 32) | (0xFFFFFFFF - token)], np.uint64))
+    hip.call("nc_decode_advance", [ids, tokens, best, pos, x, dt], [cap, H, V])
+    hip.sync()
+    assert tokens.numpy()[3] == token and ids.numpy()[0] == token and pos.numpy()[0] == 3
+    assert best.numpy()[0] == 0 and np.array_equal(x.numpy(), table[token])
+    best.upload(np.array([0], np.uint64))          # no argmax: the key names id 2^32 - 1
+    hip.call("nc_decode_advance", [ids, tokens, best, pos, x, dt], [cap, H, V])
+    with pytest.raises(KernelError, match="out of range"):
+        hip.sync()
+    assert not x.numpy().any()
