@@ -262,9 +262,14 @@ int32_t nc_pack_rows64(void **p, const int64_t *s);
 
 /* logits = x @ table.T with each row summed in k order, multiply then add
  * (the reference's float32 matmul kernel, lower.py:255-269), and best[m] the
- * 64-bit argmax key of row m (first index of the maximum).
- * p: [logits f32[M,V] or NULL, best u64[M] or NULL, x f32[M,H], packed table];
- * s: [M, V, H] */
+ * 64-bit argmax key of row m (first index of the maximum). With gamma, x is
+ * rms-normed first (eps = s[3] as float32 bits). With bias, + bias[n] after the
+ * sum, and with residual, residual + that: the reference's float32 linear
+ * (nn.py:24-31) and residual add, so the same kernel is the float32 model's
+ * projections.
+ * p: [logits f32[M,V] or NULL, best u64[M] or NULL, x f32[M,H], packed table,
+ *     gamma f32[H] or NULL, bias f32[V] or NULL, residual f32[M,V] or NULL];
+ * s: [M, V, H, eps bits] */
 int32_t nc_lm_head(void **p, const int64_t *s);
 
 /* p: [best u64[n]];  s: [n]  (zeroes the argmax keys before nc_lm_head) */

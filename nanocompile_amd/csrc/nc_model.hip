@@ -60,10 +60,21 @@ __device__ float sum4(float v, float *scratch) {
     return __fadd_rn(__fadd_rn(scratch[0], scratch[1]), __fadd_rn(scratch[2], scratch[3]));
 }
 
+// logits[m, n] = acc, + bias[n] when given, and residual[m, n] + that when
+// given (the reference's linear, nn.py:24-31, and its residual add): with a
+// residual the output is usually the residual itself, updated in place.
+__device__ __forceinline__ float head_epilogue(float acc, int64_t m, int64_t n, int64_t V,
+                                               const float *__restrict__ bias, const float *residual) {
+    if (bias) acc = __fadd_rn(acc, bias[n]);
+    if (residual) acc = __fadd_rn(residual[(size_t)m * V + n], acc);
+    return acc;
+}
+
 template <int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void lm_head(float *__restrict__ logits, unsigned long long *__restrict__ best,
+__global__ __launch_bounds__(64 * WAVES) void lm_head(float *logits, unsigned long long *__restrict__ best,
                                                       const float *__restrict__ x, const float4 *__restrict__ packed,
-                                                      int64_t V, int H, const float *__restrict__ gamma, float eps) {
+                                                      int64_t V, int H, const float *__restrict__ gamma, float eps,
+                                                      const float *__restrict__ bias, const float *residual) {
     extern __shared__ float sxh[];
     __shared__ float scratch[4];
     const int m = blockIdx.y;
@@ -99,7 +110,7 @@ __global__ __launch_bounds__(64 * WAVES) void lm_head(float *__restrict__ logits
         acc = __fadd_rn(acc, __fmul_rn(xv.w, w.w));
     }
     const bool valid = n < V;
-    if (logits && valid) logits[(size_t)m * V + n] = acc;
+    if (logits && valid) logits[(size_t)m * V + n] = head_epilogue(acc, m, n, V, bias, residual);
     if (best) {
         unsigned long long key = valid ? argmax_key(acc, n) : 0ull;
 #pragma unroll
@@ -118,11 +129,11 @@ __global__ __launch_bounds__(64 * WAVES) void lm_head(float *__restrict__ logits
 // issues a batch of loads and then consumes it lets the batch drain to zero
 // at every iteration, half its loads in flight on average.
 template <int WAVES, int H, int R>
-__global__ __launch_bounds__(64 * WAVES) void lm_head_ring(float *__restrict__ logits,
-                                                           unsigned long long *__restrict__ best,
+__global__ __launch_bounds__(64 * WAVES) void lm_head_ring(float *logits, unsigned long long *__restrict__ best,
                                                            const float *__restrict__ x,
                                                            const float4 *__restrict__ packed, int64_t V,
-                                                           const float *__restrict__ gamma, float eps) {
+                                                           const float *__restrict__ gamma, float eps,
+                                                           const float *__restrict__ bias, const float *residual) {
     static_assert(H % 4 == 0 && R <= H / 4, "ring of at most H / 4 loads");
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     constexpr int K4 = H / 4;
@@ -165,7 +176,7 @@ __global__ __launch_bounds__(64 * WAVES) void lm_head_ring(float *__restrict__ l
     }
     const int64_t n = blk * 64 + lane;
     const bool valid = n < V;
-    if (logits && valid) logits[(size_t)m * V + n] = acc;
+    if (logits && valid) logits[(size_t)m * V + n] = head_epilogue(acc, m, n, V, bias, residual);
     if (best) {
         unsigned long long key = valid ? argmax_key(acc, n) : 0ull;
 #pragma unroll
@@ -218,10 +229,16 @@ NC_EXPORT int32_t nc_pack_rows64(void **p, const int64_t *s) {
 // logits[m, n] = sum_k x[m, k] * table[n, k] in k order, and best[m] the
 // argmax key of row m (atomic maximum: clear it first with nc_argmax_clear).
 // With gamma (p[4]), x is rms-normed first with eps = s[3] (as float32 bits).
-// p: [logits f32[M,V] | NULL, best u64[M] | NULL, x f32[M,H], packed table, gamma f32[H] | NULL];
+// With bias (p[5]) the sum is followed by + bias[n]; with residual (p[6]),
+// logits = residual + that (the reference's float32 linear and residual add;
+// the argmax, when asked for, is of the plain sums).
+// p: [logits f32[M,V] | NULL, best u64[M] | NULL, x f32[M,H], packed table, gamma f32[H] | NULL,
+//     bias f32[V] | NULL, residual f32[M,V] | NULL (may be logits itself)];
 // s: [M, V, H, eps bits]
 NC_EXPORT int32_t nc_lm_head(void **p, const int64_t *s) {
     NC_REQUIRE(p && s && p[2] && p[3] && (p[0] || p[1]), "nc_lm_head: null operand");
+    NC_REQUIRE(p[0] || (!p[5] && !p[6]), "nc_lm_head: a bias or residual needs the logits output");
+    const float *bias = (const float *)p[5], *residual = (const float *)p[6];
     NC_REQUIRE(s[0] >= 0 && s[0] < 65536 && s[1] > 0 && s[1] < (1LL << 31) && s[2] > 0 && s[2] % 4 == 0 &&
                    s[2] <= 16384,
                "nc_lm_head: bad shape (H a multiple of 4, at most 16384)");
@@ -232,13 +249,13 @@ NC_EXPORT int32_t nc_lm_head(void **p, const int64_t *s) {
     if (s[2] == 896) {       // the model's width: the ring kernel, 24 loads (24 KB) in flight per wave
         hipLaunchKernelGGL((lm_head_ring<W, 896, 24>), grid, dim3(64 * W), 0, nc::stream(), (float *)p[0],
                            (unsigned long long *)p[1], (const float *)p[2], (const float4 *)p[3], s[1],
-                           (const float *)p[4], bits_to_float(s[3]));
+                           (const float *)p[4], bits_to_float(s[3]), bias, residual);
         return nc::launched("lm_head_ring");
     }
     hipLaunchKernelGGL((lm_head<W>), dim3((unsigned)((blocks + W - 1) / W), (unsigned)s[0]), dim3(64 * W),
                        (size_t)s[2] * sizeof(float), nc::stream(), (float *)p[0], (unsigned long long *)p[1],
                        (const float *)p[2], (const float4 *)p[3], s[1], (int)s[2], (const float *)p[4],
-                       bits_to_float(s[3]));
+                       bits_to_float(s[3]), bias, residual);
     return nc::launched("lm_head");
 }
 

@@ -23,7 +23,10 @@ the north star's mode: per-row int8 weights, per-token int8 activations,
 exact int32 accumulation. ``"int8"`` and ``"int8-vnni"`` are the reference's
 own modes (quantize.py:127-164): float32 activations times int8 weights in
 its 32-chain order, or 32-wide int8 activation blocks in its VNNI order, each
-bit for bit with its generated C (nc_matmul_i8, nc_matmul_i8_vnni).
+bit for bit with its generated C (nc_matmul_i8, nc_matmul_i8_vnni). ``"f32"``
+is the reference's float32 model (``quantization=None``): every projection
+is its float32 matmul kernel's order (k in order, multiply then add, then +
+bias), which is the LM head's kernel over a packed table (nc_lm_head).
 
 Memory: the weights go into one device arena, made once; activations for up
 to ``max_tokens`` new tokens into a second, also made once; the KV cache is a
@@ -42,7 +45,7 @@ from nanocompile_amd.hip import DeviceArray
 from nanocompile_amd.kernels import attention_workspace_bytes, float_bits, pack_chains, pack_chains_vnni
 from nanocompile_amd.models.config import Qwen2Config
 
-QUANTIZATIONS = ("int8-token", "int8", "int8-vnni")
+QUANTIZATIONS = ("int8-token", "int8", "int8-vnni", "f32")
 BLOCK = 32          # matmul_i8_vnni's activation block (quantize.py:44)
 ALIGN = 256
 
@@ -146,10 +149,17 @@ class Qwen2:
             raise ValueError("hidden and intermediate sizes must be multiples of 16")
         vblocks = -(-V // 64) * 64
 
-        per_layer = [((H,), np.float32), ((H,), np.float32), ((W, H), np.int8), ((W,), np.float32),
-                     ((W,), np.float32), ((H, Q), np.int8), ((H,), np.float32), ((I, H), np.int8),
-                     ((I,), np.float32), ((I, H), np.int8), ((I,), np.float32), ((H, I), np.int8), ((H,), np.float32)]
-        if quantization != "int8-token":       # the reference modes' packed copies (pack_chains*)
+        pad = lambda n: -(-n // 64) * 64       # rows of a packed float32 table (nc_pack_rows64)
+        if quantization == "f32":              # the reference's float32 model: packed f32 projections
+            per_layer = [((H,), np.float32), ((H,), np.float32), ((pad(W), H), np.float32), ((W,), np.float32),
+                         ((pad(H), Q), np.float32), ((pad(I), H), np.float32), ((pad(I), H), np.float32),
+                         ((pad(H), I), np.float32)]
+        else:
+            per_layer = [((H,), np.float32), ((H,), np.float32), ((W, H), np.int8), ((W,), np.float32),
+                         ((W,), np.float32), ((H, Q), np.int8), ((H,), np.float32), ((I, H), np.int8),
+                         ((I,), np.float32), ((I, H), np.int8), ((I,), np.float32), ((H, I), np.int8),
+                         ((H,), np.float32)]
+        if quantization in ("int8", "int8-vnni"):   # the reference modes' packed copies (pack_chains*)
             per_layer += [((_packed_bytes(quantization, n, k),), np.int8)
                           for n, k in ((W, H), (H, Q), (I, H), (I, H), (H, I))]
         shapes = per_layer * L + [((V, H), np.float32), ((vblocks, H), np.float32), ((H,), np.float32),
@@ -163,7 +173,22 @@ class Qwen2:
 
         def quantized(names: Sequence[str], rows: int, k: int) -> tuple:
             """Per-row int8 of the named matrices stacked row-wise (quantize.py:55-70, on the device),
-            plus, for the reference's modes, the packed copy their kernels read (made once)."""
+            plus, for the reference's modes, the packed copy their kernels read (made once); in the
+            float32 mode, (None, None, the stacked float32 rows packed as nc_lm_head reads them)."""
+            if quantization == "f32":
+                at = 0
+                for name in names:
+                    w = np.ascontiguousarray(weights[name], np.float32)
+                    if w.shape[1] != k:
+                        raise ValueError(f"{name} has width {w.shape[1]}, expected {k}")
+                    stage.view(w.shape, np.float32, offset_bytes=at * k * 4).upload(w)
+                    at += w.shape[0]
+                if at != rows:
+                    raise ValueError(f"{names} have {at} rows, expected {rows}")
+                packed = self.weights.take((pad(rows), k), np.float32)
+                hip.call("nc_pack_rows64", [packed, stage], [rows, k])
+                hip.sync()
+                return None, None, packed
             q, s = self.weights.take((rows, k), np.int8), self.weights.take((rows,), np.float32)
             at = 0
             for name in names:
@@ -292,9 +317,10 @@ class Qwen2:
             hip.call("nc_matmul_i8_token", [self.x, self.xq, self.xs, q, s, None, self.x], [m, H, I, s_down])
 
     def _layers_reference_modes(self, m: int, past: int, cache: KVCache, pos: DeviceArray | None) -> None:
-        """The layers with the reference's own int8 modes (quantize.py:127-164): float32 activations
-        into matmul_i8 ("int8"), or 32-wide int8 blocks into matmul_i8_vnni ("int8-vnni"), each in the
-        reference's k order; rms_norm, RoPE, attention and the LM head as in "int8-token"."""
+        """The layers with the reference's own modes (quantize.py:127-164): float32 activations
+        into matmul_i8 ("int8"), 32-wide int8 blocks into matmul_i8_vnni ("int8-vnni"), or float32
+        weights ("f32"), each in the reference's k order; rms_norm, RoPE, attention and the LM head
+        as in "int8-token"."""
         c = self.config
         H, I, D = c.hidden_size, c.intermediate_size, c.head_dim
         heads, kv, W = c.num_attention_heads, c.num_key_value_heads, self.width
@@ -317,7 +343,9 @@ class Qwen2:
 
     def _project(self, weight, x, y, m: int, n: int, k: int, bias=None, residual=None) -> None:
         q, s, packed = weight
-        if self.quantization == "int8":
+        if self.quantization == "f32":        # the reference's float32 linear: k in order, then + bias
+            hip.call("nc_lm_head", [y, None, x, packed, None, bias, residual], [m, n, k, 0])
+        elif self.quantization == "int8":
             hip.call("nc_matmul_i8", [y, x, packed, q, s, bias, residual], [m, n, k])
         else:
             hip.call("nc_quantize_blocks", [self.xq, self.xsb, self.xoff, x], [m, k, BLOCK])

@@ -1,13 +1,14 @@
 """The whole tiny Qwen2 on the GPU against the reference's own compiled C (tests/golden G5).
 
 make_golden.py ran the reference's Qwen2 through its C backend
-(models/qwen2.py with CBackend) on a seeded tiny model in its two int8 modes
-and recorded greedy tokens for four prompts, the logits of an 11-token
-prompt, and a decode step's logits. The GPU model in the same mode must give
-the same greedy tokens and logits within 1e-4 of the largest logit: its int8
-projections are the reference's kernels bit for bit (test_modes_gpu.py), and
-only the float reductions around them (rms_norm's sum, the softmax) are
-summed in a tree where the reference sums in index order.
+(models/qwen2.py with CBackend) on a seeded tiny model in its float32 and two
+int8 modes and recorded greedy tokens for four prompts, the logits of an
+11-token prompt, and a decode step's logits. The GPU model in the same mode
+must give the same greedy tokens and logits within 1e-4 of the largest logit:
+its projections are the reference's kernels bit for bit (test_modes_gpu.py;
+the float32 ones are the LM head's k-ordered kernel), and only the float
+reductions around them (rms_norm's sum, the softmax) are summed in a tree
+where the reference sums in index order.
 """
 
 from __future__ import annotations
@@ -22,7 +23,7 @@ import pytest
 pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).resolve().parent / "golden"
 PROMPTS = ([4, 5, 6], [7, 8], [1], [3, 1, 4, 1, 5, 9, 2, 6, 5, 3, 5])     # make_golden.py's G5 prompts
-MODES = [("int8", "int8"), ("int8-vnni", "vnni")]
+MODES = [("int8", "int8"), ("int8-vnni", "vnni"), ("f32", "f32")]
 TOLERANCE = 1e-4          # max |ours - reference| over max |reference|, per logits array
 
 
@@ -78,5 +79,5 @@ def test_logits_are_the_references(model, golden):
 def test_the_modes_differ_from_each_other(model, golden):
     """The fixture holds distinct results per mode, so passing above is not a coincidence of modes."""
     _, tag = model
-    other = "vnni" if tag == "int8" else "int8"
-    assert close(golden[f"g5_{other}_logits"], golden[f"g5_{tag}_logits"]) > 10 * TOLERANCE
+    for other in {"int8", "vnni", "f32"} - {tag}:
+        assert close(golden[f"g5_{other}_logits"], golden[f"g5_{tag}_logits"]) > 10 * TOLERANCE
