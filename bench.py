@@ -331,7 +331,7 @@ def decode(steps: int, warmup: int, cpu: bool, seed: int = 0, graph: bool = True
     evs = [(Event(), Event()) for _ in range(reps)]
     for a, b in evs:
         a.record()
-        hip.call("nc_lm_head", [None, model.best, model.normed, model.head], [1, V, H])
+        hip.call("nc_lm_head", [None, model.best, model.normed, model.head], [1, V, H, 0, 1])
         b.record()
     hip.sync()
     lm_ms = statistics.fmean(a.elapsed_ms(b) for a, b in evs)

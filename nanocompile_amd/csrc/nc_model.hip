@@ -60,6 +60,35 @@ __device__ float sum4(float v, float *scratch) {
     return __fadd_rn(__fadd_rn(scratch[0], scratch[1]), __fadd_rn(scratch[2], scratch[3]));
 }
 
+// Row m's argmax key from this workgroup: the wave maxima, then either one
+// atomic maximum per wave into best[m] (slots == 0), or the workgroup's
+// maximum stored at best[m * slots + blockIdx.x] for the consumer to reduce
+// (slots == gridDim.x: no atomics, whose same-address serialization costs
+// 4-9 us over a head's 594 workgroups, and nothing to clear beforehand).
+// Every thread of the workgroup must call this.
+template <int WAVES>
+__device__ __forceinline__ void publish_argmax(unsigned long long key, unsigned long long *best, int64_t m, int slots,
+                                               unsigned long long *wkeys) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long other = __shfl_xor(key, off, 64);
+        key = other > key ? other : key;
+    }
+    if (slots == 0) {
+        if (lane == 0 && key != 0ull) atomicMax(best + m, key);
+        return;
+    }
+    if (lane == 0) wkeys[wave] = key;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long k = wkeys[0];
+#pragma unroll
+        for (int i = 1; i < WAVES; ++i) k = wkeys[i] > k ? wkeys[i] : k;
+        best[m * slots + blockIdx.x] = k;
+    }
+}
+
 // logits[m, n] = acc, + bias[n] when given, and residual[m, n] + that when
 // given (the reference's linear, nn.py:24-31, and its residual add): with a
 // residual the output is usually the residual itself, updated in place.
@@ -74,9 +103,11 @@ template <int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void lm_head(float *logits, unsigned long long *__restrict__ best,
                                                       const float *__restrict__ x, const float4 *__restrict__ packed,
                                                       int64_t V, int H, const float *__restrict__ gamma, float eps,
-                                                      const float *__restrict__ bias, const float *residual) {
+                                                      const float *__restrict__ bias, const float *residual,
+                                                      int slots) {
     extern __shared__ float sxh[];
     __shared__ float scratch[4];
+    __shared__ unsigned long long wkeys[WAVES];
     const int m = blockIdx.y;
     float ss = 0.0f;
     for (int i = threadIdx.x; i < H; i += 64 * WAVES) {
@@ -95,12 +126,12 @@ __global__ __launch_bounds__(64 * WAVES) void lm_head(float *logits, unsigned lo
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t blk = (int64_t)blockIdx.x * WAVES + wave;
     const int64_t n = blk * 64 + lane;
-    if (blk * 64 >= V) return;
+    const bool live = blk * 64 < V;
     const int k4n = H / 4;
-    const float4 *e = packed + blk * k4n * 64 + lane;
+    const float4 *e = packed + (live ? blk : 0) * k4n * 64 + lane;
     float acc = 0.0f;
 #pragma unroll 16
-    for (int k4 = 0; k4 < k4n; ++k4) {
+    for (int k4 = 0; k4 < (live ? k4n : 0); ++k4) {
         typedef float f32x4 __attribute__((ext_vector_type(4)));
         const f32x4 w = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(e + (size_t)k4 * 64));
         const float4 xv = *reinterpret_cast<const float4 *>(sxh + 4 * k4);
@@ -111,15 +142,7 @@ __global__ __launch_bounds__(64 * WAVES) void lm_head(float *logits, unsigned lo
     }
     const bool valid = n < V;
     if (logits && valid) logits[(size_t)m * V + n] = head_epilogue(acc, m, n, V, bias, residual);
-    if (best) {
-        unsigned long long key = valid ? argmax_key(acc, n) : 0ull;
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const unsigned long long other = __shfl_xor(key, off, 64);
-            key = other > key ? other : key;
-        }
-        if (lane == 0) atomicMax(best + m, key);
-    }
+    if (best) publish_argmax<WAVES>(valid ? argmax_key(acc, n) : 0ull, best, m, slots, wkeys);
 }
 
 // The same head for a width known at compile time, its loads kept in flight
@@ -133,12 +156,14 @@ __global__ __launch_bounds__(64 * WAVES) void lm_head_ring(float *logits, unsign
                                                            const float *__restrict__ x,
                                                            const float4 *__restrict__ packed, int64_t V,
                                                            const float *__restrict__ gamma, float eps,
-                                                           const float *__restrict__ bias, const float *residual) {
+                                                           const float *__restrict__ bias, const float *residual,
+                                                           int slots) {
     static_assert(H % 4 == 0 && R <= H / 4, "ring of at most H / 4 loads");
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     constexpr int K4 = H / 4;
     __shared__ __align__(16) float sxh[H];
     __shared__ float scratch[4];
+    __shared__ unsigned long long wkeys[WAVES];
     const int m = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t blk = (int64_t)blockIdx.x * WAVES + wave;
@@ -162,30 +187,23 @@ __global__ __launch_bounds__(64 * WAVES) void lm_head_ring(float *logits, unsign
         for (int i = threadIdx.x; i < H; i += 64 * WAVES) sxh[i] = __fmul_rn(__fmul_rn(sxh[i], rcp), gamma[i]);
         __syncthreads();
     }
-    if (!live) return;
     float acc = 0.0f;
+    if (live) {           // (a dead wave's ring read block 0: in bounds, unused)
 #pragma unroll
-    for (int k4 = 0; k4 < K4; ++k4) {
-        const f32x4 w = ring[k4 % R];
-        if (k4 + R < K4) ring[k4 % R] = __builtin_nontemporal_load(e + (size_t)(k4 + R) * 64);
-        const float4 xv = *reinterpret_cast<const float4 *>(sxh + 4 * k4);
-        acc = __fadd_rn(acc, __fmul_rn(xv.x, w.x));
-        acc = __fadd_rn(acc, __fmul_rn(xv.y, w.y));
-        acc = __fadd_rn(acc, __fmul_rn(xv.z, w.z));
-        acc = __fadd_rn(acc, __fmul_rn(xv.w, w.w));
+        for (int k4 = 0; k4 < K4; ++k4) {
+            const f32x4 w = ring[k4 % R];
+            if (k4 + R < K4) ring[k4 % R] = __builtin_nontemporal_load(e + (size_t)(k4 + R) * 64);
+            const float4 xv = *reinterpret_cast<const float4 *>(sxh + 4 * k4);
+            acc = __fadd_rn(acc, __fmul_rn(xv.x, w.x));
+            acc = __fadd_rn(acc, __fmul_rn(xv.y, w.y));
+            acc = __fadd_rn(acc, __fmul_rn(xv.z, w.z));
+            acc = __fadd_rn(acc, __fmul_rn(xv.w, w.w));
+        }
     }
     const int64_t n = blk * 64 + lane;
     const bool valid = n < V;
     if (logits && valid) logits[(size_t)m * V + n] = head_epilogue(acc, m, n, V, bias, residual);
-    if (best) {
-        unsigned long long key = valid ? argmax_key(acc, n) : 0ull;
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const unsigned long long other = __shfl_xor(key, off, 64);
-            key = other > key ? other : key;
-        }
-        if (lane == 0) atomicMax(best + m, key);
-    }
+    if (best) publish_argmax<WAVES>(valid ? argmax_key(acc, n) : 0ull, best, m, slots, wkeys);
 }
 
 float bits_to_float(int64_t bits) {
@@ -199,9 +217,49 @@ __global__ void fill_u64(unsigned long long *p, int n) {
     if (i < n) p[i] = 0ull;
 }
 
+__device__ __forceinline__ int64_t key_index(unsigned long long key) {
+    return (int64_t)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
+}
+
+// The maximum of keys[0 .. slots - 1] in every thread of a 256-thread
+// workgroup (each thread's share loaded four at a time, all in flight).
+__device__ unsigned long long reduce_keys(const unsigned long long *__restrict__ keys, int slots,
+                                          unsigned long long *wkeys) {
+    unsigned long long k = 0ull;
+    for (int base = 0; base < slots; base += 4 * 256) {
+        unsigned long long v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = base + threadIdx.x + 256 * u;
+            v[u] = i < slots ? keys[i] : 0ull;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) k = v[u] > k ? v[u] : k;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long other = __shfl_xor(k, off, 64);
+        k = other > k ? other : k;
+    }
+    if ((threadIdx.x & 63) == 0) wkeys[threadIdx.x >> 6] = k;
+    __syncthreads();
+    k = wkeys[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) k = wkeys[i] > k ? wkeys[i] : k;
+    return k;
+}
+
 __global__ void argmax_decode(int64_t *__restrict__ index, const unsigned long long *__restrict__ best, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) index[i] = (int64_t)(0xFFFFFFFFu - (uint32_t)(best[i] & 0xFFFFFFFFull));
+    if (i < n) index[i] = key_index(best[i]);
+}
+
+// Row blockIdx.x's index from its per-workgroup keys.
+__global__ __launch_bounds__(256) void argmax_reduce(int64_t *__restrict__ index,
+                                                     const unsigned long long *__restrict__ best, int slots) {
+    __shared__ unsigned long long wkeys[4];
+    const unsigned long long k = reduce_keys(best + (size_t)blockIdx.x * slots, slots, wkeys);
+    if (threadIdx.x == 0) index[blockIdx.x] = key_index(k);
 }
 
 }  // namespace
@@ -231,10 +289,13 @@ NC_EXPORT int32_t nc_pack_rows64(void **p, const int64_t *s) {
 // With gamma (p[4]), x is rms-normed first with eps = s[3] (as float32 bits).
 // With bias (p[5]) the sum is followed by + bias[n]; with residual (p[6]),
 // logits = residual + that (the reference's float32 linear and residual add;
-// the argmax, when asked for, is of the plain sums).
-// p: [logits f32[M,V] | NULL, best u64[M] | NULL, x f32[M,H], packed table, gamma f32[H] | NULL,
+// the argmax, when asked for, is of the plain sums). With s[4] = 1 the argmax
+// is left as one key per workgroup, best u64[M, G] with G = ceil(ceil(V / 64) / 4),
+// for nc_argmax_index / nc_decode_advance to reduce (no atomics, no clear);
+// with s[4] = 0, best u64[M] gets atomic maxima (clear it first).
+// p: [logits f32[M,V] | NULL, best | NULL, x f32[M,H], packed table, gamma f32[H] | NULL,
 //     bias f32[V] | NULL, residual f32[M,V] | NULL (may be logits itself)];
-// s: [M, V, H, eps bits]
+// s: [M, V, H, eps bits, key per workgroup 0 | 1]
 NC_EXPORT int32_t nc_lm_head(void **p, const int64_t *s) {
     NC_REQUIRE(p && s && p[2] && p[3] && (p[0] || p[1]), "nc_lm_head: null operand");
     NC_REQUIRE(p[0] || (!p[5] && !p[6]), "nc_lm_head: a bias or residual needs the logits output");
@@ -244,18 +305,19 @@ NC_EXPORT int32_t nc_lm_head(void **p, const int64_t *s) {
                "nc_lm_head: bad shape (H a multiple of 4, at most 16384)");
     if (s[0] == 0) return NC_OK;
     constexpr int W = 4;
+    NC_REQUIRE(s[4] == 0 || s[4] == 1, "nc_lm_head: s[4] must be 0 (one key per row) or 1 (a key per workgroup)");
     const int64_t blocks = (s[1] + 63) / 64;
     const dim3 grid((unsigned)((blocks + W - 1) / W), (unsigned)s[0]);
+    const int slots = s[4] ? (int)grid.x : 0;
     if (s[2] == 896) {       // the model's width: the ring kernel, 24 loads (24 KB) in flight per wave
         hipLaunchKernelGGL((lm_head_ring<W, 896, 24>), grid, dim3(64 * W), 0, nc::stream(), (float *)p[0],
                            (unsigned long long *)p[1], (const float *)p[2], (const float4 *)p[3], s[1],
-                           (const float *)p[4], bits_to_float(s[3]), bias, residual);
+                           (const float *)p[4], bits_to_float(s[3]), bias, residual, slots);
         return nc::launched("lm_head_ring");
     }
-    hipLaunchKernelGGL((lm_head<W>), dim3((unsigned)((blocks + W - 1) / W), (unsigned)s[0]), dim3(64 * W),
-                       (size_t)s[2] * sizeof(float), nc::stream(), (float *)p[0], (unsigned long long *)p[1],
-                       (const float *)p[2], (const float4 *)p[3], s[1], (int)s[2], (const float *)p[4],
-                       bits_to_float(s[3]), bias, residual);
+    hipLaunchKernelGGL((lm_head<W>), grid, dim3(64 * W), (size_t)s[2] * sizeof(float), nc::stream(), (float *)p[0],
+                       (unsigned long long *)p[1], (const float *)p[2], (const float4 *)p[3], s[1], (int)s[2],
+                       (const float *)p[4], bits_to_float(s[3]), bias, residual, slots);
     return nc::launched("lm_head");
 }
 
@@ -268,10 +330,17 @@ NC_EXPORT int32_t nc_argmax_clear(void **p, const int64_t *s) {
     return nc::launched("fill_u64");
 }
 
-// p: [index i64[n], best u64[n]];  s: [n]
+// p: [index i64[n], best u64[n] or u64[n, G]];  s: [n, G] (G = 0: one key per row; else the
+// per-workgroup keys nc_lm_head leaves with s[4] = 1)
 NC_EXPORT int32_t nc_argmax_index(void **p, const int64_t *s) {
-    NC_REQUIRE(p && s && p[0] && p[1] && s[0] >= 0 && s[0] < (1 << 24), "nc_argmax_index: bad operand");
+    NC_REQUIRE(p && s && p[0] && p[1] && s[0] >= 0 && s[0] < (1 << 24) && s[1] >= 0 && s[1] < (1 << 24),
+               "nc_argmax_index: bad operand");
     if (s[0] == 0) return NC_OK;
+    if (s[1] > 0) {
+        hipLaunchKernelGGL(argmax_reduce, dim3((unsigned)s[0]), dim3(256), 0, nc::stream(), (int64_t *)p[0],
+                           (const unsigned long long *)p[1], (int)s[1]);
+        return nc::launched("argmax_reduce");
+    }
     hipLaunchKernelGGL(argmax_decode, dim3((unsigned)((s[0] + 255) / 256)), dim3(256), 0, nc::stream(),
                        (int64_t *)p[0], (const unsigned long long *)p[1], (int)s[0]);
     return nc::launched("argmax_decode");
@@ -280,20 +349,22 @@ NC_EXPORT int32_t nc_argmax_index(void **p, const int64_t *s) {
 namespace {
 // One greedy step's bookkeeping on the device: the argmax of the step just run
 // becomes the next input token and is appended to the history at position
-// pos + 1; pos advances; the argmax key is cleared for the next step. With x,
-// the token's embedding row is gathered into x too (the next step's input, as
-// nc_embed would: an id outside 0..V-1 records Fail code 1 and leaves x zero).
+// pos + 1; pos advances; a single argmax key is cleared for the next step
+// (per-workgroup keys, slots > 0, are reduced here and need no clearing). With
+// x, the token's embedding row is gathered into x too (the next step's input,
+// as nc_embed would: an id outside 0..V-1 records Fail code 1 and leaves x zero).
 __global__ __launch_bounds__(256) void decode_advance(int64_t *__restrict__ ids, int64_t *__restrict__ tokens,
-                                                      unsigned long long *__restrict__ best,
+                                                      unsigned long long *__restrict__ best, int slots,
                                                       int64_t *__restrict__ pos, int64_t capacity,
                                                       float *__restrict__ x, const float *__restrict__ table, int H,
                                                       int64_t V, int32_t *__restrict__ error) {
+    __shared__ unsigned long long wkeys[4];
     const int64_t p = *pos;
-    const int64_t token = (int64_t)(0xFFFFFFFFu - (uint32_t)(best[0] & 0xFFFFFFFFull));
     if (p < -1 || p + 1 >= capacity) {
         if (threadIdx.x == 0) atomicCAS(error, 0, NC_FAIL_CAPACITY);
         return;
     }
+    const int64_t token = key_index(slots > 0 ? reduce_keys(best, slots, wkeys) : best[0]);
     if (x) {
         const bool bad = token < 0 || token >= V;
         if (bad && threadIdx.x == 0) atomicCAS(error, 0, NC_FAIL_INDEX);
@@ -305,20 +376,23 @@ __global__ __launch_bounds__(256) void decode_advance(int64_t *__restrict__ ids,
     tokens[p + 1] = token;
     ids[0] = token;
     *pos = p + 1;
-    best[0] = 0ull;
+    if (slots == 0) best[0] = 0ull;
 }
 }  // namespace
 
 // The greedy loop's step on the device (models/qwen2.py:362-367 does it on
 // the host: argmax, append, feed back), so a captured decode step needs no
 // host round trip.
-// p: [ids i64[1], tokens i64[capacity], best u64[1], pos i64[1], x f32[H] | NULL, table f32[V,H] | NULL];
-// s: [capacity, H, V] (H and V read only with x)
+// p: [ids i64[1], tokens i64[capacity], best u64[1] or u64[G], pos i64[1], x f32[H] | NULL,
+//     table f32[V,H] | NULL];
+// s: [capacity, H, V, G] (H and V read only with x; G = 0: one argmax key, else nc_lm_head's
+//    per-workgroup keys)
 NC_EXPORT int32_t nc_decode_advance(void **p, const int64_t *s) {
-    NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3] && s[0] > 0, "nc_decode_advance: bad operand");
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3] && s[0] > 0 && s[3] >= 0 && s[3] < (1 << 24),
+               "nc_decode_advance: bad operand");
     NC_REQUIRE(!p[4] || (p[5] && s[1] > 0 && s[1] < (1 << 24) && s[2] > 0), "nc_decode_advance: x needs the table");
     hipLaunchKernelGGL(decode_advance, dim3(1), dim3(256), 0, nc::stream(), (int64_t *)p[0], (int64_t *)p[1],
-                       (unsigned long long *)p[2], (int64_t *)p[3], s[0], (float *)p[4], (const float *)p[5],
-                       p[4] ? (int)s[1] : 0, p[4] ? s[2] : 0, nc::error_word());
+                       (unsigned long long *)p[2], (int)s[3], (int64_t *)p[3], s[0], (float *)p[4],
+                       (const float *)p[5], p[4] ? (int)s[1] : 0, p[4] ? s[2] : 0, nc::error_word());
     return nc::launched("decode_advance");
 }

@@ -43,6 +43,11 @@ def attention_workspace_bytes(heads: int, head_dim: int, rows: int, keys: int) -
     return heads * rows * -(-keys // 64) * (head_dim + 2) * 4
 
 
+def argmax_slots(vocab: int) -> int:
+    """Argmax keys per row that nc_lm_head leaves with s[4] = 1: one per workgroup of 4 x 64 rows."""
+    return -(-(-(-vocab // 64)) // 4)
+
+
 def _int8_weight(op: str, q: DeviceArray, scales: DeviceArray, k: int) -> int:
     """Check ``q: i8[N, K]`` and ``scales: f32[N]`` against width ``k``; return N (ir.py:381-389)."""
     if q.dtype != I8 or len(q.shape) != 2:

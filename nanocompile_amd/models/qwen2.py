@@ -42,7 +42,7 @@ import numpy as np
 
 from nanocompile_amd import hip
 from nanocompile_amd.hip import DeviceArray
-from nanocompile_amd.kernels import attention_workspace_bytes, float_bits, pack_chains, pack_chains_vnni
+from nanocompile_amd.kernels import argmax_slots, attention_workspace_bytes, float_bits, pack_chains, pack_chains_vnni
 from nanocompile_amd.models.config import Qwen2Config
 
 QUANTIZATIONS = ("int8-token", "int8", "int8-vnni", "f32")
@@ -247,14 +247,16 @@ class Qwen2:
         M = max_tokens
         act = [((M, H), np.float32), ((M, W), np.float32), ((M, Q), np.float32), ((M, I), np.float32),
                ((M, max(I, H, Q)), np.int8), ((M,), np.float32), ((M, H), np.float32), ((M,), np.int64),
-               ((M,), np.uint64), ((1, V), np.float32), ((M,), np.int64), ((M, I), np.float32),
+               ((argmax_slots(V),), np.uint64), ((1, V), np.float32), ((M,), np.int64), ((M, I), np.float32),
                ((M, I), np.float32), ((M, -(-max(I, H, Q) // BLOCK)), np.float32), ((M,), np.float32)]
         self.acts = Arena(Arena.size(act))
         self.x, self.qkv = self.acts.take((M, H), np.float32), self.acts.take((M, W), np.float32)
         self.ctx, self.h = self.acts.take((M, Q), np.float32), self.acts.take((M, I), np.float32)
         self.xq, self.xs = self.acts.take((M, max(I, H, Q)), np.int8), self.acts.take((M,), np.float32)
         self.normed, self.ids = self.acts.take((M, H), np.float32), self.acts.take((M,), np.int64)
-        self.best, self.logits_row = self.acts.take((M,), np.uint64), self.acts.take((1, V), np.float32)
+        # the LM head leaves one argmax key per workgroup; the consumer reduces them
+        self.slots = argmax_slots(V)
+        self.best, self.logits_row = self.acts.take((self.slots,), np.uint64), self.acts.take((1, V), np.float32)
         self.argmax = self.acts.take((M,), np.int64)
         # the reference modes: gate and up apart, and the block quantizer's scales and offsets
         self.gate, self.up = self.acts.take((M, I), np.float32), self.acts.take((M, I), np.float32)
@@ -408,9 +410,8 @@ class Qwen2:
         self._layers(m, past, cache)
         hip.call("nc_rms_norm_quant", [self.normed, self.xq, self.xs, self.x.ptr + (m - 1) * H * 4, self.norm],
                  [1, H, float_bits(c.rms_norm_eps)])
-        hip.call("nc_argmax_clear", [self.best], [1])
-        hip.call("nc_lm_head", [None, self.best, self.normed, self.head], [1, V, H])
-        hip.call("nc_argmax_index", [self.argmax, self.best], [1])
+        hip.call("nc_lm_head", [None, self.best, self.normed, self.head], [1, V, H, 0, 1])
+        hip.call("nc_argmax_index", [self.argmax, self.best], [1, self.slots])
         out = np.empty(1, np.int64)
         hip.load().nc_memcpy_d2h(out.ctypes.data, self.argmax.ptr, 8)
         hip.sync()
@@ -421,11 +422,12 @@ class Qwen2:
     # -- greedy decoding on the device -------------------------------------------------
 
     def _head_argmax(self, row_ptr: int) -> None:
-        """Final rms_norm of one row and the LM head (one kernel), its argmax key into ``best``."""
+        """Final rms_norm of one row and the LM head (one kernel), its argmax keys (one per
+        workgroup) into ``best``."""
         c = self.config
         H, V = c.hidden_size, c.vocab_size
         hip.call("nc_lm_head", [None, self.best, row_ptr, self.head, self.norm],
-                 [1, V, H, float_bits(c.rms_norm_eps)])
+                 [1, V, H, float_bits(c.rms_norm_eps), 1])
 
     def generate(self, prompt_ids: Sequence[int], max_new_tokens: int, timer=None, graph: bool = True) -> list[int]:
         """Greedy decoding with the whole loop on the device; the same tokens as :func:`greedy`.
@@ -453,11 +455,11 @@ class Qwen2:
         self.ids.view((m,)).upload(prompt)
         hip.call("nc_embed", [self.x, self.embed, self.ids], [m, H, V])
         self._layers(m, 0, cache)
-        hip.call("nc_argmax_clear", [self.best], [1])
         self._head_argmax(self.x.ptr + (m - 1) * H * 4)
         pos.upload(np.array([m - 1], np.int64))
         # the advance also gathers the next token's embedding row into x
-        advance = ("nc_decode_advance", [one_id, tokens, self.best, pos, self.x, self.embed], [capacity, H, V])
+        advance = ("nc_decode_advance", [one_id, tokens, self.best, pos, self.x, self.embed],
+                   [capacity, H, V, self.slots])
         hip.call(*advance)
 
         def step() -> None:

@@ -140,6 +140,42 @@ def test_lm_head_and_argmax(gpu):
     got = logits.numpy()
     assert np.array_equal(bits(got), bits(expected))
     assert list(index.numpy()) == [int(np.argmax(expected[0])), 0]
+    # one key per workgroup (s[4] = 1), reduced by nc_argmax_index: no clear needed, same answers
+    from nanocompile_amd.kernels import argmax_slots
+    slots = argmax_slots(v)
+    keys = DeviceArray((2, slots), np.uint64)
+    keys.upload(np.full((2, slots), 12345, np.uint64))                  # stale keys are overwritten
+    hip.call("nc_lm_head", [None, keys, DeviceArray.from_host(x), packed], [2, v, h, 0, 1])
+    hip.call("nc_argmax_index", [index, keys], [2, slots])
+    hip.sync()
+    assert list(index.numpy()) == [int(np.argmax(expected[0])), 0]
+
+
+@pytest.mark.parametrize("v", [64, 255, 256, 1000, 151936])
+def test_argmax_per_workgroup_keys_break_ties_low(gpu, v):
+    """Per-workgroup keys reduced by nc_argmax_index and by nc_decode_advance: numpy.argmax's first
+    index, with the maximum placed in the last workgroup and tied in the first."""
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import DeviceArray
+    from nanocompile_amd.kernels import argmax_slots
+    print(f"argmax slots v={v}", flush=True)
+    rng = np.random.default_rng(v)
+    h = 896 if v == 151936 else 64
+    table = (rng.standard_normal((v, h)) * 0.1).astype(np.float32)
+    table[v - 1] = 1.0
+    table[min(3, v - 1)] = 1.0                                  # a tie with an earlier row
+    x = np.ones((1, h), np.float32)
+    packed = DeviceArray((-(-v // 64) * 64, h), np.float32)
+    hip.call("nc_pack_rows64", [packed, DeviceArray.from_host(table)], [v, h])
+    slots = argmax_slots(v)
+    keys, index = DeviceArray((slots,), np.uint64), DeviceArray((1,), np.int64)
+    hip.call("nc_lm_head", [None, keys, DeviceArray.from_host(x), packed], [1, v, h, 0, 1])
+    hip.call("nc_argmax_index", [index, keys], [1, slots])
+    ids, tokens = DeviceArray((1,), np.int64), DeviceArray.from_host(np.zeros(4, np.int64))
+    pos = DeviceArray.from_host(np.array([0], np.int64))
+    hip.call("nc_decode_advance", [ids, tokens, keys, pos], [4, 0, 0, slots])
+    hip.sync()
+    assert index.numpy()[0] == min(3, v - 1) and tokens.numpy()[1] == min(3, v - 1)
 
 
 # -- the model ------------------------------------------------------------------------
