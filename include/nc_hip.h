@@ -266,16 +266,21 @@ int32_t nc_pack_rows64(void **p, const int64_t *s);
  * rms-normed first (eps = s[3] as float32 bits). With bias, + bias[n] after the
  * sum, and with residual, residual + that: the reference's float32 linear
  * (nn.py:24-31) and residual add, so the same kernel is the float32 model's
- * projections.
- * p: [logits f32[M,V] or NULL, best u64[M] or NULL, x f32[M,H], packed table,
+ * projections. With s[4] = 1 the argmax is left as one key per workgroup,
+ * best u64[M, G] with G = ceil(ceil(V/64)/4), for nc_argmax_index or
+ * nc_decode_advance to reduce (no atomics, nothing to clear); with s[4] = 0,
+ * best u64[M] receives atomic maxima and must be cleared first.
+ * p: [logits f32[M,V] or NULL, best or NULL, x f32[M,H], packed table,
  *     gamma f32[H] or NULL, bias f32[V] or NULL, residual f32[M,V] or NULL];
- * s: [M, V, H, eps bits] */
+ * s: [M, V, H, eps bits, key per workgroup 0 or 1] */
 int32_t nc_lm_head(void **p, const int64_t *s);
 
 /* p: [best u64[n]];  s: [n]  (zeroes the argmax keys before nc_lm_head) */
 int32_t nc_argmax_clear(void **p, const int64_t *s);
 
-/* p: [index i64[n], best u64[n]];  s: [n]  (argmax keys to token ids) */
+/* Argmax keys to token ids: one key per row (G = 0), or each row's G
+ * per-workgroup keys from nc_lm_head with s[4] = 1, reduced.
+ * p: [index i64[n], best u64[n] or u64[n,G]];  s: [n, G] */
 int32_t nc_argmax_index(void **p, const int64_t *s);
 
 /* Greedy decoding's bookkeeping on the device (models/qwen2.py:362-367 does it
@@ -285,8 +290,9 @@ int32_t nc_argmax_index(void **p, const int64_t *s);
  * NC_FAIL_CAPACITY when pos + 1 reaches the capacity. With x, the token's
  * embedding row is gathered into x as well (nc_embed's gather and Fail code 1),
  * so the next step needs no separate embedding launch.
- * p: [ids i64[1], tokens i64[capacity], best u64[1], pos i64[1], x f32[H] or NULL,
- *     table f32[V,H] or NULL];  s: [capacity, H, V] (H, V read only with x)
+ * With G > 0, best holds nc_lm_head's G per-workgroup keys, reduced here.
+ * p: [ids i64[1], tokens i64[capacity], best u64[1] or u64[G], pos i64[1], x f32[H] or NULL,
+ *     table f32[V,H] or NULL];  s: [capacity, H, V, G] (H, V read only with x)
  * nc_rope_append and nc_attention take pos as an optional p[4], read on the
  * device in place of s[4] (past). */
 int32_t nc_decode_advance(void **p, const int64_t *s);
