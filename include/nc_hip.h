@@ -237,7 +237,7 @@ int32_t nc_rope_append(void **p, const int64_t *s);
  * reference's repeat_kv as index arithmetic, nn.py:109-120). The softmax and
  * the context are computed in 64-key chunks combined afterwards, the order
  * nc_attention_decode shares, so prefill and decode agree bit for bit. One
- * workgroup per (64-key chunk, KV head, 8 query rows) attends the rows' query
+ * workgroup per (64-key chunk, KV head, 4 query rows) attends the rows' query
  * heads of the group to its chunk; a second launch combines the chunks. The
  * reference materializes the [heads, M, keys] scores instead (README.md:317).
  * p: [ctx f32[M,heads*D], qkv (q rotated), kcache, vcache, pos i64[1] or NULL,

@@ -1,7 +1,7 @@
 """Attention on the GPU, bit for bit against the host oracle's chunked order.
 
 Both kernels stage each 64-key chunk in LDS once per KV head (and, in a
-prompt, per block of 8 query rows), attend every query head of the group to
+prompt, per block of 4 query rows), attend every query head of the group to
 it, and combine the chunk results in a second launch; these tests cover both
 sides of every chunk edge, long contexts, every head width, groups of more
 than 8 query heads, prompts taken in slabs when the workspace is small, the
