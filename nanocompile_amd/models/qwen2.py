@@ -192,6 +192,18 @@ class Qwen2:
             q, s = self.weights.take((rows, k), np.int8), self.weights.take((rows,), np.float32)
             at = 0
             for name in names:
+                if f"{name}@int8" in weights:
+                    # already quantized (the reference's quantized_weights, quantize.py:167-180,
+                    # whose quantize_int8 is the same arithmetic as nc_quantize_rows_i8)
+                    wq = np.ascontiguousarray(weights[f"{name}@int8"], np.int8)
+                    ws = np.ascontiguousarray(weights[f"{name}@scales"], np.float32)
+                    n = wq.shape[0]
+                    if wq.shape[1] != k or ws.shape != (n,):
+                        raise ValueError(f"{name}@int8 / @scales have shapes {wq.shape} / {ws.shape}")
+                    q.view((n, k), np.int8, offset_bytes=at * k).upload(wq)
+                    s.view((n,), np.float32, offset_bytes=at * 4).upload(ws)
+                    at += n
+                    continue
                 w = np.ascontiguousarray(weights[name], np.float32)
                 n = w.shape[0]
                 if w.shape[1] != k:

@@ -1,0 +1,165 @@
+"""The reference's ``Runner`` on the GPU: ``HIPBackend(config)(graph, inputs, weights) -> dict``.
+
+The reference's model driver runs every step as ``run(graph, inputs, weights)``
+(models/qwen2.py:229 declares the protocol, 337-342 calls it): ``graph`` is the
+forward pass from ``build_qwen2`` (models/qwen2.py:167-224), rewritten by
+``quantize.quantize`` in the int8 modes (quantize.py:127-164); ``inputs`` are
+``token_ids`` and the host cache's filled part, ``past_keys`` and
+``past_values`` ``[layers, kv_heads, past, head_dim]``; ``weights`` are what the
+graph reads (``quantize.quantized_weights``, quantize.py:167-180: ``W@int8``
+and ``W@scales`` for each int8 projection, float32 for the rest). It returns
+``logits`` (``[seq, vocab]``, or ``[1, vocab]`` for ``qwen2_last``) and the
+new tokens' ``keys`` and ``values`` ``[layers, kv_heads, seq, head_dim]`` as
+host arrays, as the reference's compiled runtime does (runtime.py:245-301).
+
+``HIPBackend`` is that callable for these graphs, so the reference's own
+``Qwen2(config, weights, run=HIPBackend(config), quantization=...)`` and its
+``greedy`` run their steps on this package's kernels. It recognises a graph
+by its interface (names, inputs, outputs, the weights it reads and their
+shapes) and by its int8 primitive (``matmul_i8``: the reference's "int8" mode,
+``matmul_i8_vnni`` with block 32: "int8-vnni", neither: float32), and runs the
+GPU model in the same mode, whose kernels compute the reference's kernels'
+bits (the int8 and float32 projections) or its operations in a stated order
+(rms_norm, softmax, attention). Any other graph raises NotImplementedError:
+this backend accelerates the Qwen2 path, not arbitrary graphs.
+
+Each call uploads the past keys and values it is given (the reference keeps
+its cache on the host and hands it over every step); the model, with its
+weights uploaded and packed, is made once per weights mapping and mode.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+from collections.abc import Mapping
+
+import numpy as np
+
+from nanocompile_amd.models.config import Qwen2Config
+
+INPUTS = ("token_ids", "past_keys", "past_values")
+OUTPUTS = {"logits", "keys", "values"}
+INT8_OPS = {"matmul_i8": "int8", "matmul_i8_vnni": "int8-vnni"}
+VNNI_BLOCK = 32
+PROJECTIONS = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+               "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
+
+
+class HIPBackend:
+    """A ``Runner`` (models/qwen2.py:229) for the Qwen2 forward graphs, on the GPU.
+
+    ``config`` is the model's configuration (the reference's ``Qwen2Config``
+    or this package's: the same fields). ``max_tokens`` bounds the tokens of
+    one call (a prompt); ``schedule`` is passed to the model
+    (``"default"`` or an ``autotune.Autotuner``).
+    """
+
+    def __init__(self, config, max_tokens: int = 512, device: int = 0, schedule="default") -> None:
+        fields = [f.name for f in dataclasses.fields(Qwen2Config)]
+        self.config = Qwen2Config(**{name: getattr(config, name) for name in fields})
+        self.max_tokens, self.device, self.schedule = max_tokens, device, schedule
+        self._models: list[tuple[Mapping, str, object]] = []
+
+    # -- recognising a graph ----------------------------------------------------------------
+
+    def mode(self, graph) -> str:
+        """The quantization mode a Qwen2 graph was built in: "f32", "int8" or "int8-vnni"."""
+        found = {INT8_OPS[node.op] for node in graph.nodes if node.op in INT8_OPS}
+        if len(found) > 1:
+            raise NotImplementedError(f"graph {graph.name!r} mixes matmul_i8 and matmul_i8_vnni")
+        mode = found.pop() if found else "f32"
+        if mode == "int8-vnni":
+            blocks = {node.attrs["block"] for node in graph.nodes if node.op == "matmul_i8_vnni"}
+            if blocks != {VNNI_BLOCK}:
+                raise NotImplementedError(f"matmul_i8_vnni with block {sorted(blocks)}; this backend "
+                                          f"runs block {VNNI_BLOCK} (quantize.py:44)")
+        return mode
+
+    def expected_weights(self, mode: str) -> dict[str, tuple[str, tuple[int, ...]]]:
+        """The weights a Qwen2 graph of this configuration reads in ``mode``: name -> (dtype, shape)."""
+        c = self.config
+        h, inter, d = c.hidden_size, c.intermediate_size, c.head_dim
+        q_out, kv_out = c.num_attention_heads * d, c.num_key_value_heads * d
+        out: dict[str, tuple[str, tuple[int, ...]]] = {"model.embed_tokens.weight": ("f32", (c.vocab_size, h)),
+                                                       "model.norm.weight": ("f32", (h,))}
+        if not c.tie_word_embeddings:
+            out["lm_head.weight"] = ("f32", (c.vocab_size, h))
+        shapes = {"self_attn.q_proj": (q_out, h), "self_attn.k_proj": (kv_out, h),
+                  "self_attn.v_proj": (kv_out, h), "self_attn.o_proj": (h, q_out),
+                  "mlp.gate_proj": (inter, h), "mlp.up_proj": (inter, h), "mlp.down_proj": (h, inter)}
+        for layer in range(c.num_hidden_layers):
+            p = f"model.layers.{layer}"
+            out[f"{p}.input_layernorm.weight"] = ("f32", (h,))
+            out[f"{p}.post_attention_layernorm.weight"] = ("f32", (h,))
+            for name in ("q_proj", "k_proj", "v_proj"):
+                out[f"{p}.self_attn.{name}.bias"] = ("f32", (shapes[f"self_attn.{name}"][0],))
+            for proj in PROJECTIONS:
+                w = f"{p}.{proj}.weight"
+                if mode == "f32":
+                    out[w] = ("f32", shapes[proj])
+                else:
+                    out[f"{w}@int8"] = ("i8", shapes[proj])
+                    out[f"{w}@scales"] = ("f32", (shapes[proj][0],))
+        return out
+
+    def last_only(self, graph, mode: str) -> bool:
+        """Check ``graph`` is a Qwen2 forward of this configuration; True for the last-row variant."""
+        if graph.name not in ("qwen2", "qwen2_last"):
+            raise NotImplementedError(f"graph {graph.name!r}: this backend runs the Qwen2 forward graphs "
+                                      f"(models/qwen2.py:167-224), 'qwen2' and 'qwen2_last'")
+        names = tuple(node.attrs["name"] for node in graph.inputs)
+        if names != INPUTS or set(graph.outputs) != OUTPUTS:
+            raise NotImplementedError(f"graph {graph.name!r} has inputs {names} and outputs "
+                                      f"{sorted(graph.outputs)}, not a Qwen2 forward's")
+        expected = self.expected_weights(mode)
+        reads = {name: (str(node.dtype), tuple(int(str(d)) for d in node.shape))
+                 for name, node in graph.weights.items()}
+        if reads != expected:
+            missing, extra = sorted(set(expected) - set(reads)), sorted(set(reads) - set(expected))
+            wrong = sorted(n for n in set(reads) & set(expected) if reads[n] != expected[n])
+            raise NotImplementedError(f"graph {graph.name!r} is not this configuration's Qwen2 in mode "
+                                      f"{mode!r}: weights missing {missing[:3]}, unexpected {extra[:3]}, "
+                                      f"of another shape {wrong[:3]}")
+        return graph.name == "qwen2_last"
+
+    # -- running it -----------------------------------------------------------------------------
+
+    def _model(self, mode: str, weights: Mapping):
+        for held, held_mode, model in self._models:
+            if held is weights and held_mode == mode:
+                return model
+        from nanocompile_amd.models.qwen2 import Qwen2
+        model = Qwen2(self.config, weights, quantization=mode, max_tokens=self.max_tokens, device=self.device,
+                      schedule=self.schedule)
+        self._models.append((weights, mode, model))
+        return model
+
+    def __call__(self, graph, inputs: Mapping[str, np.ndarray], weights: Mapping[str, np.ndarray]) -> dict:
+        mode = self.mode(graph)
+        last_only = self.last_only(graph, mode)
+        c = self.config
+        ids = np.asarray(inputs["token_ids"], np.int64)
+        past_keys = np.asarray(inputs["past_keys"], np.float32)
+        past_values = np.asarray(inputs["past_values"], np.float32)
+        layout = (c.num_hidden_layers, c.num_key_value_heads)
+        if ids.ndim != 1 or ids.size == 0:
+            raise ValueError(f"token_ids must be a non-empty 1-D array, got shape {ids.shape}")
+        if (past_keys.shape[:2] != layout or past_keys.shape[3:] != (c.head_dim,)
+                or past_values.shape != past_keys.shape):
+            raise ValueError(f"past_keys / past_values of shapes {past_keys.shape} / {past_values.shape}; "
+                             f"expected [{layout[0]}, {layout[1]}, past, {c.head_dim}]")
+        m, past = int(ids.size), int(past_keys.shape[2])
+        if m > self.max_tokens:
+            raise ValueError(f"{m} tokens in one call; this backend was made with max_tokens={self.max_tokens}")
+        model = self._model(mode, weights)
+        cache = model.new_cache(past + m)
+        if past:
+            for host, device in ((past_keys, cache.keys), (past_values, cache.values)):
+                full = np.zeros(device.shape, np.float32)
+                full[:, :, :past] = host
+                device.upload(full)
+        cache.length = past
+        logits = model.forward(ids, cache, last_only=last_only)
+        keys = np.ascontiguousarray(cache.keys.numpy()[:, :, past:past + m])
+        values = np.ascontiguousarray(cache.values.numpy()[:, :, past:past + m])
+        return {"logits": logits, "keys": keys, "values": values}

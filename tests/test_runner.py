@@ -1,0 +1,79 @@
+"""HIPBackend recognises the reference's Qwen2 graphs (recorded from the reference itself in
+tests/golden/runner_graphs.json) and refuses anything else, before touching a GPU."""
+
+from __future__ import annotations
+
+import copy
+import json
+
+import pytest
+
+from tests import runner_graphs
+
+
+@pytest.fixture(scope="module")
+def fixture():
+    return runner_graphs.load()
+
+
+def backend():
+    from nanocompile_amd.models.config import TINY
+    from nanocompile_amd.runner import HIPBackend
+    return HIPBackend(TINY)
+
+
+@pytest.mark.parametrize("mode", ["f32", "int8", "int8-vnni"])
+def test_graphs_are_recognised(fixture, mode):
+    b = backend()
+    for key, last in (("graph", False), ("graph_last", True)):
+        g = runner_graphs.stand_in(fixture["modes"][mode][key])
+        assert b.mode(g) == mode
+        assert b.last_only(g, mode) is last
+
+
+@pytest.mark.parametrize("mode", ["f32", "int8", "int8-vnni"])
+def test_expected_weights_are_the_references(fixture, mode):
+    """The weight names, dtypes and shapes a graph reads, and the names the reference's driver
+    passes (quantize.quantized_weights), are exactly what the backend expects."""
+    b = backend()
+    desc = fixture["modes"][mode]["graph"]
+    recorded = {k: (t, tuple(int(d) for d in s)) for k, (t, s) in desc["weights"].items()}
+    assert recorded == b.expected_weights(mode)
+    assert set(fixture["modes"][mode]["weights_passed"]) == set(b.expected_weights(mode))
+
+
+def test_the_reference_calls_the_last_row_graph_with_the_cache_so_far(fixture):
+    """The protocol the GPU test's driver restates: a prompt, then one token a call."""
+    for mode, data in fixture["modes"].items():
+        calls = data["calls"]
+        prompt = fixture["prompt"]
+        assert [c["graph"] for c in calls] == ["qwen2_last"] * 3
+        assert calls[0]["token_ids"] == prompt and calls[0]["past"] == 0
+        for i, c in enumerate(calls[1:], start=1):
+            assert c["token_ids"] == [data["tokens"][i - 1]] and c["past"] == len(prompt) + i - 1
+            assert c["outputs"]["logits"] == [1, 256] and c["outputs"]["keys"] == [2, 2, 1, 32]
+
+
+def test_other_graphs_are_refused(fixture):
+    b = backend()
+    desc = fixture["modes"]["int8"]["graph"]
+    other = copy.deepcopy(desc)
+    other["name"] = "mlp"
+    with pytest.raises(NotImplementedError, match="Qwen2 forward"):
+        b.last_only(runner_graphs.stand_in(other), "int8")
+    wider = copy.deepcopy(desc)
+    wider["weights"]["model.norm.weight"][1] = ["256"]
+    with pytest.raises(NotImplementedError, match="another shape"):
+        b.last_only(runner_graphs.stand_in(wider), "int8")
+    fewer = copy.deepcopy(desc)
+    del fewer["weights"]["model.layers.1.mlp.up_proj.weight@int8"]
+    with pytest.raises(NotImplementedError, match="missing"):
+        b.last_only(runner_graphs.stand_in(fewer), "int8")
+    mixed = copy.deepcopy(desc)
+    mixed["ops"]["matmul_i8_vnni"] = 1
+    with pytest.raises(NotImplementedError, match="mixes"):
+        b.mode(runner_graphs.stand_in(mixed))
+    block = copy.deepcopy(fixture["modes"]["int8-vnni"]["graph"])
+    block["int8_attrs"] = [json.dumps({"block": 64})]
+    with pytest.raises(NotImplementedError, match="block"):
+        b.mode(runner_graphs.stand_in(block))
