@@ -26,11 +26,16 @@ this backend accelerates the Qwen2 path, not arbitrary graphs.
 Each call uploads the past keys and values it is given (the reference keeps
 its cache on the host and hands it over every step); the model, with its
 weights uploaded and packed, is made once per weights mapping and mode.
+``HIPCompiledGraph`` is the per-graph form, the reference's
+``CompiledGraph(graph, ...)(inputs, weights, bindings, profile)``
+(runtime.py:167-301), which ``HIPBackend.compiled`` makes once per graph as
+the reference's ``CBackend.compiled`` does (runtime.py:321-333).
 """
 
 from __future__ import annotations
 
 import dataclasses
+import time
 from collections.abc import Mapping
 
 import numpy as np
@@ -59,6 +64,7 @@ class HIPBackend:
         self.config = Qwen2Config(**{name: getattr(config, name) for name in fields})
         self.max_tokens, self.device, self.schedule = max_tokens, device, schedule
         self._models: list[tuple[Mapping, str, object]] = []
+        self._compiled: list[tuple[object, "HIPCompiledGraph"]] = []
 
     # -- recognising a graph ----------------------------------------------------------------
 
@@ -134,9 +140,20 @@ class HIPBackend:
         self._models.append((weights, mode, model))
         return model
 
+    def compiled(self, graph) -> "HIPCompiledGraph":
+        """The graph bound once, on first use (the reference's CBackend.compiled, runtime.py:321-333)."""
+        for held, bound in self._compiled:
+            if held is graph:
+                return bound
+        bound = HIPCompiledGraph(graph, self.config, backend=self)
+        self._compiled.append((graph, bound))
+        return bound
+
     def __call__(self, graph, inputs: Mapping[str, np.ndarray], weights: Mapping[str, np.ndarray]) -> dict:
-        mode = self.mode(graph)
-        last_only = self.last_only(graph, mode)
+        return self.compiled(graph)(inputs, weights)
+
+    def run(self, graph, mode: str, last_only: bool, inputs: Mapping[str, np.ndarray],
+            weights: Mapping[str, np.ndarray]) -> dict:
         c = self.config
         ids = np.asarray(inputs["token_ids"], np.int64)
         past_keys = np.asarray(inputs["past_keys"], np.float32)
@@ -163,3 +180,36 @@ class HIPBackend:
         keys = np.ascontiguousarray(cache.keys.numpy()[:, :, past:past + m])
         values = np.ascontiguousarray(cache.values.numpy()[:, :, past:past + m])
         return {"logits": logits, "keys": keys, "values": values}
+
+
+class HIPCompiledGraph:
+    """One Qwen2 graph bound to the GPU model: the reference's ``CompiledGraph(graph, fuse, schedule)``
+    and its ``__call__(inputs, weights, bindings=None, profile=None) -> dict`` (runtime.py:167-301).
+
+    The graph is recognised here, once (``NotImplementedError`` for anything but the Qwen2 forward
+    graphs of ``config``). ``bindings``, when given, must agree with the inputs' symbols (``seq``,
+    ``past``), as the reference's ``check_arguments`` requires; ``profile``, when given, accumulates
+    the seconds of the call under "qwen2_forward" (the whole forward is one sequence of GPU
+    kernels, not one call per graph primitive).
+    """
+
+    def __init__(self, graph, config, fuse: bool = True, schedule="default", backend: HIPBackend | None = None,
+                 max_tokens: int = 512, device: int = 0) -> None:
+        self.graph = graph
+        self.backend = backend or HIPBackend(config, max_tokens=max_tokens, device=device, schedule=schedule)
+        self.mode = self.backend.mode(graph)
+        self.last_only = self.backend.last_only(graph, self.mode)
+
+    def __call__(self, inputs: Mapping[str, np.ndarray], weights: Mapping[str, np.ndarray],
+                 bindings: Mapping[str, int] | None = None, profile: dict[str, float] | None = None) -> dict:
+        if bindings:
+            bound = {"seq": int(np.asarray(inputs["token_ids"]).shape[0]),
+                     "past": int(np.asarray(inputs["past_keys"]).shape[2])}
+            for name, value in bindings.items():
+                if name not in bound or bound[name] != int(value):
+                    raise ValueError(f"binding {name}={value} disagrees with the inputs ({bound})")
+        started = time.perf_counter()
+        out = self.backend.run(self.graph, self.mode, self.last_only, inputs, weights)
+        if profile is not None:
+            profile["qwen2_forward"] = profile.get("qwen2_forward", 0.0) + time.perf_counter() - started
+        return out

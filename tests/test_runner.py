@@ -77,3 +77,20 @@ def test_other_graphs_are_refused(fixture):
     block["int8_attrs"] = [json.dumps({"block": 64})]
     with pytest.raises(NotImplementedError, match="block"):
         b.mode(runner_graphs.stand_in(block))
+
+
+def test_compiled_graph_binds_once_and_checks_bindings(fixture):
+    from nanocompile_amd.models.config import TINY
+    from nanocompile_amd.runner import HIPBackend, HIPCompiledGraph
+    import numpy as np
+    b = HIPBackend(TINY)
+    g = runner_graphs.stand_in(fixture["modes"]["int8-vnni"]["graph_last"])
+    assert b.compiled(g) is b.compiled(g)
+    cg = HIPCompiledGraph(g, TINY)
+    assert cg.mode == "int8-vnni" and cg.last_only
+    inputs = {"token_ids": np.array([1, 2]), "past_keys": np.zeros((2, 2, 3, 32), np.float32),
+              "past_values": np.zeros((2, 2, 3, 32), np.float32)}
+    with pytest.raises(ValueError, match="disagrees"):
+        cg(inputs, {}, bindings={"seq": 3})
+    with pytest.raises(NotImplementedError):
+        HIPCompiledGraph(runner_graphs.stand_in({**fixture["modes"]["int8"]["graph"], "name": "other"}), TINY)
