@@ -18,7 +18,10 @@ keeps those rules for the GPU library:
   Candidates run in alternation, each round starting from a different one;
   the cost is the median over rounds.
 * **Correctness**: each candidate runs once on random operands before it is
-  timed, and its output must equal schedule 0's bit for bit.
+  timed, and its output must equal schedule 0's bit for bit; the output sits
+  between two guard regions of a sentinel pattern, which must be intact after
+  every candidate's run (the reference's guard regions, autotune.py:86-87,
+  256-286: a schedule writing past its output fails, it is not timed).
 * **Choice**: every legal candidate is measured (the space is small); the best
   then runs against the incumbent with twice the rounds and replaces it only
   if faster by more than ``margin``.
@@ -50,10 +53,25 @@ OPS = ("matmul_i8_token", "matmul_i8_token_swiglu")
 STREAM_BYTES = 512 * 2**20      # weight bytes one sample cycles through: past the 256 MB Infinity Cache
 MAX_COPIES = 64
 CACHE_VERSION = 1
+GUARD = 4096                    # float32 words of sentinel before and after a candidate's output
+SENTINEL = 0x7FC0DEAD           # a quiet NaN's bits: no projection writes it
 
 
 class TuningError(RuntimeError):
-    """A candidate failed its bit-for-bit check or could not be measured."""
+    """A candidate failed its bit-for-bit check or its guard regions, or could not be measured."""
+
+
+def guarded(words: int) -> np.ndarray:
+    """An output of ``words`` float32 words between two guard regions, as host bits to upload."""
+    return np.full(GUARD + words + GUARD, SENTINEL, np.uint32)
+
+
+def guards_broken(bits: np.ndarray) -> list[int]:
+    """Word offsets, relative to the output's first word, of guard words that are not the sentinel."""
+    bits = np.asarray(bits, np.uint32)
+    head, tail = bits[:GUARD], bits[len(bits) - GUARD:]
+    return ([int(i) - GUARD for i in np.flatnonzero(head != SENTINEL)] +
+            [int(i) + len(bits) - 2 * GUARD for i in np.flatnonzero(tail != SENTINEL)])
 
 
 # -- the space ---------------------------------------------------------------------------
@@ -92,7 +110,8 @@ class Problem:
         self.q = [[DeviceArray.from_host(w) for w in host] for _ in range(self.copies)]
         self.scales = [DeviceArray.from_host((rng.random(n) * 1e-3).astype(np.float32)) for _ in range(matrices)]
         self.bias = DeviceArray.from_host(rng.standard_normal(n).astype(np.float32))
-        self.y = DeviceArray((m, n), np.float32)
+        self.guarded = DeviceArray.from_host(guarded(m * n))
+        self.y = self.guarded.view((m, n), np.float32, offset_bytes=GUARD * 4)
 
     def launch(self, schedule: int, copy: int = 0) -> None:
         q = self.q[copy % self.copies]
@@ -105,9 +124,16 @@ class Problem:
                      [self.m, self.n, self.k, schedule])
 
     def output(self, schedule: int) -> np.ndarray:
+        """The schedule's output bits; TuningError if it wrote into a guard region."""
+        self.guarded.upload(guarded(self.m * self.n))
         self.launch(schedule, 0)
         hip.sync()
-        return self.y.numpy().view(np.uint32).copy()
+        bits = self.guarded.numpy()
+        broken = guards_broken(bits)
+        if broken:
+            raise TuningError(f"{self.op} schedule {schedule} on {(self.m, self.n, self.k)} wrote outside its "
+                              f"output, at word offsets {broken[:4]}")
+        return bits[GUARD:GUARD + self.m * self.n].copy()
 
 
 def measure(problem: Problem, schedules: list[int], rounds: int, reps: int) -> list[float]:
@@ -208,10 +234,12 @@ class TuningCache:
     def _load(self) -> dict:
         try:
             data = json.loads(self.path.read_text(encoding="utf-8"))
-        except (FileNotFoundError, json.JSONDecodeError):
+        except (FileNotFoundError, json.JSONDecodeError, UnicodeDecodeError):
             return {"version": CACHE_VERSION, "machines": {}}
-        if data.get("version") != CACHE_VERSION:
-            return {"version": CACHE_VERSION, "machines": {}}
+        if (not isinstance(data, dict) or data.get("version") != CACHE_VERSION
+                or not isinstance(data.get("machines"), dict)
+                or not all(isinstance(v, dict) for v in data["machines"].values())):
+            return {"version": CACHE_VERSION, "machines": {}}       # another version, or not ours: start over
         return data
 
     def get(self, machine: str, key: str) -> dict | None:

@@ -98,6 +98,26 @@ def test_cache_roundtrip_and_version(tmp_path):
     assert cache.get("m", "k") is None                          # another version: ignored
     path.write_text("{not json")
     assert cache.get("m", "k") is None
+    for junk in ("[1, 2]", '{"version": 1, "machines": [3]}', '{"version": 1, "machines": {"m": 4}}'):
+        path.write_text(junk)                                   # valid JSON, not a cache: ignored
+        assert cache.get("m", "k") is None
+    path.write_bytes(b"\xff\xfe\x00")
+    assert cache.get("m", "k") is None
+    cache.put("m", "k", {"winner": 3})                          # and a put starts it over
+    assert cache.get("m", "k") == {"winner": 3}
+
+
+def test_guard_regions_catch_writes_outside_the_output():
+    """A candidate's output sits between sentinel guards; any write outside it is reported."""
+    import numpy as np
+    words = 100
+    bits = autotune.guarded(words)
+    assert autotune.guards_broken(bits) == []
+    bits[autotune.GUARD:autotune.GUARD + words] = 7             # the output itself may hold anything
+    assert autotune.guards_broken(bits) == []
+    bits[autotune.GUARD - 1] = 0                                # one word before
+    bits[autotune.GUARD + words + 2] = np.uint32(0x3F800000)    # three words after the last
+    assert autotune.guards_broken(bits) == [-1, words + 2]
 
 
 def test_problem_key_covers_shape_and_space():
