@@ -56,17 +56,46 @@ __global__ __launch_bounds__(kThreads) void quantize_rows(int8_t *__restrict__ q
     if (threadIdx.x == 0) scales[blockIdx.x] = scale;
 }
 
-// Per-token quantization of a row already in registers/LDS-free form.
+// Per-token quantization of one row per workgroup: the row read once into
+// registers, PER_THREAD values a thread with every load in flight at once (a
+// loop over a run-time K waits for each load before the next), its maximum,
+// then the int8 values. Rows wider than 32 * kThreads take the loop.
+template <int PER_THREAD>
 __global__ __launch_bounds__(kThreads) void quantize_token(int8_t *__restrict__ xq, float *__restrict__ xs,
                                                            const float *__restrict__ x, int K) {
     __shared__ float scratch[4];
     const float *row = x + (size_t)blockIdx.x * K;
-    float mag = 0.0f;
-    for (int k = threadIdx.x; k < K; k += kThreads) mag = fmaxf(mag, fabsf(row[k]));
-    const float scale = nc::token_scale(block_max(mag, scratch));
     int8_t *out = xq + (size_t)blockIdx.x * K;
-    for (int k = threadIdx.x; k < K; k += kThreads) out[k] = nc::quantize_value(row[k], scale);
-    if (threadIdx.x == 0) xs[blockIdx.x] = scale;
+    float mag = 0.0f;
+    if constexpr (PER_THREAD > 0) {
+        float v[PER_THREAD];
+#pragma unroll
+        for (int i = 0; i < PER_THREAD; ++i) {
+            const int k = threadIdx.x + i * kThreads;
+            v[i] = k < K ? row[k] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < PER_THREAD; ++i) mag = fmaxf(mag, fabsf(v[i]));
+        const float scale = nc::token_scale(block_max(mag, scratch));
+#pragma unroll
+        for (int i = 0; i < PER_THREAD; ++i) {
+            const int k = threadIdx.x + i * kThreads;
+            if (k < K) out[k] = nc::quantize_value(v[i], scale);
+        }
+        if (threadIdx.x == 0) xs[blockIdx.x] = scale;
+    } else {
+        for (int k = threadIdx.x; k < K; k += kThreads) mag = fmaxf(mag, fabsf(row[k]));
+        const float scale = nc::token_scale(block_max(mag, scratch));
+        for (int k = threadIdx.x; k < K; k += kThreads) out[k] = nc::quantize_value(row[k], scale);
+        if (threadIdx.x == 0) xs[blockIdx.x] = scale;
+    }
+}
+
+template <int PER_THREAD>
+int32_t launch_token(void **p, int M, int K) {
+    hipLaunchKernelGGL(quantize_token<PER_THREAD>, dim3((unsigned)M), dim3(kThreads), 0, nc::stream(),
+                       (int8_t *)p[0], (float *)p[1], (const float *)p[2], K);
+    return nc::launched("quantize_token");
 }
 
 // rms_norm (nn.py:34-38: (x * (1 / sqrt(sum(x*x) / K + eps))) * gamma) and
@@ -137,9 +166,12 @@ NC_EXPORT int32_t nc_quantize_token_i8(void **p, const int64_t *s) {
     NC_REQUIRE(p && s && p[0] && p[1] && p[2], "nc_quantize_token_i8: null operand");
     NC_REQUIRE(s[0] >= 0 && s[1] > 0 && s[0] < (1 << 26) && s[1] < (1 << 26), "nc_quantize_token_i8: bad shape");
     if (s[0] == 0) return NC_OK;
-    hipLaunchKernelGGL(quantize_token, dim3((unsigned)s[0]), dim3(kThreads), 0, nc::stream(), (int8_t *)p[0],
-                       (float *)p[1], (const float *)p[2], (int)s[1]);
-    return nc::launched("quantize_token");
+    const int M = (int)s[0], K = (int)s[1];
+    if (K <= 4 * kThreads) return launch_token<4>(p, M, K);
+    if (K <= 8 * kThreads) return launch_token<8>(p, M, K);
+    if (K <= 20 * kThreads) return launch_token<20>(p, M, K);
+    if (K <= 32 * kThreads) return launch_token<32>(p, M, K);
+    return launch_token<0>(p, M, K);
 }
 
 // p: [normed f32[M,K] | NULL, xq i8[M,K], xs f32[M], x f32[M,K], gamma f32[K]];

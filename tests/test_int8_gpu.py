@@ -196,3 +196,16 @@ def test_token_quantizer_at_half_integers(gpu):
     xq, xs = kernels.quantize_token(x)
     eq, es = R.quantize_token(x)
     assert np.array_equal(xq.numpy(), eq) and np.array_equal(bits(xs.numpy()), bits(es))
+
+
+@pytest.mark.parametrize("k", [1, 255, 1024, 4864, 5121, 8192, 9000])
+def test_token_quantizer_every_row_width(gpu, k):
+    """Each register-resident width class (up to 4, 8, 20, 32 values a thread) and the loop past it."""
+    from nanocompile_amd import kernels
+    rng = np.random.default_rng(k)
+    x = rng.standard_normal((5, k)).astype(np.float32)
+    x[rng.random(x.shape) < 0.01] *= 20
+    x[2] = 0.0
+    xq, xs = kernels.quantize_token(x)
+    exq, exs = R.quantize_token(x)
+    assert np.array_equal(xq.numpy(), exq) and np.array_equal(bits(xs.numpy()), bits(exs))
