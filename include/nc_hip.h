@@ -228,7 +228,9 @@ int32_t nc_softmax_causal(void **p, const int64_t *s);
 /* Rotates the q and k heads of each qkv row by RoPE (q in place) and appends
  * k and v to the cache at positions past+i (models/qwen2.py:134-145: keys are
  * cached after rotation).
- * p: [qkv f32[M,(heads+2*kv)*D], kcache f32[kv,C,D], vcache f32[kv,C,D], inv_freq f32[D/2]];
+ * cos and sin come from the cache's table (nc_rope_table) when given: the same bits.
+ * p: [qkv f32[M,(heads+2*kv)*D], kcache f32[kv,C,D], vcache f32[kv,C,D], inv_freq f32[D/2],
+ *     pos i64[1] or NULL, rope table f32[2,C,D/2] or NULL];
  * s: [M, heads, kv, D, past, C] */
 int32_t nc_rope_append(void **p, const int64_t *s);
 

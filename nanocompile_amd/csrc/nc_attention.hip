@@ -94,12 +94,15 @@ __device__ __forceinline__ void rope_pair(float x0, float x1, float c, float s, 
 }
 
 // qkv[M, (H + 2 * KV * D)] rows: q heads rotated in place; k heads rotated and
-// written with v into the cache at positions past + i.
+// written with v into the cache at positions past + i. cos and sin come from
+// the cache's table (nc_rope_table: the same nc_cosf / nc_sinf bits) when
+// given, else are computed here.
 __global__ __launch_bounds__(kThreads) void rope_append(float *__restrict__ qkv, float *__restrict__ kcache,
                                                         float *__restrict__ vcache,
                                                         const float *__restrict__ inv_freq, int heads, int kv_heads,
                                                         int D, int past, int capacity,
-                                                        const int64_t *__restrict__ pos_ptr, int32_t *__restrict__ error) {
+                                                        const int64_t *__restrict__ pos_ptr, int32_t *__restrict__ error,
+                                                        const float *__restrict__ table) {
     if (pos_ptr && !position_fits(pos_ptr, (int)gridDim.x, capacity, error, past)) return;
     const int i = blockIdx.x;
     const int half = D / 2;
@@ -110,8 +113,15 @@ __global__ __launch_bounds__(kThreads) void rope_append(float *__restrict__ qkv,
     const int pairs = (heads + kv_heads) * half;
     for (int u = threadIdx.x; u < pairs; u += kThreads) {
         const int head = u / half, j = u - head * half;
-        const float ang = __fmul_rn(fpos, inv_freq[j]);
-        const float c = nc_cosf(ang), s = nc_sinf(ang);
+        float c, s;
+        if (table) {
+            c = table[(size_t)pos * half + j];
+            s = table[((size_t)capacity + pos) * half + j];
+        } else {
+            const float ang = __fmul_rn(fpos, inv_freq[j]);
+            c = nc_cosf(ang);
+            s = nc_sinf(ang);
+        }
         float *x = row + head * D;
         float y0, y1;
         rope_pair(x[j], x[j + half], c, s, y0, y1);
@@ -395,7 +405,8 @@ float bits_to_float(int64_t bits) {
 }  // namespace
 
 // p: [qkv f32[M, (H + 2*KV*D)] (q rotated in place), kcache f32[KV, C, D], vcache f32[KV, C, D],
-//     inv_freq f32[D/2], pos i64[1] | NULL];  s: [M, heads, kv_heads, D, past, capacity]
+//     inv_freq f32[D/2], pos i64[1] | NULL, rope table f32[2, C, D/2] | NULL];
+// s: [M, heads, kv_heads, D, past, capacity]
 // With pos, past is read from the device when the kernel runs (s[4] is ignored).
 NC_EXPORT int32_t nc_rope_append(void **p, const int64_t *s) {
     NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3], "nc_rope_append: null operand");
@@ -407,7 +418,7 @@ NC_EXPORT int32_t nc_rope_append(void **p, const int64_t *s) {
     if (M == 0) return NC_OK;
     hipLaunchKernelGGL(rope_append, dim3((unsigned)M), dim3(kThreads), 0, nc::stream(), (float *)p[0],
                        (float *)p[1], (float *)p[2], (const float *)p[3], (int)heads, (int)kv, (int)D,
-                       pos ? 0 : (int)past, (int)cap, pos, nc::error_word());
+                       pos ? 0 : (int)past, (int)cap, pos, nc::error_word(), (const float *)p[5]);
     return nc::launched("rope_append");
 }
 

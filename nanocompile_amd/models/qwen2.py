@@ -316,7 +316,7 @@ class Qwen2:
             hip.call("nc_rms_norm_quant", [None, self.xq, self.xs, self.x, w["g1"]], [m, H, eps])
             q, s = w["qkv"]
             hip.call("nc_matmul_i8_token", [self.qkv, self.xq, self.xs, q, s, w["qkv_b"], None], [m, W, H, s_qkv])
-            hip.call("nc_rope_append", [self.qkv, kc, vc, self.inv_freq, pos],
+            hip.call("nc_rope_append", [self.qkv, kc, vc, self.inv_freq, pos, cache.rope],
                      [m, heads, kv, D, past, cache.capacity])
             hip.call("nc_attention", [self.ctx, self.qkv, kc, vc, pos, cache.work],
                      [m, heads, kv, D, past, cache.capacity, float_bits(self.scale), cache.work_bytes])
@@ -344,7 +344,7 @@ class Qwen2:
             kc, vc = cache.layer(i)
             hip.call("nc_rms_norm_quant", [self.normed, self.xq, self.xs, self.x, w["g1"]], [m, H, eps])
             self._project(w["qkv"], self.normed, self.qkv, m, W, H, bias=w["qkv_b"])
-            hip.call("nc_rope_append", [self.qkv, kc, vc, self.inv_freq, pos],
+            hip.call("nc_rope_append", [self.qkv, kc, vc, self.inv_freq, pos, cache.rope],
                      [m, heads, kv, D, past, cache.capacity])
             hip.call("nc_attention", [self.ctx, self.qkv, kc, vc, pos, cache.work],
                      [m, heads, kv, D, past, cache.capacity, float_bits(self.scale), cache.work_bytes])

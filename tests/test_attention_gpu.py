@@ -177,3 +177,31 @@ def test_decode_attention_with_the_rope_table(gpu, host, past):
                  [heads, kv, d, past, cap, float_bits(scale), nbytes])
         assert np.array_equal(bits(ctx.numpy()), bits(expected)), tab is None
 
+
+
+@pytest.mark.parametrize("m,past", [(1, 0), (5, 37), (512, 0), (130, 70)])
+def test_rope_append_with_the_table_is_the_oracle(gpu, host, m, past):
+    """nc_rope_append reading cos and sin from the cache's table gives the oracle's bits
+    (rotated q in place, rotated k and v in the cache), as computing them does."""
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import DeviceArray
+    print(f"rope_append table m={m} past={past}", flush=True)
+    rng = np.random.default_rng(m + past)
+    heads, kv, d = 14, 2, 64
+    cap = past + m + 3
+    qkv, kc, vc = setup(rng, heads, kv, d, cap, m)
+    inv = inverse_frequencies(d, 1e6)
+    dinv = DeviceArray.from_host(inv)
+    table = DeviceArray((2, cap, d // 2), np.float32)
+    hip.call("nc_rope_table", [table, dinv], [cap, d])
+    results = []
+    for tab in (table, None):
+        dq, dk, dv = DeviceArray.from_host(qkv), DeviceArray.from_host(kc), DeviceArray.from_host(vc)
+        hip.call("nc_rope_append", [dq, dk, dv, dinv, None, tab], [m, heads, kv, d, past, cap])
+        results.append([bits(a.numpy()) for a in (dq, dk, dv)])
+    for got, want in zip(results[0], results[1]):
+        assert np.array_equal(got, want)
+    hq, hk, hv = qkv.copy(), kc.copy(), vc.copy()
+    host.rope_append_attention(hq, hk, hv, inv, heads, kv, d, past, 0.125)     # rotates and appends in place
+    assert np.array_equal(results[0][0], bits(hq)) and np.array_equal(results[0][1], bits(hk))
+    assert np.array_equal(results[0][2], bits(hv))
