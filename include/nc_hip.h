@@ -242,10 +242,12 @@ int32_t nc_rope_append(void **p, const int64_t *s);
  * workgroup per (64-key chunk, KV head, 4 query rows) attends the rows' query
  * heads of the group to its chunk; a second launch combines the chunks. The
  * reference materializes the [heads, M, keys] scores instead (README.md:317).
+ * With xq and xs, ctx's per-token int8 (nc_quantize_token_i8's bits) is written
+ * too, by the combine itself when a row's chunk results fit its LDS.
  * p: [ctx f32[M,heads*D], qkv (q rotated), kcache, vcache, pos i64[1] or NULL,
  *     work f32 (the chunk results: heads * ceil(keys / 64) * (D + 2) floats per query
  *     row, keys = C with pos, else past + M; fewer than M rows' worth takes the rows
- *     in slabs)];
+ *     in slabs), xq i8[M,heads*D] or NULL, xs f32[M] or NULL];
  * s: [M, heads, kv, D, past, C, scale as float32 bits, work bytes] (D 16, 32 or 64;
  *    at most 16384 keys) */
 int32_t nc_attention(void **p, const int64_t *s);

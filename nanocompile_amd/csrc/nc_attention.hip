@@ -271,6 +271,56 @@ __global__ __launch_bounds__(64) void attention_combine(float *__restrict__ ctx,
     if (lane < D) ctx[(size_t)(i0 + r) * heads * D + h * D + lane] = out;
 }
 
+// The combine of a whole query row, one wave per head (grid rows, heads x 64
+// threads), then the row's per-token int8 quantization (nc_quant.hip's
+// quantize_token: the maximum of |ctx| over the row, its scale, each value
+// quantized) in the same launch: ctx, xq and xs with the bits of a combine
+// followed by nc_quantize_token_i8.
+template <int D>
+__global__ __launch_bounds__(1024) void attention_combine_quant(float *__restrict__ ctx, int8_t *__restrict__ xq,
+                                                                float *__restrict__ xs, const float *__restrict__ part,
+                                                                int heads, int past, int capacity, int i0, int rows,
+                                                                int M, int jstride, const int64_t *__restrict__ pos_ptr) {
+    if (pos_ptr) {
+        const int64_t p = *pos_ptr;
+        if (p < 0 || p + M > capacity) return;            // the chunk kernel reported it
+        past = (int)p;
+    }
+    extern __shared__ __align__(16) float results_all[];   // [heads][jstride][D + 2]
+    __shared__ float maxima[16];
+    const int r = blockIdx.x, lane = threadIdx.x & 63, h = threadIdx.x >> 6;
+    const int J = (past + i0 + r + 1 + nc::kChunk - 1) / nc::kChunk;
+    float *results = results_all + (size_t)h * jstride * (D + 2);
+    const float *src = chunk_result(part, h, rows, r, jstride, 0, D);
+    const int total = J * (D + 2);
+    constexpr int kBatch = 8;
+    for (int base = 0; base < total; base += 64 * kBatch) {
+        float v[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int at = base + lane + 64 * u;
+            v[u] = at < total ? src[at] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int at = base + lane + 64 * u;
+            if (at < total) results[at] = v[u];
+        }
+    }
+    const float out = nc::combine_chunks(J, lane < D ? lane : 0,
+                                         [&](int c, int k) { return results[c * (D + 2) + k]; });
+    const size_t at = (size_t)(i0 + r) * heads * D + h * D + lane;
+    if (lane < D) ctx[at] = out;
+    const float mag = nc::wave_max_f32(lane < D ? fabsf(out) : 0.0f);
+    if (lane == 0) maxima[h] = mag;
+    __syncthreads();
+    float row_max = maxima[0];
+    for (int i = 1; i < heads; ++i) row_max = fmaxf(row_max, maxima[i]);
+    const float scale = nc::token_scale(row_max);
+    if (lane < D) xq[at] = nc::quantize_value(out, scale);
+    if (threadIdx.x == 0) xs[i0 + r] = scale;
+}
+
 // Decode: one new token at position past. Grid (chunks, kv_heads). Wave w
 // attends query head g * group + w (then + 8, ... for larger groups), each
 // wave rotating its own head's query; wave 0 of the chunk holding the new key
@@ -444,6 +494,16 @@ int32_t launch_combine(float *ctx, const float *part, int64_t heads, int64_t pas
     return nc::launched("attention_combine");
 }
 
+template <int D>
+int32_t launch_combine_quant(void **p, const float *part, int64_t heads, int64_t past, int64_t cap, int64_t i0,
+                             int64_t rows, int64_t M, int64_t jstride, const int64_t *pos) {
+    const size_t lds = (size_t)heads * jstride * (D + 2) * sizeof(float);
+    hipLaunchKernelGGL(attention_combine_quant<D>, dim3((unsigned)rows), dim3((unsigned)(64 * heads)), lds,
+                       nc::stream(), (float *)p[0], (int8_t *)p[6], (float *)p[7], part, (int)heads, (int)past,
+                       (int)cap, (int)i0, (int)rows, (int)M, (int)jstride, pos);
+    return nc::launched("attention_combine_quant");
+}
+
 // Query rows in slabs whose chunk results fit the workspace; each slab is a
 // chunk launch and a combine launch.
 template <int D>
@@ -454,6 +514,10 @@ int32_t launch_prefill(void **p, int64_t M, int64_t heads, int64_t kv, int64_t p
     int64_t slab = std::min<int64_t>(M, work_bytes / row_bytes);
     NC_REQUIRE(slab >= 1, "nc_attention: the workspace is smaller than one query row's chunk results "
                           "(heads * ceil(keys / 64) * (head_dim + 2) floats)");
+    // with xq and xs, the per-token int8 of ctx too: in the combine's own launch
+    // while a row's chunk results fit its workgroup's LDS, else after
+    const bool quantize = p[6] && p[7];
+    const bool fused = quantize && heads <= 16 && heads * jstride * (D + 2) * (int64_t)sizeof(float) <= 64 * 1024;
     if (slab < M && slab >= kRowsPerBlock) slab -= slab % kRowsPerBlock;
     const int64_t host_past = pos ? 0 : past;
     for (int64_t i0 = 0; i0 < M; i0 += slab) {
@@ -465,9 +529,14 @@ int32_t launch_prefill(void **p, int64_t M, int64_t heads, int64_t kv, int64_t p
                            (const float *)p[3], (int)heads, (int)kv, (int)host_past, (int)cap, scale, (int)i0,
                            (int)rows, (int)M, (int)jstride, pos, nc::error_word());
         int32_t rc = nc::launched("attention_rows_chunks");
-        if (rc == NC_OK) rc = launch_combine<D>((float *)p[0], work, heads, host_past, cap, i0, rows, M, jstride, pos);
+        if (rc == NC_OK && fused)
+            rc = launch_combine_quant<D>(p, work, heads, host_past, cap, i0, rows, M, jstride, pos);
+        else if (rc == NC_OK)
+            rc = launch_combine<D>((float *)p[0], work, heads, host_past, cap, i0, rows, M, jstride, pos);
         if (rc != NC_OK) return rc;
     }
+    if (quantize && !fused)        // ctx whole first: the per-token scale spans every head of a row
+        return nc::quantize_token_rows((int8_t *)p[6], (float *)p[7], (const float *)p[0], (int)M, (int)(heads * D));
     return NC_OK;
 }
 
@@ -490,7 +559,7 @@ int32_t launch_decode(void **p, const int64_t *s, const int64_t *pos, float *wor
 }  // namespace
 
 // p: [ctx f32[M, heads*D], qkv f32[M, (H + 2*KV*D)] (q rotated), kcache, vcache, pos i64[1] | NULL,
-//     work f32[...]];
+//     work f32[...], xq i8[M, heads*D] | NULL, xs f32[M] | NULL (with both: ctx's per-token int8 too)];
 // s: [M, heads, kv_heads, D, past, capacity, scale as float32 bits, work bytes]  (D 16, 32 or 64)
 // With pos, past is read from the device when the kernels run (s[4] is ignored). The workspace
 // holds the chunk results; one query row needs heads * ceil(keys / 64) * (D + 2) floats, keys =

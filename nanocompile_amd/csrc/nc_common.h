@@ -173,6 +173,8 @@ int32_t gemm_i8_token(int tile, int epi, void *out, const int8_t *xq, const floa
                       const float *ws2, int M, int N, int K);
 // A tile's primitives: [BM, BN, BK, WM, WN, NS, threads, LDS bytes]; NC_BAD_ARGS past the table.
 int32_t gemm_tile_info(int tile, int64_t *out);
+// The per-token quantizer (nc_quant.hip) on M rows of K: xq, xs from x.
+int32_t quantize_token_rows(int8_t *xq, float *xs, const float *x, int M, int K);
 }  // namespace nc
 
 // A launcher's argument checks: on failure, record why and return NC_BAD_ARGS.

@@ -161,17 +161,23 @@ NC_EXPORT int32_t nc_quantize_rows_i8(void **p, const int64_t *s) {
     return nc::launched("quantize_rows");
 }
 
-// p: [xq i8[M,K], xs f32[M], x f32[M,K]];  s: [M, K]
-NC_EXPORT int32_t nc_quantize_token_i8(void **p, const int64_t *s) {
-    NC_REQUIRE(p && s && p[0] && p[1] && p[2], "nc_quantize_token_i8: null operand");
-    NC_REQUIRE(s[0] >= 0 && s[1] > 0 && s[0] < (1 << 26) && s[1] < (1 << 26), "nc_quantize_token_i8: bad shape");
-    if (s[0] == 0) return NC_OK;
-    const int M = (int)s[0], K = (int)s[1];
+namespace nc {
+int32_t quantize_token_rows(int8_t *xq, float *xs, const float *x, int M, int K) {
+    void *p[3] = {xq, xs, const_cast<float *>(x)};
+    if (M == 0) return NC_OK;
     if (K <= 4 * kThreads) return launch_token<4>(p, M, K);
     if (K <= 8 * kThreads) return launch_token<8>(p, M, K);
     if (K <= 20 * kThreads) return launch_token<20>(p, M, K);
     if (K <= 32 * kThreads) return launch_token<32>(p, M, K);
     return launch_token<0>(p, M, K);
+}
+}  // namespace nc
+
+// p: [xq i8[M,K], xs f32[M], x f32[M,K]];  s: [M, K]
+NC_EXPORT int32_t nc_quantize_token_i8(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2], "nc_quantize_token_i8: null operand");
+    NC_REQUIRE(s[0] >= 0 && s[1] > 0 && s[0] < (1 << 26) && s[1] < (1 << 26), "nc_quantize_token_i8: bad shape");
+    return nc::quantize_token_rows((int8_t *)p[0], (float *)p[1], (const float *)p[2], (int)s[0], (int)s[1]);
 }
 
 // p: [normed f32[M,K] | NULL, xq i8[M,K], xs f32[M], x f32[M,K], gamma f32[K]];

@@ -9,8 +9,8 @@ driver only uploads token ids and downloads what the caller asks for:
     rms_norm + per-token int8 ......... nc_rms_norm_quant
     q, k, v projections + bias ........ nc_matmul_i8_token (rows concatenated)
     RoPE, cache append ................ nc_rope_append
-    attention (GQA, causal) ........... nc_attention
-    per-token int8 of the context ..... nc_quantize_token_i8
+    attention (GQA, causal), and the
+    per-token int8 of the context ..... nc_attention
     o projection + residual ........... nc_matmul_i8_token (in place on x)
     rms_norm + per-token int8 ......... nc_rms_norm_quant
     gate, up, silu(gate) * up ......... nc_matmul_i8_token_swiglu
@@ -318,9 +318,9 @@ class Qwen2:
             hip.call("nc_matmul_i8_token", [self.qkv, self.xq, self.xs, q, s, w["qkv_b"], None], [m, W, H, s_qkv])
             hip.call("nc_rope_append", [self.qkv, kc, vc, self.inv_freq, pos, cache.rope],
                      [m, heads, kv, D, past, cache.capacity])
-            hip.call("nc_attention", [self.ctx, self.qkv, kc, vc, pos, cache.work],
+            # attention, its combine also quantizing ctx per token for the o projection
+            hip.call("nc_attention", [self.ctx, self.qkv, kc, vc, pos, cache.work, self.xq, self.xs],
                      [m, heads, kv, D, past, cache.capacity, float_bits(self.scale), cache.work_bytes])
-            hip.call("nc_quantize_token_i8", [self.xq, self.xs, self.ctx], [m, Q])
             q, s = w["o"]
             hip.call("nc_matmul_i8_token", [self.x, self.xq, self.xs, q, s, None, self.x], [m, H, Q, s_o])
             hip.call("nc_rms_norm_quant", [None, self.xq, self.xs, self.x, w["g2"]], [m, H, eps])

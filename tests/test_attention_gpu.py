@@ -205,3 +205,33 @@ def test_rope_append_with_the_table_is_the_oracle(gpu, host, m, past):
     host.rope_append_attention(hq, hk, hv, inv, heads, kv, d, past, 0.125)     # rotates and appends in place
     assert np.array_equal(results[0][0], bits(hq)) and np.array_equal(results[0][1], bits(hk))
     assert np.array_equal(results[0][2], bits(hv))
+
+
+@pytest.mark.parametrize("d,heads,kv,m,past,slab", [(64, 14, 2, 130, 70, None), (64, 14, 2, 130, 70, 8),
+                                                    (32, 4, 2, 9, 0, None), (64, 18, 2, 20, 5, None),
+                                                    (64, 14, 2, 8, 1200, None)])
+def test_prefill_attention_quantizes_ctx_per_token(gpu, host, d, heads, kv, m, past, slab):
+    """nc_attention with xq and xs: ctx unchanged and its per-token int8 the oracle's, whether the
+    combine quantizes (a row's chunk results in LDS) or a separate launch does (more than 16 heads,
+    contexts whose chunk results do not fit)."""
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import DeviceArray
+    from nanocompile_amd.kernels import float_bits
+    from oracle import reference as R
+    print(f"attention quantize d={d} heads={heads} m={m} past={past} slab={slab}", flush=True)
+    rng = np.random.default_rng(m + past + heads)
+    cap = past + m
+    qkv, kc, vc = setup(rng, heads, kv, d, cap, m)
+    inv = inverse_frequencies(d, 1e6)
+    scale = float(np.float32(d ** -0.5))
+    expected = host.rope_append_attention(qkv.copy(), kc.copy(), vc.copy(), inv, heads, kv, d, past, scale)
+    dq, dk, dv = DeviceArray.from_host(qkv), DeviceArray.from_host(kc), DeviceArray.from_host(vc)
+    hip.call("nc_rope_append", [dq, dk, dv, DeviceArray.from_host(inv)], [m, heads, kv, d, past, cap])
+    work, nbytes = workspace(heads, d, slab or m, past + m)
+    ctx = DeviceArray((m, heads * d), np.float32)
+    xq, xs = DeviceArray((m, heads * d), np.int8), DeviceArray((m,), np.float32)
+    hip.call("nc_attention", [ctx, dq, dk, dv, None, work, xq, xs],
+             [m, heads, kv, d, past, cap, float_bits(scale), nbytes])
+    assert np.array_equal(bits(ctx.numpy()), bits(expected))
+    eq, es = R.quantize_token(expected)
+    assert np.array_equal(xq.numpy(), eq) and np.array_equal(bits(xs.numpy()), bits(es))

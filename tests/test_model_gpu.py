@@ -305,3 +305,28 @@ def test_decode_advance_gathers_the_next_row(gpu):
     with pytest.raises(KernelError, match="out of range"):
         hip.sync()
     assert not x.numpy().any()
+
+
+def test_long_prompt_in_attention_slabs_is_bitwise_one_pass(gpu, monkeypatch):
+    """A 300-token prompt whose attention workspace holds only a few rows' chunk results (so
+    nc_attention takes the rows in slabs) gives the same logits and cache, bit for bit, as one pass."""
+    from nanocompile_amd.kernels import attention_workspace_bytes
+    from nanocompile_amd.models import qwen2
+    weights = random_weights(TINY, seed=5, std=TINY_STD)
+    model = qwen2.Qwen2(TINY, weights, max_tokens=320)
+    prompt = np.random.default_rng(8).integers(0, TINY.vocab_size, 300)
+    runs = []
+    for rows in (None, 5):
+        if rows is not None:                       # 5 rows' worth of chunk results: 60 slabs of 5 rows
+            per_row = attention_workspace_bytes(TINY.num_attention_heads, TINY.head_dim, 1, 310)
+            monkeypatch.setattr(qwen2, "WORKSPACE_BYTES", per_row * rows)
+        cache = model.new_cache(310)
+        assert rows is None or cache.work_bytes == attention_workspace_bytes(
+            TINY.num_attention_heads, TINY.head_dim, rows, 310)
+        logits = model.forward(prompt, cache)
+        step = model.forward([int(np.argmax(logits[-1]))], cache, last_only=True)
+        filled = cache.length                      # rows past it are whatever the allocation held
+        runs.append((bits(logits), bits(step), bits(cache.keys.numpy()[:, :, :filled]),
+                     bits(cache.values.numpy()[:, :, :filled])))
+    for a, b in zip(*runs):
+        assert np.array_equal(a, b)
