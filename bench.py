@@ -251,7 +251,7 @@ def block_measurements(model, seed: int = 7) -> dict:
                            "bytes_per_block": BLOCK_DECODE_BYTES,
                            "gbps": round(BLOCK_DECODE_BYTES / (per_block * 1e-6) / 1e9, 1),
                            "frac": round(BLOCK_DECODE_BYTES / (per_block * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
-                           "kernels_per_block": 5}
+                           "kernels_per_block": 6}
 
     # config 4: one block's prefill at seq = 512, past = 0 (all 24 blocks, per block), and its GEMMs alone
     m = 512

@@ -227,14 +227,14 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void attention_rows_chunks(
 
 // The combine of one query's chunk results: grid (heads, rows), one wave.
 // Row r of the slab is query row i0 + r at position past + i0 + r. The first
-// 512 floats of the row's results (every chunk up to 7 chunks at D = 64) are
-// loaded before the position is read.
+// 1024 floats of the row's results (every chunk up to 15 chunks, 960 keys, at
+// D = 64) are loaded before the position is read.
 template <int D>
 __global__ __launch_bounds__(64) void attention_combine(float *__restrict__ ctx, const float *__restrict__ part,
                                                         int heads, int past, int capacity, int i0, int rows, int M,
                                                         int jstride, const int64_t *__restrict__ pos_ptr) {
     extern __shared__ __align__(16) float results[];     // [J][D + 2]
-    constexpr int kBatch = 8;                            // independent loads a lane keeps in flight
+    constexpr int kBatch = 16;                           // independent loads a lane keeps in flight
     const int h = blockIdx.x, r = blockIdx.y, lane = threadIdx.x;
     const float *src = chunk_result(part, h, rows, r, jstride, 0, D);
     const int all = jstride * (D + 2);
