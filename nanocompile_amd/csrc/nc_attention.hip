@@ -30,7 +30,6 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kMaxKeys = 16384;     // dynamic LDS: one float per visible key
 
-__device__ __forceinline__ float nan_max(float a, float b) { return (a < b || b != b) ? b : a; }
 
 // The row-sum order of every float sum over a row in this library, for a
 // value per virtual thread already accumulated in `v` (thread tid holds
@@ -47,12 +46,12 @@ __device__ float row_sum(float v, float *scratch) {
 }
 
 __device__ float row_max(float v, float *scratch) {
-    v = nc::butterfly<64>(v, [](float a, float b) { return nan_max(a, b); });
+    v = nc::butterfly<64>(v, [](float a, float b) { return nc::nan_max(a, b); });
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     __syncthreads();
     if (lane == 0) scratch[wave] = v;
     __syncthreads();
-    const float r = nan_max(nan_max(scratch[0], scratch[1]), nan_max(scratch[2], scratch[3]));
+    const float r = nc::nan_max(nc::nan_max(scratch[0], scratch[1]), nc::nan_max(scratch[2], scratch[3]));
     __syncthreads();
     return r;
 }
@@ -60,7 +59,7 @@ __device__ float row_max(float v, float *scratch) {
 // Softmax over e[0..T) in LDS, in place: z -> p, in the stated order.
 __device__ void softmax_lds(float *e, int T, float *scratch) {
     float m = -__builtin_inff();
-    for (int t = threadIdx.x; t < T; t += kThreads) m = nan_max(m, e[t]);
+    for (int t = threadIdx.x; t < T; t += kThreads) m = nc::nan_max(m, e[t]);
     m = row_max(m, scratch);
     float partial = 0.0f;
     for (int t = threadIdx.x; t < T; t += kThreads) {
@@ -446,11 +445,6 @@ __global__ __launch_bounds__(kThreads) void rope_rows(float *__restrict__ y, con
     }
 }
 
-float bits_to_float(int64_t bits) {
-    union { uint32_t u; float f; } c;
-    c.u = (uint32_t)bits;
-    return c.f;
-}
 
 }  // namespace
 
@@ -549,7 +543,7 @@ int32_t launch_decode(void **p, const int64_t *s, const int64_t *pos, float *wor
     const int64_t host_past = pos ? 0 : past;
     hipLaunchKernelGGL((attention_decode_chunks<D, TABLE>), dim3((unsigned)jstride, (unsigned)kv), dim3(64 * kWaves), 0,
                        nc::stream(), work, (const float *)p[1], (float *)p[2], (float *)p[3], (const float *)p[4],
-                       (const float *)p[6], (int)heads, (int)kv, (int)host_past, (int)cap, bits_to_float(s[5]),
+                       (const float *)p[6], (int)heads, (int)kv, (int)host_past, (int)cap, nc::bits_to_float(s[5]),
                        (int)jstride, pos, nc::error_word());
     const int32_t rc = nc::launched("attention_decode_chunks");
     if (rc != NC_OK) return rc;
@@ -573,7 +567,7 @@ NC_EXPORT int32_t nc_attention(void **p, const int64_t *s) {
                    M <= cap && M < 65536 && heads < 65536 && work_bytes >= 0,
                "nc_attention: bad shape (head_dim 16, 32 or 64; at most 16384 keys)");
     if (M == 0) return NC_OK;
-    const float scale = bits_to_float(s[6]);
+    const float scale = nc::bits_to_float(s[6]);
     float *work = (float *)p[5];
     if (D == 64) return launch_prefill<64>(p, M, heads, kv, past, cap, scale, pos, work, work_bytes);
     if (D == 32) return launch_prefill<32>(p, M, heads, kv, past, cap, scale, pos, work, work_bytes);

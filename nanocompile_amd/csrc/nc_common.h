@@ -177,6 +177,16 @@ int32_t gemm_tile_info(int tile, int64_t *out);
 int32_t quantize_token_rows(int8_t *xq, float *xs, const float *x, int M, int K);
 }  // namespace nc
 
+namespace nc {
+// A float32 passed through an int64 size slot (eps, scale): its bits in the low 32.
+inline float bits_to_float(int64_t bits) {
+    const uint32_t u = (uint32_t)bits;
+    float f;
+    __builtin_memcpy(&f, &u, sizeof f);
+    return f;
+}
+}  // namespace nc
+
 // A launcher's argument checks: on failure, record why and return NC_BAD_ARGS.
 #define NC_REQUIRE(cond, text)                 \
     do {                                       \

@@ -160,11 +160,6 @@ __global__ __launch_bounds__(64 * W) void gemv_decode(float *__restrict__ out, c
     }
 }
 
-float bits_to_float(int64_t bits) {
-    union { uint32_t u; float f; } c;
-    c.u = (uint32_t)bits;
-    return c.f;
-}
 
 // Lanes per row: 8 (one 128-byte line per load), or 16 for the long down
 // projection (half the loads each). Waves per workgroup: 1, or 4 for the long
@@ -191,7 +186,7 @@ int32_t launch_decode(void **p, int N, float eps) {
 NC_EXPORT int32_t nc_decode_projection(void **p, const int64_t *s) {
     NC_REQUIRE(p && s && p[0] && p[1] && p[3] && p[4], "nc_decode_projection: null operand");
     const int64_t N = s[0], K = s[1], kind = s[2];
-    const float eps = bits_to_float(s[3]);
+    const float eps = nc::bits_to_float(s[3]);
     NC_REQUIRE(N > 0 && N < (1 << 24) && kind >= 0 && kind <= 2, "nc_decode_projection: bad shape");
     NC_REQUIRE(kind == 1 || p[2], "nc_decode_projection: rms_norm needs gamma");
     NC_REQUIRE(kind != 0 || p[5], "nc_decode_projection: q, k, v need their bias");

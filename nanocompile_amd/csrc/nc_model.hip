@@ -206,11 +206,6 @@ __global__ __launch_bounds__(64 * WAVES) void lm_head_ring(float *logits, unsign
     if (best) publish_argmax<WAVES>(valid ? argmax_key(acc, n) : 0ull, best, m, slots, wkeys);
 }
 
-float bits_to_float(int64_t bits) {
-    union { uint32_t u; float f; } c;
-    c.u = (uint32_t)bits;
-    return c.f;
-}
 
 __global__ void fill_u64(unsigned long long *p, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -312,12 +307,12 @@ NC_EXPORT int32_t nc_lm_head(void **p, const int64_t *s) {
     if (s[2] == 896) {       // the model's width: the ring kernel, 24 loads (24 KB) in flight per wave
         hipLaunchKernelGGL((lm_head_ring<W, 896, 24>), grid, dim3(64 * W), 0, nc::stream(), (float *)p[0],
                            (unsigned long long *)p[1], (const float *)p[2], (const float4 *)p[3], s[1],
-                           (const float *)p[4], bits_to_float(s[3]), bias, residual, slots);
+                           (const float *)p[4], nc::bits_to_float(s[3]), bias, residual, slots);
         return nc::launched("lm_head_ring");
     }
     hipLaunchKernelGGL((lm_head<W>), grid, dim3(64 * W), (size_t)s[2] * sizeof(float), nc::stream(), (float *)p[0],
                        (unsigned long long *)p[1], (const float *)p[2], (const float4 *)p[3], s[1], (int)s[2],
-                       (const float *)p[4], bits_to_float(s[3]), bias, residual, slots);
+                       (const float *)p[4], nc::bits_to_float(s[3]), bias, residual, slots);
     return nc::launched("lm_head");
 }
 

@@ -143,11 +143,6 @@ int32_t launch_rms(void **p, int M, int K, float eps) {
     return nc::launched("rms_norm_quant");
 }
 
-float bits_to_float(int64_t bits) {
-    union { uint32_t u; float f; } c;
-    c.u = (uint32_t)bits;
-    return c.f;
-}
 
 }  // namespace
 
@@ -186,7 +181,7 @@ NC_EXPORT int32_t nc_rms_norm_quant(void **p, const int64_t *s) {
     NC_REQUIRE(p && s && p[1] && p[2] && p[3] && p[4], "nc_rms_norm_quant: null operand");
     NC_REQUIRE(s[0] >= 0 && s[1] > 0 && s[0] < (1 << 26) && s[1] <= 32 * kThreads, "nc_rms_norm_quant: bad shape");
     const int M = (int)s[0], K = (int)s[1];
-    const float eps = bits_to_float(s[2]);
+    const float eps = nc::bits_to_float(s[2]);
     if (M == 0) return NC_OK;
     if (K <= 4 * kThreads) return launch_rms<4>(p, M, K, eps);
     if (K <= 8 * kThreads) return launch_rms<8>(p, M, K, eps);
