@@ -226,14 +226,15 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void attention_rows_chunks(
 
 // The combine of one query's chunk results: grid (heads, rows), one wave.
 // Row r of the slab is query row i0 + r at position past + i0 + r. The first
-// 1024 floats of the row's results (every chunk up to 15 chunks, 960 keys, at
-// D = 64) are loaded before the position is read.
-template <int D>
+// 64 * BATCH floats of the row's results (BATCH = 8: up to 7 chunks, 448 keys,
+// at D = 64; 16: up to 15 chunks, 960 keys) are loaded before the position is
+// read, all in flight at once.
+template <int D, int BATCH>
 __global__ __launch_bounds__(64) void attention_combine(float *__restrict__ ctx, const float *__restrict__ part,
                                                         int heads, int past, int capacity, int i0, int rows, int M,
                                                         int jstride, const int64_t *__restrict__ pos_ptr) {
     extern __shared__ __align__(16) float results[];     // [J][D + 2]
-    constexpr int kBatch = 16;                           // independent loads a lane keeps in flight
+    constexpr int kBatch = BATCH;                        // independent loads a lane keeps in flight
     const int h = blockIdx.x, r = blockIdx.y, lane = threadIdx.x;
     const float *src = chunk_result(part, h, rows, r, jstride, 0, D);
     const int all = jstride * (D + 2);
@@ -470,12 +471,12 @@ namespace {
 
 // LDS of a combine: J chunk results of D + 2 floats, 67.6 KB at 16384 keys and
 // D = 64, past the 64 KB a launch gets without asking.
-template <int D>
-int32_t launch_combine(float *ctx, const float *part, int64_t heads, int64_t past, int64_t cap, int64_t i0,
-                       int64_t rows, int64_t M, int64_t jstride, const int64_t *pos) {
+template <int D, int BATCH>
+int32_t launch_combine_batch(float *ctx, const float *part, int64_t heads, int64_t past, int64_t cap, int64_t i0,
+                             int64_t rows, int64_t M, int64_t jstride, const int64_t *pos) {
     static bool raised = false;
     if (!raised) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&attention_combine<D>),
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&attention_combine<D, BATCH>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024) != hipSuccess) {
             nc::set_message("attention: could not raise the LDS limit of the combine");
             return NC_LAUNCH_FAILED;
@@ -483,9 +484,19 @@ int32_t launch_combine(float *ctx, const float *part, int64_t heads, int64_t pas
         raised = true;
     }
     const size_t lds = (size_t)jstride * (D + 2) * sizeof(float);
-    hipLaunchKernelGGL(attention_combine<D>, dim3((unsigned)heads, (unsigned)rows), dim3(64), lds, nc::stream(), ctx,
-                       part, (int)heads, (int)past, (int)cap, (int)i0, (int)rows, (int)M, (int)jstride, pos);
+    hipLaunchKernelGGL((attention_combine<D, BATCH>), dim3((unsigned)heads, (unsigned)rows), dim3(64), lds,
+                       nc::stream(), ctx, part, (int)heads, (int)past, (int)cap, (int)i0, (int)rows, (int)M,
+                       (int)jstride, pos);
     return nc::launched("attention_combine");
+}
+
+// The first batch of loads sized to the chunk results a row can have.
+template <int D>
+int32_t launch_combine(float *ctx, const float *part, int64_t heads, int64_t past, int64_t cap, int64_t i0,
+                       int64_t rows, int64_t M, int64_t jstride, const int64_t *pos) {
+    if (jstride * (D + 2) <= 64 * 8)
+        return launch_combine_batch<D, 8>(ctx, part, heads, past, cap, i0, rows, M, jstride, pos);
+    return launch_combine_batch<D, 16>(ctx, part, heads, past, cap, i0, rows, M, jstride, pos);
 }
 
 template <int D>
