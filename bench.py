@@ -54,7 +54,7 @@ PROMPT, NEW_TOKENS = 128, 256
 CALIBRATION_BYTES = 256 * 2**20
 
 
-LM_HEAD_KERNEL = "lm_head_ring<4, 896, 24>"     # nc_lm_head at the model's width (nc_model.hip)
+LM_HEAD_KERNEL = "lm_head_ring<896, 24>"     # nc_lm_head at the model's width (nc_model.hip)
 
 
 def gemv_bytes(m: int, n: int, k: int) -> int:

@@ -270,8 +270,8 @@ int32_t nc_pack_rows64(void **p, const int64_t *s);
  * rms-normed first (eps = s[3] as float32 bits). With bias, + bias[n] after the
  * sum, and with residual, residual + that: the reference's float32 linear
  * (nn.py:24-31) and residual add, so the same kernel is the float32 model's
- * projections. With s[4] = 1 the argmax is left as one key per workgroup,
- * best u64[M, G] with G = ceil(ceil(V/64)/4), for nc_argmax_index or
+ * projections. With s[4] = 1 the argmax is left as one key per workgroup
+ * (of 64 rows), best u64[M, G] with G = ceil(V/64), for nc_argmax_index or
  * nc_decode_advance to reduce (no atomics, nothing to clear); with s[4] = 0,
  * best u64[M] receives atomic maxima and must be cleared first.
  * p: [logits f32[M,V] or NULL, best or NULL, x f32[M,H], packed table,

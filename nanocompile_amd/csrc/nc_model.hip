@@ -48,44 +48,54 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int64_t n) {
     return ((unsigned long long)ord << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)n);
 }
 
-// With gamma, x is first rms-normed (nn.py:34-38) in the row kernels' order:
-// thread t sums x[t]^2, x[t+256]^2, ... in order; butterfly per wave;
-// (w0 + w1) + (w2 + w3). The workgroup is 256 threads, so thread t is virtual
-// thread t of that order.
-__device__ float sum4(float v, float *scratch) {
-    v = nc::wave_sum_f32(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) scratch[wave] = v;
-    __syncthreads();
-    return __fadd_rn(__fadd_rn(scratch[0], scratch[1]), __fadd_rn(scratch[2], scratch[3]));
+// Row m of x into LDS (sxh[0 .. H - 1]), rms-normed first (nn.py:34-38) when
+// gamma is given, in the row kernels' order: virtual thread t of 256 sums
+// x[t]^2, x[t+256]^2, ... in order; the butterfly over each group of 64
+// virtual threads; (w0 + w1) + (w2 + w3). The workgroup is one wave: lane l
+// holds virtual threads l, l + 64, l + 128 and l + 192.
+__device__ void head_prologue(float *sxh, const float *__restrict__ x, int H, const float *__restrict__ gamma,
+                              float eps) {
+    const int lane = threadIdx.x;
+    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int base = 0; base < H; base += 256) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int i = base + 64 * g + lane;
+            if (i < H) {
+                const float v = x[i];
+                sxh[i] = v;
+                s[g] = __fadd_rn(s[g], __fmul_rn(v, v));
+            }
+        }
+    }
+    if (gamma) {
+        float w[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) w[g] = nc::wave_sum_f32(s[g]);
+        const float total = __fadd_rn(__fadd_rn(w[0], w[1]), __fadd_rn(w[2], w[3]));
+        const float rcp = nc::div_rn(1.0f, nc::sqrt_rn(__fadd_rn(nc::div_rn(total, (float)H), eps)));
+        for (int i = lane; i < H; i += 64) sxh[i] = __fmul_rn(__fmul_rn(sxh[i], rcp), gamma[i]);
+    }
+    // (one wave: its own LDS writes land before its later reads)
 }
 
-// Row m's argmax key from this workgroup: the wave maxima, then either one
-// atomic maximum per wave into best[m] (slots == 0), or the workgroup's
-// maximum stored at best[m * slots + blockIdx.x] for the consumer to reduce
-// (slots == gridDim.x: no atomics, whose same-address serialization costs
-// 4-9 us over a head's 594 workgroups, and nothing to clear beforehand).
-// Every thread of the workgroup must call this.
-template <int WAVES>
-__device__ __forceinline__ void publish_argmax(unsigned long long key, unsigned long long *best, int64_t m, int slots,
-                                               unsigned long long *wkeys) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// Row m's argmax key from this workgroup (one wave): the wave maximum, then
+// either an atomic maximum into best[m] (slots == 0), or stored at
+// best[m * slots + blockIdx.x] for the consumer to reduce (slots == gridDim.x:
+// no atomics, whose same-address serialization costs 4-9 us over a head's
+// workgroups, and nothing to clear beforehand).
+__device__ __forceinline__ void publish_argmax(unsigned long long key, unsigned long long *best, int64_t m,
+                                               int slots) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         const unsigned long long other = __shfl_xor(key, off, 64);
         key = other > key ? other : key;
     }
+    if (threadIdx.x != 0) return;
     if (slots == 0) {
-        if (lane == 0 && key != 0ull) atomicMax(best + m, key);
-        return;
-    }
-    if (lane == 0) wkeys[wave] = key;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned long long k = wkeys[0];
-#pragma unroll
-        for (int i = 1; i < WAVES; ++i) k = wkeys[i] > k ? wkeys[i] : k;
-        best[m * slots + blockIdx.x] = k;
+        if (key != 0ull) atomicMax(best + m, key);
+    } else {
+        best[m * slots + blockIdx.x] = key;
     }
 }
 
@@ -99,32 +109,20 @@ __device__ __forceinline__ float head_epilogue(float acc, int64_t m, int64_t n, 
     return acc;
 }
 
-template <int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void lm_head(float *logits, unsigned long long *__restrict__ best,
-                                                      const float *__restrict__ x, const float4 *__restrict__ packed,
-                                                      int64_t V, int H, const float *__restrict__ gamma, float eps,
-                                                      const float *__restrict__ bias, const float *residual,
-                                                      int slots) {
+// One wave a workgroup, one block of 64 rows a wave: 2374 one-wave workgroups
+// for the model's vocabulary spread over the 256 CUs at most 10 waves a CU,
+// where workgroups of 4 waves left some CUs 12 (measured on MI355X: 91.1 us
+// for V = 151936 with 4-wave workgroups, as long as V = 163840's 10 waves a
+// CU, against 73.0 us for V = 131072's even 8).
+__global__ __launch_bounds__(64) void lm_head(float *logits, unsigned long long *__restrict__ best,
+                                              const float *__restrict__ x, const float4 *__restrict__ packed,
+                                              int64_t V, int H, const float *__restrict__ gamma, float eps,
+                                              const float *__restrict__ bias, const float *residual, int slots) {
     extern __shared__ float sxh[];
-    __shared__ float scratch[4];
-    __shared__ unsigned long long wkeys[WAVES];
     const int m = blockIdx.y;
-    float ss = 0.0f;
-    for (int i = threadIdx.x; i < H; i += 64 * WAVES) {
-        const float v = x[(size_t)m * H + i];
-        sxh[i] = v;
-        ss = __fadd_rn(ss, __fmul_rn(v, v));
-    }
-    __syncthreads();
-    if (gamma) {
-        static_assert(WAVES == 4, "the row-sum order needs 256 threads");
-        const float total = sum4(ss, scratch);
-        const float rcp = nc::div_rn(1.0f, nc::sqrt_rn(__fadd_rn(nc::div_rn(total, (float)H), eps)));
-        for (int i = threadIdx.x; i < H; i += 64 * WAVES) sxh[i] = __fmul_rn(__fmul_rn(sxh[i], rcp), gamma[i]);
-        __syncthreads();
-    }
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t blk = (int64_t)blockIdx.x * WAVES + wave;
+    head_prologue(sxh, x + (size_t)m * H, H, gamma, eps);
+    const int lane = threadIdx.x;
+    const int64_t blk = blockIdx.x;
     const int64_t n = blk * 64 + lane;
     const bool live = blk * 64 < V;
     const int k4n = H / 4;
@@ -142,7 +140,7 @@ __global__ __launch_bounds__(64 * WAVES) void lm_head(float *logits, unsigned lo
     }
     const bool valid = n < V;
     if (logits && valid) logits[(size_t)m * V + n] = head_epilogue(acc, m, n, V, bias, residual);
-    if (best) publish_argmax<WAVES>(valid ? argmax_key(acc, n) : 0ull, best, m, slots, wkeys);
+    if (best) publish_argmax(valid ? argmax_key(acc, n) : 0ull, best, m, slots);
 }
 
 // The same head for a width known at compile time, its loads kept in flight
@@ -151,42 +149,25 @@ __global__ __launch_bounds__(64 * WAVES) void lm_head(float *logits, unsigned lo
 // loads issued since), the first R issued before the x prologue. A loop that
 // issues a batch of loads and then consumes it lets the batch drain to zero
 // at every iteration, half its loads in flight on average.
-template <int WAVES, int H, int R>
-__global__ __launch_bounds__(64 * WAVES) void lm_head_ring(float *logits, unsigned long long *__restrict__ best,
-                                                           const float *__restrict__ x,
-                                                           const float4 *__restrict__ packed, int64_t V,
-                                                           const float *__restrict__ gamma, float eps,
-                                                           const float *__restrict__ bias, const float *residual,
-                                                           int slots) {
+template <int H, int R>
+__global__ __launch_bounds__(64) void lm_head_ring(float *logits, unsigned long long *__restrict__ best,
+                                                   const float *__restrict__ x, const float4 *__restrict__ packed,
+                                                   int64_t V, const float *__restrict__ gamma, float eps,
+                                                   const float *__restrict__ bias, const float *residual,
+                                                   int slots) {
     static_assert(H % 4 == 0 && R <= H / 4, "ring of at most H / 4 loads");
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     constexpr int K4 = H / 4;
     __shared__ __align__(16) float sxh[H];
-    __shared__ float scratch[4];
-    __shared__ unsigned long long wkeys[WAVES];
     const int m = blockIdx.y;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t blk = (int64_t)blockIdx.x * WAVES + wave;
+    const int lane = threadIdx.x;
+    const int64_t blk = blockIdx.x;
     const bool live = blk * 64 < V;
     const f32x4 *e = reinterpret_cast<const f32x4 *>(packed) + (live ? blk : 0) * K4 * 64 + lane;
     f32x4 ring[R];
 #pragma unroll
     for (int i = 0; i < R; ++i) ring[i] = __builtin_nontemporal_load(e + (size_t)i * 64);
-
-    float ss = 0.0f;
-    for (int i = threadIdx.x; i < H; i += 64 * WAVES) {
-        const float v = x[(size_t)m * H + i];
-        sxh[i] = v;
-        ss = __fadd_rn(ss, __fmul_rn(v, v));
-    }
-    __syncthreads();
-    if (gamma) {
-        static_assert(WAVES == 4, "the row-sum order needs 256 threads");
-        const float total = sum4(ss, scratch);
-        const float rcp = nc::div_rn(1.0f, nc::sqrt_rn(__fadd_rn(nc::div_rn(total, (float)H), eps)));
-        for (int i = threadIdx.x; i < H; i += 64 * WAVES) sxh[i] = __fmul_rn(__fmul_rn(sxh[i], rcp), gamma[i]);
-        __syncthreads();
-    }
+    head_prologue(sxh, x + (size_t)m * H, H, gamma, eps);
     float acc = 0.0f;
     if (live) {           // (a dead wave's ring read block 0: in bounds, unused)
 #pragma unroll
@@ -203,7 +184,7 @@ __global__ __launch_bounds__(64 * WAVES) void lm_head_ring(float *logits, unsign
     const int64_t n = blk * 64 + lane;
     const bool valid = n < V;
     if (logits && valid) logits[(size_t)m * V + n] = head_epilogue(acc, m, n, V, bias, residual);
-    if (best) publish_argmax<WAVES>(valid ? argmax_key(acc, n) : 0ull, best, m, slots, wkeys);
+    if (best) publish_argmax(valid ? argmax_key(acc, n) : 0ull, best, m, slots);
 }
 
 
@@ -217,19 +198,22 @@ __device__ __forceinline__ int64_t key_index(unsigned long long key) {
 }
 
 // The maximum of keys[0 .. slots - 1] in every thread of a 256-thread
-// workgroup (each thread's share loaded four at a time, all in flight).
+// workgroup: each thread's share loaded 12 at a time, all in flight (one
+// memory round trip for up to 3072 keys: the model's vocabulary leaves 2374).
 __device__ unsigned long long reduce_keys(const unsigned long long *__restrict__ keys, int slots,
                                           unsigned long long *wkeys) {
+    constexpr int kBatch = 12;
     unsigned long long k = 0ull;
-    for (int base = 0; base < slots; base += 4 * 256) {
-        unsigned long long v[4];
+    for (int base = 0; base < slots; base += kBatch * 256) {
+        unsigned long long v[kBatch];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < kBatch; ++u) {       // (clamped, not guarded: a guarded load is a branch)
             const int i = base + threadIdx.x + 256 * u;
-            v[u] = i < slots ? keys[i] : 0ull;
+            const unsigned long long x = keys[min(i, slots - 1)];
+            v[u] = i < slots ? x : 0ull;
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) k = v[u] > k ? v[u] : k;
+        for (int u = 0; u < kBatch; ++u) k = v[u] > k ? v[u] : k;
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -285,7 +269,7 @@ NC_EXPORT int32_t nc_pack_rows64(void **p, const int64_t *s) {
 // With bias (p[5]) the sum is followed by + bias[n]; with residual (p[6]),
 // logits = residual + that (the reference's float32 linear and residual add;
 // the argmax, when asked for, is of the plain sums). With s[4] = 1 the argmax
-// is left as one key per workgroup, best u64[M, G] with G = ceil(ceil(V / 64) / 4),
+// is left as one key per workgroup, best u64[M, G] with G = ceil(V / 64),
 // for nc_argmax_index / nc_decode_advance to reduce (no atomics, no clear);
 // with s[4] = 0, best u64[M] gets atomic maxima (clear it first).
 // p: [logits f32[M,V] | NULL, best | NULL, x f32[M,H], packed table, gamma f32[H] | NULL,
@@ -299,18 +283,17 @@ NC_EXPORT int32_t nc_lm_head(void **p, const int64_t *s) {
                    s[2] <= 16384,
                "nc_lm_head: bad shape (H a multiple of 4, at most 16384)");
     if (s[0] == 0) return NC_OK;
-    constexpr int W = 4;
     NC_REQUIRE(s[4] == 0 || s[4] == 1, "nc_lm_head: s[4] must be 0 (one key per row) or 1 (a key per workgroup)");
     const int64_t blocks = (s[1] + 63) / 64;
-    const dim3 grid((unsigned)((blocks + W - 1) / W), (unsigned)s[0]);
+    const dim3 grid((unsigned)blocks, (unsigned)s[0]);
     const int slots = s[4] ? (int)grid.x : 0;
     if (s[2] == 896) {       // the model's width: the ring kernel, 24 loads (24 KB) in flight per wave
-        hipLaunchKernelGGL((lm_head_ring<W, 896, 24>), grid, dim3(64 * W), 0, nc::stream(), (float *)p[0],
+        hipLaunchKernelGGL((lm_head_ring<896, 24>), grid, dim3(64), 0, nc::stream(), (float *)p[0],
                            (unsigned long long *)p[1], (const float *)p[2], (const float4 *)p[3], s[1],
                            (const float *)p[4], nc::bits_to_float(s[3]), bias, residual, slots);
         return nc::launched("lm_head_ring");
     }
-    hipLaunchKernelGGL((lm_head<W>), grid, dim3(64 * W), (size_t)s[2] * sizeof(float), nc::stream(), (float *)p[0],
+    hipLaunchKernelGGL(lm_head, grid, dim3(64), (size_t)s[2] * sizeof(float), nc::stream(), (float *)p[0],
                        (unsigned long long *)p[1], (const float *)p[2], (const float4 *)p[3], s[1], (int)s[2],
                        (const float *)p[4], nc::bits_to_float(s[3]), bias, residual, slots);
     return nc::launched("lm_head");

@@ -44,8 +44,8 @@ def attention_workspace_bytes(heads: int, head_dim: int, rows: int, keys: int) -
 
 
 def argmax_slots(vocab: int) -> int:
-    """Argmax keys per row that nc_lm_head leaves with s[4] = 1: one per workgroup of 4 x 64 rows."""
-    return -(-(-(-vocab // 64)) // 4)
+    """Argmax keys per row that nc_lm_head leaves with s[4] = 1: one per workgroup of 64 rows."""
+    return -(-vocab // 64)
 
 
 def _int8_weight(op: str, q: DeviceArray, scales: DeviceArray, k: int) -> int:
