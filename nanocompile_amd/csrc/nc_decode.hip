@@ -39,7 +39,8 @@ enum Epilogue { kBias = 0, kResidual = 1, kSwiglu = 2 };
 template <int K, int PRO, int W>
 __device__ float activation_prologue(int8_t *__restrict__ sxq, const float *__restrict__ x,
                                      const float *__restrict__ gamma, float eps, float *scratch) {
-    static_assert(W == 1 || W == 4, "one wave, or the row order's 256 threads");
+    static_assert(PRO == kQuant ? (W >= 1 && W <= 4) : (W == 1 || W == 4),
+                  "rms_norm: one wave, or the row order's 256 threads; a maximum alone: up to 4 waves");
     constexpr int T = 64 * W;
     constexpr int PER = (K + T - 1) / T;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -89,7 +90,9 @@ __device__ float activation_prologue(int8_t *__restrict__ sxq, const float *__re
     if constexpr (W > 1) {
         if (lane == 0) scratch[4 + wave] = mag;
         __syncthreads();
-        mag = fmaxf(fmaxf(scratch[4], scratch[5]), fmaxf(scratch[6], scratch[7]));
+        mag = scratch[4];
+#pragma unroll
+        for (int w = 1; w < W; ++w) mag = fmaxf(mag, scratch[4 + w]);
     }
     const float scale = nc::token_scale(mag);
 #pragma unroll
@@ -101,24 +104,35 @@ __device__ float activation_prologue(int8_t *__restrict__ sxq, const float *__re
     return scale;
 }
 
-template <int K, int L>
+// A lane's chunks of its weight row: B bytes (16, 8 or 4) a load, L lanes
+// a row, loads issued back to back. Integer sums are exact in any order, so
+// every (L, B) gives the same accumulators.
+template <int K, int L, int B>
 struct RowChunks {
-    static constexpr int STEP = L * 16;
+    static_assert(B == 16 || B == 8 || B == 4, "16-, 8- or 4-byte chunks");
+    static constexpr int STEP = L * B;
     static constexpr int ITERS = K / STEP;
-    static_assert(K % STEP == 0, "K must be a multiple of 16 L");
-    i8x16 w[ITERS];
+    static constexpr int DW = B / 4;                       // dwords a chunk
+    static_assert(K % STEP == 0, "K must be a multiple of L B");
+    int32_t w[ITERS][DW];
 
-    // The lane's 16-byte chunks of its weight row, loads issued back to back.
     __device__ __forceinline__ void load(const int8_t *__restrict__ row, int sub) {
 #pragma unroll
-        for (int it = 0; it < ITERS; ++it) w[it] = nc::load16_stream(row + it * STEP + sub * 16);
+        for (int it = 0; it < ITERS; ++it) {
+            const int32_t *q = reinterpret_cast<const int32_t *>(row + it * STEP + sub * B);
+#pragma unroll
+            for (int d = 0; d < DW; ++d) w[it][d] = __builtin_nontemporal_load(q + d);
+        }
     }
 
     __device__ __forceinline__ int32_t dot(const int8_t *__restrict__ sxq, int sub) const {
         int32_t acc = 0;
 #pragma unroll
-        for (int it = 0; it < ITERS; ++it)
-            acc = nc::dot16(w[it], *reinterpret_cast<const i8x16 *>(sxq + it * STEP + sub * 16), acc);
+        for (int it = 0; it < ITERS; ++it) {
+            const int32_t *x = reinterpret_cast<const int32_t *>(sxq + it * STEP + sub * B);
+#pragma unroll
+            for (int d = 0; d < DW; ++d) acc = nc::dot4(w[it][d], x[d], acc);
+        }
         return acc;
     }
 };
@@ -127,7 +141,7 @@ struct RowChunks {
 // for SwiGLU), L lanes per row. The weight loads are issued first, so they
 // are in flight while the workgroup computes its activation prologue, which
 // its W waves share.
-template <int K, int PRO, int EPI, int L, int W>
+template <int K, int PRO, int EPI, int L, int W, int B>
 __global__ __launch_bounds__(64 * W) void gemv_decode(float *__restrict__ out, const float *__restrict__ x,
                                                       const float *__restrict__ gamma, float eps,
                                                       const int8_t *__restrict__ q, const float *__restrict__ ws,
@@ -139,7 +153,7 @@ __global__ __launch_bounds__(64 * W) void gemv_decode(float *__restrict__ out, c
     const int n = blockIdx.x * (W * 64 / L) + (threadIdx.x >> 6) * (64 / L) + lane / L;
     const bool valid = n < N;
     const int nr = valid ? n : 0;
-    RowChunks<K, L> w1, w2;
+    RowChunks<K, L, B> w1, w2;
     w1.load(q + (size_t)nr * K, sub);
     if constexpr (EPI == kSwiglu) w2.load(q2 + (size_t)nr * K, sub);
     const float xs = activation_prologue<K, PRO, W>(sxq, x, gamma, eps, scratch);
@@ -161,15 +175,22 @@ __global__ __launch_bounds__(64 * W) void gemv_decode(float *__restrict__ out, c
 }
 
 
-// Lanes per row: 8 (one 128-byte line per load), or 16 for the long down
-// projection (half the loads each). Waves per workgroup: 1, or 4 for the long
-// down projection, whose 4864-wide prologue would otherwise cost each lane 76
-// correctly rounded divisions (measured on MI355X: 7.3 us with one wave,
-// 5.4 us with four; the 896-wide projections are faster with one).
-template <int K, int PRO, int EPI, int L = (K >= 4096 ? 16 : kL), int W = (K >= 4096 ? 4 : 1)>
+// The 896-wide projections: one wave, 8 lanes a row, 16-byte loads (one
+// 128-byte line a load), 8 rows a workgroup. The long down projection: 4 waves,
+// whose 4864-wide prologue would otherwise cost each lane 76 correctly rounded
+// divisions, and a whole wave a row with 4-byte loads (a 256-byte line a
+// load), so a workgroup holds 4 rows and the 896 rows spread over 224
+// workgroups, not the 56 that 16 lanes of 16 bytes a row give. Measured on
+// MI355X, decode tok/s in one box: down with 4 waves x (64 lanes, 4 B) 1642-1650,
+// (32 lanes, 8 B) 1608-1611, (16 lanes, 16 B) 1589; with 2 or 1 waves x
+// (64 lanes, 4 B) 1530 / 1496; the 896-wide projections with 4 waves of 32
+// lanes of 4 B (the prologue shared) 1508-1592, with 2 or 4 rows a one-wave
+// workgroup (more workgroups) unchanged.
+template <int K, int PRO, int EPI, int L = (K >= 4096 ? 64 : kL), int W = (K >= 4096 ? 4 : 1),
+          int B = (K >= 4096 ? 4 : 16)>
 int32_t launch_decode(void **p, int N, float eps) {
     constexpr int ROWS = W * 64 / L;
-    hipLaunchKernelGGL((gemv_decode<K, PRO, EPI, L, W>), dim3((N + ROWS - 1) / ROWS), dim3(64 * W), 0, nc::stream(),
+    hipLaunchKernelGGL((gemv_decode<K, PRO, EPI, L, W, B>), dim3((N + ROWS - 1) / ROWS), dim3(64 * W), 0, nc::stream(),
                        (float *)p[0], (const float *)p[1], (const float *)p[2], eps, (const int8_t *)p[3],
                        (const float *)p[4], (const float *)p[5], (const int8_t *)p[6], (const float *)p[7], N);
     return nc::launched("gemv_decode");
