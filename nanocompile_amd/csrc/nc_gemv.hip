@@ -42,6 +42,24 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_i8_token(
         out = static_cast<char *>(out) + z * (size_t)M * N * 4;
     }
 
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane & (L - 1), grp = lane / L;
+    const int n = blockIdx.x * ROWS + wave * (64 / L) + grp;
+    const int8_t *row = q + (size_t)(n < N ? n : 0) * K;
+
+    // With K known here, the row's chunks are loaded into registers first, so
+    // they are in flight while the activations are staged (a row left in the
+    // loop below would wait for the staging's barrier before its first load).
+    constexpr int KITERS = KS ? (KS + STEP - 1) / STEP : 1;
+    i8x16 w[KITERS];
+    if constexpr (KS > 0) {
+#pragma unroll
+        for (int it = 0; it < KITERS; ++it) {
+            const int c = it * STEP + sub * 16;
+            if (KS % STEP == 0 || c < KS) w[it] = nc::load16_stream(row + c);
+        }
+    }
+
     const int m0 = blockIdx.y * MT;
     const int mt = min(MT, M - m0);
     const int chunks = K / 16;
@@ -53,24 +71,28 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_i8_token(
     }
     __syncthreads();
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int sub = lane & (L - 1), grp = lane / L;
-    const int n = blockIdx.x * ROWS + wave * (64 / L) + grp;
-
     int32_t acc[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[m] = 0;
-    if (n < N) {
-        const int8_t *row = q + (size_t)n * K;
-        const int iters = (K + STEP - 1) / STEP;
+    if constexpr (KS > 0) {
 #pragma unroll
+        for (int it = 0; it < KITERS; ++it) {
+            const int c = it * STEP + sub * 16;
+            if (KS % STEP == 0 || c < KS) {
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+                    acc[m] = nc::dot16(w[it], *reinterpret_cast<const i8x16 *>(sx + m * K + c), acc[m]);
+            }
+        }
+    } else if (n < N) {
+        const int iters = (K + STEP - 1) / STEP;
         for (int it = 0; it < iters; ++it) {
             const int c = it * STEP + sub * 16;
             if (K % STEP == 0 || c < K) {
-                const i8x16 w = nc::load16_stream(row + c);
+                const i8x16 wv = nc::load16_stream(row + c);
 #pragma unroll
                 for (int m = 0; m < MT; ++m)
-                    acc[m] = nc::dot16(w, *reinterpret_cast<const i8x16 *>(sx + m * K + c), acc[m]);
+                    acc[m] = nc::dot16(wv, *reinterpret_cast<const i8x16 *>(sx + m * K + c), acc[m]);
             }
         }
     }
