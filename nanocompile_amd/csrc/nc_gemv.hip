@@ -264,6 +264,14 @@ int auto_tile(int M, int N, int K) {
     return 2;
 }
 
+// The SwiGLU pair's default: its tiles stage two weight blocks, so where a
+// single projection takes 64 x 64 the pair takes 32 x 64 (measured on MI355X
+// at M = 512, N = 4864, K = 896: 20.7-20.9 us against 22.4-23.3 for 64 x 64).
+int auto_tile_pair(int M, int N, int K) {
+    const int tile = auto_tile(M, N, K);
+    return tile == 5 ? 1 : tile;
+}
+
 template <int KS, int MT, bool ACC_OUT>
 int32_t dispatch_schedule(const Args &a, int schedule) {
 #define NC_GEMV_CASE(I, L, W) \
@@ -411,7 +419,7 @@ NC_EXPORT int32_t nc_matmul_i8_token_swiglu(void **p, const int64_t *s) {
     auto sg = (const float *)p[4];
     auto qu = (const int8_t *)p[5];
     auto su = (const float *)p[6];
-    if (schedule == 0 && M >= kGemmMinTokens) schedule = kGemmFirst + auto_tile(M, N, K);
+    if (schedule == 0 && M >= kGemmMinTokens) schedule = kGemmFirst + auto_tile_pair(M, N, K);
     if (schedule >= kGemmFirst)
         return nc::gemm_i8_token(schedule - kGemmFirst, 2, h, xq, xs, qg, sg, nullptr, nullptr, qu, su, M, N, K);
     if (K == 896) return swiglu_tokens<896>(h, xq, xs, qg, sg, qu, su, M, N, K);
