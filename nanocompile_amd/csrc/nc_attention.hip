@@ -164,7 +164,11 @@ constexpr int kWaves = 8;              // decode: waves of a chunk workgroup, on
 // workgroups per CU, one staging its chunk while the other computes (measured
 // on MI355X at 512 rows: 58 us, against 62 with 8-row workgroups, 63 with 2,
 // 99 with 1; interleaving two heads per wave, or reloading the chunk from LDS
-// per head for occupancy, was slower).
+// per head for occupancy, was slower; so were capping the registers at three
+// waves a SIMD, which spills (168 us), and reading each head's query with
+// scalar loads instead of staging it in LDS (69-73 us: the loads sit on every
+// head's critical path, and the probabilities read back for P V still hold
+// 64 VGPRs, so two waves a SIMD remain).
 constexpr int kRowsPerBlock = 4;
 constexpr int kHeadBatch = 8;          // prefill: query heads of a row held in LDS at once
 
