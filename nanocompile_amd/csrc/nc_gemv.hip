@@ -252,24 +252,32 @@ constexpr int kGemmFirst = 16;
 constexpr int kGemmTiles = 9;
 constexpr int kGemmMinTokens = 16;
 
-// The MFMA tile for a shape when the caller asks for the default (measured on
-// MI355X at M = 512): 64 x 64 tiles once they give every CU two workgroups,
-// 32 x 64 with 8 stages in flight for long k loops, 32 x 64 while there are
-// still most of a workgroup per CU, else 32 x 32.
+// The MFMA tile for a shape when the caller asks for the default, from a sweep
+// of every tile on MI355X over the model's shapes at M = 128 .. 4096:
+// 64 x 128 (8 waves) for the largest problems and for long k loops with many
+// tiles; 64 x 64 from 144 such tiles on (gate at M = 128: 5.30 us against
+// 5.78 with 32 x 64; qkv at M = 512: 5.29 against 5.74); for long k loops
+// below that, 32 x 64 with 8 stages in flight once there are 192 such tiles,
+// else 32 x 32 (down at M = 128 / 256: 7.93 / 8.46 us against 10.9 / 11.1);
+// 32 x 64 with 192 tiles or more; else 32 x 32.
 int auto_tile(int M, int N, int K) {
     auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-    if (tiles(64, 64) >= 512) return 5;
-    if (K >= 2048) return 4;
+    const int t64 = tiles(64, 64);
+    if (t64 >= 1792 || (K >= 2048 && t64 >= 256)) return 6;
+    if (t64 >= 144) return 5;
+    if (K >= 2048) return tiles(32, 64) >= 192 ? 4 : 2;
     if (tiles(32, 64) >= 192) return 1;
     return 2;
 }
 
-// The SwiGLU pair's default: its tiles stage two weight blocks, so where a
-// single projection takes 64 x 64 the pair takes 32 x 64 (measured on MI355X
-// at M = 512, N = 4864, K = 896: 20.7-20.9 us against 22.4-23.3 for 64 x 64).
+// The SwiGLU pair's default: its tiles stage two weight blocks, so it keeps
+// smaller tiles: 32 x 64 once there are 512 of them, else 32 x 32 (measured at
+// N = 4864, K = 896: M = 512 20.7 us against 22.4-23.3 for 64 x 64; M = 128
+// 8.90 us with 32 x 32 against 10.58 with 32 x 64; M = 256 13.5 with 32 x 64).
 int auto_tile_pair(int M, int N, int K) {
-    const int tile = auto_tile(M, N, K);
-    return tile == 5 ? 1 : tile;
+    (void)K;
+    const int t = ((M + 31) / 32) * ((N + 63) / 64);
+    return t >= 512 ? 1 : 2;
 }
 
 template <int KS, int MT, bool ACC_OUT>
