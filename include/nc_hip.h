@@ -234,6 +234,15 @@ int32_t nc_softmax_causal(void **p, const int64_t *s);
  * s: [M, heads, kv, D, past, C] */
 int32_t nc_rope_append(void **p, const int64_t *s);
 
+/* A prompt's qkv projection with RoPE and the cache append in its epilogue
+ * (models/qwen2.py:113-145, the projection then rotate-and-cache): the bits of
+ * nc_matmul_i8_token (bias, no residual) followed by nc_rope_append with the
+ * cache's table, in one launch on MFMA tiles one head wide.
+ * p: [qkv f32[M,W] (out), xq i8[M,K], xs f32[M], q i8[W,K], scales f32[W], bias f32[W] or NULL,
+ *     kcache f32[kv,C,D], vcache f32[kv,C,D], rope table f32[2,C,D/2], pos i64[1] or NULL];
+ * s: [M, W, K, heads, kv, D, past, C] (W = (heads + 2*kv)*D, D 32 or 64, K a multiple of 16) */
+int32_t nc_matmul_i8_token_rope(void **p, const int64_t *s);
+
 /* Grouped-query attention of each new row over the cache, causal
  * (models/qwen2.py:113-155; query head h reads KV head h / (heads / kv), the
  * reference's repeat_kv as index arithmetic, nn.py:109-120). The softmax and

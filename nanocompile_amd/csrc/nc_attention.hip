@@ -23,6 +23,7 @@
 
 #include "nc_common.h"
 #include "nc_attend.h"
+#include "nc_epilogue.h"
 #include "nc_math.h"
 
 namespace {
@@ -86,11 +87,7 @@ __device__ __forceinline__ bool position_fits(const int64_t *pos_ptr, int m, int
     return true;
 }
 
-__device__ __forceinline__ void rope_pair(float x0, float x1, float c, float s, float &y0, float &y1) {
-    // y[j] = x[j] * c + (-x[j + h]) * s;  y[j + h] = x[j + h] * c + x[j] * s
-    y0 = __fadd_rn(__fmul_rn(x0, c), __fmul_rn(-x1, s));
-    y1 = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(x0, s));
-}
+using nc::rope_pair;
 
 // qkv[M, (H + 2 * KV * D)] rows: q heads rotated in place; k heads rotated and
 // written with v into the cache at positions past + i. cos and sin come from

@@ -38,7 +38,17 @@ namespace {
 using nc::i8x16;
 typedef int32_t v4i __attribute__((ext_vector_type(4)));
 
-enum Epilogue { kDequant = 0, kAccOut = 1, kSwiglu = 2 };
+enum Epilogue { kDequant = 0, kAccOut = 1, kSwiglu = 2, kRope = 3 };
+
+// The qkv projection's RoPE and cache append, as nc_rope_append does them
+// after it (nc_attention.hip): with tiles exactly one head wide (BN = D).
+struct RopeArgs {
+    float *kcache, *vcache;            // [kv, capacity, D]
+    const float *table;                // cos, sin [2, capacity, D / 2] (nc_rope_table)
+    const int64_t *pos;                // the position of row 0, or NULL: past
+    int32_t *error;
+    int heads, kv, past, capacity;
+};
 
 struct GemmArgs {
     void *out;
@@ -51,6 +61,7 @@ struct GemmArgs {
     const int8_t *q2;        // SwiGLU: the up projection
     const float *ws2;
     int M, N, K;
+    RopeArgs rope;
 };
 
 __device__ __forceinline__ int tile_of(int id, int total) {
@@ -182,7 +193,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_i8_mfma(GemmA
                 const int n = min(n0 + wn + j * 16 + nq + r, N - 1);
                 w1_r[j][r] = a.ws[n];
                 if constexpr (EPI == kSwiglu) w2_r[j][r] = a.ws2[n];
-                if constexpr (EPI == kDequant) b_r[j][r] = a.bias ? a.bias[n] : 0.0f;
+                if constexpr (EPI == kDequant || EPI == kRope) b_r[j][r] = a.bias ? a.bias[n] : 0.0f;
             }
     }
 
@@ -216,6 +227,73 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_i8_mfma(GemmA
             store_stage((j + 1) & 1, ra[(j + 1) % NS], rb[(j + 1) % NS]);
             __syncthreads();
         }
+    }
+
+    if constexpr (EPI == kRope) {
+        // The tile is one head, [BM rows][BN = D columns]: dequantized (+ bias)
+        // into LDS, then each pair (j, j + D/2) of a row rotated at the row's
+        // position (q heads, written back in place; k heads, into the cache)
+        // or copied (v heads, into the cache). The qkv rows of k and v keep
+        // their unrotated values, as after nc_rope_append.
+        static_assert(BM * BN * sizeof(float) <= sizeof(sA), "the tile must fit the staging LDS");
+        const RopeArgs &ro = a.rope;
+        int past = ro.past;
+        bool rotate = true;
+        if (ro.pos) {
+            const int64_t p = *ro.pos;
+            if (p < 0 || p + M > ro.capacity) {
+                if (blockIdx.x == 0 && threadIdx.x == 0) atomicCAS(ro.error, 0, NC_FAIL_CAPACITY);
+                rotate = false;                      // as nc_rope_append: qkv as projected, nothing appended
+            } else {
+                past = (int)p;
+            }
+        }
+        __syncthreads();                             // every wave is done with the staging buffers
+        float *tile = reinterpret_cast<float *>(&sA[0][0]);
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+#pragma unroll
+            for (int j = 0; j < NI; ++j) {
+                float *t = tile + (wm + i * 16 + row16) * BN + wn + j * 16 + nq;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float v = nc::dequant(acc[0][i][j][r], xs_r[i], w1_r[j][r]);
+                    if (a.bias) v = __fadd_rn(v, b_r[j][r]);
+                    t[r] = v;
+                }
+            }
+        }
+        __syncthreads();
+        constexpr int HALF = BN / 2;
+        const int head = n0 / BN;
+        for (int idx = tid; idx < BM * HALF; idx += THREADS) {
+            const int mm = idx / HALF, jj = idx - mm * HALF, m = m0 + mm;
+            if (m >= M) continue;
+            const float x0 = tile[mm * BN + jj], x1 = tile[mm * BN + jj + HALF];
+            float *y = static_cast<float *>(a.out) + (size_t)m * N + n0;
+            const int position = past + m;
+            float y0 = x0, y1 = x1;
+            if (rotate && head < ro.heads + ro.kv) {
+                const float c = ro.table[(size_t)position * HALF + jj];
+                const float sn = ro.table[((size_t)ro.capacity + position) * HALF + jj];
+                nc::rope_pair(x0, x1, c, sn, y0, y1);
+            }
+            if (head < ro.heads && rotate) {
+                y[jj] = y0;
+                y[jj + HALF] = y1;
+            } else {
+                y[jj] = x0;
+                y[jj + HALF] = x1;
+            }
+            if (rotate && head >= ro.heads) {
+                const bool is_k = head < ro.heads + ro.kv;
+                const int g = head - ro.heads - (is_k ? 0 : ro.kv);
+                float *c = (is_k ? ro.kcache : ro.vcache) + ((size_t)g * ro.capacity + position) * BN;
+                c[jj] = is_k ? y0 : x0;
+                c[jj + HALF] = is_k ? y1 : x1;
+            }
+        }
+        return;
     }
 
     // Epilogue: lane holds n = 4 * (lane / 16) + r, r = 0..3, of each 16 x 16
@@ -328,6 +406,28 @@ int32_t gemm_i8_token(int tile, int epi, void *out, const int8_t *xq, const floa
 #undef NC_TILE_CASE
 }
 
+// The qkv projection with RoPE and the cache append in its epilogue: tiles one
+// head wide (BN = head_dim) only.
+template <int BM, int BN, int BK, int WM, int WN, int NS>
+int32_t launch_rope_tile(const GemmArgs &a) {
+    if constexpr (BN == 32 || BN == 64) {
+        return launch_tile<BM, BN, BK, WM, WN, NS, kRope>(a);
+    } else {
+        set_message("nc_matmul_i8_token_rope: the tile is not one head wide");
+        return NC_BAD_ARGS;
+    }
+}
+
+int32_t gemm_i8_token_rope(int tile, const GemmArgs &a) {
+#define NC_ROPE_CASE(I, BM, BN, BK, WM, WN, NS) \
+    case I: return launch_rope_tile<BM, BN, BK, WM, WN, NS>(a);
+    switch (tile) {
+        NC_GEMM_TILES(NC_ROPE_CASE)
+        default: set_message("nc_matmul_i8_token_rope: no such tile"); return NC_BAD_ARGS;
+    }
+#undef NC_ROPE_CASE
+}
+
 // out: [BM, BN, BK, WM, WN, NS, workgroup threads, LDS bytes (dequantize epilogue)]
 int32_t gemm_tile_info(int tile, int64_t *out) {
 #define NC_TILE_INFO(I, BM, BN, BK, WM, WN, NS)                                          \
@@ -345,3 +445,31 @@ int32_t gemm_tile_info(int tile, int64_t *out) {
 }
 
 }  // namespace nc
+
+// The qkv projection of a prompt with RoPE and the KV-cache append fused into
+// its epilogue: the bits of nc_matmul_i8_token (bias, no residual) followed by
+// nc_rope_append with the cache's table (q rotated in place; k rotated and v
+// copied into the cache at positions past + i; k and v left in qkv as
+// projected), in one launch. The tile is one head wide: 64 x 64 when that
+// gives 144 tiles or more, else 32 x 64 (head_dim 64); 32 x 32 (head_dim 32).
+// p: [qkv f32[M,W] (out), xq i8[M,K], xs f32[M], q i8[W,K], scales f32[W], bias f32[W] | NULL,
+//     kcache f32[kv,C,D], vcache f32[kv,C,D], rope table f32[2,C,D/2], pos i64[1] | NULL];
+// s: [M, W, K, heads, kv, D, past, C]  (W = (heads + 2 kv) D, D 32 or 64, K a multiple of 16)
+NC_EXPORT int32_t nc_matmul_i8_token_rope(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3] && p[4] && p[6] && p[7] && p[8],
+               "nc_matmul_i8_token_rope: null operand");
+    const int64_t M = s[0], W = s[1], K = s[2], heads = s[3], kv = s[4], D = s[5], past = s[6], C = s[7];
+    const int64_t *pos = (const int64_t *)p[9];
+    NC_REQUIRE(M >= 0 && M < (1 << 24) && K > 0 && K % 16 == 0 && K < (1 << 24) && heads > 0 && kv > 0 &&
+                   heads % kv == 0 && (D == 32 || D == 64) && W == (heads + 2 * kv) * D && C > 0 &&
+                   C < (1 << 24) && (pos || (past >= 0 && past + M <= C)),
+               "nc_matmul_i8_token_rope: bad shape (W = (heads + 2 kv) D, D 32 or 64, past + M <= C)");
+    if (M == 0) return NC_OK;
+    int tile = 2;
+    if (D == 64) tile = ((M + 63) / 64) * (W / 64) >= 144 ? 5 : 1;
+    GemmArgs a{p[0], (const int8_t *)p[1], (const float *)p[2], (const int8_t *)p[3], (const float *)p[4],
+               (const float *)p[5], nullptr, nullptr, nullptr, (int)M, (int)W, (int)K};
+    a.rope = RopeArgs{(float *)p[6], (float *)p[7], (const float *)p[8], pos, nc::error_word(), (int)heads,
+                      (int)kv, pos ? 0 : (int)past, (int)C};
+    return nc::gemm_i8_token_rope(tile, a);
+}

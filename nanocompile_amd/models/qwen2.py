@@ -315,9 +315,16 @@ class Qwen2:
             kc, vc = cache.layer(i)
             hip.call("nc_rms_norm_quant", [None, self.xq, self.xs, self.x, w["g1"]], [m, H, eps])
             q, s = w["qkv"]
-            hip.call("nc_matmul_i8_token", [self.qkv, self.xq, self.xs, q, s, w["qkv_b"], None], [m, W, H, s_qkv])
-            hip.call("nc_rope_append", [self.qkv, kc, vc, self.inv_freq, pos, cache.rope],
-                     [m, heads, kv, D, past, cache.capacity])
+            if s_qkv == 0 and D in (32, 64) and cache.rope is not None:
+                # RoPE and the cache append in the projection's epilogue (one launch)
+                hip.call("nc_matmul_i8_token_rope",
+                         [self.qkv, self.xq, self.xs, q, s, w["qkv_b"], kc, vc, cache.rope, pos],
+                         [m, W, H, heads, kv, D, past, cache.capacity])
+            else:
+                hip.call("nc_matmul_i8_token", [self.qkv, self.xq, self.xs, q, s, w["qkv_b"], None],
+                         [m, W, H, s_qkv])
+                hip.call("nc_rope_append", [self.qkv, kc, vc, self.inv_freq, pos, cache.rope],
+                         [m, heads, kv, D, past, cache.capacity])
             # attention, its combine also quantizing ctx per token for the o projection
             hip.call("nc_attention", [self.ctx, self.qkv, kc, vc, pos, cache.work, self.xq, self.xs],
                      [m, heads, kv, D, past, cache.capacity, float_bits(self.scale), cache.work_bytes])

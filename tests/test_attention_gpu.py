@@ -235,3 +235,60 @@ def test_prefill_attention_quantizes_ctx_per_token(gpu, host, d, heads, kv, m, p
     assert np.array_equal(bits(ctx.numpy()), bits(expected))
     eq, es = R.quantize_token(expected)
     assert np.array_equal(xq.numpy(), eq) and np.array_equal(bits(xs.numpy()), bits(es))
+
+
+@pytest.mark.parametrize("heads,kv,d,k", [(14, 2, 64, 896), (4, 2, 32, 128)])
+@pytest.mark.parametrize("m,past", [(1, 0), (16, 5), (130, 70), (512, 0)])
+def test_qkv_projection_with_rope_is_projection_then_rope_append(gpu, heads, kv, d, k, m, past):
+    """nc_matmul_i8_token_rope (RoPE and the cache append in the GEMM's epilogue) leaves qkv and
+    both caches bit for bit as nc_matmul_i8_token followed by nc_rope_append with the table does,
+    with the position from the host and from the device."""
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import DeviceArray
+    print(f"qkv rope epilogue heads={heads} d={d} m={m} past={past}", flush=True)
+    rng = np.random.default_rng(m * 7 + past + d)
+    w = (heads + 2 * kv) * d
+    cap = past + m + 3
+    xq = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    xs = (rng.random(m) * 0.05 + 1e-3).astype(np.float32)
+    q = rng.integers(-127, 128, (w, k)).astype(np.int8)
+    qs = (rng.random(w) * 1e-3 + 1e-4).astype(np.float32)
+    bias = rng.standard_normal(w).astype(np.float32)
+    kc0 = rng.standard_normal((kv, cap, d)).astype(np.float32)
+    vc0 = rng.standard_normal((kv, cap, d)).astype(np.float32)
+    inv = inverse_frequencies(d, 1e6)
+    table = DeviceArray((2, cap, d // 2), np.float32)
+    hip.call("nc_rope_table", [table, DeviceArray.from_host(inv)], [cap, d])
+    dxq, dxs, dq, dqs, db = (DeviceArray.from_host(a) for a in (xq, xs, q, qs, bias))
+    pos = DeviceArray.from_host(np.array([past], np.int64))
+    for use_pos in (False, True):
+        outs = []
+        for fused in (False, True):
+            qkv = DeviceArray((m, w), np.float32)
+            kc, vc = DeviceArray.from_host(kc0), DeviceArray.from_host(vc0)
+            p = pos if use_pos else None
+            host_past = 0 if use_pos else past
+            if fused:
+                hip.call("nc_matmul_i8_token_rope", [qkv, dxq, dxs, dq, dqs, db, kc, vc, table, p],
+                         [m, w, k, heads, kv, d, host_past, cap])
+            else:
+                hip.call("nc_matmul_i8_token", [qkv, dxq, dxs, dq, dqs, db, None], [m, w, k, 0])
+                hip.call("nc_rope_append", [qkv, kc, vc, DeviceArray.from_host(inv), p, table],
+                         [m, heads, kv, d, host_past, cap])
+            outs.append((qkv.numpy(), kc.numpy(), vc.numpy()))
+        for a, b in zip(*outs):
+            assert np.array_equal(bits(a), bits(b)), use_pos
+
+
+def test_qkv_projection_with_rope_rejects_bad_shapes(gpu):
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import DeviceArray
+    x = DeviceArray((1 << 16,), np.float32)
+    with pytest.raises(hip.KernelError, match="bad shape"):        # W is not (heads + 2 kv) * D
+        hip.call("nc_matmul_i8_token_rope", [x, x, x, x, x, None, x, x, x], [4, 1000, 896, 14, 2, 64, 0, 8])
+    with pytest.raises(hip.KernelError, match="bad shape"):        # head_dim 48
+        hip.call("nc_matmul_i8_token_rope", [x, x, x, x, x, None, x, x, x], [4, 18 * 48, 896, 14, 2, 48, 0, 8])
+    with pytest.raises(hip.KernelError, match="bad shape"):        # past + M past the capacity
+        hip.call("nc_matmul_i8_token_rope", [x, x, x, x, x, None, x, x, x], [4, 1152, 896, 14, 2, 64, 6, 8])
+    with pytest.raises(hip.KernelError, match="null operand"):     # no table
+        hip.call("nc_matmul_i8_token_rope", [x, x, x, x, x, None, x, x, None], [4, 1152, 896, 14, 2, 64, 0, 8])
