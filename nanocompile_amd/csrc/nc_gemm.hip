@@ -196,6 +196,34 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_i8_mfma(GemmA
                 if constexpr (EPI == kDequant || EPI == kRope) b_r[j][r] = a.bias ? a.bias[n] : 0.0f;
             }
     }
+    // RoPE: the tile's rows' positions and this thread's pairs' cos and sin,
+    // also fetched before the k loop (pair u of the thread: idx = tid + u THREADS).
+    constexpr int HALF = BN / 2;
+    constexpr int PAIRS = EPI == kRope ? BM * HALF / THREADS : 1;
+    static_assert(EPI != kRope || BM * HALF % THREADS == 0, "whole pairs per thread");
+    float rc[PAIRS], rs[PAIRS];
+    int rope_past = 0;
+    bool rotate = true;
+    if constexpr (EPI == kRope) {
+        const RopeArgs &ro = a.rope;
+        rope_past = ro.past;
+        if (ro.pos) {
+            const int64_t p = *ro.pos;
+            if (p < 0 || p + M > ro.capacity) {
+                if (blockIdx.x == 0 && threadIdx.x == 0) atomicCAS(ro.error, 0, NC_FAIL_CAPACITY);
+                rotate = false;                      // as nc_rope_append: qkv as projected, nothing appended
+            } else {
+                rope_past = (int)p;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < PAIRS; ++u) {
+            const int idx = tid + u * THREADS, mm = idx / HALF, jj = idx - mm * HALF;
+            const int position = rotate ? rope_past + min(m0 + mm, M - 1) : 0;
+            rc[u] = ro.table[(size_t)position * HALF + jj];
+            rs[u] = ro.table[((size_t)ro.capacity + position) * HALF + jj];
+        }
+    }
 
     // Step s: refill slot s % NS with stage s + NS, multiply stage s from LDS
     // buffer s & 1, write stage s + 1 (slot (s + 1) % NS) into the other
@@ -237,17 +265,6 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_i8_mfma(GemmA
         // their unrotated values, as after nc_rope_append.
         static_assert(BM * BN * sizeof(float) <= sizeof(sA), "the tile must fit the staging LDS");
         const RopeArgs &ro = a.rope;
-        int past = ro.past;
-        bool rotate = true;
-        if (ro.pos) {
-            const int64_t p = *ro.pos;
-            if (p < 0 || p + M > ro.capacity) {
-                if (blockIdx.x == 0 && threadIdx.x == 0) atomicCAS(ro.error, 0, NC_FAIL_CAPACITY);
-                rotate = false;                      // as nc_rope_append: qkv as projected, nothing appended
-            } else {
-                past = (int)p;
-            }
-        }
         __syncthreads();                             // every wave is done with the staging buffers
         float *tile = reinterpret_cast<float *>(&sA[0][0]);
 #pragma unroll
@@ -264,20 +281,16 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_i8_mfma(GemmA
             }
         }
         __syncthreads();
-        constexpr int HALF = BN / 2;
         const int head = n0 / BN;
-        for (int idx = tid; idx < BM * HALF; idx += THREADS) {
-            const int mm = idx / HALF, jj = idx - mm * HALF, m = m0 + mm;
+#pragma unroll
+        for (int u = 0; u < PAIRS; ++u) {
+            const int idx = tid + u * THREADS, mm = idx / HALF, jj = idx - mm * HALF, m = m0 + mm;
             if (m >= M) continue;
             const float x0 = tile[mm * BN + jj], x1 = tile[mm * BN + jj + HALF];
             float *y = static_cast<float *>(a.out) + (size_t)m * N + n0;
-            const int position = past + m;
+            const int position = rope_past + m;
             float y0 = x0, y1 = x1;
-            if (rotate && head < ro.heads + ro.kv) {
-                const float c = ro.table[(size_t)position * HALF + jj];
-                const float sn = ro.table[((size_t)ro.capacity + position) * HALF + jj];
-                nc::rope_pair(x0, x1, c, sn, y0, y1);
-            }
+            if (rotate && head < ro.heads + ro.kv) nc::rope_pair(x0, x1, rc[u], rs[u], y0, y1);
             if (head < ro.heads && rotate) {
                 y[jj] = y0;
                 y[jj + HALF] = y1;
