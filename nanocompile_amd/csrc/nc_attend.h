@@ -99,15 +99,17 @@ struct ChunkResult {
     float m, l, o;    // the chunk's max and sum (every lane), and o[d] in lane d
 };
 
-// Attend q (D floats in LDS, read by every lane) to the first n keys of a
-// staged chunk whose rows past the context are zeros; `pbuf` is 64 floats of
-// LDS owned by the calling wave. The whole wavefront must call this together;
-// the chunk must be staged (and a barrier passed) before.
+// The two halves of attending one query to the first n keys of a staged
+// chunk whose rows past the context are zeros. The whole wavefront must call
+// each together; the chunk must be staged (and a barrier passed) before.
+//
+// chunk_scores: s_t, m, p_t = exp(s_t - m) and l from q (D floats in LDS,
+// read by every lane); p_t goes to p[t] (64 floats of LDS owned by the wave,
+// which may be q itself: every read of q comes before the write).
 template <int D>
-__device__ __forceinline__ ChunkResult attend_staged(const float *q, const Staged<D> &st, int n, float scale,
-                                                     float *pbuf) {
+__device__ __forceinline__ void chunk_scores(const float *q, const Staged<D> &st, int n, float scale, float *p,
+                                             float &m_out, float &l_out) {
     const int lane = threadIdx.x & 63;
-    const int dl = lane < D ? lane : 0;
     float acc = 0.0f;
     const float *krow = st.keys + lane * Staged<D>::kKeyStride;
 #pragma unroll
@@ -123,24 +125,99 @@ __device__ __forceinline__ ChunkResult attend_staged(const float *q, const Stage
     // (scores are never -0, so nan_max commutes up to which NaN propagates)
     float m = butterfly<64>(s, [](float a, float b) { return nan_max(a, b); });
     m = lane_value(m, 0);
-    const float p = nc_expf(__fsub_rn(s, m));        // exp(-inf) = 0 for lanes past the chunk
-    const float l = wave_sum_f32(p);
+    const float pt = nc_expf(__fsub_rn(s, m));       // exp(-inf) = 0 for lanes past the chunk
+    l_out = wave_sum_f32(pt);
+    m_out = m;
+    p[lane] = pt;
+}
 
-    // o[d] in key order, p read back from LDS four at a time (the wave's own
-    // write lands before its reads). A key past n adds 0 * v = +-0 (v a real
-    // key, masked, or a zero row) to an accumulator that starts at +0 and is
-    // never -0: exact, no change.
-    pbuf[lane] = p;
+// chunk_values: o[d] in key order from the p_t that chunk_scores left in LDS
+// (the wave's own write lands before its reads), four at a time. A key past n
+// adds 0 * v = +-0 (v a real key, masked, or a zero row) to an accumulator
+// that starts at +0 and is never -0: exact, no change.
+template <int D>
+__device__ __forceinline__ float chunk_values(const float *p, const Staged<D> &st) {
+    const int lane = threadIdx.x & 63;
+    const int dl = lane < D ? lane : 0;
     float o = 0.0f;
 #pragma unroll
     for (int i = 0; i < kChunk / 4; ++i) {
-        const float4 pi = *reinterpret_cast<const float4 *>(pbuf + 4 * i);
+        const float4 pi = *reinterpret_cast<const float4 *>(p + 4 * i);
         o = __fadd_rn(o, __fmul_rn(pi.x, st.values[(4 * i + 0) * D + dl]));
         o = __fadd_rn(o, __fmul_rn(pi.y, st.values[(4 * i + 1) * D + dl]));
         o = __fadd_rn(o, __fmul_rn(pi.z, st.values[(4 * i + 2) * D + dl]));
         o = __fadd_rn(o, __fmul_rn(pi.w, st.values[(4 * i + 3) * D + dl]));
     }
-    return {m, l, o};
+    return o;
+}
+
+// Both halves for one query, with `pbuf` (64 floats of LDS owned by the
+// calling wave) holding the p_t between them.
+template <int D>
+__device__ __forceinline__ ChunkResult attend_staged(const float *q, const Staged<D> &st, int n, float scale,
+                                                     float *pbuf) {
+    ChunkResult r;
+    chunk_scores<D>(q, st, n, scale, pbuf, r.m, r.l);
+    r.o = chunk_values<D>(pbuf, st);
+    return r;
+}
+
+// The same two halves for H queries at once, each in the order above: the
+// products run d (or key) outermost and query innermost, so each key or value
+// element is read from LDS once for the H chains and neither the key row nor
+// the value column stays in registers. qp[u] holds query u (D floats) and
+// receives its p_t.
+template <int D, int H>
+__device__ __forceinline__ void chunk_scores_n(float (*qp)[kChunk], const Staged<D> &st, int n, float scale,
+                                               float (&m)[H], float (&l)[H]) {
+    const int lane = threadIdx.x & 63;
+    float acc[H];
+#pragma unroll
+    for (int u = 0; u < H; ++u) acc[u] = 0.0f;
+    const float *krow = st.keys + lane * Staged<D>::kKeyStride;
+#pragma unroll 2
+    for (int i = 0; i < D / 4; ++i) {
+        const float4 k = *reinterpret_cast<const float4 *>(krow + 4 * i);
+#pragma unroll
+        for (int u = 0; u < H; ++u) {
+            const float4 qi = *reinterpret_cast<const float4 *>(qp[u] + 4 * i);
+            acc[u] = __fadd_rn(acc[u], __fmul_rn(qi.x, k.x));
+            acc[u] = __fadd_rn(acc[u], __fmul_rn(qi.y, k.y));
+            acc[u] = __fadd_rn(acc[u], __fmul_rn(qi.z, k.z));
+            acc[u] = __fadd_rn(acc[u], __fmul_rn(qi.w, k.w));
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < H; ++u) {
+        const float s = lane < n ? __fadd_rn(__fmul_rn(acc[u], scale), 0.0f) : -__builtin_inff();
+        float mu = butterfly<64>(s, [](float a, float b) { return nan_max(a, b); });
+        mu = lane_value(mu, 0);
+        const float pt = nc_expf(__fsub_rn(s, mu));
+        l[u] = wave_sum_f32(pt);
+        m[u] = mu;
+        qp[u][lane] = pt;
+    }
+}
+
+template <int D, int H>
+__device__ __forceinline__ void chunk_values_n(float (*qp)[kChunk], const Staged<D> &st, float (&o)[H]) {
+    const int lane = threadIdx.x & 63;
+    const int dl = lane < D ? lane : 0;
+#pragma unroll
+    for (int u = 0; u < H; ++u) o[u] = 0.0f;
+#pragma unroll 2
+    for (int i = 0; i < kChunk / 4; ++i) {
+        const float v0 = st.values[(4 * i + 0) * D + dl], v1 = st.values[(4 * i + 1) * D + dl];
+        const float v2 = st.values[(4 * i + 2) * D + dl], v3 = st.values[(4 * i + 3) * D + dl];
+#pragma unroll
+        for (int u = 0; u < H; ++u) {
+            const float4 pi = *reinterpret_cast<const float4 *>(qp[u] + 4 * i);
+            o[u] = __fadd_rn(o[u], __fmul_rn(pi.x, v0));
+            o[u] = __fadd_rn(o[u], __fmul_rn(pi.y, v1));
+            o[u] = __fadd_rn(o[u], __fmul_rn(pi.z, v2));
+            o[u] = __fadd_rn(o[u], __fmul_rn(pi.w, v3));
+        }
+    }
 }
 
 // Store a chunk result at part[0 .. D + 1] (m_j, l_j, o_j).

@@ -155,17 +155,18 @@ __global__ __launch_bounds__(kThreads) void rope_append(float *__restrict__ qkv,
 // e = 0 (m_j), 1 (l_j), 2 + d (o_j[d]); jstride = the chunks of the longest
 // context of the call.
 constexpr int kWaves = 8;              // decode: waves of a chunk workgroup, one query head each
-// Prefill: 4 query rows per workgroup, one per wave. Each wave keeps its chunk's
-// key row and value column in registers across the group's heads (~220
-// VGPRs), so a SIMD holds two waves; with 4-wave workgroups that is two
-// workgroups per CU, one staging its chunk while the other computes (measured
-// on MI355X at 512 rows: 58 us, against 62 with 8-row workgroups, 63 with 2,
-// 99 with 1; interleaving two heads per wave, or reloading the chunk from LDS
-// per head for occupancy, was slower; so were capping the registers at three
-// waves a SIMD, which spills (168 us), and reading each head's query with
-// scalar loads instead of staging it in LDS (69-73 us: the loads sit on every
-// head's critical path, and the probabilities read back for P V still hold
-// 64 VGPRs, so two waves a SIMD remain).
+// Prefill: 4 query rows per workgroup, one per wave. A wave attends its row's
+// heads of the group together (nc_attend.h's chunk_scores_n and
+// chunk_values_n: every key or value element read from LDS once for all the
+// heads' chains, the d and key loops unrolled by two so the compiler does not
+// issue every head's broadcast reads at once), 120 VGPRs, so LDS (42 KB a
+// workgroup) is what bounds a CU at three workgroups. Measured on MI355X at
+// 512 rows, chunks + combine: 49 us, against 58 us when each head was
+// attended alone with the key row and value column held in registers across
+// the heads (~220 VGPRs, two waves a SIMD); 8-row workgroups: 49 us. Earlier
+// variants of the one-head-at-a-time kernel, all slower: 8, 2 or 1 rows a
+// workgroup (62, 63, 99 us), registers capped at three waves a SIMD (spills:
+// 168 us), each head's query read with scalar loads (69-73 us).
 constexpr int kRowsPerBlock = 4;
 constexpr int kHeadBatch = 8;          // prefill: query heads of a row held in LDS at once
 
@@ -174,27 +175,41 @@ __device__ __forceinline__ F *chunk_result(F *part, int h, int rows, int r, int 
     return part + (((size_t)h * rows + r) * jstride + j) * (D + 2);
 }
 
-// Prefill: grid (chunks, kv_heads, ceil(rows / 4)) over the slab of query rows
-// i0 .. i0 + rows - 1 of a call of M rows; row i sits at position past + i and
-// sees keys 0 .. past + i (the cache already holds them, nc_rope_append).
-template <int D>
-__global__ __launch_bounds__(64 * kRowsPerBlock) void attention_rows_chunks(
+// H heads of one query row attended to a staged chunk (nc_attend.h's two
+// halves for H queries), their chunk results stored head_stride floats apart.
+template <int D, int H>
+__device__ __forceinline__ void attend_heads(float (*qp)[nc::kChunk], const nc::Staged<D> &st, int n, float scale,
+                                             float *dst, size_t head_stride) {
+    float m[H], l[H], o[H];
+    nc::chunk_scores_n<D, H>(qp, st, n, scale, m, l);
+    nc::chunk_values_n<D, H>(qp, st, o);
+#pragma unroll
+    for (int u = 0; u < H; ++u) nc::keep_result<D>(dst + u * head_stride, nc::ChunkResult{m[u], l[u], o[u]});
+}
+
+// Prefill: grid (chunks, kv_heads, ceil(rows / ROWS)) over the slab of query
+// rows i0 .. i0 + rows - 1 of a call of M rows; row i sits at position past + i
+// and sees keys 0 .. past + i (the cache already holds them, nc_rope_append).
+// A wave takes its row's heads in batches of up to 8 in two phases: the
+// scores, softmax and sums of every head of the batch (each head's
+// probabilities written over its query in LDS), then every head's P V.
+template <int D, int ROWS>
+__global__ __launch_bounds__(64 * ROWS) void attention_rows_chunks(
     float *__restrict__ part, const float *__restrict__ qkv, const float *__restrict__ kcache,
     const float *__restrict__ vcache, int heads, int kv_heads, int past, int capacity, float scale, int i0, int rows,
     int M, int jstride, const int64_t *__restrict__ pos_ptr, int32_t *__restrict__ error) {
     if (pos_ptr && !position_fits(pos_ptr, M, capacity, error, past)) return;
     const int j = blockIdx.x, g = blockIdx.y, t0 = j * nc::kChunk;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r_last = min((int)blockIdx.z * kRowsPerBlock + kRowsPerBlock, rows) - 1;
+    const int r_last = min((int)blockIdx.z * ROWS + ROWS, rows) - 1;
     if (past + i0 + r_last + 1 <= t0) return;             // no row of the block sees this chunk
     __shared__ __align__(16) float lds[nc::Staged<D>::kFloats];
-    __shared__ __align__(16) float qs[kRowsPerBlock][kHeadBatch][D];   // per wave: up to 8 query heads of its row
-    __shared__ __align__(16) float pbuf[kRowsPerBlock][nc::kChunk];
+    __shared__ __align__(16) float qp[ROWS][kHeadBatch][nc::kChunk];   // per wave: a head's query, then its p
     const nc::Staged<D> st(lds);
     const int group = heads / kv_heads, width = (heads + 2 * kv_heads) * D;
-    nc::ChunkLoad<D, 64 * kRowsPerBlock> load;
+    nc::ChunkLoad<D, 64 * ROWS> load;
     load.issue(kcache + (size_t)g * capacity * D, vcache + (size_t)g * capacity * D, t0, capacity - 1);
-    const int r = blockIdx.z * kRowsPerBlock + wave, i = i0 + r;
+    const int r = blockIdx.z * ROWS + wave, i = i0 + r;
     const bool valid = r < rows && past + i + 1 > t0;
     const float *qrow = qkv + (size_t)(valid ? i : 0) * width + (size_t)g * group * D;
     float qv[kHeadBatch];
@@ -203,24 +218,30 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void attention_rows_chunks(
     load.store(st, -1, past + M - t0);                    // keys past + M and on: not yet in the cache
 #pragma unroll
     for (int u = 0; u < kHeadBatch; ++u)
-        if (u < group && lane < D) qs[wave][u][lane] = qv[u];
+        if (u < group && lane < D) qp[wave][u][lane] = qv[u];
     __syncthreads();
     if (!valid) return;
     const int n = min(nc::kChunk, past + i + 1 - t0);
-    // heads of the group two at a time (two independent chains per wave), in
-    // batches of 8 held in qs; a batch's odd head alone
     for (int h0 = 0; h0 < group; h0 += kHeadBatch) {
         if (h0 > 0) {                                       // groups of more than 8 heads (wave-local)
 #pragma unroll
             for (int u = 0; u < kHeadBatch; ++u) qv[u] = (h0 + u < group && lane < D) ? qrow[(h0 + u) * D + lane] : 0.0f;
 #pragma unroll
             for (int u = 0; u < kHeadBatch; ++u)
-                if (lane < D) qs[wave][u][lane] = qv[u];
+                if (lane < D) qp[wave][u][lane] = qv[u];
         }
         const int hn = min(kHeadBatch, group - h0);
-        for (int u = 0; u < hn; ++u) {
-            const nc::ChunkResult res = nc::attend_staged<D>(qs[wave][u], st, n, scale, pbuf[wave]);
-            nc::keep_result<D>(chunk_result(part, g * group + h0 + u, rows, r, jstride, j, D), res);
+        float *dst = chunk_result(part, g * group + h0, rows, r, jstride, j, D);
+        const size_t head_stride = (size_t)rows * jstride * (D + 2);
+        switch (hn) {
+        case 1: attend_heads<D, 1>(qp[wave], st, n, scale, dst, head_stride); break;
+        case 2: attend_heads<D, 2>(qp[wave], st, n, scale, dst, head_stride); break;
+        case 3: attend_heads<D, 3>(qp[wave], st, n, scale, dst, head_stride); break;
+        case 4: attend_heads<D, 4>(qp[wave], st, n, scale, dst, head_stride); break;
+        case 5: attend_heads<D, 5>(qp[wave], st, n, scale, dst, head_stride); break;
+        case 6: attend_heads<D, 6>(qp[wave], st, n, scale, dst, head_stride); break;
+        case 7: attend_heads<D, 7>(qp[wave], st, n, scale, dst, head_stride); break;
+        default: attend_heads<D, 8>(qp[wave], st, n, scale, dst, head_stride); break;
         }
     }
 }
@@ -529,7 +550,7 @@ int32_t launch_prefill(void **p, int64_t M, int64_t heads, int64_t kv, int64_t p
     for (int64_t i0 = 0; i0 < M; i0 += slab) {
         const int64_t rows = std::min(slab, M - i0);
         const int64_t chunks = pos ? jstride : (past + i0 + rows + nc::kChunk - 1) / nc::kChunk;
-        hipLaunchKernelGGL(attention_rows_chunks<D>,
+        hipLaunchKernelGGL((attention_rows_chunks<D, kRowsPerBlock>),
                            dim3((unsigned)chunks, (unsigned)kv, (unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock)),
                            dim3(64 * kRowsPerBlock), 0, nc::stream(), work, (const float *)p[1], (const float *)p[2],
                            (const float *)p[3], (int)heads, (int)kv, (int)host_past, (int)cap, scale, (int)i0,
