@@ -156,19 +156,21 @@ __global__ __launch_bounds__(kThreads) void rope_append(float *__restrict__ qkv,
 // context of the call.
 constexpr int kWaves = 8;              // decode: waves of a chunk workgroup, one query head each
 // Prefill: 4 query rows per workgroup, one per wave. A wave attends its row's
-// heads of the group together (nc_attend.h's chunk_scores_n and
-// chunk_values_n: every key or value element read from LDS once for all the
-// heads' chains, the d and key loops unrolled by two so the compiler does not
-// issue every head's broadcast reads at once), 120 VGPRs, so LDS (42 KB a
-// workgroup) is what bounds a CU at three workgroups. Measured on MI355X at
-// 512 rows, chunks + combine: 49 us, against 58 us when each head was
-// attended alone with the key row and value column held in registers across
-// the heads (~220 VGPRs, two waves a SIMD); 8-row workgroups: 49 us. Earlier
-// variants of the one-head-at-a-time kernel, all slower: 8, 2 or 1 rows a
-// workgroup (62, 63, 99 us), registers capped at three waves a SIMD (spills:
-// 168 us), each head's query read with scalar loads (69-73 us).
+// heads of the group together, up to 7 at a time (nc_attend.h's
+// chunk_scores_n and chunk_values_n: every key or value element read from LDS
+// once for all the heads' chains, the d and key loops unrolled by two so the
+// compiler does not issue every head's broadcast reads at once): 108 VGPRs,
+// and 40 KB of LDS a workgroup (the staged chunk and 7 query/probability rows
+// a wave), so a CU holds four workgroups, four waves a SIMD. Measured on
+// MI355X at 512 rows, chunks + combine: 46 us; 49 us with 8-head batches
+// (42 KB: three workgroups a CU), also with 8-row workgroups; 58 us when each
+// head was attended alone with the key row and value column held in
+// registers across the heads (~220 VGPRs, two waves a SIMD). Earlier variants
+// of that one-head kernel, all slower: 8, 2 or 1 rows a workgroup (62, 63, 99
+// us), registers capped at three waves a SIMD (spills: 168 us), each head's
+// query read with scalar loads (69-73 us).
 constexpr int kRowsPerBlock = 4;
-constexpr int kHeadBatch = 8;          // prefill: query heads of a row held in LDS at once
+constexpr int kHeadBatch = 7;          // prefill: query heads of a row held in LDS at once (a group, in Qwen2)
 
 template <typename F>
 __device__ __forceinline__ F *chunk_result(F *part, int h, int rows, int r, int jstride, int j, int D) {
@@ -185,6 +187,16 @@ __device__ __forceinline__ void attend_heads(float (*qp)[nc::kChunk], const nc::
     nc::chunk_values_n<D, H>(qp, st, o);
 #pragma unroll
     for (int u = 0; u < H; ++u) nc::keep_result<D>(dst + u * head_stride, nc::ChunkResult{m[u], l[u], o[u]});
+}
+
+// attend_heads<D, hn> for a run-time hn in 1 .. H.
+template <int D, int H>
+__device__ __forceinline__ void attend_heads_upto(int hn, float (*qp)[nc::kChunk], const nc::Staged<D> &st, int n,
+                                                  float scale, float *dst, size_t head_stride) {
+    if constexpr (H > 1) {
+        if (hn < H) return attend_heads_upto<D, H - 1>(hn, qp, st, n, scale, dst, head_stride);
+    }
+    attend_heads<D, H>(qp, st, n, scale, dst, head_stride);
 }
 
 // Prefill: grid (chunks, kv_heads, ceil(rows / ROWS)) over the slab of query
@@ -233,16 +245,7 @@ __global__ __launch_bounds__(64 * ROWS) void attention_rows_chunks(
         const int hn = min(kHeadBatch, group - h0);
         float *dst = chunk_result(part, g * group + h0, rows, r, jstride, j, D);
         const size_t head_stride = (size_t)rows * jstride * (D + 2);
-        switch (hn) {
-        case 1: attend_heads<D, 1>(qp[wave], st, n, scale, dst, head_stride); break;
-        case 2: attend_heads<D, 2>(qp[wave], st, n, scale, dst, head_stride); break;
-        case 3: attend_heads<D, 3>(qp[wave], st, n, scale, dst, head_stride); break;
-        case 4: attend_heads<D, 4>(qp[wave], st, n, scale, dst, head_stride); break;
-        case 5: attend_heads<D, 5>(qp[wave], st, n, scale, dst, head_stride); break;
-        case 6: attend_heads<D, 6>(qp[wave], st, n, scale, dst, head_stride); break;
-        case 7: attend_heads<D, 7>(qp[wave], st, n, scale, dst, head_stride); break;
-        default: attend_heads<D, 8>(qp[wave], st, n, scale, dst, head_stride); break;
-        }
+        attend_heads_upto<D, kHeadBatch>(hn, qp[wave], st, n, scale, dst, head_stride);
     }
 }
 
