@@ -19,9 +19,15 @@
 //    tile; wave w computes a WM x WN sub-tile as (WM / 16) x (WN / 16) MFMAs.
 //  * Each k stage moves BM x BK bytes of xq and BN x BK bytes of q (twice for
 //    the SwiGLU pair) from HBM/L2 into registers with 16-byte loads, 8 or 4
-//    lanes per 128- or 64-byte row segment, then into LDS rows padded by 16
-//    bytes so the 16-byte MFMA operand reads of 16 consecutive rows fall in
-//    distinct banks. A ring of NS register stages keeps the loads of stages
+//    lanes per 128- or 64-byte row segment, then into unpadded LDS rows whose
+//    16-byte chunks are permuted (chunk c of row r at c ^ ((r / 2) mod the
+//    chunks a row)), so neither the stores nor the 16-byte MFMA operand reads
+//    of 16 consecutive rows meet a bank conflict (rocprofv3
+//    SQ_LDS_BANK_CONFLICT: 0 cycles for 128- and 64-byte rows, against about
+//    2.6 an LDS instruction with rows padded by 16 bytes, and 3 permuting by
+//    r mod the chunks a row at 64 bytes; 11.5 against 12.4 us on (896,4864)
+//    at M = 512).
+//    A ring of NS register stages keeps the loads of stages
 //    t + 1 .. t + NS - 1 in flight while stage t is multiplied out of one of
 //    two LDS buffers; one barrier per stage.
 //  * Tiles are handed to the 8 XCDs (workgroup i runs on XCD i % 8) so that
@@ -75,7 +81,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_i8_mfma(GemmA
     constexpr int THREADS = WAVES * 64;
     constexpr int NB = EPI == kSwiglu ? 2 : 1;        // weight matrices per tile
     constexpr int CPR = BK / 16;                      // 16-byte chunks per row per stage
-    constexpr int STRIDE = BK + 16;                   // padded LDS row
+    constexpr int STRIDE = BK;                        // LDS row, unpadded
+    static_assert(BK == 64 || BK == 128, "LDS chunk permutation measured for 64- and 128-byte rows");
+    // The byte offset in an LDS buffer of 16-byte chunk c of row r: the chunks
+    // of a row permuted by (r / 2) mod CPR, so the 16-byte fragment reads of
+    // 16 consecutive rows at one k, and the stores of a row's consecutive
+    // chunks, meet no bank conflict (measured, both row lengths).
+    auto lds_at = [](int r, int c) { return r * STRIDE + ((c ^ ((r >> 1) & (CPR - 1))) << 4); };
     constexpr int A_PER = BM * CPR / THREADS;
     constexpr int B_PER = NB * BN * CPR / THREADS;
     constexpr int MI = WM / 16, NI = WN / 16;
@@ -101,7 +113,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_i8_mfma(GemmA
     for (int i = 0; i < A_PER; ++i) {
         const int id = tid + i * THREADS, r = id / CPR, c = id % CPR;
         srcA[i] = a.xq + (size_t)min(m0 + r, M - 1) * K;
-        dstA[i] = r * STRIDE + c * 16;
+        dstA[i] = lds_at(r, c);
         colA[i] = c * 16;
     }
     const int8_t *srcB[B_PER];
@@ -111,7 +123,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_i8_mfma(GemmA
         const int id = tid + i * THREADS, r = id / CPR, c = id % CPR;   // r < NB * BN
         const int8_t *base = (NB == 2 && r >= BN) ? a.q2 : a.q;
         srcB[i] = base + (size_t)min(n0 + r % BN, N - 1) * K;
-        dstB[i] = r * STRIDE + c * 16;
+        dstB[i] = lds_at(r, c);
         colB[i] = c * 16;
     }
 
@@ -164,13 +176,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_i8_mfma(GemmA
             v4i fa[MI];
 #pragma unroll
             for (int i = 0; i < MI; ++i)
-                fa[i] = *reinterpret_cast<const v4i *>(&sA[buf][(wm + i * 16 + row16) * STRIDE + kk + kq]);
+                fa[i] = *reinterpret_cast<const v4i *>(&sA[buf][lds_at(wm + i * 16 + row16, (kk + kq) >> 4)]);
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
 #pragma unroll
                 for (int j = 0; j < NI; ++j) {
                     const v4i fb =
-                        *reinterpret_cast<const v4i *>(&sB[buf][(b * BN + wn + j * 16 + row16) * STRIDE + kk + kq]);
+                        *reinterpret_cast<const v4i *>(&sB[buf][lds_at(b * BN + wn + j * 16 + row16, (kk + kq) >> 4)]);
 #pragma unroll
                     for (int i = 0; i < MI; ++i)
                         acc[b][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb, fa[i], acc[b][i][j], 0, 0, 0);
