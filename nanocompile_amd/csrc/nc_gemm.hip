@@ -279,11 +279,20 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_i8_mfma(GemmA
         const RopeArgs &ro = a.rope;
         __syncthreads();                             // every wave is done with the staging buffers
         float *tile = reinterpret_cast<float *>(&sA[0][0]);
+        // Element (row, col) of the tile: the row's 4-float granules permuted by
+        // a bijection of the row index (consecutive rows taking opposite halves),
+        // so the 16-byte stores of 16 rows at one column, and the reads of two
+        // consecutive rows, meet no bank conflict.
+        constexpr int G = BN / 4;
+        auto tile_at = [](int row, int col) {
+            const int f = (row ^ ((row & 1) * (G / 2))) & (G - 1);
+            return row * BN + ((((col >> 2) ^ f)) << 2) + (col & 3);
+        };
 #pragma unroll
         for (int i = 0; i < MI; ++i) {
 #pragma unroll
             for (int j = 0; j < NI; ++j) {
-                float *t = tile + (wm + i * 16 + row16) * BN + wn + j * 16 + nq;
+                float *t = tile + tile_at(wm + i * 16 + row16, wn + j * 16 + nq);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     float v = nc::dequant(acc[0][i][j][r], xs_r[i], w1_r[j][r]);
@@ -298,7 +307,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_i8_mfma(GemmA
         for (int u = 0; u < PAIRS; ++u) {
             const int idx = tid + u * THREADS, mm = idx / HALF, jj = idx - mm * HALF, m = m0 + mm;
             if (m >= M) continue;
-            const float x0 = tile[mm * BN + jj], x1 = tile[mm * BN + jj + HALF];
+            const float x0 = tile[tile_at(mm, jj)], x1 = tile[tile_at(mm, jj + HALF)];
             float *y = static_cast<float *>(a.out) + (size_t)m * N + n0;
             const int position = rope_past + m;
             float y0 = x0, y1 = x1;
