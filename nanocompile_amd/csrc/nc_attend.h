@@ -199,14 +199,17 @@ __device__ __forceinline__ void chunk_scores_n(float (*qp)[kChunk], const Staged
     }
 }
 
+// (keys from n on add +-0 to accumulators that are never -0, so the key loop
+// stops at the first group of four that holds none of the n keys)
 template <int D, int H>
-__device__ __forceinline__ void chunk_values_n(float (*qp)[kChunk], const Staged<D> &st, float (&o)[H]) {
+__device__ __forceinline__ void chunk_values_n(float (*qp)[kChunk], const Staged<D> &st, int n, float (&o)[H]) {
     const int lane = threadIdx.x & 63;
     const int dl = lane < D ? lane : 0;
 #pragma unroll
     for (int u = 0; u < H; ++u) o[u] = 0.0f;
+    const int groups = (n + 3) >> 2;
 #pragma unroll 2
-    for (int i = 0; i < kChunk / 4; ++i) {
+    for (int i = 0; i < groups; ++i) {
         const float v0 = st.values[(4 * i + 0) * D + dl], v1 = st.values[(4 * i + 1) * D + dl];
         const float v2 = st.values[(4 * i + 2) * D + dl], v3 = st.values[(4 * i + 3) * D + dl];
 #pragma unroll

@@ -184,7 +184,7 @@ __device__ __forceinline__ void attend_heads(float (*qp)[nc::kChunk], const nc::
                                              float *dst, size_t head_stride) {
     float m[H], l[H], o[H];
     nc::chunk_scores_n<D, H>(qp, st, n, scale, m, l);
-    nc::chunk_values_n<D, H>(qp, st, o);
+    nc::chunk_values_n<D, H>(qp, st, n, o);
 #pragma unroll
     for (int u = 0; u < H; ++u) nc::keep_result<D>(dst + u * head_stride, nc::ChunkResult{m[u], l[u], o[u]});
 }
