@@ -301,7 +301,7 @@ __global__ __launch_bounds__(64) void attention_combine(float *__restrict__ ctx,
 // quantize_token: the maximum of |ctx| over the row, its scale, each value
 // quantized) in the same launch: ctx, xq and xs with the bits of a combine
 // followed by nc_quantize_token_i8.
-template <int D>
+template <int D, int BATCH>
 __global__ __launch_bounds__(1024) void attention_combine_quant(float *__restrict__ ctx, int8_t *__restrict__ xq,
                                                                 float *__restrict__ xs, const float *__restrict__ part,
                                                                 int heads, int past, int capacity, int i0, int rows,
@@ -318,7 +318,7 @@ __global__ __launch_bounds__(1024) void attention_combine_quant(float *__restric
     float *results = results_all + (size_t)h * jstride * (D + 2);
     const float *src = chunk_result(part, h, rows, r, jstride, 0, D);
     const int total = J * (D + 2);
-    constexpr int kBatch = 8;
+    constexpr int kBatch = BATCH;                        // loads a lane keeps in flight
     for (int base = 0; base < total; base += 64 * kBatch) {
         float v[kBatch];
 #pragma unroll
@@ -524,13 +524,17 @@ int32_t launch_combine(float *ctx, const float *part, int64_t heads, int64_t pas
     return launch_combine_batch<D, 16>(ctx, part, heads, past, cap, i0, rows, M, jstride, pos);
 }
 
+// A head's chunk results in one batch of loads up to 9 chunks at D = 64 (576
+// floats: a 512-token prompt's 8 chunks in one memory round trip), else in
+// batches of 16 loads a lane.
 template <int D>
 int32_t launch_combine_quant(void **p, const float *part, int64_t heads, int64_t past, int64_t cap, int64_t i0,
                              int64_t rows, int64_t M, int64_t jstride, const int64_t *pos) {
     const size_t lds = (size_t)heads * jstride * (D + 2) * sizeof(float);
-    hipLaunchKernelGGL(attention_combine_quant<D>, dim3((unsigned)rows), dim3((unsigned)(64 * heads)), lds,
-                       nc::stream(), (float *)p[0], (int8_t *)p[6], (float *)p[7], part, (int)heads, (int)past,
-                       (int)cap, (int)i0, (int)rows, (int)M, (int)jstride, pos);
+    auto kernel = jstride * (D + 2) <= 64 * 9 ? attention_combine_quant<D, 9> : attention_combine_quant<D, 16>;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)rows), dim3((unsigned)(64 * heads)), lds, nc::stream(), (float *)p[0],
+                       (int8_t *)p[6], (float *)p[7], part, (int)heads, (int)past, (int)cap, (int)i0, (int)rows,
+                       (int)M, (int)jstride, pos);
     return nc::launched("attention_combine_quant");
 }
 
