@@ -253,31 +253,31 @@ constexpr int kGemmTiles = 9;
 constexpr int kGemmMinTokens = 16;
 
 // The MFMA tile for a shape when the caller asks for the default, from a sweep
-// of every tile on MI355X over the model's shapes at M = 128 .. 4096:
-// 64 x 128 (8 waves) for the largest problems and for long k loops with many
-// tiles; 64 x 64 from 144 such tiles on (gate at M = 128: 5.30 us against
-// 5.78 with 32 x 64; qkv at M = 512: 5.29 against 5.74); for long k loops
-// below that, 32 x 64 with 8 stages in flight once there are 192 such tiles,
-// else 32 x 32 (down at M = 128 / 256: 7.93 / 8.46 us against 10.9 / 11.1);
-// 32 x 64 with 192 tiles or more; else 32 x 32.
+// of every tile on MI355X over the model's shapes at M = 128 .. 1024 (with the
+// GEMM's conflict-free LDS layout): 64 x 128 (8 waves) for the largest
+// problems and for long k loops with many tiles; 64 x 64 from 200 such tiles
+// (gate at M = 512: 10.19 us against 11.65 with 32 x 64; down at M = 1024:
+// 15.97 against 17.5-20.9); else 32 x 32 (at M = 512: q/o 4.53 us against
+// 4.70 with 32 x 64, qkv 5.25 against 5.52 with 64 x 64, down 11.09 against
+// 11.30 with 32 x 64 and 8 stages; gate at M = 128: 5.29 against 5.57).
 int auto_tile(int M, int N, int K) {
     auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
     const int t64 = tiles(64, 64);
     if (t64 >= 1792 || (K >= 2048 && t64 >= 256)) return 6;
-    if (t64 >= 144) return 5;
-    if (K >= 2048) return tiles(32, 64) >= 192 ? 4 : 2;
-    if (tiles(32, 64) >= 192) return 1;
+    if (t64 >= 200) return 5;
     return 2;
 }
 
-// The SwiGLU pair's default: its tiles stage two weight blocks, so it keeps
-// smaller tiles: 32 x 64 once there are 512 of them, else 32 x 32 (measured at
-// N = 4864, K = 896: M = 512 20.7 us against 22.4-23.3 for 64 x 64; M = 128
-// 8.90 us with 32 x 32 against 10.58 with 32 x 64; M = 256 13.5 with 32 x 64).
+// The SwiGLU pair's default: 64 x 64 with two register stages (its tiles
+// stage two weight blocks, so deeper rings cost occupancy) from 400 such
+// tiles, else 32 x 32 (measured at N = 4864, K = 896: M = 384 / 512 / 1024 /
+// 2048: 15.7 / 19.3 / 30.5 / 54.1 us against 16.8 / 20.6 / 35.2 / 68.1 with
+// 32 x 32 and 17.3 / 20.6 / 34.9 / 63.3 with 32 x 64; M = 128 / 256: 8.41 /
+// 12.13 us with 32 x 32 against 11.0 / 14.6 with 64 x 64).
 int auto_tile_pair(int M, int N, int K) {
     (void)K;
-    const int t = ((M + 31) / 32) * ((N + 63) / 64);
-    return t >= 512 ? 1 : 2;
+    const int t64 = ((M + 63) / 64) * ((N + 63) / 64);
+    return t64 >= 400 ? 5 : 2;
 }
 
 template <int KS, int MT, bool ACC_OUT>
