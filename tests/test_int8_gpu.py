@@ -107,6 +107,19 @@ def test_weight_quantizer_special_rows(gpu):
     assert list(kernels.quantize_int8(quirk)[0].numpy()[0]) == [1, 127, -1, 0]
 
 
+@pytest.mark.parametrize("k", [67, 4864])
+def test_token_quantizer_both_load_widths(gpu, k):
+    """Rows of a multiple of 4 floats take 16-byte loads, others 4-byte ones: both are the oracle."""
+    from nanocompile_amd import kernels
+    rng = np.random.default_rng(k)
+    x = rng.standard_normal((5, k)).astype(np.float32)
+    x[rng.random(x.shape) < 0.01] *= 20
+    x[4] = 0.0
+    xq, xs = kernels.quantize_token(x)
+    exq, exs = R.quantize_token(x)
+    assert np.array_equal(xq.numpy(), exq) and np.array_equal(bits(xs.numpy()), bits(exs))
+
+
 def test_token_quantizer_edges(gpu):
     from nanocompile_amd import kernels
     x = np.zeros((4, 64), np.float32)
