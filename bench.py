@@ -7,13 +7,18 @@ Prints ONE JSON line.
 ``decode`` (default): a random-init Qwen2.5-0.5B-shaped
 model (24 layers, hidden 896, 14/2 heads of 64, MLP 4864, vocab 151936, tied
 float32 LM head), all 168 projections per-row int8 with per-token int8
-activations; a 128-token prompt of uniform-random ids, then greedy decoding.
-A step is one decode token: one replay of the captured decode step (every
-layer, the LM head, the argmax, the feedback of the token). K steps are timed
-with HIP events on the library stream (default 255, so 256 tokens in all with
-the prompt's). The host C model (oracle/nc_model.c) decodes the same prompt
-on this machine's cores in the same run; its tokens must equal the GPU's, and
-its decode rate is the CPU baseline.
+activations; a 128-token prompt of uniform-random ids, then 256 greedy tokens
+(past to 384) whatever ``--steps`` is. A step is one decode token: one replay
+of the captured decode step (every layer, the LM head, the argmax, the
+feedback of the token). The timed region is the last K of the 255 replays
+(default all 255), ending at past 383, bracketed by HIP events on the library
+stream; the mean over all 255 is reported under ``config.all_replays``. Each
+kernel group of the step (qkv, attention, o, gate/up, down, LM head) is then
+timed live, and the time-dominant one is the line's ``roofline``. The host C
+model (oracle/nc_model.c) decodes the same prompt on this machine's cores in
+the same run; all 256 of its tokens must equal the GPU's, and a thread sweep
+of its decode steps is the CPU baseline, with config 1's GEMV on the host
+(thread sweep, GB/s) beside it.
 
 ``gemv``: the decode projection [1,896] x [4864,896]^T,
 weights rotated through 128 device copies (560 MB, past the 256 MB Infinity
@@ -58,7 +63,11 @@ PROMPT, NEW_TOKENS = 128, 256
 CALIBRATION_BYTES = 256 * 2**20
 
 
-LM_HEAD_KERNEL = "lm_head_ring<896, 24>"     # nc_lm_head at the model's width (nc_model.hip)
+# Each decode-step kernel group's kernel symbol (as a rocprofv3 kernel trace names it).
+KERNEL_SYMBOLS = {"qkv": "gemv_decode<896, 0, 0, 8, 1, 16>",
+                  "attention": "attention_decode_chunks<64, true> + attention_combine<64, 8>",
+                  "o": "gemv_decode<896, 1, 1, 8, 1, 16>", "gate/up": "gemv_decode<896, 0, 2, 8, 1, 16>",
+                  "down": "gemv_decode<4864, 1, 1, 64, 4, 4>", "lm head": "lm_head_ring<896, 24>"}
 
 
 def gemv_bytes(m: int, n: int, k: int) -> int:
@@ -312,16 +321,108 @@ def block_measurements(model, seed: int = 7) -> dict:
 
 # -- config 5: the whole model, greedy decode ----------------------------------------
 
+LM_HEAD_BYTES = 4 * 151936 * 896 + 4 * 896 + 8
+
+
+def decode_kernel_bytes(label: str, past: int) -> int:
+    """Algorithmic bytes of one launch of a decode-step kernel group at the model's widths
+    (H 896, MLP 4864, q/k/v rows 1152, 14/2 heads of 64), its token at position ``past``."""
+    H, I, W, heads, kv, D = 896, 4864, 1152, 14, 2, 64
+    if label == "qkv":           # int8 rows, scales, bias, x, gamma, out
+        return W * H + 4 * W + 4 * W + 4 * H + 4 * H + 4 * W
+    if label == "attention":     # cached K and V read, the q/k/v row, cos/sin, ctx out, the k/v append
+        return 2 * kv * past * D * 4 + 4 * W + 4 * D + 4 * heads * D + 2 * kv * D * 4
+    if label == "o":             # int8 rows, scales, ctx, residual read and written
+        return H * heads * D + 4 * H + 4 * heads * D + 8 * H
+    if label == "gate/up":       # two int8 matrices and scales, x, gamma, h out
+        return 2 * I * H + 8 * I + 4 * H + 4 * H + 4 * I
+    if label == "down":          # int8 rows, scales, h, residual read and written
+        return H * I + 4 * H + 4 * I + 8 * H
+    if label == "lm head":       # float32 table, x, the argmax key
+        return LM_HEAD_BYTES
+    raise KeyError(label)
+
+
+def decode_kernel_table(model, cache, past: int) -> dict:
+    """Each kernel group of one decode step at position ``past``, timed live on the library
+    stream: a captured graph of the group's launches (one per layer, each layer's own weights,
+    so they stream from HBM as in the step) replayed between HIP events, per launch."""
+    from nanocompile_amd import hip
+    from nanocompile_amd.kernels import float_bits
+    c = model.config
+    groups: dict[str, list] = {}
+    for label, name, pointers, sizes in model.decode_layer_calls(cache, past):
+        groups.setdefault(label, []).append((name, pointers, sizes))
+    H, V = c.hidden_size, c.vocab_size
+    head = ("nc_lm_head", [None, model.best, model.normed, model.head, model.norm],
+            [1, V, H, float_bits(c.rms_norm_eps), 1])
+    groups["lm head"] = [head] * 8
+    table = {}
+    for label, calls in groups.items():
+        per_step = 1 if label == "lm head" else len(calls)
+        us = graph_us(lambda i, calls=calls: hip.call(*calls[i]), len(calls), rounds=7)
+        nbytes = decode_kernel_bytes(label, past)
+        table[label] = {"launch_us": round(us, 3), "launches_per_step": per_step,
+                        "step_us": round(us * per_step, 2), "bytes_per_launch": nbytes,
+                        "gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                        "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+    return table
+
+
+def cpu_decode(config, weights, prompt, gpu_tokens, seconds: float = 16.0) -> dict:
+    """The host C int8 model (oracle/nc_model.c) on this machine's cores: every token checked
+    against the GPU's, then a thread sweep of decode steps at the config's positions."""
+    from oracle import host
+    from oracle.host_model import HostQwen2
+    cores = os.cpu_count() or 1
+    counts = sorted({1, 2, 4, 8, 16, min(cores, 64)} & set(range(1, min(cores, 64) + 1)))
+    t0 = time.perf_counter()
+    ref = HostQwen2(config, weights, capacity=PROMPT + NEW_TOKENS)
+    log(f"cpu: host model built in {time.perf_counter() - t0:.1f} s")
+    host.set_threads(counts[-1])
+    t0 = time.perf_counter()
+    _, first = ref.forward(prompt)
+    prefill_s = time.perf_counter() - t0
+    tokens = [first]
+    t0 = time.perf_counter()
+    for _ in range(NEW_TOKENS - 1):
+        tokens.append(ref.forward([tokens[-1]])[1])
+    all_cores_full = (NEW_TOKENS - 1) / (time.perf_counter() - t0)
+    if tokens != gpu_tokens:
+        first_diff = next(i for i, (a, b) in enumerate(zip(tokens, gpu_tokens)) if a != b)
+        log(f"cpu: TOKENS DIFFER from the GPU's at position {first_diff}")
+    # the sweep: each thread count decodes steps at the config's last positions (past 383 - n
+    # .. 382), feeding the same tokens, for about seconds / len(counts) each
+    rates = {}
+    for t in counts:
+        host.set_threads(t)
+        n = max(2, min(NEW_TOKENS - 2, int(seconds / len(counts) * (all_cores_full if t == counts[-1]
+                                                                          else all_cores_full * t / counts[-1]))))
+        ref.length = PROMPT + NEW_TOKENS - 1 - n
+        t0 = time.perf_counter()
+        for j in range(n):
+            ref.forward([tokens[NEW_TOKENS - 1 - n + j]])
+        rates[t] = n / (time.perf_counter() - t0)
+    best = max(rates, key=rates.get)
+    return {"tok_s": rates[best], "threads": best, "all_cores_tok_s": rates[counts[-1]],
+            "all_cores": counts[-1], "by_threads": {str(k): round(v, 2) for k, v in rates.items()},
+            "full_run_tok_s": all_cores_full, "prefill_s": prefill_s, "cores": cores, "isa": host.isa(),
+            "tokens_identical": tokens == gpu_tokens}
+
 
 def decode(steps: int, warmup: int, cpu: bool, seed: int = 0, graph: bool = True, blocks: bool = True) -> dict:
-    from nanocompile_amd import hip
+    """Config 5 as stated: 256 greedy tokens after the 128-token prompt, whatever ``steps`` is;
+    the last ``steps`` of the 255 replays (ending at past 383, the config's expensive end) are
+    the timed region, and the mean over all 255 is reported beside them."""
     from nanocompile_amd.hip import Event
     from nanocompile_amd.models.config import QWEN25_05B
     from nanocompile_amd.models.config import random_weights
     from nanocompile_amd.models.qwen2 import Qwen2
 
     config = QWEN25_05B
-    new_tokens = steps + 1
+    replays = NEW_TOKENS - 1
+    if not 1 <= steps <= replays:
+        raise SystemExit(f"--steps {steps}: config 5 has {replays} decode steps after the prompt's token")
     t0 = time.perf_counter()
     weights = random_weights(config, seed=seed)
     prompt = [int(t) for t in np.random.default_rng(seed + 1).integers(0, config.vocab_size, PROMPT)]
@@ -331,62 +432,31 @@ def decode(steps: int, warmup: int, cpu: bool, seed: int = 0, graph: bool = True
     log(f"decode: model uploaded and quantized on the GPU in {time.perf_counter() - t0:.1f} s")
 
     for _ in range(warmup):
-        model.generate(prompt, min(16, new_tokens), graph=graph)
-    start, stop = Event(), Event()
+        model.generate(prompt, 16, graph=graph)
+    marks = {0: Event(), replays - steps: Event(), replays: Event()}
 
-    def timer(what: str) -> None:
-        (start if what == "start" else stop).record()
+    def timer(i: int) -> None:
+        if i in marks:
+            marks[i].record()
 
     t0 = time.perf_counter()
-    tokens = model.generate(prompt, new_tokens, timer=timer, graph=graph)
+    tokens = model.generate(prompt, NEW_TOKENS, timer=timer, graph=graph)
     wall = time.perf_counter() - t0
-    decode_ms = start.elapsed_ms(stop)
-    result = {"tokens": tokens, "decode_ms": decode_ms, "steps": steps, "wall_s": wall,
-              "tok_s": steps / (decode_ms * 1e-3)}
-
-    # the dominant kernel, timed alone on the library stream: the float32 LM head
-    H, V = config.hidden_size, config.vocab_size
-    reps = 20
-    evs = [(Event(), Event()) for _ in range(reps)]
-    for a, b in evs:
-        a.record()
-        hip.call("nc_lm_head", [None, model.best, model.normed, model.head], [1, V, H, 0, 1])
-        b.record()
-    hip.sync()
-    lm_ms = statistics.fmean(a.elapsed_ms(b) for a, b in evs)
-    lm_bytes = 4 * V * H + 4 * H + 8
-    result.update({"lm_head_us": lm_ms * 1e3, "lm_head_gbps": lm_bytes / (lm_ms * 1e-3) / 1e9, "lm_bytes": lm_bytes})
-    step_bytes = 904_503_808 + 24_576 * (PROMPT + new_tokens // 2)
-    result["step_bytes_mid"] = step_bytes
+    timed_ms = marks[replays - steps].elapsed_ms(marks[replays])
+    all_ms = marks[0].elapsed_ms(marks[replays])
+    # the timed replays run at past PROMPT + replays - steps .. PROMPT + replays - 1
+    mean_past = PROMPT + replays - (steps + 1) / 2
+    result = {"tokens": tokens, "timed_ms": timed_ms, "steps": steps, "wall_s": wall,
+              "tok_s": steps / (timed_ms * 1e-3), "all_ms": all_ms, "all_tok_s": replays / (all_ms * 1e-3),
+              "step_bytes": 904_503_808 + 24_576 * mean_past}
+    cache = model.new_cache(PROMPT + NEW_TOKENS)
+    result["kernels"] = decode_kernel_table(model, cache, PROMPT + replays - 1)
     if blocks:
         t0 = time.perf_counter()
         result["blocks"] = block_measurements(model)
         log(f"blocks: configs 2-4 measured in {time.perf_counter() - t0:.1f} s")
-
     if cpu:
-        from oracle import host
-        from oracle.host_model import HostQwen2
-        cores = os.cpu_count() or 1
-        threads = min(cores, 64)
-        host.set_threads(threads)
-        t0 = time.perf_counter()
-        ref = HostQwen2(config, weights, capacity=PROMPT + new_tokens)
-        log(f"decode: host model built in {time.perf_counter() - t0:.1f} s")
-        t0 = time.perf_counter()
-        _, first = ref.forward(prompt)
-        prefill_s = time.perf_counter() - t0
-        cpu_tokens = [first]
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            _, tok = ref.forward([cpu_tokens[-1]])
-            cpu_tokens.append(tok)
-        cpu_s = time.perf_counter() - t0
-        result["cpu"] = {"tok_s": steps / cpu_s, "prefill_s": prefill_s, "threads": threads, "cores": cores,
-                         "isa": host.isa()}
-        result["tokens_identical"] = cpu_tokens == tokens
-        if cpu_tokens != tokens:
-            first_diff = next(i for i, (a, b) in enumerate(zip(cpu_tokens, tokens)) if a != b)
-            log(f"decode: TOKENS DIFFER from the host C model at position {first_diff}")
+        result["cpu"] = cpu_decode(config, weights, prompt, tokens)
     return result
 
 
@@ -447,8 +517,14 @@ def main() -> int:
     global USE_GRAPHS
     USE_GRAPHS = not args.no_graph
     d = decode(args.steps, args.warmup, cpu=not args.no_cpu, graph=not args.no_graph, blocks=not args.no_blocks)
-    log(f"decode: {d['tok_s']:.1f} tok/s on the GPU; LM head {d['lm_head_us']:.1f} us = {d['lm_head_gbps']:.0f} GB/s")
+    kernels = d["kernels"]
+    dominant = max(kernels, key=lambda k: kernels[k]["step_us"])
+    top = kernels[dominant]
+    log(f"decode: {d['tok_s']:.1f} tok/s on the GPU (last {args.steps} replays), {d['all_tok_s']:.1f} over all "
+        f"{NEW_TOKENS - 1}; time-dominant kernel {dominant}: {top['step_us']:.1f} us a step")
     cpu = d.get("cpu")
+    cpu_g = None if args.no_cpu else cpu_gemv(seconds=8.0)
+    step_gbps = d["step_bytes"] * d["tok_s"] / 1e9
     record = {
         "metric": "decode tok/s, Qwen2-0.5B-shape int8 on 1 MI355X",
         "value": round(d["tok_s"], 2),
@@ -456,31 +532,46 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(d["decode_ms"] / args.steps, 4),
+        "ms_per_step": round(d["timed_ms"] / args.steps, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic (random-init weights N(0,0.02), uniform-random 128-token prompt)",
         "config": {"workload": "config 5: Qwen2.5-0.5B-shaped, int8 projections with per-token int8 activations, "
-                               "fp32 tied LM head; 128-token prompt then greedy decode",
-                   "prompt_tokens": PROMPT, "new_tokens": args.steps + 1, "device": info["arch"],
+                               "fp32 tied LM head; 128-token prompt then 256 greedy tokens (past to 384); the "
+                               "timed steps are the last `steps` decode replays, ending at past 383",
+                   "prompt_tokens": PROMPT, "new_tokens": NEW_TOKENS, "device": info["arch"],
                    "compute_units": info["compute_units"],
-                   "tokens_identical_to_host_c": d.get("tokens_identical"),
-                   "decode_ms_total": round(d["decode_ms"], 3), "gemv": gemv_record,
+                   "tokens_identical_to_host_c": None if cpu is None else cpu["tokens_identical"],
+                   "tokens_checked": NEW_TOKENS,
+                   "all_replays": {"replays": NEW_TOKENS - 1, "ms": round(d["all_ms"], 3),
+                                   "tok_s": round(d["all_tok_s"], 2)},
+                   "kernels_per_step": kernels,
+                   "gemv": gemv_record,
                    "blocks": d.get("blocks")},
-        "roofline": {"bound": "hbm", "achieved": round(d["lm_head_gbps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(d["lm_head_gbps"] / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(LM_HEAD_KERNEL),
+        "roofline": {"bound": "hbm", "achieved": top["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": top["frac"], "traffic": measured_traffic(KERNEL_SYMBOLS[dominant]),
                      "traffic_source": "profiles/traffic.json (rocprofv3 PMC, calibrated)",
-                     "kernel": f"{LM_HEAD_KERNEL} (fp32 tied LM head, 60% of a decode step's bytes)",
-                     "bytes_per_launch": d["lm_bytes"], "launch_us": round(d["lm_head_us"], 3),
-                     "step_bytes": d["step_bytes_mid"],
-                     "step_gbps": round(d["step_bytes_mid"] * d["tok_s"] / 1e9, 1)},
+                     "kernel": f"{KERNEL_SYMBOLS[dominant]} ({dominant}: the decode step's time-dominant kernel "
+                               f"group, {top['launches_per_step']} launches, {top['step_us']} us a step)",
+                     "bytes_per_launch": top["bytes_per_launch"], "launch_us": top["launch_us"],
+                     "step": {"bytes": int(d["step_bytes"]), "gbps": round(step_gbps, 1),
+                              "frac": round(step_gbps / HBM_PEAK_GBPS, 4)},
+                     "lm_head": kernels["lm head"]},
         "cpu_baseline": None if cpu is None else {
             "value": round(cpu["tok_s"], 2), "unit": "tok/s", "cores": cpu["threads"], "kind": "port",
-            "sample": f"the same prompt and {args.steps} greedy decode steps on the host C int8 model "
-                      f"(oracle/nc_model.c), {cpu['isa']}",
-            "host_cores": cpu["cores"], "prefill_s": round(cpu["prefill_s"], 3)},
+            "sample": f"decode steps at the config's last positions on the host C int8 model (oracle/nc_model.c, "
+                      f"the build's own C: the reference has no per-token int8 mode), {cpu['isa']}; threads swept "
+                      f"{list(cpu['by_threads'])}, best {cpu['threads']}",
+            "by_threads": cpu["by_threads"], "all_cores": cpu["all_cores"],
+            "all_cores_tok_s": round(cpu["all_cores_tok_s"], 2), "host_cores": cpu["cores"],
+            "full_run_tok_s": round(cpu["full_run_tok_s"], 2), "prefill_s": round(cpu["prefill_s"], 3),
+            "gemv": None if cpu_g is None else {
+                "value": round(cpu_g["gbps"], 2), "unit": "GB/s", "threads": cpu_g["threads"],
+                "by_threads": cpu_g["by_threads"], "isa": cpu_g["isa"],
+                "all_cores_gbps": cpu_g["by_threads"][str(max(map(int, cpu_g["by_threads"])))],
+                "sample": "config 1's GEMV over 240 rotated weight copies (1 GB, past the host's LLC)"}},
     }
     print(json.dumps(record), flush=True)
     return 0

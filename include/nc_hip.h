@@ -47,6 +47,10 @@ int32_t nc_device_info(char *arch, int64_t arch_len, int64_t *compute_units, int
  * key of the tuning cache (the reference keys on compiler, CPU and threads,
  * autotune.py:481-484). */
 int32_t nc_runtime_version(int64_t *runtime, int64_t *driver);
+/* A hash of the library's kernel sources and build flags: part of the tuning
+ * cache's key, so winners measured on one build are not reused on another
+ * (the reference keys its caches on source and flags, codegen_c.py:303-313). */
+const char *nc_library_digest(void);
 
 /* Device memory: the reference's one 64-byte-aligned arena (runtime.py:39,
  * 239-243) becomes one hipMalloc arena the Python runtime carves up. */
@@ -126,7 +130,8 @@ int32_t nc_matmul_i8_token(void **p, const int64_t *s);
 /* A schedule's launch shape, for the tuner (no device call): out[0] = 0 for
  * the GEMV, then [lanes per row, waves, bytes per load]; out[0] = 1 for the
  * MFMA GEMM, then [tile m, tile n, k stage, wave m, wave n, register stages,
- * threads, LDS bytes]. NC_BAD_ARGS for 0 or an unknown index. The
+ * threads, LDS bytes with one weight matrix, LDS bytes with the SwiGLU pair's
+ * two]. NC_BAD_ARGS for 0 or an unknown index. The
  * reference's schedule space is schedules.SPACES (schedules.py:96). */
 int32_t nc_schedule_info(int32_t schedule, int64_t *out);
 

@@ -30,7 +30,9 @@ keeps those rules for the GPU library:
   scored over a mix of workloads (the reference's DECODE/PREFILL weights,
   autotune.py:65-69, exist because its C is compiled once for all seq).
 * **The cache** is JSON keyed by machine (arch, HIP runtime and driver
-  versions, CU count) and by problem (op, M, N, K, the space).
+  versions, CU count) and by problem (op, M, N, K, the space, and the
+  library's digest of its kernel sources and flags, so a rebuilt kernel is
+  measured afresh).
 """
 
 from __future__ import annotations
@@ -281,7 +283,8 @@ class Autotuner:
 
     @staticmethod
     def problem_key(op: str, m: int, n: int, k: int, space: list[dict]) -> str:
-        material = json.dumps({"op": op, "m": m, "n": n, "k": k, "space": space}, sort_keys=True)
+        material = json.dumps({"op": op, "m": m, "n": n, "k": k, "space": space,
+                               "library": hip.library_digest()}, sort_keys=True)
         return hashlib.sha256(material.encode()).hexdigest()[:20]
 
     def schedule(self, op: str, m: int, n: int, k: int) -> int:

@@ -11,6 +11,7 @@ kernels spell out correctly rounded division and square root themselves.
 
 from __future__ import annotations
 
+import hashlib
 import os
 import shutil
 import subprocess
@@ -50,9 +51,21 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
-def _compile(src: Path) -> Path:
+def library_digest() -> str:
+    """A hash of every kernel source and header and the flags: the library's version.
+
+    Compiled into the library (``nc_library_digest``) so that what was measured
+    on one build (tuning winners) is not reused on another.
+    """
+    h = hashlib.sha256("\0".join(HIPCC_FLAGS).encode())
+    for path in sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.h")):
+        h.update(path.name.encode() + b"\0" + path.read_bytes())
+    return h.hexdigest()[:16]
+
+
+def _compile(src: Path, digest: str) -> Path:
     obj = OBJ_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{CSRC}", f'-DNC_LIBRARY_DIGEST="{digest}"', "-c", str(src), "-o", str(obj)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
         raise BuildError(f"hipcc failed on {src.name}:\n{result.stderr[-6000:]}")
@@ -64,8 +77,9 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     OBJ_DIR.mkdir(parents=True, exist_ok=True)
     srcs = sources()
     jobs = jobs or min(len(srcs), os.cpu_count() or 4, 16)
+    digest = library_digest()
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
-        objs = list(pool.map(_compile, srcs))
+        objs = list(pool.map(lambda src: _compile(src, digest), srcs))
     scratch = LIBRARY.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(scratch), *map(str, objs)]
     result = subprocess.run(cmd, capture_output=True, text=True)

@@ -33,8 +33,6 @@ namespace nc {
 
 constexpr int kChunk = 64;    // keys per chunk: one per lane of a wavefront
 
-__device__ __forceinline__ float nan_max(float a, float b) { return (a < b || b != b) ? b : a; }
-
 __device__ __forceinline__ float lane_value(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }

@@ -340,7 +340,7 @@ __global__ __launch_bounds__(1024) void attention_combine_quant(float *__restric
     if (lane == 0) maxima[h] = mag;
     __syncthreads();
     float row_max = maxima[0];
-    for (int i = 1; i < heads; ++i) row_max = fmaxf(row_max, maxima[i]);
+    for (int i = 1; i < heads; ++i) row_max = nc::nan_max(row_max, maxima[i]);
     const float scale = nc::token_scale(row_max);
     if (lane < D) xq[at] = nc::quantize_value(out, scale);
     if (threadIdx.x == 0) xs[i0 + r] = scale;

@@ -124,8 +124,14 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
     return butterfly<64>(v, [](float a, float b) { return __fadd_rn(a, b); });
 }
 
+// max that propagates NaN from either side, as the reference's reduce_max
+// does (acc < v || v != v, fusion.py:603-609) and numpy's max does; fmaxf
+// would drop a NaN and give a NaN row a finite int8 scale.
+__device__ __forceinline__ float nan_max(float a, float b) { return (a < b || b != b) ? b : a; }
+
+// Maximum over a wavefront, the same xor butterfly; NaN propagates.
 __device__ __forceinline__ float wave_max_f32(float v) {
-    return butterfly<64>(v, [](float a, float b) { return fmaxf(a, b); });
+    return butterfly<64>(v, [](float a, float b) { return nan_max(a, b); });
 }
 
 // Correctly rounded float32 square root. Not __fsqrt_rn: without

@@ -85,14 +85,14 @@ __device__ float activation_prologue(int8_t *__restrict__ sxq, const float *__re
     }
     float mag = 0.0f;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) mag = fmaxf(mag, fabsf(v[i]));
+    for (int i = 0; i < PER; ++i) mag = nc::nan_max(mag, fabsf(v[i]));
     mag = nc::wave_max_f32(mag);
     if constexpr (W > 1) {
         if (lane == 0) scratch[4 + wave] = mag;
         __syncthreads();
         mag = scratch[4];
 #pragma unroll
-        for (int w = 1; w < W; ++w) mag = fmaxf(mag, scratch[4 + w]);
+        for (int w = 1; w < W; ++w) mag = nc::nan_max(mag, scratch[4 + w]);
     }
     const float scale = nc::token_scale(mag);
 #pragma unroll

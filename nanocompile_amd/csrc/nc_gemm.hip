@@ -462,13 +462,15 @@ int32_t gemm_i8_token_rope(int tile, const GemmArgs &a) {
 #undef NC_ROPE_CASE
 }
 
-// out: [BM, BN, BK, WM, WN, NS, workgroup threads, LDS bytes (dequantize epilogue)]
+// out: [BM, BN, BK, WM, WN, NS, workgroup threads, LDS bytes with one weight matrix,
+//       LDS bytes with the SwiGLU pair's two]: the kernel's two unpadded buffers of
+//       BM activation rows and NB * BN weight rows of BK bytes.
 int32_t gemm_tile_info(int tile, int64_t *out) {
 #define NC_TILE_INFO(I, BM, BN, BK, WM, WN, NS)                                          \
     case I: {                                                                            \
-        const int64_t v[8] = {BM, BN, BK, WM, WN, NS, (BM / WM) * (BN / WN) * 64,        \
-                              2 * (BM + BN) * (BK + 16)};                                \
-        for (int i = 0; i < 8; ++i) out[i] = v[i];                                       \
+        const int64_t v[9] = {BM, BN, BK, WM, WN, NS, (BM / WM) * (BN / WN) * 64,        \
+                              2 * (BM + BN) * BK, 2 * (BM + 2 * BN) * BK};               \
+        for (int i = 0; i < 9; ++i) out[i] = v[i];                                       \
         return NC_OK;                                                                    \
     }
     switch (tile) {

@@ -330,7 +330,8 @@ int32_t run(const Args &a, int schedule) {
 // What schedule index `schedule` of the projection is, for the tuner; a
 // table lookup, no device call.
 // out[0] = 0 (GEMV): out[1..3] = [lanes per row, waves per workgroup, bytes per lane load];
-// out[0] = 1 (MFMA GEMM): out[1..8] = [BM, BN, BK, WM, WN, NS, threads, LDS bytes].
+// out[0] = 1 (MFMA GEMM): out[1..9] = [BM, BN, BK, WM, WN, NS, threads, LDS bytes with one
+// weight matrix, LDS bytes with the SwiGLU pair].
 // Schedule 0 (the default) reports NC_BAD_ARGS: it is a choice, not a schedule.
 NC_EXPORT int32_t nc_schedule_info(int32_t schedule, int64_t *out) {
     if (!out) return NC_BAD_ARGS;

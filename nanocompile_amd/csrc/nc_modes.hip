@@ -147,7 +147,7 @@ __global__ __launch_bounds__(256) void quantize_blocks(int8_t *__restrict__ xq, 
     for (int b = threadIdx.x; b < nb; b += 256) {
         const float *v = row + (size_t)b * block;
         float mag = 0.0f;
-        for (int i = 0; i < block; ++i) mag = fmaxf(mag, fabsf(v[i]));
+        for (int i = 0; i < block; ++i) mag = nc::nan_max(mag, fabsf(v[i]));
         const float scale = nc::token_scale(mag);
         int32_t sum = 0;
         for (int i = 0; i < block; ++i) {

@@ -21,7 +21,7 @@ __device__ float block_max(float v, float *scratch) {
     __syncthreads();
     if (lane == 0) scratch[wave] = v;
     __syncthreads();
-    return fmaxf(fmaxf(scratch[0], scratch[1]), fmaxf(scratch[2], scratch[3]));
+    return nc::nan_max(nc::nan_max(scratch[0], scratch[1]), nc::nan_max(scratch[2], scratch[3]));
 }
 
 __device__ float block_sum(float v, float *scratch) {
@@ -41,7 +41,7 @@ __global__ __launch_bounds__(kThreads) void quantize_rows(int8_t *__restrict__ q
     __shared__ float scratch[4];
     const float *row = w + (size_t)blockIdx.x * K;
     float mag = 0.0f;
-    for (int k = threadIdx.x; k < K; k += kThreads) mag = fmaxf(mag, fabsf(row[k]));
+    for (int k = threadIdx.x; k < K; k += kThreads) mag = nc::nan_max(mag, fabsf(row[k]));
     mag = block_max(mag, scratch);
     float scale = nc::div_rn(mag, 127.0f);
     if (scale == 0.0f) scale = 1.0f;
@@ -75,7 +75,7 @@ __global__ __launch_bounds__(kThreads) void quantize_token(int8_t *__restrict__ 
             v[i] = k < K ? row[k] : 0.0f;
         }
 #pragma unroll
-        for (int i = 0; i < PER_THREAD; ++i) mag = fmaxf(mag, fabsf(v[i]));
+        for (int i = 0; i < PER_THREAD; ++i) mag = nc::nan_max(mag, fabsf(v[i]));
         const float scale = nc::token_scale(block_max(mag, scratch));
 #pragma unroll
         for (int i = 0; i < PER_THREAD; ++i) {
@@ -84,7 +84,7 @@ __global__ __launch_bounds__(kThreads) void quantize_token(int8_t *__restrict__ 
         }
         if (threadIdx.x == 0) xs[blockIdx.x] = scale;
     } else {
-        for (int k = threadIdx.x; k < K; k += kThreads) mag = fmaxf(mag, fabsf(row[k]));
+        for (int k = threadIdx.x; k < K; k += kThreads) mag = nc::nan_max(mag, fabsf(row[k]));
         const float scale = nc::token_scale(block_max(mag, scratch));
         for (int k = threadIdx.x; k < K; k += kThreads) out[k] = nc::quantize_value(row[k], scale);
         if (threadIdx.x == 0) xs[blockIdx.x] = scale;
@@ -110,7 +110,8 @@ __global__ __launch_bounds__(kThreads) void quantize_token4(int8_t *__restrict__
     float mag = 0.0f;
 #pragma unroll
     for (int i = 0; i < V4; ++i)
-        mag = fmaxf(mag, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+        mag = nc::nan_max(mag, nc::nan_max(nc::nan_max(fabsf(v[i].x), fabsf(v[i].y)),
+                                           nc::nan_max(fabsf(v[i].z), fabsf(v[i].w))));
     const float scale = nc::token_scale(block_max(mag, scratch));
 #pragma unroll
     for (int i = 0; i < V4; ++i) {
@@ -160,7 +161,7 @@ __global__ __launch_bounds__(kThreads) void rms_norm_quant(float *__restrict__ n
     for (int i = 0; i < PER_THREAD; ++i) {
         const int k = threadIdx.x + i * kThreads;
         v[i] = k < K ? __fmul_rn(__fmul_rn(v[i], rcp), gamma[k]) : 0.0f;
-        mag = fmaxf(mag, fabsf(v[i]));
+        mag = nc::nan_max(mag, fabsf(v[i]));
     }
     const float scale = nc::token_scale(block_max(mag, scratch));
 #pragma unroll

@@ -76,6 +76,13 @@ NC_EXPORT int32_t nc_device_info(char *name, int64_t name_len, int64_t *compute_
 
 // The HIP runtime and driver versions (hipRuntimeGetVersion, hipDriverGetVersion):
 // part of the key under which tuned schedules are cached.
+#ifndef NC_LIBRARY_DIGEST
+#define NC_LIBRARY_DIGEST "unversioned"
+#endif
+
+// A hash of the library's sources and build flags (made by the build).
+NC_EXPORT const char *nc_library_digest(void) { return NC_LIBRARY_DIGEST; }
+
 NC_EXPORT int32_t nc_runtime_version(int64_t *runtime, int64_t *driver) {
     int r = 0, d = 0;
     int32_t rc = record(hipRuntimeGetVersion(&r), "hipRuntimeGetVersion");

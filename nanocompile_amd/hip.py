@@ -45,6 +45,7 @@ _RUNTIME = {
     "nc_init": (ctypes.c_int32, [ctypes.c_int32]),
     "nc_device_info": (ctypes.c_int32, [ctypes.c_char_p, ctypes.c_int64] + [ctypes.POINTER(ctypes.c_int64)] * 4),
     "nc_runtime_version": (ctypes.c_int32, [ctypes.POINTER(ctypes.c_int64)] * 2),
+    "nc_library_digest": (ctypes.c_char_p, []),
     "nc_schedule_info": (ctypes.c_int32, [ctypes.c_int32, ctypes.POINTER(ctypes.c_int64)]),
     "nc_malloc": (ctypes.c_void_p, [ctypes.c_int64]),
     "nc_free": (ctypes.c_int32, [ctypes.c_void_p]),
@@ -123,6 +124,11 @@ def runtime_version() -> tuple[int, int]:
     return runtime.value, driver.value
 
 
+def library_digest() -> str:
+    """The hash of the sources and flags the loaded library was built from (no GPU needed)."""
+    return load().nc_library_digest().decode()
+
+
 def schedule_info(schedule: int) -> dict | None:
     """The launch shape of projection schedule ``schedule`` (a table lookup; no GPU needed)."""
     out = (ctypes.c_int64 * 16)()
@@ -132,7 +138,8 @@ def schedule_info(schedule: int) -> dict | None:
         return {"schedule": int(schedule), "kernel": "gemv", "lanes_per_row": out[1], "waves": out[2],
                 "load_bytes": out[3]}
     return {"schedule": int(schedule), "kernel": "mfma", "tile_m": out[1], "tile_n": out[2], "k_stage": out[3],
-            "wave_m": out[4], "wave_n": out[5], "stages": out[6], "threads": out[7], "lds_bytes": out[8]}
+            "wave_m": out[4], "wave_n": out[5], "stages": out[6], "threads": out[7], "lds_bytes": out[8],
+            "lds_bytes_pair": out[9]}
 
 
 def kernel(name: str):

@@ -37,6 +37,11 @@ def float_bits(value: float) -> int:
     return int(np.array(value, dtype=np.float32).view(np.uint32))
 
 
+# The most keys (cached plus new) one attention launch takes: its combine step
+# keeps one float per key of a row in LDS (nc_attention.hip kMaxKeys).
+MAX_KEYS = 16384
+
+
 def attention_workspace_bytes(heads: int, head_dim: int, rows: int, keys: int) -> int:
     """Bytes of the chunk results nc_attention / nc_attention_decode keep for ``rows``
     query rows over ``keys`` keys: (m, l, o[head_dim]) per head, row and 64-key chunk."""

@@ -1,28 +1,49 @@
 """Qwen2's hyperparameters and seeded random weights in the checkpoint's names.
 
-``Qwen2Config`` carries the fields the reference's ``Qwen2Config`` has
-(models/qwen2.py:45-96), with the same validation and the same reading of a
-HuggingFace ``config.json``. Weights are named as in the checkpoint
-(``model.layers.0.self_attn.q_proj.weight``), as the reference binds them.
+A model is described by nine numbers; their names are the ones HuggingFace's
+``config.json`` uses and the reference's model driver reads
+(models/qwen2.py:45-96), so a configuration object from either side can be
+handed to this package (``Qwen2Config.coerce`` accepts any object that has
+them). What this package needs of them is checked by ``problems``: the
+kernels assume the head width splits the hidden width, the query heads split
+evenly over the KV heads, and RoPE's half-split pairing needs an even head
+width.
 
-There is no network here for real checkpoints: ``random_weights`` draws a
-model of the real shape from a seed, in one fixed name order, so every user
-(the GPU model, the host oracle, the golden-vector script that runs the
-reference) regenerates exactly the same arrays.
+Weights are named as in the checkpoint
+(``model.layers.0.self_attn.q_proj.weight``). There is no network here for
+real checkpoints: ``random_weights`` draws a model of the real shape from a
+seed, in one fixed name order, so every user (the GPU model, the host oracle,
+the golden-vector script that runs the reference) regenerates exactly the
+same arrays.
 """
 
 from __future__ import annotations
 
 import json
 from collections.abc import Iterator, Mapping
-from dataclasses import dataclass
+from dataclasses import dataclass, fields
 from pathlib import Path
 
 import numpy as np
 
+# config.json key -> (field, type, value when the key is absent; None = required)
+_JSON_KEYS = {
+    "vocab_size": ("vocab_size", int, None),
+    "hidden_size": ("hidden_size", int, None),
+    "intermediate_size": ("intermediate_size", int, None),
+    "num_hidden_layers": ("num_hidden_layers", int, None),
+    "num_attention_heads": ("num_attention_heads", int, None),
+    "num_key_value_heads": ("num_key_value_heads", int, "num_attention_heads"),
+    "rms_norm_eps": ("rms_norm_eps", float, None),
+    "rope_theta": ("rope_theta", float, 10000.0),
+    "tie_word_embeddings": ("tie_word_embeddings", bool, False),
+}
+
 
 @dataclass(frozen=True)
 class Qwen2Config:
+    """The nine hyperparameters of a Qwen2 decoder (HuggingFace's names)."""
+
     vocab_size: int
     hidden_size: int
     intermediate_size: int
@@ -34,42 +55,68 @@ class Qwen2Config:
     tie_word_embeddings: bool
 
     def __post_init__(self) -> None:
-        if self.hidden_size % self.num_attention_heads:
-            raise ValueError("hidden_size must divide evenly into attention heads")
-        if self.num_attention_heads % self.num_key_value_heads:
-            raise ValueError("attention heads must divide evenly into KV heads")
-        if self.head_dim % 2:
-            raise ValueError("RoPE needs an even head_dim")
+        found = self.problems()
+        if found:
+            raise ValueError(f"unusable Qwen2 configuration: {'; '.join(found)}")
+
+    def problems(self) -> list[str]:
+        """What in this configuration the kernels cannot run, as sentences (empty when fine)."""
+        out = []
+        sizes = {f.name: getattr(self, f.name) for f in fields(self) if f.type in ("int", int)}
+        out += [f"{name} = {value} is not positive" for name, value in sizes.items() if value <= 0]
+        if out:
+            return out
+        heads, kv = self.num_attention_heads, self.num_key_value_heads
+        if self.hidden_size % heads:
+            out.append(f"{heads} query heads do not split hidden_size {self.hidden_size}")
+        elif (self.hidden_size // heads) % 2:
+            out.append(f"head width {self.hidden_size // heads} is odd; RoPE pairs its halves")
+        if heads % kv:
+            out.append(f"{heads} query heads do not share {kv} KV heads evenly")
+        return out
 
     @property
     def head_dim(self) -> int:
         return self.hidden_size // self.num_attention_heads
 
     @property
-    def kv_group_size(self) -> int:
+    def queries_per_kv(self) -> int:
+        """Query heads reading each KV head (head h reads KV head h // this)."""
         return self.num_attention_heads // self.num_key_value_heads
 
     @classmethod
-    def from_dict(cls, data: Mapping) -> "Qwen2Config":
-        if data.get("architectures") != ["Qwen2ForCausalLM"]:
-            raise ValueError(f"not a Qwen2 config: {data.get('architectures')}")
-        if data.get("hidden_act", "silu") != "silu":
-            raise ValueError(f"hidden_act {data['hidden_act']!r} is not implemented")
-        return cls(
-            vocab_size=int(data["vocab_size"]),
-            hidden_size=int(data["hidden_size"]),
-            intermediate_size=int(data["intermediate_size"]),
-            num_hidden_layers=int(data["num_hidden_layers"]),
-            num_attention_heads=int(data["num_attention_heads"]),
-            num_key_value_heads=int(data.get("num_key_value_heads", data["num_attention_heads"])),
-            rms_norm_eps=float(data["rms_norm_eps"]),
-            rope_theta=float(data.get("rope_theta", 10000.0)),
-            tie_word_embeddings=bool(data.get("tie_word_embeddings", False)),
-        )
+    def coerce(cls, config) -> "Qwen2Config":
+        """This package's config from any object with the nine fields (the reference's included)."""
+        if isinstance(config, cls):
+            return config
+        missing = [f.name for f in fields(cls) if not hasattr(config, f.name)]
+        if missing:
+            raise TypeError(f"{type(config).__name__} lacks Qwen2 fields {missing}")
+        return cls(**{f.name: getattr(config, f.name) for f in fields(cls)})
 
     @classmethod
-    def from_model_dir(cls, model_dir: str | Path) -> "Qwen2Config":
-        return cls.from_dict(json.loads((Path(model_dir) / "config.json").read_text(encoding="utf-8")))
+    def from_json(cls, source: str | Path | Mapping) -> "Qwen2Config":
+        """From a HuggingFace ``config.json``: a mapping, the file, or the model directory holding it."""
+        if isinstance(source, Mapping):
+            data = source
+        else:
+            path = Path(source)
+            data = json.loads((path / "config.json" if path.is_dir() else path).read_text(encoding="utf-8"))
+        arch = data.get("architectures") or []
+        if "Qwen2ForCausalLM" not in arch or data.get("hidden_act", "silu") != "silu":
+            raise ValueError(f"config.json describes {arch} with activation {data.get('hidden_act')!r}; "
+                             f"this package runs Qwen2ForCausalLM with SiLU")
+        values = {}
+        for key, (name, kind, default) in _JSON_KEYS.items():
+            if key in data:
+                values[name] = kind(data[key])
+            elif default is None:
+                raise ValueError(f"config.json has no {key!r}")
+            else:
+                values[name] = kind(data[default]) if isinstance(default, str) else default
+        return cls(**values)
+
+    from_model_dir = from_json
 
 
 # Qwen2.5-0.5B's shape (BASELINE config 5), and a tiny one for tests.

@@ -42,7 +42,8 @@ import numpy as np
 
 from nanocompile_amd import hip
 from nanocompile_amd.hip import DeviceArray
-from nanocompile_amd.kernels import argmax_slots, attention_workspace_bytes, float_bits, pack_chains, pack_chains_vnni
+from nanocompile_amd.kernels import (MAX_KEYS, argmax_slots, attention_workspace_bytes, float_bits, pack_chains,
+                                     pack_chains_vnni)
 from nanocompile_amd.models.config import Qwen2Config
 
 QUANTIZATIONS = ("int8-token", "int8", "int8-vnni", "f32")
@@ -96,8 +97,9 @@ class KVCache:
     """
 
     def __init__(self, config: Qwen2Config, capacity: int = 256) -> None:
-        if capacity <= 0:
-            raise ValueError(f"capacity must be positive, got {capacity}")
+        if not 0 < capacity <= MAX_KEYS:
+            raise ValueError(f"capacity {capacity}: a cache holds 1 to {MAX_KEYS} tokens (the attention "
+                             f"kernels' limit on keys)")
         self.config, self.capacity, self.length = config, capacity, 0
         shape = (config.num_hidden_layers, config.num_key_value_heads, capacity, config.head_dim)
         self.keys, self.values = DeviceArray(shape, np.float32), DeviceArray(shape, np.float32)
@@ -292,20 +294,8 @@ class Qwen2:
         Q = heads * D
         eps = float_bits(c.rms_norm_eps)
         if m == 1 and self.fused_decode:
-            # five kernels a layer: each projection computes its own activation
-            # prologue (nc_decode.hip), attention does RoPE and the cache append
-            for i, w in enumerate(self.layers):
-                kc, vc = cache.layer(i)
-                q, s = w["qkv"]
-                hip.call("nc_decode_projection", [self.qkv, self.x, w["g1"], q, s, w["qkv_b"]], [W, H, 0, eps])
-                hip.call("nc_attention_decode", [self.ctx, self.qkv, kc, vc, self.inv_freq, pos, cache.rope, cache.work],
-                         [heads, kv, D, past, cache.capacity, float_bits(self.scale), cache.work_bytes])
-                q, s = w["o"]
-                hip.call("nc_decode_projection", [self.x, self.ctx, None, q, s], [H, Q, 1, eps])
-                (qg, sg), (qu, su) = w["gate"], w["up"]
-                hip.call("nc_decode_projection", [self.h, self.x, w["g2"], qg, sg, None, qu, su], [I, H, 2, eps])
-                q, s = w["down"]
-                hip.call("nc_decode_projection", [self.x, self.h, None, q, s], [H, I, 1, eps])
+            for _, name, pointers, sizes in self.decode_layer_calls(cache, past, pos):
+                hip.call(name, pointers, sizes)
             return
         if self.quantization != "int8-token":
             self._layers_reference_modes(m, past, cache, pos)
@@ -336,6 +326,33 @@ class Qwen2:
             hip.call("nc_quantize_token_i8", [self.xq, self.xs, self.h], [m, I])
             q, s = w["down"]
             hip.call("nc_matmul_i8_token", [self.x, self.xq, self.xs, q, s, None, self.x], [m, H, I, s_down])
+
+    def decode_layer_calls(self, cache: KVCache, past: int = 0, pos: DeviceArray | None = None) -> list[tuple]:
+        """One token's pass through every layer as launches ``(label, entry point, pointers, sizes)``:
+        five a layer, each projection computing its own activation prologue (nc_decode.hip) and
+        attention doing RoPE and the cache append. The labels name the kernel groups a profile
+        of the decode step reports: "qkv", "attention", "o", "gate/up", "down"."""
+        c = self.config
+        H, I, D = c.hidden_size, c.intermediate_size, c.head_dim
+        heads, kv, W = c.num_attention_heads, c.num_key_value_heads, self.width
+        Q = heads * D
+        eps = float_bits(c.rms_norm_eps)
+        calls = []
+        for i, w in enumerate(self.layers):
+            kc, vc = cache.layer(i)
+            q, s = w["qkv"]
+            calls.append(("qkv", "nc_decode_projection", [self.qkv, self.x, w["g1"], q, s, w["qkv_b"]], [W, H, 0, eps]))
+            calls.append(("attention", "nc_attention_decode",
+                          [self.ctx, self.qkv, kc, vc, self.inv_freq, pos, cache.rope, cache.work],
+                          [heads, kv, D, past, cache.capacity, float_bits(self.scale), cache.work_bytes]))
+            q, s = w["o"]
+            calls.append(("o", "nc_decode_projection", [self.x, self.ctx, None, q, s], [H, Q, 1, eps]))
+            (qg, sg), (qu, su) = w["gate"], w["up"]
+            calls.append(("gate/up", "nc_decode_projection", [self.h, self.x, w["g2"], qg, sg, None, qu, su],
+                          [I, H, 2, eps]))
+            q, s = w["down"]
+            calls.append(("down", "nc_decode_projection", [self.x, self.h, None, q, s], [H, I, 1, eps]))
+        return calls
 
     def _layers_reference_modes(self, m: int, past: int, cache: KVCache, pos: DeviceArray | None) -> None:
         """The layers with the reference's own modes (quantize.py:127-164): float32 activations
@@ -431,11 +448,10 @@ class Qwen2:
                  [1, H, float_bits(c.rms_norm_eps)])
         hip.call("nc_lm_head", [None, self.best, self.normed, self.head], [1, V, H, 0, 1])
         hip.call("nc_argmax_index", [self.argmax, self.best], [1, self.slots])
-        out = np.empty(1, np.int64)
-        hip.load().nc_memcpy_d2h(out.ctypes.data, self.argmax.ptr, 8)
-        hip.sync()
+        token = int(self.argmax.view((1,)).numpy()[0])      # waits for the stream; a failed copy raises
+        hip.sync()                                             # a kernel's failure code raises KernelError
         cache.length = past + m
-        return int(out[0])
+        return token
 
 
     # -- greedy decoding on the device -------------------------------------------------
@@ -455,7 +471,10 @@ class Qwen2:
         a HIP graph holding a whole decode step (embedding, every layer, the
         LM head, the argmax and the bookkeeping that feeds the token back),
         with the position read on the device. ``timer``, if given, is called
-        as ``timer("start")`` and ``timer("stop")`` around the replays.
+        as ``timer(i)`` before replay ``i`` (0 .. max_new_tokens - 2) and as
+        ``timer(max_new_tokens - 1)`` after the last, from the host as the
+        replays are enqueued (a caller records events on the library stream
+        at the indices it wants).
         """
         prompt = np.asarray(prompt_ids, dtype=np.int64)
         m = int(prompt.size)
@@ -490,12 +509,12 @@ class Qwen2:
             self._projection_schedules(1)          # any tuning happens now, not under capture
         hip.sync()
         replay = hip.Graph.capture(step).launch if graph else step
-        if timer:
-            timer("start")
-        for _ in range(max_new_tokens - 1):
+        for i in range(max_new_tokens - 1):
+            if timer:
+                timer(i)
             replay()
         if timer:
-            timer("stop")
+            timer(max_new_tokens - 1)
         hip.sync()
         cache.length = capacity - 1
         return [int(t) for t in tokens.numpy()[m:capacity]]

@@ -34,7 +34,6 @@ the reference's ``CBackend.compiled`` does (runtime.py:321-333).
 
 from __future__ import annotations
 
-import dataclasses
 import time
 from collections.abc import Mapping
 
@@ -60,10 +59,11 @@ class HIPBackend:
     """
 
     def __init__(self, config, max_tokens: int = 512, device: int = 0, schedule="default") -> None:
-        fields = [f.name for f in dataclasses.fields(Qwen2Config)]
-        self.config = Qwen2Config(**{name: getattr(config, name) for name in fields})
+        self.config = Qwen2Config.coerce(config)
         self.max_tokens, self.device, self.schedule = max_tokens, device, schedule
-        self._models: list[tuple[Mapping, str, object]] = []
+        # one model per mode, for the weights mapping it was last called with: a new
+        # mapping replaces (and frees) the model made for the old one
+        self._models: dict[str, tuple[Mapping, object]] = {}
         self._compiled: list[tuple[object, "HIPCompiledGraph"]] = []
 
     # -- recognising a graph ----------------------------------------------------------------
@@ -131,13 +131,14 @@ class HIPBackend:
     # -- running it -----------------------------------------------------------------------------
 
     def _model(self, mode: str, weights: Mapping):
-        for held, held_mode, model in self._models:
-            if held is weights and held_mode == mode:
-                return model
+        held = self._models.get(mode)
+        if held is not None and held[0] is weights:
+            return held[1]
+        self._models.pop(mode, None)          # drop the old weights' device arena before uploading new ones
         from nanocompile_amd.models.qwen2 import Qwen2
         model = Qwen2(self.config, weights, quantization=mode, max_tokens=self.max_tokens, device=self.device,
                       schedule=self.schedule)
-        self._models.append((weights, mode, model))
+        self._models[mode] = (weights, model)
         return model
 
     def compiled(self, graph) -> "HIPCompiledGraph":

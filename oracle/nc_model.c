@@ -62,9 +62,10 @@ static float row_sum_values(const float *row, int64_t n) {
     return row_sum_virtual(partial);
 }
 
-static float nan_max(float a, float b) { return (a < b || b != b) ? b : a; }
-
 /* -- rms_norm + per-token quantization ----------------------------------- */
+
+/* max propagating NaN from either side (the reference's reduce_max, fusion.py:603-609) */
+static float nan_max(float a, float b) { return (a < b || b != b) ? b : a; }
 
 static void rms_row(float *normed, const float *x, const float *gamma, int64_t k, float eps) {
     const float ss = row_sum_squares(x, k);
@@ -74,7 +75,7 @@ static void rms_row(float *normed, const float *x, const float *gamma, int64_t k
 
 static float quantize_row(int8_t *xq, const float *x, int64_t k) {
     float mag = 0.0f;
-    for (int64_t i = 0; i < k; ++i) mag = fmaxf(mag, fabsf(x[i]));
+    for (int64_t i = 0; i < k; ++i) mag = nan_max(mag, fabsf(x[i]));
     const float scale = mag <= 0.0f ? 1.0f : mag / 127.0f;
     for (int64_t i = 0; i < k; ++i) {
         float r = roundf(x[i] / scale);

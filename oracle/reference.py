@@ -63,6 +63,15 @@ def quantize_int8(weights: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     return values, scales.astype(F32)
 
 
+def clamp_int8(rounded: np.ndarray) -> np.ndarray:
+    """The activation quantizer's clamp as two selects (quantize.py:116-118):
+    ``where(r <= 127, r, 127)`` then ``where(-127 <= c, c, -127)``, so a NaN
+    (a row whose scale is NaN or infinite) becomes 127, not numpy's cast of NaN."""
+    clamped = np.where(rounded <= F32(INT8_MAX), rounded, F32(INT8_MAX))
+    clamped = np.where(F32(-INT8_MAX) <= clamped, clamped, F32(-INT8_MAX))
+    return clamped.astype(np.int8)
+
+
 def quantize_token(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     """Per-token int8 activations: quantize.py:102-124 with one block spanning the row.
 
@@ -73,8 +82,7 @@ def quantize_token(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     magnitude = np.max(np.where(F32(0) <= x, x, -x), axis=-1) if x.shape[-1] else np.zeros(x.shape[:-1], F32)
     scale = np.where(magnitude <= 0, F32(1.0), (magnitude / F32(INT8_MAX)).astype(F32)).astype(F32)
     rounded = round_half_away((x / scale[..., None]).astype(F32))
-    clamped = np.clip(rounded, -INT8_MAX, INT8_MAX)
-    return clamped.astype(np.int8), scale
+    return clamp_int8(rounded), scale
 
 
 def quantize_blocks(x: np.ndarray, block: int = 32) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
@@ -92,7 +100,7 @@ def quantize_blocks(x: np.ndarray, block: int = 32) -> tuple[np.ndarray, np.ndar
     magnitude = np.max(np.where(F32(0) <= groups, groups, -groups), axis=-1)
     scale = np.where(magnitude <= 0, F32(1.0), (magnitude / F32(INT8_MAX)).astype(F32)).astype(F32)
     rounded = round_half_away((groups / scale[..., None]).astype(F32))
-    values = np.clip(rounded, -INT8_MAX, INT8_MAX).astype(np.int8)
+    values = clamp_int8(rounded)
     block_sums = values.astype(np.int32).sum(-1).astype(F32)
     terms = (block_sums * scale).astype(F32)
     total = np.zeros(lead, F32)

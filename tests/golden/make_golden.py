@@ -32,6 +32,7 @@ import hashlib
 import json
 import os
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -42,7 +43,8 @@ ROOT = HERE.parent.parent
 REFERENCE = Path(os.environ.get("NANOCOMPILE_REFERENCE", "/root/reference"))
 sys.path.insert(0, str(ROOT))
 sys.path.insert(0, str(REFERENCE))
-os.environ.setdefault("NANOCOMPILE_CACHE", str(ROOT / "_work" / "ncache"))
+# The reference compiles its generated C into a cache directory; keep it out of the repository.
+os.environ.setdefault("NANOCOMPILE_CACHE", tempfile.mkdtemp(prefix="nanocompile-cache-"))
 
 from nanocompile import dtypes, interpreter, nn, quantize  # noqa: E402  (the reference)
 from nanocompile.frontend import GraphBuilder  # noqa: E402

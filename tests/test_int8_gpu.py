@@ -132,6 +132,44 @@ def test_token_quantizer_edges(gpu):
     assert xs.numpy()[0] == 1.0 and list(xq.numpy()[1, :3]) == [64, -127, 1]
 
 
+def same_floats(a, b) -> bool:
+    """Bitwise equal, except that any NaN matches any NaN (payloads are not specified)."""
+    a, b = np.asarray(a), np.asarray(b)
+    nan = np.isnan(a)
+    return bool(np.array_equal(nan, np.isnan(b)) and np.array_equal(bits(a[~nan]), bits(b[~nan])))
+
+
+@pytest.mark.filterwarnings("ignore::RuntimeWarning")
+@pytest.mark.parametrize("k", [67, 896, 4864])
+def test_quantizers_propagate_nan(gpu, k):
+    """A NaN or infinity in a row: the scale is NaN (or inf) as the reference's max gives it,
+    and the int8 values are the reference's selects' (127 for NaN), in every quantizer."""
+    from nanocompile_amd import kernels
+    print(f"nan rows k={k}", flush=True)
+    rng = np.random.default_rng(k + 11)
+    x = rng.standard_normal((4, k)).astype(np.float32)
+    x[0, k // 3] = np.nan
+    x[1, k - 1] = np.inf
+    x[2, 0] = -np.inf
+    xq, xs = kernels.quantize_token(x)
+    exq, exs = R.quantize_token(x)
+    assert np.isnan(xs.numpy()[0]) and same_floats(xs.numpy(), exs)
+    assert np.array_equal(xq.numpy(), exq)
+    g = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    normed, nq, ns = kernels.rms_norm_quant(x, g, 1e-6)
+    en, enq, ens = R.rms_norm_quant_gpu_order(x, g, 1e-6)
+    assert same_floats(normed.numpy(), en) and same_floats(ns.numpy(), ens)
+    assert np.isnan(ns.numpy()[:3]).all() and np.array_equal(nq.numpy(), enq)
+    q, s = kernels.quantize_int8(x)
+    eq, es = R.quantize_int8(x)
+    assert np.isnan(s.numpy()[0]) and same_floats(s.numpy(), es) and np.array_equal(q.numpy(), eq)
+    if k % 32 == 0:
+        bq, bs, off = kernels.quantize_blocks(x, 32)
+        ebq, ebs, eoff = R.quantize_blocks(x, 32)
+        assert np.array_equal(bq.numpy(), ebq) and same_floats(bs.numpy(), ebs)
+        assert same_floats(off.numpy(), eoff[:, 0])
+
+
 @pytest.mark.parametrize("m", [1, 64, 512])
 @pytest.mark.parametrize("k", [896, 4864, 64, 100])
 def test_rms_norm_quant(gpu, m, k):

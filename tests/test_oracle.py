@@ -107,6 +107,30 @@ def test_quantize_token_invariants():
     assert np.all(np.abs(xq - s) <= 0.5)
 
 
+@pytest.mark.filterwarnings("ignore::RuntimeWarning")
+def test_quantizers_propagate_nan_as_the_reference_does():
+    """A NaN in a row (or block) makes its scale NaN: the reference takes maxima with
+    ``acc < v || v != v`` (fusion.py:603-609) and numpy's max. Its clamp is two selects
+    (quantize.py:116-118), so every x / NaN becomes 127; an infinite maximum makes the
+    finite values 0 and the infinite ones inf / inf = NaN -> 127. A max that skips NaN
+    (fmaxf) gives a finite scale instead and fails here. The weight quantizer clips with
+    numpy, whose cast of NaN to int8 is 0 on this platform."""
+    x = np.ones((3, 64), np.float32)
+    x[0, 5] = np.nan
+    x[1, 7] = np.inf
+    xq, xs = R.quantize_token(x)
+    assert np.isnan(xs[0]) and np.all(xq[0] == 127)
+    assert xs[1] == np.inf and xq[1, 7] == 127 and not np.delete(xq[1], 7).any()
+    assert xs[2] == np.float32(1 / 127) and np.all(xq[2] == 127)
+    bq, bs, off = R.quantize_blocks(x, 32)
+    assert np.isnan(bs[0, 0]) and bs[0, 1] == np.float32(1 / 127) and np.isnan(off[0, 0])
+    assert np.all(bq[0, :32] == 127)
+    w = np.ones((2, 8), np.float32)
+    w[0, 3] = np.nan
+    q, s = R.quantize_int8(w)
+    assert np.isnan(s[0]) and not q[0].any() and s[1] == np.float32(1 / 127)
+
+
 def test_quantize_blocks_offset_is_128_times_the_scaled_block_sums():
     rng = np.random.default_rng(4)
     x = (rng.standard_normal((3, 96)) * 2).astype(np.float32)
