@@ -208,6 +208,20 @@ int32_t nc_decode_projection(void **p, const int64_t *s);
  * s: [heads, kv, D, past, C, scale as float32 bits, work bytes] (D 16, 32 or 64, C <= 16384) */
 int32_t nc_attention_decode(void **p, const int64_t *s);
 
+/* nc_attention_decode without an allocation or a workspace argument: the same
+ * kernels and the same bits, the chunk results kept in a 1 MiB device array
+ * the library holds on each GPU until the process ends (its address looked up
+ * by nc_init). No counterpart in the reference: it is for callers that cannot
+ * call hipMalloc or pass a workspace (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation). Calls that overlap on one
+ * GPU share that array and race; consecutive calls need no clearing.
+ * p: [ctx f32[heads*D], qkv f32[(heads+2*kv)*D] (unrotated), kcache f32[kv,C,D],
+ *     vcache f32[kv,C,D], inv_freq f32[D/2], pos i64[1] or NULL, rope table f32[2,C,D/2] or NULL];
+ * s: [heads, kv, D, past, C, scale as float32 bits]; NC_BAD_ARGS when
+ * heads * ceil(keys / 64) * (D + 2) floats (keys = C with pos, else past + 1)
+ * exceed 1 MiB (the model's 14 heads of 64 fit every capacity up to 16384). */
+int32_t nc_attention_decode_static(void **p, const int64_t *s);
+
 /* RoPE's cos and sin for every position of a cache, computed once with the
  * kernels' own nc_cosf / nc_sinf of f32(position) * inv_freq[i] (the reference
  * builds the same angles as rope_tables, nn.py:78-94).

@@ -635,6 +635,67 @@ NC_EXPORT int32_t nc_attention_decode(void **p, const int64_t *s) {
 }
 
 
+// -- decode attention with no allocation ---------------------------------------
+//
+// nc_attention_decode_static is nc_attention_decode (the same kernels, the same
+// bits) with its chunk-result workspace in a device array the library holds
+// for the life of the process, for callers that cannot allocate (code under
+// graph capture, serving loops, harnesses that forbid hipMalloc). Each GPU has
+// its own copy, at its own address, looked up once per device by nc_init (the
+// array's name in host code is a host-side stand-in, not a device address).
+// Every call on a GPU shares that GPU's copy, so calls that overlap on one GPU
+// (two streams, two threads) race. Nothing in it needs clearing between calls:
+// a call's chunk kernel writes every chunk result its combine then reads.
+namespace {
+constexpr int64_t kScratchBytes = 1 << 20;     // 14 heads x 256 chunks (16384 keys) x 66 floats fit
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+float *g_scratch[kMaxDevices] = {};            // each device's address of `scratch`
+}  // namespace
+
+int32_t nc::attention_scratch_init(int device) {
+    if (device < 0 || device >= kMaxDevices) {
+        set_message("nc_init: device index beyond the library's table of workspace addresses");
+        return NC_BAD_ARGS;
+    }
+    if (g_scratch[device]) return NC_OK;
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+        set_message("nc_init: hipGetSymbolAddress of the attention workspace failed");
+        return NC_LAUNCH_FAILED;
+    }
+    g_scratch[device] = static_cast<float *>(ptr);
+    return NC_OK;
+}
+
+// p: [ctx f32[heads*D], qkv f32[(heads+2*kv)*D] (unrotated, with bias), kcache f32[kv,C,D],
+//     vcache f32[kv,C,D], inv_freq f32[D/2], pos i64[1] | NULL, rope table f32[2,C,D/2] | NULL];
+// s: [heads, kv, D, past, C, scale as float32 bits]; heads * ceil(keys / 64) * (D + 2) floats
+//    (keys = C with pos, else past + 1) must fit the 1 MiB workspace.
+NC_EXPORT int32_t nc_attention_decode_static(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3] && p[4], "nc_attention_decode_static: null operand");
+    const int64_t heads = s[0], kv = s[1], D = s[2], past = s[3], cap = s[4];
+    const int64_t *pos = (const int64_t *)p[5];
+    NC_REQUIRE(heads > 0 && kv > 0 && heads % kv == 0 && heads < 65536 && (D == 64 || D == 32 || D == 16) &&
+                   cap > 0 && cap <= kMaxKeys && (pos || (past >= 0 && past + 1 <= cap)),
+               "nc_attention_decode_static: bad shape (head_dim 16, 32 or 64, capacity at most 16384)");
+    const int dev = nc::device();
+    NC_REQUIRE(dev >= 0 && dev < kMaxDevices && g_scratch[dev], "nc_attention_decode_static: call nc_init first");
+    const int64_t keys = pos ? cap : past + 1;
+    NC_REQUIRE(heads * ((keys + nc::kChunk - 1) / nc::kChunk) * (D + 2) * (int64_t)sizeof(float) <= kScratchBytes,
+               "nc_attention_decode_static: heads * ceil(keys / 64) * (head_dim + 2) floats exceed the "
+               "library's 1 MiB workspace; use nc_attention_decode with a workspace of that size");
+    float *work = g_scratch[dev];
+    const bool table = p[6] != nullptr;
+    if (D == 64) return table ? launch_decode<64, true>(p, s, pos, work, kScratchBytes)
+                              : launch_decode<64, false>(p, s, pos, work, kScratchBytes);
+    if (D == 32) return table ? launch_decode<32, true>(p, s, pos, work, kScratchBytes)
+                              : launch_decode<32, false>(p, s, pos, work, kScratchBytes);
+    return table ? launch_decode<16, true>(p, s, pos, work, kScratchBytes)
+                 : launch_decode<16, false>(p, s, pos, work, kScratchBytes);
+}
+
 // p: [y f32[heads, seq, past+seq], s f32[heads, seq, past+seq]];  s: [heads, seq, past]
 NC_EXPORT int32_t nc_softmax_causal(void **p, const int64_t *s) {
     NC_REQUIRE(p && s && p[0] && p[1], "nc_softmax_causal: null operand");

@@ -166,6 +166,7 @@ __device__ __forceinline__ float token_scale(float magnitude) {
 // every launcher.
 namespace nc {
 hipStream_t stream();
+int device();              // the device nc_init bound the library to, or -1
 int32_t *error_word();
 // NC_OK, or NC_LAUNCH_FAILED with the message recorded for nc_last_error().
 int32_t launched(const char *what);
@@ -179,6 +180,10 @@ int32_t gemm_i8_token(int tile, int epi, void *out, const int8_t *xq, const floa
                       const float *ws2, int M, int N, int K);
 // A tile's primitives: [BM, BN, BK, WM, WN, NS, threads, LDS bytes]; NC_BAD_ARGS past the table.
 int32_t gemm_tile_info(int tile, int64_t *out);
+// Looks up, with `device` current, the address of that device's copy of the
+// attention workspace the library holds for nc_attention_decode_static
+// (nc_attention.hip); called once per device by nc_init.
+int32_t attention_scratch_init(int device);
 // The per-token quantizer (nc_quant.hip) on M rows of K: xq, xs from x.
 int32_t quantize_token_rows(int8_t *xq, float *xs, const float *x, int M, int K);
 }  // namespace nc

@@ -30,6 +30,7 @@ int32_t record(hipError_t e, const char *what) {
 
 namespace nc {
 hipStream_t stream() { return g_stream; }
+int device() { return g_device; }
 int32_t *error_word() { return g_error; }
 int32_t launched(const char *what) { return record(hipGetLastError(), what); }
 void set_message(const char *text) { snprintf(g_message, sizeof g_message, "%s", text); }
@@ -57,6 +58,8 @@ NC_EXPORT int32_t nc_init(int32_t device) {
     if (rc) return rc;
     rc = record(hipMemset(g_error, 0, 256), "hipMemset(error word)");
     if (rc) return rc;
+    rc = nc::attention_scratch_init(device);      // the no-allocation entry point's workspace address
+    if (rc) return rc;
     g_device = device;
     return record(hipDeviceSynchronize(), "hipDeviceSynchronize");
 }
@@ -74,8 +77,6 @@ NC_EXPORT int32_t nc_device_info(char *name, int64_t name_len, int64_t *compute_
     return NC_OK;
 }
 
-// The HIP runtime and driver versions (hipRuntimeGetVersion, hipDriverGetVersion):
-// part of the key under which tuned schedules are cached.
 #ifndef NC_LIBRARY_DIGEST
 #define NC_LIBRARY_DIGEST "unversioned"
 #endif
@@ -83,6 +84,8 @@ NC_EXPORT int32_t nc_device_info(char *name, int64_t name_len, int64_t *compute_
 // A hash of the library's sources and build flags (made by the build).
 NC_EXPORT const char *nc_library_digest(void) { return NC_LIBRARY_DIGEST; }
 
+// The HIP runtime and driver versions (hipRuntimeGetVersion, hipDriverGetVersion):
+// part of the key under which tuned schedules are cached.
 NC_EXPORT int32_t nc_runtime_version(int64_t *runtime, int64_t *driver) {
     int r = 0, d = 0;
     int32_t rc = record(hipRuntimeGetVersion(&r), "hipRuntimeGetVersion");
