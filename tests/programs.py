@@ -1,0 +1,135 @@
+"""The reference's recorded programs (tests/golden/programs.json.gz) and a restatement of its model driver.
+
+TEST INFRASTRUCTURE. ``make_programs.py`` recorded, in the build container,
+what the reference's compiler makes of a zoo of small graphs and of the
+tiny golden Qwen2 (G5) in its three modes, with the reference's C outputs on
+seeded inputs. The driver below restates the reference's ``Qwen2.forward``,
+``KVCache`` and ``greedy`` (models/qwen2.py:232-368): the host cache handed
+to each call as ``past_keys``/``past_values``, the new keys and values
+appended after it, argmax decoding, so the recorded graphs can be driven
+through any ``run(graph_name, inputs, weights)``.
+"""
+
+from __future__ import annotations
+
+from functools import lru_cache
+from pathlib import Path
+
+import numpy as np
+
+from nanocompile_amd import lir
+from nanocompile_amd.models.config import TINY, TINY_STD, random_weights
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+TAGS = {"f32": None, "int8": "int8", "vnni": "int8-vnni"}
+PROMPTS = ([4, 5, 6], [7, 8], [1], [3, 1, 4, 1, 5, 9, 2, 6, 5, 3, 5])     # golden G5's
+
+# Outputs computed through exp, sin or cos: the C library's and this package's
+# differ by an ulp on rare inputs, so these are held to the reference's own
+# tolerance for those functions (test_codegen.py:28-29); everything else is bitwise.
+APPROX = {"unary": {"exp", "sin", "cos"}, "softmax_mask": {"p"}, "rope": {"y"}}
+APPROX_PREFIX = ("mlp_",)
+RTOL, ATOL = 2e-6, 1e-6
+
+
+@lru_cache(maxsize=None)
+def fixture():
+    return lir.load_programs(GOLDEN / "programs.json.gz"), np.load(GOLDEN / "programs.npz", allow_pickle=False)
+
+
+def zoo_names() -> list[str]:
+    return sorted(fixture()[0]["zoo"])
+
+
+def zoo(name: str, variant: str = "program") -> lir.Program:
+    doc, arrays = fixture()
+    return lir.program_from_json(doc["zoo"][name][variant], arrays)
+
+
+def zoo_cases(name: str):
+    """[(inputs, expected outputs or None, error text or None)] and the weights."""
+    doc, arrays = fixture()
+    entry = doc["zoo"][name]
+    weights = {w: arrays[key] for w, key in entry["weights"].items()}
+    cases = []
+    for case in entry["cases"]:
+        inputs = {k: arrays[v] for k, v in case["inputs"].items()}
+        outputs = {k: arrays[v] for k, v in case["outputs"].items()} if "error" not in case else None
+        cases.append((inputs, outputs, case.get("error")))
+    return cases, weights
+
+
+def approx(name: str) -> set[str]:
+    if name.startswith(APPROX_PREFIX):
+        return {"y"}
+    return APPROX.get(name, set())
+
+
+def qwen2(tag: str, which: str) -> lir.Program:
+    doc, arrays = fixture()
+    return lir.program_from_json(doc["qwen2"][tag][which], arrays)
+
+
+def qwen2_weights(tag: str) -> dict[str, np.ndarray]:
+    """The tiny model's weights as the reference hands them to its runner (quantize.py:167-180):
+    float32 by name, and for each int8 projection ``W@int8`` / ``W@scales`` from the reference's
+    per-row quantizer (restated in oracle/reference.py, pinned by golden G1)."""
+    from oracle import reference as R
+    doc, _ = fixture()
+    names = doc["qwen2"][tag]["weight_names"]
+    base = random_weights(TINY, seed=5, std=TINY_STD)
+    out = {}
+    for name in names:
+        if name.endswith("@int8") or name.endswith("@scales"):
+            w = name.rsplit("@", 1)[0]
+            q, s = R.quantize_int8(base[w])
+            out[name] = q if name.endswith("@int8") else s
+        else:
+            out[name] = base[name]
+    return out
+
+
+class Driver:
+    """The reference's Qwen2 forward and greedy loop over a runner ``run(which, inputs) -> outputs``,
+    ``which`` being "full" or "last" (models/qwen2.py:316-368)."""
+
+    def __init__(self, run, config=TINY) -> None:
+        self.run, self.config = run, config
+
+    def empty(self) -> tuple[np.ndarray, np.ndarray]:
+        c = self.config
+        z = np.zeros((c.num_hidden_layers, c.num_key_value_heads, 0, c.head_dim), np.float32)
+        return z, z
+
+    def forward(self, ids, cache=None, last_only=False) -> np.ndarray:
+        ids = np.asarray(ids, np.int64)
+        past_keys, past_values = cache if cache is not None else self.empty()
+        out = self.run("last" if last_only else "full",
+                       {"token_ids": ids, "past_keys": past_keys, "past_values": past_values})
+        if cache is not None:
+            cache[0] = np.concatenate([cache[0], out["keys"]], axis=2)
+            cache[1] = np.concatenate([cache[1], out["values"]], axis=2)
+        return out["logits"]
+
+    def greedy(self, prompt, n: int) -> list[int]:
+        cache = list(self.empty())
+        pending, out = list(prompt), []
+        for _ in range(n):
+            token = int(np.argmax(self.forward(pending, cache, last_only=True)[0]))
+            out.append(token)
+            pending = [token]
+        return out
+
+
+def prebuild(jobs: int = 8) -> int:
+    """Build every recorded program's library (default GPU schedules) into the codegen cache,
+    in parallel, so that GPU runs find them built; returns how many were compiled afresh."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    from nanocompile_amd import compiled
+    doc, _ = fixture()
+    progs = [zoo(n, v) for n in zoo_names() for v in ("program", "unfused", "scheduled")]
+    progs += [qwen2(tag, which) for tag, entry in doc["qwen2"].items() for which in entry if which != "weight_names"]
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        results = list(pool.map(compiled.prebuild, progs))
+    return sum(1 for _, cached in results if not cached)
