@@ -20,12 +20,15 @@ shapes) and by its int8 primitive (``matmul_i8``: the reference's "int8" mode,
 ``matmul_i8_vnni`` with block 32: "int8-vnni", neither: float32), and runs the
 GPU model in the same mode, whose kernels compute the reference's kernels'
 bits (the int8 and float32 projections) or its operations in a stated order
-(rms_norm, softmax, attention). Any other graph raises NotImplementedError:
-this backend accelerates the Qwen2 path, not arbitrary graphs.
+(rms_norm, softmax, attention). Any other graph runs as generated HIP: the
+reference's compiled program for it, lowered by codegen_hip with GPU
+schedules and run from one device arena (compiled.py), the reference's own
+kernels' arithmetic in the reference's order.
 
-Each call uploads the past keys and values it is given (the reference keeps
-its cache on the host and hands it over every step); the model, with its
-weights uploaded and packed, is made once per weights mapping and mode.
+On the model path each call uploads the past keys and values it is given
+(the reference keeps its cache on the host and hands it over every step);
+the model, with its weights uploaded and packed, is made once per mode and
+kept for the weights mapping it was last called with.
 ``HIPCompiledGraph`` is the per-graph form, the reference's
 ``CompiledGraph(graph, ...)(inputs, weights, bindings, profile)``
 (runtime.py:167-301), which ``HIPBackend.compiled`` makes once per graph as
@@ -50,17 +53,20 @@ PROJECTIONS = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self
 
 
 class HIPBackend:
-    """A ``Runner`` (models/qwen2.py:229) for the Qwen2 forward graphs, on the GPU.
+    """A ``Runner`` (models/qwen2.py:229) on the GPU: ``run(graph, inputs, weights) -> dict``.
 
-    ``config`` is the model's configuration (the reference's ``Qwen2Config``
-    or this package's: the same fields). ``max_tokens`` bounds the tokens of
-    one call (a prompt); ``schedule`` is passed to the model
-    (``"default"`` or an ``autotune.Autotuner``).
+    Each graph is compiled once, on first use (the reference's CBackend, runtime.py:321-337), by
+    :class:`HIPCompiledGraph`: Qwen2 forward graphs of ``config`` (the reference's ``Qwen2Config``
+    or this package's: the same fields) on the model library, every other graph as generated HIP.
+    ``max_tokens`` bounds one call's tokens on the model path; ``schedule``, ``fuse`` and ``lower``
+    are passed to each HIPCompiledGraph.
     """
 
-    def __init__(self, config, max_tokens: int = 512, device: int = 0, schedule="default") -> None:
-        self.config = Qwen2Config.coerce(config)
+    def __init__(self, config=None, max_tokens: int = 512, device: int = 0, schedule="default",
+                 fuse: bool = True, lower=None) -> None:
+        self.config = None if config is None else Qwen2Config.coerce(config)
         self.max_tokens, self.device, self.schedule = max_tokens, device, schedule
+        self.fuse, self.lower = fuse, lower
         # one model per mode, for the weights mapping it was last called with: a new
         # mapping replaces (and frees) the model made for the old one
         self._models: dict[str, tuple[Mapping, object]] = {}
@@ -110,6 +116,8 @@ class HIPBackend:
 
     def last_only(self, graph, mode: str) -> bool:
         """Check ``graph`` is a Qwen2 forward of this configuration; True for the last-row variant."""
+        if self.config is None:
+            raise NotImplementedError("no Qwen2 configuration given: every graph runs as generated code")
         if graph.name not in ("qwen2", "qwen2_last"):
             raise NotImplementedError(f"graph {graph.name!r}: this backend runs the Qwen2 forward graphs "
                                       f"(models/qwen2.py:167-224), 'qwen2' and 'qwen2_last'")
@@ -146,7 +154,8 @@ class HIPBackend:
         for held, bound in self._compiled:
             if held is graph:
                 return bound
-        bound = HIPCompiledGraph(graph, self.config, backend=self)
+        bound = HIPCompiledGraph(graph, self.config, self.fuse, self.schedule, backend=self, device=self.device,
+                                 lower=self.lower)
         self._compiled.append((graph, bound))
         return bound
 
@@ -184,25 +193,56 @@ class HIPBackend:
 
 
 class HIPCompiledGraph:
-    """One Qwen2 graph bound to the GPU model: the reference's ``CompiledGraph(graph, fuse, schedule)``
-    and its ``__call__(inputs, weights, bindings=None, profile=None) -> dict`` (runtime.py:167-301).
+    """A graph compiled for the GPU: the reference's ``CompiledGraph(graph, fuse, schedule)`` and its
+    ``__call__(inputs, weights, bindings=None, profile=None) -> dict`` (runtime.py:167-301).
 
-    The graph is recognised here, once (``NotImplementedError`` for anything but the Qwen2 forward
-    graphs of ``config``). ``bindings``, when given, must agree with the inputs' symbols (``seq``,
-    ``past``), as the reference's ``check_arguments`` requires; ``profile``, when given, accumulates
-    the seconds of the call under "qwen2_forward" (the whole forward is one sequence of GPU
-    kernels, not one call per graph primitive).
+    Two paths, chosen once:
+
+    * a Qwen2 forward graph of ``config`` (recognised by interface and int8 primitive) runs on the
+      hand-written model library (models/qwen2.py), whose kernels compute the reference's bits for
+      the projections and its operations in a stated order elsewhere; ``fuse`` does not change its
+      result (the reference holds fused and unfused programs bitwise equal, test_codegen.py:40-52);
+    * any other graph, or any ``program`` given, runs as generated HIP: the reference's compiled
+      program (``fusion.fuse(passes.optimize(graph))``, or ``lower.lower(graph)`` with
+      ``fuse=False``; its runtime.py:186) lowered by codegen_hip with GPU schedules, on one device
+      arena (compiled.CompiledProgram). ``program`` may be the reference's Program or a recorded
+      one (lir.program_from_json); ``lower(graph, fuse)`` may supply the compilation, else the
+      reference's own passes are imported (the host framework a drop-in backend runs inside).
+
+    ``schedule`` is ``"default"``, a projection ``autotune.Autotuner`` (the model path), or for
+    generated code a function ``(kernel, calls) -> (kernel, Launch)`` or an object with
+    ``schedule_program(program)`` (a codegen tuner). ``bindings``, when given, must agree with the
+    inputs' symbols (``check_arguments``); ``profile`` accumulates seconds per primitive (generated
+    code) or under "qwen2_forward" (the model path, one sequence of kernels).
     """
 
-    def __init__(self, graph, config, fuse: bool = True, schedule="default", backend: HIPBackend | None = None,
-                 max_tokens: int = 512, device: int = 0) -> None:
-        self.graph = graph
-        self.backend = backend or HIPBackend(config, max_tokens=max_tokens, device=device, schedule=schedule)
-        self.mode = self.backend.mode(graph)
-        self.last_only = self.backend.last_only(graph, self.mode)
+    def __init__(self, graph=None, config=None, fuse: bool = True, schedule="default",
+                 backend: HIPBackend | None = None, max_tokens: int = 512, device: int = 0, *,
+                 program=None, lower=None) -> None:
+        self.graph, self.fuse, self.schedule = graph, fuse, schedule
+        self.path = "codegen"
+        if program is None and graph is not None and (backend is not None or config is not None):
+            self.backend = backend or HIPBackend(config, max_tokens=max_tokens, device=device, schedule=schedule)
+            try:
+                self.mode = self.backend.mode(graph)
+                self.last_only = self.backend.last_only(graph, self.mode)
+                self.path = "model"
+            except NotImplementedError:
+                pass
+        if self.path == "codegen":
+            from nanocompile_amd import autotune
+            from nanocompile_amd.compiled import CompiledProgram
+            if program is None:
+                if graph is None:
+                    raise ValueError("HIPCompiledGraph needs a graph or a compiled program")
+                program = lower(graph, fuse) if lower is not None else _reference_compile(graph, fuse)
+            codegen_schedule = "default" if isinstance(schedule, autotune.Autotuner) else schedule
+            self.program = CompiledProgram(program, schedule=codegen_schedule, device=device)
 
     def __call__(self, inputs: Mapping[str, np.ndarray], weights: Mapping[str, np.ndarray],
                  bindings: Mapping[str, int] | None = None, profile: dict[str, float] | None = None) -> dict:
+        if self.path == "codegen":
+            return self.program(inputs, weights, bindings, profile)
         if bindings:
             bound = {"seq": int(np.asarray(inputs["token_ids"]).shape[0]),
                      "past": int(np.asarray(inputs["past_keys"]).shape[2])}
@@ -214,3 +254,17 @@ class HIPCompiledGraph:
         if profile is not None:
             profile["qwen2_forward"] = profile.get("qwen2_forward", 0.0) + time.perf_counter() - started
         return out
+
+
+def _reference_compile(graph, fuse: bool):
+    """The reference's own compilation of ``graph`` (runtime.py:186): its passes, run where it is installed."""
+    try:
+        from nanocompile.fusion import fuse as fuse_graph
+        from nanocompile.lower import lower
+        from nanocompile.passes import optimize
+    except ImportError as error:
+        raise NotImplementedError(
+            f"graph {getattr(graph, 'name', graph)!r} is not a Qwen2 forward this backend runs natively, and "
+            f"the reference's compiler (nanocompile) is not importable to lower it; pass program= or lower=") \
+            from error
+    return fuse_graph(optimize(graph)) if fuse else lower(graph)

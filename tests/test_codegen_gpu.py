@@ -101,3 +101,34 @@ def test_memory_plan_reuses_the_arena(tiny):
     plan = compiled["full"].last_plan
     assert plan.region_bytes < plan.unshared_bytes
     assert compiled["full"]._arena.nbytes >= compiled["full"]._region + plan.region_bytes
+
+
+def test_compiled_graph_and_backend_run_any_program_as_generated_code(gpu):
+    """The reference's CompiledGraph/CBackend interface (runtime.py:167-337): a program given
+    directly, and a graph that is not a Qwen2 forward lowered by a supplied compilation."""
+    from types import SimpleNamespace
+
+    from nanocompile_amd.models.config import TINY
+    from nanocompile_amd.runner import HIPBackend, HIPCompiledGraph
+    cases, weights = P.zoo_cases("rms_norm")
+    inputs, want, _ = cases[1]
+    compiled = HIPCompiledGraph(program=P.zoo("rms_norm"))
+    assert compiled.path == "codegen"
+    profile = {}
+    check("rms_norm", compiled(inputs, weights, profile=profile), want)
+    assert set(profile) == {"row"} and profile["row"] > 0
+    graph = SimpleNamespace(name="rms_norm", nodes=[])                  # stands in for the reference's Graph
+    lowered = []
+
+    def lower(g, fuse):
+        lowered.append((g, fuse))
+        return P.zoo("rms_norm", "program" if fuse else "unfused")
+
+    for config in (None, TINY):
+        backend = HIPBackend(config, lower=lower)
+        check("rms_norm", backend(graph, inputs, weights), want)
+        check("rms_norm", backend(graph, inputs, weights), want)        # compiled once per graph
+    assert lowered == [(graph, True), (graph, True)]
+    unfused = HIPBackend(None, fuse=False, lower=lower)
+    check("rms_norm", unfused(graph, inputs, weights), want)
+    assert lowered[-1] == (graph, False)

@@ -94,3 +94,13 @@ def test_compiled_graph_binds_once_and_checks_bindings(fixture):
         cg(inputs, {}, bindings={"seq": 3})
     with pytest.raises(NotImplementedError):
         HIPCompiledGraph(runner_graphs.stand_in({**fixture["modes"]["int8"]["graph"], "name": "other"}), TINY)
+
+
+def test_a_graph_nothing_can_lower_is_refused_with_the_way_out():
+    """Without the reference's compiler installed and no lowering given, a graph that is not a
+    Qwen2 forward cannot become a program: the error says what to pass."""
+    from types import SimpleNamespace
+
+    from nanocompile_amd.runner import HIPCompiledGraph
+    with pytest.raises(NotImplementedError, match="program= or lower="):
+        HIPCompiledGraph(SimpleNamespace(name="mystery", nodes=[]))
