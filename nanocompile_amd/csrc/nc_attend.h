@@ -10,18 +10,19 @@
 // the chunks combined after):
 //
 //   per chunk j of keys t = 64 j .. 64 j + n_j - 1:
-//     s_t  = (sum_d q[d] * k_t[d], in order of d) * scale + 0
+//     s_t  = (a = 0; a = fma(q[d], k_t[d], a) in order of d) * scale + 0
 //     m_j  = max_t s_t                       (NaN propagates)
 //     p_t  = exp(s_t - m_j)
 //     l_j  = sum_t p_t                       (wavefront butterfly, xor 32 .. 1, over 64 lanes, 0 past n_j)
-//     o_j  = sum_t p_t * v_t                 (in order of t, from +0)
+//     o_j  = (o = 0; o = fma(p_t, v_t, o) in order of t)
 //   over the chunks j = 0 .. J - 1, in order:
 //     m    = max_j m_j
 //     w_j  = exp(m_j - m)
 //     L    = sum_j l_j * w_j,   O = sum_j o_j * w_j   (in order of j, from +0)
 //     out  = O / L
 //
-// Every multiply and add rounds once (-ffp-contract=off); exp is nc_expf.
+// Each fma rounds once, every other multiply and add rounds once
+// (-ffp-contract=off forms no other fused operation); exp is nc_expf.
 // The chunk results (m_j, l_j, o_j) of a query travel between the two
 // kernels as D + 2 floats: m_j, l_j, o_j[0 .. D - 1].
 #pragma once
@@ -114,10 +115,10 @@ __device__ __forceinline__ void chunk_scores(const float *q, const Staged<D> &st
     for (int i = 0; i < D / 4; ++i) {
         const float4 k = *reinterpret_cast<const float4 *>(krow + 4 * i);
         const float4 qi = *reinterpret_cast<const float4 *>(q + 4 * i);
-        acc = __fadd_rn(acc, __fmul_rn(qi.x, k.x));
-        acc = __fadd_rn(acc, __fmul_rn(qi.y, k.y));
-        acc = __fadd_rn(acc, __fmul_rn(qi.z, k.z));
-        acc = __fadd_rn(acc, __fmul_rn(qi.w, k.w));
+        acc = __builtin_fmaf(qi.x, k.x, acc);
+        acc = __builtin_fmaf(qi.y, k.y, acc);
+        acc = __builtin_fmaf(qi.z, k.z, acc);
+        acc = __builtin_fmaf(qi.w, k.w, acc);
     }
     const float s = lane < n ? __fadd_rn(__fmul_rn(acc, scale), 0.0f) : -__builtin_inff();
     // (scores are never -0, so nan_max commutes up to which NaN propagates)
@@ -131,8 +132,8 @@ __device__ __forceinline__ void chunk_scores(const float *q, const Staged<D> &st
 
 // chunk_values: o[d] in key order from the p_t that chunk_scores left in LDS
 // (the wave's own write lands before its reads), four at a time. A key past n
-// adds 0 * v = +-0 (v a real key, masked, or a zero row) to an accumulator
-// that starts at +0 and is never -0: exact, no change.
+// has p = 0, and fma(0, v, o) = o + (+-0) = o exactly (v a real key, masked,
+// or a zero row; o starts at +0 and is never -0).
 template <int D>
 __device__ __forceinline__ float chunk_values(const float *p, const Staged<D> &st) {
     const int lane = threadIdx.x & 63;
@@ -141,10 +142,10 @@ __device__ __forceinline__ float chunk_values(const float *p, const Staged<D> &s
 #pragma unroll
     for (int i = 0; i < kChunk / 4; ++i) {
         const float4 pi = *reinterpret_cast<const float4 *>(p + 4 * i);
-        o = __fadd_rn(o, __fmul_rn(pi.x, st.values[(4 * i + 0) * D + dl]));
-        o = __fadd_rn(o, __fmul_rn(pi.y, st.values[(4 * i + 1) * D + dl]));
-        o = __fadd_rn(o, __fmul_rn(pi.z, st.values[(4 * i + 2) * D + dl]));
-        o = __fadd_rn(o, __fmul_rn(pi.w, st.values[(4 * i + 3) * D + dl]));
+        o = __builtin_fmaf(pi.x, st.values[(4 * i + 0) * D + dl], o);
+        o = __builtin_fmaf(pi.y, st.values[(4 * i + 1) * D + dl], o);
+        o = __builtin_fmaf(pi.z, st.values[(4 * i + 2) * D + dl], o);
+        o = __builtin_fmaf(pi.w, st.values[(4 * i + 3) * D + dl], o);
     }
     return o;
 }
@@ -179,10 +180,10 @@ __device__ __forceinline__ void chunk_scores_n(float (*qp)[kChunk], const Staged
 #pragma unroll
         for (int u = 0; u < H; ++u) {
             const float4 qi = *reinterpret_cast<const float4 *>(qp[u] + 4 * i);
-            acc[u] = __fadd_rn(acc[u], __fmul_rn(qi.x, k.x));
-            acc[u] = __fadd_rn(acc[u], __fmul_rn(qi.y, k.y));
-            acc[u] = __fadd_rn(acc[u], __fmul_rn(qi.z, k.z));
-            acc[u] = __fadd_rn(acc[u], __fmul_rn(qi.w, k.w));
+            acc[u] = __builtin_fmaf(qi.x, k.x, acc[u]);
+            acc[u] = __builtin_fmaf(qi.y, k.y, acc[u]);
+            acc[u] = __builtin_fmaf(qi.z, k.z, acc[u]);
+            acc[u] = __builtin_fmaf(qi.w, k.w, acc[u]);
         }
     }
 #pragma unroll
@@ -197,8 +198,8 @@ __device__ __forceinline__ void chunk_scores_n(float (*qp)[kChunk], const Staged
     }
 }
 
-// (keys from n on add +-0 to accumulators that are never -0, so the key loop
-// stops at the first group of four that holds none of the n keys)
+// (keys from n on have p = 0 and leave the accumulators unchanged, so the key
+// loop stops at the first group of four that holds none of the n keys)
 template <int D, int H>
 __device__ __forceinline__ void chunk_values_n(float (*qp)[kChunk], const Staged<D> &st, int n, float (&o)[H]) {
     const int lane = threadIdx.x & 63;
@@ -213,10 +214,10 @@ __device__ __forceinline__ void chunk_values_n(float (*qp)[kChunk], const Staged
 #pragma unroll
         for (int u = 0; u < H; ++u) {
             const float4 pi = *reinterpret_cast<const float4 *>(qp[u] + 4 * i);
-            o[u] = __fadd_rn(o[u], __fmul_rn(pi.x, v0));
-            o[u] = __fadd_rn(o[u], __fmul_rn(pi.y, v1));
-            o[u] = __fadd_rn(o[u], __fmul_rn(pi.z, v2));
-            o[u] = __fadd_rn(o[u], __fmul_rn(pi.w, v3));
+            o[u] = __builtin_fmaf(pi.x, v0, o[u]);
+            o[u] = __builtin_fmaf(pi.y, v1, o[u]);
+            o[u] = __builtin_fmaf(pi.z, v2, o[u]);
+            o[u] = __builtin_fmaf(pi.w, v3, o[u]);
         }
     }
 }

@@ -153,9 +153,10 @@ typedef struct {
 } attn_ctx;
 
 /* Attention of one query row in the chunked order of the GPU kernels
- * (nanocompile_amd/csrc/nc_attend.h): per chunk of 64 keys the scores in
- * order of d, the chunk max, p = exp(s - max), the chunk sum as the
- * wavefront butterfly over 64 lanes (0 past the chunk), o in key order; then
+ * (nanocompile_amd/csrc/nc_attend.h): per chunk of 64 keys the scores as an
+ * fmaf chain in order of d, the chunk max, p = exp(s - max), the chunk sum as
+ * the wavefront butterfly over 64 lanes (0 past the chunk), o as an fmaf chain
+ * in key order; then
  * the chunks combined in order: m = max m_j, w_j = exp(m_j - m),
  * L = sum l_j w_j, O = sum o_j w_j, out = O / L. */
 #define CHUNK 64
@@ -179,7 +180,7 @@ static void attend_row(float *out, const float *q, const float *K, const float *
         float m = -INFINITY;
         for (int64_t i = 0; i < n; ++i) {
             float acc = 0.0f;
-            for (int64_t k = 0; k < d; ++k) acc = acc + q[k] * K[(t0 + i) * d + k];
+            for (int64_t k = 0; k < d; ++k) acc = fmaf(q[k], K[(t0 + i) * d + k], acc);
             s[i] = (acc * scale) + 0.0f;
             m = nan_max(m, s[i]);
         }
@@ -191,7 +192,7 @@ static void attend_row(float *out, const float *q, const float *K, const float *
         pj[1] = butterfly64(lanes);
         for (int64_t k = 0; k < d; ++k) {
             float o = 0.0f;
-            for (int64_t i = 0; i < n; ++i) o = o + p[i] * V[(t0 + i) * d + k];
+            for (int64_t i = 0; i < n; ++i) o = fmaf(p[i], V[(t0 + i) * d + k], o);
             pj[2 + k] = o;
         }
     }
