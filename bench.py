@@ -552,7 +552,8 @@ def main() -> int:
                    "blocks": d.get("blocks")},
         "roofline": {"bound": "hbm", "achieved": top["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": top["frac"], "traffic": measured_traffic(KERNEL_SYMBOLS[dominant]),
-                     "traffic_source": "profiles/traffic.json (rocprofv3 PMC, calibrated)",
+                     "traffic_source": "profiles/traffic.json (rocprofv3 PMC, calibrated); null when no pass "
+                                       "exists for this kernel (profiles/decode_step_config5.md)",
                      "kernel": f"{KERNEL_SYMBOLS[dominant]} ({dominant}: the decode step's time-dominant kernel "
                                f"group, {top['launches_per_step']} launches, {top['step_us']} us a step)",
                      "bytes_per_launch": top["bytes_per_launch"], "launch_us": top["launch_us"],
