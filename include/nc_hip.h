@@ -191,9 +191,15 @@ int32_t nc_quantize_blocks(void **p, const int64_t *s);
  * bit, as nc_rms_norm_quant followed by nc_matmul_i8_token(_swiglu).
  * p: [out f32[N] (holds the residual for kind 1), x f32[K], gamma f32[K] or NULL,
  *     q i8[N,K], scales f32[N], bias f32[N] or NULL, q2 i8[N,K] or NULL, scales2 f32[N] or NULL];
- * s: [N, K, kind, eps as float32 bits]; K in {896, 4864} (and the test model's 128, 256);
- * other widths take the unfused kernels. */
+ * s: [N, K, kind, eps as float32 bits, schedule]; K in {896, 4864} (and the test model's 128, 256);
+ * other widths take the unfused kernels. schedule 0 is the library's launch shape; 1..5 a row of
+ * the width's table of (lanes a row, waves a workgroup, bytes a load), for the tuner: the
+ * reference's schedule knobs (schedules.py:87-128) as GPU launch shapes, every one the same bits. */
 int32_t nc_decode_projection(void **p, const int64_t *s);
+
+/* A decode projection schedule, for the tuner (no device call): out = [lanes a row, waves a
+ * workgroup, bytes a load]; NC_BAD_ARGS when it does not exist for width K and kind. */
+int32_t nc_decode_schedule_info(int64_t K, int64_t kind, int64_t schedule, int64_t *out);
 
 /* Attention of one new token (models/qwen2.py:113-155 at seq = 1) with RoPE of
  * its q and k heads and the cache append fused in: the same arithmetic, bit for
@@ -276,9 +282,14 @@ int32_t nc_matmul_i8_token_rope(void **p, const int64_t *s);
  *     work f32 (the chunk results: heads * ceil(keys / 64) * (D + 2) floats per query
  *     row, keys = C with pos, else past + M; fewer than M rows' worth takes the rows
  *     in slabs), xq i8[M,heads*D] or NULL, xs f32[M] or NULL];
- * s: [M, heads, kv, D, past, C, scale as float32 bits, work bytes] (D 16, 32 or 64;
- *    at most 16384 keys) */
+ * s: [M, heads, kv, D, past, C, scale as float32 bits, work bytes, schedule] (D 16, 32 or 64;
+ *    at most 16384 keys; schedule 0 the library's query rows a chunk workgroup, 1..4 the
+ *    tuner's choices, nc_attention_schedule_info; every schedule the same bits) */
 int32_t nc_attention(void **p, const int64_t *s);
+
+/* A prefill attention schedule, for the tuner (no device call): out = [query rows a chunk
+ * workgroup]; NC_BAD_ARGS outside 1..4. */
+int32_t nc_attention_schedule_info(int64_t schedule, int64_t *out);
 
 /* -- the model's ends ---------------------------------------------------------- */
 

@@ -102,6 +102,7 @@ class Problem:
     def __init__(self, op: str, m: int, n: int, k: int, seed: int = 0,
                  stream_bytes: int = STREAM_BYTES) -> None:
         self.op, self.m, self.n, self.k = op, m, n, k
+        self.shape = (m, n, k)
         rng = np.random.default_rng(seed)
         per_copy = n * k * (2 if op == "matmul_i8_token_swiglu" else 1)
         self.copies = int(min(MAX_COPIES, max(2, -(-stream_bytes // max(per_copy, 1)))))
@@ -125,17 +126,115 @@ class Problem:
                      [self.y, self.xq, self.xs, q[0], self.scales[0], q[1], self.scales[1]],
                      [self.m, self.n, self.k, schedule])
 
+    def space(self) -> list[dict]:
+        return legal_space(self.op, self.m, self.n, self.k)
+
     def output(self, schedule: int) -> np.ndarray:
         """The schedule's output bits; TuningError if it wrote into a guard region."""
         self.guarded.upload(guarded(self.m * self.n))
         self.launch(schedule, 0)
-        hip.sync()
-        bits = self.guarded.numpy()
-        broken = guards_broken(bits)
-        if broken:
-            raise TuningError(f"{self.op} schedule {schedule} on {(self.m, self.n, self.k)} wrote outside its "
-                              f"output, at word offsets {broken[:4]}")
-        return bits[GUARD:GUARD + self.m * self.n].copy()
+        return checked_output(self, schedule, self.guarded, self.m * self.n)
+
+
+def checked_output(problem, schedule: int, region: DeviceArray, words: int) -> np.ndarray:
+    """After a launch into ``region`` (GUARD words, the output, GUARD words): the output's bits,
+    or TuningError if a guard word changed."""
+    hip.sync()
+    bits = region.numpy()
+    broken = guards_broken(bits)
+    if broken:
+        raise TuningError(f"{problem.op} schedule {schedule} on {problem.shape} wrote outside its output, "
+                          f"at word offsets {broken[:4]}")
+    return bits[GUARD:GUARD + words].copy()
+
+
+class DecodeProblem:
+    """One decode projection (nc_decode_projection) of ``kind`` over N rows of width K: the step's
+    activation row, its prologue and epilogue operands, and the weights in rotating copies so they
+    stream from HBM as a decode step's do. Kinds: 0 rms_norm + bias (q, k, v), 1 quantize +
+    residual (o, down), 2 rms_norm + SwiGLU pair (gate, up)."""
+
+    op = "decode_projection"
+
+    def __init__(self, kind: int, n: int, k: int, seed: int = 0, stream_bytes: int = STREAM_BYTES) -> None:
+        self.kind, self.n, self.k = kind, n, k
+        self.shape = (kind, n, k)
+        rng = np.random.default_rng(seed)
+        matrices = 2 if kind == 2 else 1
+        self.copies = int(min(MAX_COPIES, max(2, -(-stream_bytes // max(n * k * matrices, 1)))))
+        self.x = DeviceArray.from_host(rng.standard_normal(k).astype(np.float32))
+        self.gamma = DeviceArray.from_host((1 + 0.1 * rng.standard_normal(k)).astype(np.float32))
+        host = [rng.integers(-127, 128, (n, k)).astype(np.int8) for _ in range(matrices)]
+        self.q = [[DeviceArray.from_host(w) for w in host] for _ in range(self.copies)]
+        self.scales = [DeviceArray.from_host((rng.random(n) * 1e-3).astype(np.float32)) for _ in range(matrices)]
+        self.bias = DeviceArray.from_host(rng.standard_normal(n).astype(np.float32))
+        self.residual = rng.standard_normal(n).astype(np.float32)
+        self.guarded = DeviceArray.from_host(guarded(n))
+        self.y = self.guarded.view((n,), np.float32, offset_bytes=GUARD * 4)
+
+    def space(self) -> list[dict]:
+        out = [{"schedule": 0, "kernel": "default"}]
+        for s in range(1, 8):
+            shape = hip.decode_schedule_info(self.k, self.kind, s)
+            if shape is not None:
+                out.append({"schedule": s, "kernel": "gemv_decode", **shape})
+        return out
+
+    def launch(self, schedule: int, copy: int = 0) -> None:
+        from nanocompile_amd.kernels import float_bits
+        q = self.q[copy % self.copies]
+        gamma = None if self.kind == 1 else self.gamma
+        bias = self.bias if self.kind == 0 else None
+        q2, s2 = (q[1], self.scales[1]) if self.kind == 2 else (None, None)
+        hip.call("nc_decode_projection", [self.y, self.x, gamma, q[0], self.scales[0], bias, q2, s2],
+                 [self.n, self.k, self.kind, float_bits(1e-6), schedule])
+
+    def output(self, schedule: int) -> np.ndarray:
+        bits = guarded(self.n)
+        if self.kind == 1:                       # the output holds the residual the projection adds to
+            bits[GUARD:GUARD + self.n] = self.residual.view(np.uint32)
+        self.guarded.upload(bits)
+        self.launch(schedule, 0)
+        return checked_output(self, schedule, self.guarded, self.n)
+
+
+class AttentionProblem:
+    """A prompt's attention (nc_attention) over M rows at past 0 with heads / kv heads of width D:
+    rotated q, k and v rows, the cache holding the prompt's keys and values, the chunk workspace."""
+
+    op = "attention_prefill"
+
+    def __init__(self, m: int, heads: int, kv: int, d: int, seed: int = 0) -> None:
+        from nanocompile_amd.kernels import attention_workspace_bytes
+        self.m, self.heads, self.kv, self.d = m, heads, kv, d
+        self.shape = (m, heads, kv, d)
+        rng = np.random.default_rng(seed)
+        self.qkv = DeviceArray.from_host(rng.standard_normal((m, (heads + 2 * kv) * d)).astype(np.float32))
+        self.kc = DeviceArray.from_host(rng.standard_normal((kv, m, d)).astype(np.float32))
+        self.vc = DeviceArray.from_host(rng.standard_normal((kv, m, d)).astype(np.float32))
+        self.work_bytes = attention_workspace_bytes(heads, d, m, m)
+        self.work = DeviceArray((self.work_bytes // 4,), np.float32)
+        self.guarded = DeviceArray.from_host(guarded(m * heads * d))
+        self.ctx = self.guarded.view((m, heads * d), np.float32, offset_bytes=GUARD * 4)
+
+    def space(self) -> list[dict]:
+        out = [{"schedule": 0, "kernel": "default"}]
+        for s in range(1, 8):
+            rows = hip.attention_schedule_info(s)
+            if rows is not None:
+                out.append({"schedule": s, "kernel": "attention_rows_chunks", "rows": rows})
+        return out
+
+    def launch(self, schedule: int, copy: int = 0) -> None:
+        from nanocompile_amd.kernels import float_bits
+        hip.call("nc_attention", [self.ctx, self.qkv, self.kc, self.vc, None, self.work],
+                 [self.m, self.heads, self.kv, self.d, 0, self.m, float_bits(self.d ** -0.5), self.work_bytes,
+                  schedule])
+
+    def output(self, schedule: int) -> np.ndarray:
+        self.guarded.upload(guarded(self.m * self.heads * self.d))
+        self.launch(schedule, 0)
+        return checked_output(self, schedule, self.guarded, self.m * self.heads * self.d)
 
 
 def measure(problem: Problem, schedules: list[int], rounds: int, reps: int) -> list[float]:
@@ -172,7 +271,7 @@ class Evaluation:
 class TuneRecord:
     key: str
     op: str
-    shape: tuple[int, int, int]
+    shape: tuple
     space_size: int
     winner: int = 0
     default_cost: float | None = None
@@ -282,8 +381,8 @@ class Autotuner:
         self._chosen: dict[tuple, int] = {}
 
     @staticmethod
-    def problem_key(op: str, m: int, n: int, k: int, space: list[dict]) -> str:
-        material = json.dumps({"op": op, "m": m, "n": n, "k": k, "space": space,
+    def problem_key(op: str, m: int, n: int, k: int, space: list[dict], extra: tuple = ()) -> str:
+        material = json.dumps({"op": op, "m": m, "n": n, "k": k, "space": space, "extra": list(extra),
                                "library": hip.library_digest()}, sort_keys=True)
         return hashlib.sha256(material.encode()).hexdigest()[:20]
 
@@ -295,10 +394,39 @@ class Autotuner:
         return self._chosen[at]
 
     def tune(self, op: str, m: int, n: int, k: int) -> TuneRecord:
+        """Tune a projection (``matmul_i8_token`` or ``matmul_i8_token_swiglu``) on an [m, k] x [n, k]^T problem."""
+        if op not in OPS:
+            raise ValueError(f"no tuning space for {op!r}")
+        return self.tune_problem(lambda: Problem(op, m, n, k, self.seed, self.stream_bytes), op, (m, n, k),
+                                 legal_space(op, m, n, k))
+
+    def decode_schedule(self, kind: int, n: int, k: int) -> int:
+        """The schedule of a decode projection (nc_decode_projection's kind, N rows, width K)."""
+        at = ("decode_projection", kind, n, k)
+        if at not in self._chosen:
+            self._chosen[at] = self.tune_problem(
+                lambda: DecodeProblem(kind, n, k, self.seed, self.stream_bytes), "decode_projection", (kind, n, k),
+                None).winner
+        return self._chosen[at]
+
+    def attention_schedule(self, m: int, heads: int, kv: int, d: int) -> int:
+        """The schedule of a prompt's attention (nc_attention) over m rows at past 0."""
+        at = ("attention_prefill", m, heads, kv, d)
+        if at not in self._chosen:
+            self._chosen[at] = self.tune_problem(lambda: AttentionProblem(m, heads, kv, d, self.seed),
+                                                 "attention_prefill", (m, heads, kv, d), None).winner
+        return self._chosen[at]
+
+    def tune_problem(self, make, op: str, shape: tuple, space: list[dict] | None) -> TuneRecord:
+        """Measure the candidates of the problem ``make()`` builds (its ``space()`` unless given):
+        each checked bit for bit against schedule 0 inside guard regions, then timed."""
         started = time.perf_counter()
-        space = legal_space(op, m, n, k)
-        key = self.problem_key(op, m, n, k, space)
-        record = TuneRecord(key, op, (m, n, k), len(space))
+        problem = None
+        if space is None:
+            problem = make()
+            space = problem.space()
+        key = self.problem_key(op, *((list(shape) + [0, 0, 0])[:3]), space, extra=tuple(shape[3:]))
+        record = TuneRecord(key, op, tuple(shape), len(space))
         machine = machine_key()
         if self.cache is not None:
             entry = self.cache.get(machine, key)
@@ -309,12 +437,12 @@ class Autotuner:
                 self.records.append(record)
                 return record
 
-        problem = Problem(op, m, n, k, self.seed, self.stream_bytes)
+        problem = problem or make()
         schedules = [c["schedule"] for c in space]
         reference = problem.output(0)
         for s in schedules[1:]:
             if not np.array_equal(problem.output(s), reference):
-                raise TuningError(f"{op} schedule {s} on {(m, n, k)} differs from the default's bits")
+                raise TuningError(f"{op} schedule {s} on {tuple(shape)} differs from the default's bits")
 
         def cost(stage: str, candidates: list[int]) -> list[float]:
             rounds = self.rounds * 2 if stage == "confirm" else self.rounds
@@ -327,9 +455,9 @@ class Autotuner:
         self.records.append(record)
         if self.cache is not None:
             self.cache.put(machine, key, {"winner": winner, "default_cost": default_cost,
-                                          "winner_cost": winner_cost, "op": op, "shape": [m, n, k]})
+                                          "winner_cost": winner_cost, "op": op, "shape": list(shape)})
         if self.verbose:
-            print(f"tuned {op} {(m, n, k)}: {len(space)} schedules in {record.seconds:.1f} s, "
+            print(f"tuned {op} {tuple(shape)}: {len(space)} schedules in {record.seconds:.1f} s, "
                   f"schedule {winner} at {winner_cost * 1e6:.2f} us ({record.speedup:.2f}x the default)",
                   flush=True)
         return record

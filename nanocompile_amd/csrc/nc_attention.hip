@@ -169,7 +169,12 @@ constexpr int kWaves = 8;              // decode: waves of a chunk workgroup, on
 // of that one-head kernel, all slower: 8, 2 or 1 rows a workgroup (62, 63, 99
 // us), registers capped at three waves a SIMD (spills: 168 us), each head's
 // query read with scalar loads (69-73 us).
-constexpr int kRowsPerBlock = 4;
+constexpr int kRowsPerBlock = 4;         // prefill: query rows (waves) a chunk workgroup, the library's choice
+// The prefill schedules a tuner may choose: schedule s (1..4) stages each
+// chunk for kScheduleRows[s - 1] rows; schedule 0 is kRowsPerBlock. Every
+// choice computes the same bits: a row's arithmetic does not depend on which
+// workgroup holds it.
+constexpr int kScheduleRows[4] = {2, 4, 8, 16};
 constexpr int kHeadBatch = 7;          // prefill: query heads of a row held in LDS at once (a group, in Qwen2)
 
 template <typename F>
@@ -540,7 +545,7 @@ int32_t launch_combine_quant(void **p, const float *part, int64_t heads, int64_t
 
 // Query rows in slabs whose chunk results fit the workspace; each slab is a
 // chunk launch and a combine launch.
-template <int D>
+template <int D, int ROWS>
 int32_t launch_prefill(void **p, int64_t M, int64_t heads, int64_t kv, int64_t past, int64_t cap, float scale,
                        const int64_t *pos, float *work, int64_t work_bytes) {
     const int64_t jstride = ((pos ? cap : past + M) + nc::kChunk - 1) / nc::kChunk;
@@ -552,14 +557,14 @@ int32_t launch_prefill(void **p, int64_t M, int64_t heads, int64_t kv, int64_t p
     // while a row's chunk results fit its workgroup's LDS, else after
     const bool quantize = p[6] && p[7];
     const bool fused = quantize && heads <= 16 && heads * jstride * (D + 2) * (int64_t)sizeof(float) <= 64 * 1024;
-    if (slab < M && slab >= kRowsPerBlock) slab -= slab % kRowsPerBlock;
+    if (slab < M && slab >= ROWS) slab -= slab % ROWS;
     const int64_t host_past = pos ? 0 : past;
     for (int64_t i0 = 0; i0 < M; i0 += slab) {
         const int64_t rows = std::min(slab, M - i0);
         const int64_t chunks = pos ? jstride : (past + i0 + rows + nc::kChunk - 1) / nc::kChunk;
-        hipLaunchKernelGGL((attention_rows_chunks<D, kRowsPerBlock>),
-                           dim3((unsigned)chunks, (unsigned)kv, (unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock)),
-                           dim3(64 * kRowsPerBlock), 0, nc::stream(), work, (const float *)p[1], (const float *)p[2],
+        hipLaunchKernelGGL((attention_rows_chunks<D, ROWS>),
+                           dim3((unsigned)chunks, (unsigned)kv, (unsigned)((rows + ROWS - 1) / ROWS)),
+                           dim3(64 * ROWS), 0, nc::stream(), work, (const float *)p[1], (const float *)p[2],
                            (const float *)p[3], (int)heads, (int)kv, (int)host_past, (int)cap, scale, (int)i0,
                            (int)rows, (int)M, (int)jstride, pos, nc::error_word());
         int32_t rc = nc::launched("attention_rows_chunks");
@@ -594,7 +599,9 @@ int32_t launch_decode(void **p, const int64_t *s, const int64_t *pos, float *wor
 
 // p: [ctx f32[M, heads*D], qkv f32[M, (H + 2*KV*D)] (q rotated), kcache, vcache, pos i64[1] | NULL,
 //     work f32[...], xq i8[M, heads*D] | NULL, xs f32[M] | NULL (with both: ctx's per-token int8 too)];
-// s: [M, heads, kv_heads, D, past, capacity, scale as float32 bits, work bytes]  (D 16, 32 or 64)
+// s: [M, heads, kv_heads, D, past, capacity, scale as float32 bits, work bytes, schedule]
+//    (D 16, 32 or 64; schedule 0 the library's rows a workgroup, 1..4 the tuner's choices:
+//    nc_attention_schedule_info)
 // With pos, past is read from the device when the kernels run (s[4] is ignored). The workspace
 // holds the chunk results; one query row needs heads * ceil(keys / 64) * (D + 2) floats, keys =
 // past + M (capacity with pos), and a smaller workspace than M rows' takes the rows in slabs.
@@ -606,12 +613,32 @@ NC_EXPORT int32_t nc_attention(void **p, const int64_t *s) {
                    (pos ? cap <= kMaxKeys : (past >= 0 && past + M <= cap && past + M <= kMaxKeys)) &&
                    M <= cap && M < 65536 && heads < 65536 && work_bytes >= 0,
                "nc_attention: bad shape (head_dim 16, 32 or 64; at most 16384 keys)");
+    const int64_t schedule = s[8];
+    NC_REQUIRE(schedule >= 0 && schedule <= 4, "nc_attention: no such schedule (0..4)");
     if (M == 0) return NC_OK;
     const float scale = nc::bits_to_float(s[6]);
     float *work = (float *)p[5];
-    if (D == 64) return launch_prefill<64>(p, M, heads, kv, past, cap, scale, pos, work, work_bytes);
-    if (D == 32) return launch_prefill<32>(p, M, heads, kv, past, cap, scale, pos, work, work_bytes);
-    return launch_prefill<16>(p, M, heads, kv, past, cap, scale, pos, work, work_bytes);
+    const int rows = schedule == 0 ? kRowsPerBlock : kScheduleRows[schedule - 1];
+#define NC_PREFILL(R)                                                                             \
+    if (rows == R) {                                                                              \
+        if (D == 64) return launch_prefill<64, R>(p, M, heads, kv, past, cap, scale, pos, work, work_bytes); \
+        if (D == 32) return launch_prefill<32, R>(p, M, heads, kv, past, cap, scale, pos, work, work_bytes); \
+        return launch_prefill<16, R>(p, M, heads, kv, past, cap, scale, pos, work, work_bytes);    \
+    }
+    NC_PREFILL(2)
+    NC_PREFILL(4)
+    NC_PREFILL(8)
+    NC_PREFILL(16)
+#undef NC_PREFILL
+    return NC_BAD_ARGS;
+}
+
+// A prefill attention schedule's launch shape, for the tuner (no device call):
+// out = [query rows a chunk workgroup (its waves)]; NC_BAD_ARGS past the table.
+NC_EXPORT int32_t nc_attention_schedule_info(int64_t schedule, int64_t *out) {
+    if (!out || schedule < 1 || schedule > 4) return NC_BAD_ARGS;
+    out[0] = kScheduleRows[schedule - 1];
+    return NC_OK;
 }
 
 // Attention of one new token with RoPE and the cache append fused in.

@@ -196,13 +196,59 @@ int32_t launch_decode(void **p, int N, float eps) {
     return nc::launched("gemv_decode");
 }
 
+// The schedules a tuner may choose for the model's two widths: (lanes a row,
+// waves a workgroup, bytes a load), schedule s at row s - 1 (schedule 0 is the
+// library's choice, the first row). Every row computes the same bits: the
+// prologue's order does not depend on W (the row-sum order's 256 virtual
+// threads either way) and integer dot products are exact in any order. An
+// rms_norm prologue takes 1 or 4 waves.
+#define NC_DECODE_896(X) X(1, 8, 1, 16) X(2, 4, 1, 16) X(3, 16, 1, 8) X(4, 8, 4, 16) X(5, 16, 4, 8)
+#define NC_DECODE_4864(X) X(1, 64, 4, 4) X(2, 16, 4, 16) X(3, 32, 4, 8) X(4, 64, 2, 4) X(5, 32, 2, 8)
+constexpr int kDecodeSchedules = 5;
+
+template <int K, int PRO, int EPI>
+int32_t launch_scheduled(void **p, int N, float eps, int schedule) {
+#define NC_DECODE_CASE(S, L, W, B)                                                            \
+    case S:                                                                                   \
+        if constexpr (PRO == kQuant || W == 1 || W == 4) return launch_decode<K, PRO, EPI, L, W, B>(p, N, eps); \
+        break;
+    if constexpr (K == 896) {
+        switch (schedule) { NC_DECODE_896(NC_DECODE_CASE) default: break; }
+    } else if constexpr (K == 4864) {
+        switch (schedule) { NC_DECODE_4864(NC_DECODE_CASE) default: break; }
+    }
+#undef NC_DECODE_CASE
+    nc::set_message("nc_decode_projection: no such schedule for this width and kind");
+    return NC_BAD_ARGS;
+}
+
 }  // namespace
+
+// A decode projection schedule's launch shape, for the tuner (no device call):
+// out = [lanes a row, waves a workgroup, bytes a load]; NC_BAD_ARGS when the
+// schedule does not exist for width K and kind (an rms_norm prologue, kinds 0
+// and 2, takes 1 or 4 waves).
+NC_EXPORT int32_t nc_decode_schedule_info(int64_t K, int64_t kind, int64_t schedule, int64_t *out) {
+    if (!out || kind < 0 || kind > 2) return NC_BAD_ARGS;
+#define NC_DECODE_INFO(S, L, W, B)                                        \
+    if (schedule == S && (kind == 1 || W == 1 || W == 4)) {               \
+        out[0] = L;                                                       \
+        out[1] = W;                                                       \
+        out[2] = B;                                                       \
+        return NC_OK;                                                     \
+    }
+    if (K == 896) { NC_DECODE_896(NC_DECODE_INFO) }
+    if (K == 4864 && kind == 1) { NC_DECODE_4864(NC_DECODE_INFO) }
+#undef NC_DECODE_INFO
+    return NC_BAD_ARGS;
+}
 
 // One decode projection with its activation prologue (see the file header).
 // p: [out f32[N] (in: the residual for kind 1), x f32[K], gamma f32[K] | NULL,
 //     q i8[N,K], scales f32[N], bias f32[N] | NULL, q2 i8[N,K] | NULL, scales2 f32[N] | NULL];
-// s: [N, K, kind, eps as float32 bits] with kind 0 = rms_norm prologue + bias (q, k, v),
-//    1 = quantize prologue + residual (o, down), 2 = rms_norm prologue + SwiGLU pair (gate, up).
+// s: [N, K, kind, eps as float32 bits, schedule] with kind 0 = rms_norm prologue + bias (q, k, v),
+//    1 = quantize prologue + residual (o, down), 2 = rms_norm prologue + SwiGLU pair (gate, up);
+//    schedule 0 the library's shape, 1..5 a row of the width's table (nc_decode_schedule_info).
 //    K is 896 or 4864 (the model's widths; any other K uses the unfused kernels).
 NC_EXPORT int32_t nc_decode_projection(void **p, const int64_t *s) {
     NC_REQUIRE(p && s && p[0] && p[1] && p[3] && p[4], "nc_decode_projection: null operand");
@@ -212,6 +258,16 @@ NC_EXPORT int32_t nc_decode_projection(void **p, const int64_t *s) {
     NC_REQUIRE(kind == 1 || p[2], "nc_decode_projection: rms_norm needs gamma");
     NC_REQUIRE(kind != 0 || p[5], "nc_decode_projection: q, k, v need their bias");
     NC_REQUIRE(kind != 2 || (p[6] && p[7]), "nc_decode_projection: SwiGLU needs the up projection");
+    const int64_t schedule = s[4];
+    NC_REQUIRE(schedule >= 0 && schedule <= kDecodeSchedules, "nc_decode_projection: no such schedule");
+    if (schedule > 0) {
+        if (K == 896 && kind == 0) return launch_scheduled<896, kNorm, kBias>(p, (int)N, eps, (int)schedule);
+        if (K == 896 && kind == 1) return launch_scheduled<896, kQuant, kResidual>(p, (int)N, eps, (int)schedule);
+        if (K == 896 && kind == 2) return launch_scheduled<896, kNorm, kSwiglu>(p, (int)N, eps, (int)schedule);
+        if (K == 4864 && kind == 1) return launch_scheduled<4864, kQuant, kResidual>(p, (int)N, eps, (int)schedule);
+        nc::set_message("nc_decode_projection: schedules exist for the widths 896 and 4864 only");
+        return NC_BAD_ARGS;
+    }
     if (K == 896 && kind == 0) return launch_decode<896, kNorm, kBias>(p, (int)N, eps);
     if (K == 896 && kind == 1) return launch_decode<896, kQuant, kResidual>(p, (int)N, eps);
     if (K == 896 && kind == 2) return launch_decode<896, kNorm, kSwiglu>(p, (int)N, eps);

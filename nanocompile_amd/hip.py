@@ -47,6 +47,8 @@ _RUNTIME = {
     "nc_runtime_version": (ctypes.c_int32, [ctypes.POINTER(ctypes.c_int64)] * 2),
     "nc_library_digest": (ctypes.c_char_p, []),
     "nc_schedule_info": (ctypes.c_int32, [ctypes.c_int32, ctypes.POINTER(ctypes.c_int64)]),
+    "nc_decode_schedule_info": (ctypes.c_int32, [ctypes.c_int64] * 3 + [ctypes.POINTER(ctypes.c_int64)]),
+    "nc_attention_schedule_info": (ctypes.c_int32, [ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)]),
     "nc_malloc": (ctypes.c_void_p, [ctypes.c_int64]),
     "nc_free": (ctypes.c_int32, [ctypes.c_void_p]),
     "nc_host_malloc": (ctypes.c_void_p, [ctypes.c_int64]),
@@ -140,6 +142,22 @@ def schedule_info(schedule: int) -> dict | None:
     return {"schedule": int(schedule), "kernel": "mfma", "tile_m": out[1], "tile_n": out[2], "k_stage": out[3],
             "wave_m": out[4], "wave_n": out[5], "stages": out[6], "threads": out[7], "lds_bytes": out[8],
             "lds_bytes_pair": out[9]}
+
+
+def decode_schedule_info(k: int, kind: int, schedule: int) -> dict | None:
+    """A decode projection schedule's launch shape (a table lookup; no GPU needed), or None."""
+    out = (ctypes.c_int64 * 4)()
+    if load().nc_decode_schedule_info(int(k), int(kind), int(schedule), out) != NC_OK:
+        return None
+    return {"lanes_per_row": out[0], "waves": out[1], "load_bytes": out[2]}
+
+
+def attention_schedule_info(schedule: int) -> int | None:
+    """Query rows a prefill attention workgroup takes under ``schedule`` (no GPU needed), or None."""
+    out = (ctypes.c_int64 * 2)()
+    if load().nc_attention_schedule_info(int(schedule), out) != NC_OK:
+        return None
+    return int(out[0])
 
 
 def kernel(name: str):

@@ -301,6 +301,7 @@ class Qwen2:
             self._layers_reference_modes(m, past, cache, pos)
             return
         s_qkv, s_o, s_mlp, s_down = self._projection_schedules(m)
+        s_attn = self.attention_schedule(m) if pos is None else 0
         for i, w in enumerate(self.layers):
             kc, vc = cache.layer(i)
             hip.call("nc_rms_norm_quant", [None, self.xq, self.xs, self.x, w["g1"]], [m, H, eps])
@@ -317,7 +318,7 @@ class Qwen2:
                          [m, heads, kv, D, past, cache.capacity])
             # attention, its combine also quantizing ctx per token for the o projection
             hip.call("nc_attention", [self.ctx, self.qkv, kc, vc, pos, cache.work, self.xq, self.xs],
-                     [m, heads, kv, D, past, cache.capacity, float_bits(self.scale), cache.work_bytes])
+                     [m, heads, kv, D, past, cache.capacity, float_bits(self.scale), cache.work_bytes, s_attn])
             q, s = w["o"]
             hip.call("nc_matmul_i8_token", [self.x, self.xq, self.xs, q, s, None, self.x], [m, H, Q, s_o])
             hip.call("nc_rms_norm_quant", [None, self.xq, self.xs, self.x, w["g2"]], [m, H, eps])
@@ -337,21 +338,23 @@ class Qwen2:
         heads, kv, W = c.num_attention_heads, c.num_key_value_heads, self.width
         Q = heads * D
         eps = float_bits(c.rms_norm_eps)
+        s_qkv, s_o, s_mlp, s_down = self.decode_schedules()
         calls = []
         for i, w in enumerate(self.layers):
             kc, vc = cache.layer(i)
             q, s = w["qkv"]
-            calls.append(("qkv", "nc_decode_projection", [self.qkv, self.x, w["g1"], q, s, w["qkv_b"]], [W, H, 0, eps]))
+            calls.append(("qkv", "nc_decode_projection", [self.qkv, self.x, w["g1"], q, s, w["qkv_b"]],
+                          [W, H, 0, eps, s_qkv]))
             calls.append(("attention", "nc_attention_decode",
                           [self.ctx, self.qkv, kc, vc, self.inv_freq, pos, cache.rope, cache.work],
                           [heads, kv, D, past, cache.capacity, float_bits(self.scale), cache.work_bytes]))
             q, s = w["o"]
-            calls.append(("o", "nc_decode_projection", [self.x, self.ctx, None, q, s], [H, Q, 1, eps]))
+            calls.append(("o", "nc_decode_projection", [self.x, self.ctx, None, q, s], [H, Q, 1, eps, s_o]))
             (qg, sg), (qu, su) = w["gate"], w["up"]
             calls.append(("gate/up", "nc_decode_projection", [self.h, self.x, w["g2"], qg, sg, None, qu, su],
-                          [I, H, 2, eps]))
+                          [I, H, 2, eps, s_mlp]))
             q, s = w["down"]
-            calls.append(("down", "nc_decode_projection", [self.x, self.h, None, q, s], [H, I, 1, eps]))
+            calls.append(("down", "nc_decode_projection", [self.x, self.h, None, q, s], [H, I, 1, eps, s_down]))
         return calls
 
     def _layers_reference_modes(self, m: int, past: int, cache: KVCache, pos: DeviceArray | None) -> None:
@@ -389,6 +392,29 @@ class Qwen2:
             hip.call("nc_quantize_blocks", [self.xq, self.xsb, self.xoff, x], [m, k, BLOCK])
             hip.call("nc_matmul_i8_vnni", [y, self.xq, self.xsb, self.xoff, packed, q, s, bias, residual],
                      [m, n, k, BLOCK])
+
+    def decode_schedules(self) -> tuple[int, int, int, int]:
+        """Schedules of the one-token qkv, o, gate/up and down projections (nc_decode_projection):
+        0 (the library's launch shapes), or the tuner's choices, measured on first use (so call
+        this before capturing a decode step, as generate does)."""
+        if self.tuner is None or not self.fused_decode:
+            return 0, 0, 0, 0
+        if getattr(self, "_decode_schedules", None) is None:
+            c = self.config
+            H, I, Q = c.hidden_size, c.intermediate_size, c.num_attention_heads * c.head_dim
+            if (H, I) != (896, 4864):                  # the tuned table covers the model's widths
+                self._decode_schedules = (0, 0, 0, 0)
+            else:
+                t = self.tuner.decode_schedule
+                self._decode_schedules = (t(0, self.width, H), t(1, H, Q), t(2, I, H), t(1, H, I))
+        return self._decode_schedules
+
+    def attention_schedule(self, m: int) -> int:
+        """Schedule of a prompt's attention over m rows (nc_attention): 0, or the tuner's."""
+        if self.tuner is None or m < 2:
+            return 0
+        c = self.config
+        return self.tuner.attention_schedule(m, c.num_attention_heads, c.num_key_value_heads, c.head_dim)
 
     def _projection_schedules(self, m: int) -> tuple[int, int, int, int]:
         """Schedules of the qkv, o, gate/up and down projections over m tokens:
@@ -507,6 +533,7 @@ class Qwen2:
 
         if not self.fused_decode:
             self._projection_schedules(1)          # any tuning happens now, not under capture
+        self.decode_schedules()
         hip.sync()
         replay = hip.Graph.capture(step).launch if graph else step
         for i in range(max_new_tokens - 1):

@@ -128,3 +128,20 @@ def test_problem_key_covers_shape_and_space():
     assert k1 == autotune.Autotuner.problem_key("matmul_i8_token", 512, 896, 896, list(space))
     assert k1 != autotune.Autotuner.problem_key("matmul_i8_token", 128, 896, 896, space)
     assert k1 != autotune.Autotuner.problem_key("matmul_i8_token", 512, 896, 896, space + [{"schedule": 16}])
+
+
+def test_decode_and_attention_schedule_tables(library):
+    """The decode projections' (lanes a row, waves, bytes a load) and prefill attention's rows a
+    workgroup: what the tuner searches, read from the library (no GPU)."""
+    assert hip.decode_schedule_info(896, 0, 1) == {"lanes_per_row": 8, "waves": 1, "load_bytes": 16}
+    assert hip.decode_schedule_info(4864, 1, 1) == {"lanes_per_row": 64, "waves": 4, "load_bytes": 4}
+    for kind in (0, 2):                          # an rms_norm prologue takes 1 or 4 waves
+        assert all(hip.decode_schedule_info(896, kind, s)["waves"] in (1, 4)
+                   for s in range(1, 6) if hip.decode_schedule_info(896, kind, s))
+    assert hip.decode_schedule_info(4864, 1, 4)["waves"] == 2
+    assert hip.decode_schedule_info(4864, 0, 1) is None and hip.decode_schedule_info(896, 1, 6) is None
+    assert hip.decode_schedule_info(896, 1, 0) is None
+    for s in range(1, 6):
+        shape = hip.decode_schedule_info(896, 1, s)
+        assert 896 % (shape["lanes_per_row"] * shape["load_bytes"]) == 0
+    assert [hip.attention_schedule_info(s) for s in range(6)] == [None, 2, 4, 8, 16, None]
