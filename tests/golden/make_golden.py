@@ -3,7 +3,10 @@
 Run in the build container only, where /root/reference (SpookyJumpyBeans/
 nanocompile) is mounted:
 
-    NANOCOMPILE_CACHE=_work/ncache python tests/golden/make_golden.py
+    python tests/golden/make_golden.py
+
+(the reference's compile cache goes to a fresh temporary directory unless
+NANOCOMPILE_CACHE names one)
 
 It imports the reference's package from /root/reference, builds small graphs
 with its own frontend, compiles them with its own C code generator (gcc), and
