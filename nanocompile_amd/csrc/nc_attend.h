@@ -94,6 +94,16 @@ struct ChunkLoad {
     }
 };
 
+// The maximum of a chunk's scores over the wavefront, as a butterfly of
+// nan_max would give it: scores are never -0 (s * scale + 0 is +0 for any
+// zero), so plain compares give the maximum of the finite and infinite ones,
+// and a NaN in any lane (one ballot) makes the result NaN.
+__device__ __forceinline__ float scores_max(float s) {
+    float m = butterfly<64>(s, [](float a, float b) { return a < b ? b : a; });
+    m = lane_value(m, 0);
+    return __ballot(s != s) ? __builtin_nanf("") : m;
+}
+
 struct ChunkResult {
     float m, l, o;    // the chunk's max and sum (every lane), and o[d] in lane d
 };
@@ -121,9 +131,7 @@ __device__ __forceinline__ void chunk_scores(const float *q, const Staged<D> &st
         acc = __builtin_fmaf(qi.w, k.w, acc);
     }
     const float s = lane < n ? __fadd_rn(__fmul_rn(acc, scale), 0.0f) : -__builtin_inff();
-    // (scores are never -0, so nan_max commutes up to which NaN propagates)
-    float m = butterfly<64>(s, [](float a, float b) { return nan_max(a, b); });
-    m = lane_value(m, 0);
+    const float m = scores_max(s);
     const float pt = nc_expf(__fsub_rn(s, m));       // exp(-inf) = 0 for lanes past the chunk
     l_out = wave_sum_f32(pt);
     m_out = m;
@@ -189,8 +197,7 @@ __device__ __forceinline__ void chunk_scores_n(float (*qp)[kChunk], const Staged
 #pragma unroll
     for (int u = 0; u < H; ++u) {
         const float s = lane < n ? __fadd_rn(__fmul_rn(acc[u], scale), 0.0f) : -__builtin_inff();
-        float mu = butterfly<64>(s, [](float a, float b) { return nan_max(a, b); });
-        mu = lane_value(mu, 0);
+        const float mu = scores_max(s);
         const float pt = nc_expf(__fsub_rn(s, mu));
         l[u] = wave_sum_f32(pt);
         m[u] = mu;

@@ -66,6 +66,17 @@ __device__ __forceinline__ i8x16 load16_stream(const int8_t *p) {
 // xor 4 takes row_ror:4 into the banks of lanes with bit 2 set (source
 // lane - 4) and row_ror:12 into the others (source lane + 4); xor 2 and xor 1
 // are quad permutations.
+// With every row and bank enabled and a source lane for every lane (the
+// rotations and quad permutations here), a DPP move never keeps its old
+// value: mov_dpp leaves it undefined, so the compiler can fold the move into
+// the instruction that uses it (v_add_f32_dpp and the like). The xor-4
+// partner writes half the banks in each of two moves, so the first move's
+// result is the second's old value.
+template <int CTRL>
+__device__ __forceinline__ int32_t dpp_all(int32_t v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+
 template <int CTRL, int BANKS>
 __device__ __forceinline__ int32_t dpp_mov(int32_t old, int32_t v) {
     return __builtin_amdgcn_update_dpp(old, v, CTRL, 0xF, BANKS, false);
@@ -74,10 +85,10 @@ __device__ __forceinline__ int32_t dpp_mov(int32_t old, int32_t v) {
 template <int OFF>
 __device__ __forceinline__ int32_t xor_partner(int32_t v) {
     static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8, "DPP partners within a row of 16");
-    if constexpr (OFF == 1) return dpp_mov<0xB1, 0xF>(v, v);          // quad_perm [1, 0, 3, 2]
-    else if constexpr (OFF == 2) return dpp_mov<0x4E, 0xF>(v, v);     // quad_perm [2, 3, 0, 1]
+    if constexpr (OFF == 1) return dpp_all<0xB1>(v);                  // quad_perm [1, 0, 3, 2]
+    else if constexpr (OFF == 2) return dpp_all<0x4E>(v);             // quad_perm [2, 3, 0, 1]
     else if constexpr (OFF == 4) return dpp_mov<0x12C, 0x5>(dpp_mov<0x124, 0xA>(v, v), v);
-    else return dpp_mov<0x128, 0xF>(v, v);                            // row_ror:8
+    else return dpp_all<0x128>(v);                                    // row_ror:8
 }
 
 template <int OFF>

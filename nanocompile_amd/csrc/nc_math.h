@@ -36,17 +36,20 @@ NC_MATH_FN double nc_pow2i(int k) {
 
 NC_MATH_FN double nc_nearest(double x) {
     // Round to nearest integer, ties away from zero (which tie does not matter
-    // here: either neighbour keeps |r| within the polynomial's range).
-    double t = (double)(int64_t)(x + (x >= 0.0 ? 0.5 : -0.5));
-    return t;
+    // here: either neighbour keeps |r| within the polynomial's range). trunc
+    // is the conversion to int64 and back for every |x| < 2^63, in one
+    // instruction on the GPU rather than an emulated 64-bit conversion.
+    return __builtin_trunc(x + (x >= 0.0 ? 0.5 : -0.5));
 }
 
 NC_MATH_FN float nc_expf(float xf) {
-    if (xf != xf) return xf;                       // NaN
-    if (xf > 100.0f) return (float)(1e300 * 1e300);    // past FLT_MAX: +inf (up to 100 the
-                                                        // double result rounds to inf itself)
-    if (xf < -104.0f) return 0.0f;                 // below half the least subnormal
-    const double x = (double)xf;
+    // The special cases are chosen at the end, so the GPU runs one straight
+    // path with no divergent branch; their operand is replaced by 0 first.
+    const int nan = xf != xf;
+    const int big = xf > 100.0f;                   // past FLT_MAX: +inf (up to 100 the
+                                                   // double result rounds to inf itself)
+    const int tiny = xf < -104.0f;                 // below half the least subnormal: 0
+    const double x = (nan | big | tiny) ? 0.0 : (double)xf;
     const double inv_ln2 = 1.4426950408889634;
     const double ln2_hi = 6.93147180369123816490e-01;   // 33 significant bits: k * ln2_hi is exact
     const double ln2_lo = 1.90821492927058770002e-10;
@@ -69,7 +72,8 @@ NC_MATH_FN float nc_expf(float xf) {
     p = p * r + 1.0;
     const int ki = (int)k;
     // 2^k may be subnormal in float but never in double (k >= -150)
-    return (float)(p * nc_pow2i(ki));
+    const float y = (float)(p * nc_pow2i(ki));
+    return nan ? xf : big ? (float)(1e300 * 1e300) : tiny ? 0.0f : y;
 }
 
 // sin(r) and cos(r) for |r| <= pi/4 + a little, Taylor to r^17 / r^18
