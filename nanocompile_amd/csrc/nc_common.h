@@ -68,13 +68,14 @@ __device__ __forceinline__ i8x16 load16_stream(const int8_t *p) {
 // are quad permutations.
 // With every row and bank enabled and a source lane for every lane (the
 // rotations and quad permutations here), a DPP move never keeps its old
-// value: mov_dpp leaves it undefined, so the compiler can fold the move into
-// the instruction that uses it (v_add_f32_dpp and the like). The xor-4
-// partner writes half the banks in each of two moves, so the first move's
-// result is the second's old value.
+// value and never reads an invalid lane, so neither the old value nor
+// bound_ctrl changes the result; mov_dpp with bound_ctrl set is the form the
+// compiler folds into the instruction that uses it (v_add_f32_dpp and the
+// like). The xor-4 partner writes half the banks in each of two moves, so the
+// first move's result is the second's old value.
 template <int CTRL>
 __device__ __forceinline__ int32_t dpp_all(int32_t v) {
-    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
 }
 
 template <int CTRL, int BANKS>
