@@ -371,6 +371,41 @@ def decode_kernel_table(model, cache, past: int) -> dict:
     return table
 
 
+def decode_kernels(reps: int = 3, seed: int = 0) -> dict:
+    """Each kernel of config 5's decode step at its last position (past 383), launched eagerly over
+    the 24 layers' weights ``reps`` times, with no decode loop and no graph: the run rocprofv3's
+    counter passes (FETCH_SIZE, WRITE_SIZE) profile for each kernel's HBM traffic. Returns each
+    kernel's mean launch time from events around the eager launches."""
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import Event
+    from nanocompile_amd.kernels import float_bits
+    from nanocompile_amd.models.config import QWEN25_05B, random_weights
+    from nanocompile_amd.models.qwen2 import Qwen2
+
+    config = QWEN25_05B
+    model = Qwen2(config, random_weights(config, seed=seed), max_tokens=PROMPT)
+    cache = model.new_cache(PROMPT + NEW_TOKENS)
+    past = PROMPT + NEW_TOKENS - 2
+    groups: dict[str, list] = {}
+    for label, name, pointers, sizes in model.decode_layer_calls(cache, past):
+        groups.setdefault(label, []).append((name, pointers, sizes))
+    c = config
+    groups["lm head"] = [("nc_lm_head", [None, model.best, model.normed, model.head, model.norm],
+                          [1, c.vocab_size, c.hidden_size, float_bits(c.rms_norm_eps), 1])]
+    out = {}
+    for label, calls in groups.items():
+        a, b = Event(), Event()
+        a.record()
+        for _ in range(reps):
+            for call in calls:
+                hip.call(*call)
+        b.record()
+        hip.sync()
+        out[label] = {"kernel": KERNEL_SYMBOLS[label], "launch_us": round(a.elapsed_ms(b) * 1e3 / (reps * len(calls)), 3),
+                      "bytes_per_launch": decode_kernel_bytes(label, past), "launches": reps * len(calls)}
+    return out
+
+
 def cpu_decode(config, weights, prompt, gpu_tokens, seconds: float = 16.0) -> dict:
     """The host C int8 model (oracle/nc_model.c) on this machine's cores: every token checked
     against the GPU's, then a thread sweep of decode steps at the config's positions."""
@@ -467,7 +502,8 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=NEW_TOKENS - 1)
     parser.add_argument("--warmup", type=int, default=1)
-    parser.add_argument("--workload", choices=("decode", "gemv"), default="decode")
+    parser.add_argument("--workload", choices=("decode", "gemv", "kernels"), default="decode",
+                        help="kernels: each decode-step kernel launched eagerly at past 383 (for counter passes)")
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-blocks", action="store_true", help="skip the per-block measurements (configs 2-4)")
     parser.add_argument("--no-graph", action="store_true",
@@ -488,6 +524,10 @@ def main() -> int:
     hip.sync()
     del src, dst
 
+    if args.workload == "kernels":
+        print(json.dumps({"workload": "config 5's decode-step kernels, eager, past 383",
+                          "kernels": decode_kernels()}), flush=True)
+        return 0
     g = gpu_gemv(20 if args.workload == "decode" else args.steps, 3)
     log(f"gemv: stacked {g['stacked_gbps']:.0f} GB/s, single {g['single_us']:.2f} us")
     gemv_record = {"stacked_gbps": round(g["stacked_gbps"], 1), "frac": round(g["stacked_gbps"] / HBM_PEAK_GBPS, 4),
