@@ -96,6 +96,34 @@ def test_prefill_and_decode_attention_agree(gpu, host, d, heads, kv, slab):
     assert np.array_equal(bits(dk.numpy()), bits(hk))
 
 
+@pytest.mark.parametrize("d,heads,kv,m,past", [(64, 14, 2, 512, 0), (64, 14, 2, 130, 70), (64, 4, 2, 37, 5),
+                                                (64, 8, 1, 66, 0), (64, 18, 2, 40, 30), (32, 4, 2, 33, 64)])
+def test_every_prefill_schedule_is_the_oracle(gpu, host, d, heads, kv, m, past):
+    """Each prefill schedule (2, 4, 8 or 16 rows a chunk workgroup) gives the oracle's bits, in one
+    pass and with a small workspace taking the rows in slabs."""
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import DeviceArray
+    from nanocompile_amd.kernels import float_bits
+    rng = np.random.default_rng(m + heads + past)
+    cap = past + m
+    qkv, kc, vc = setup(rng, heads, kv, d, cap, m)
+    inv = inverse_frequencies(d, 1e6)
+    scale = float(np.float32(d ** -0.5))
+    hq, hk, hv = qkv.copy(), kc.copy(), vc.copy()
+    expected = host.rope_append_attention(hq, hk, hv, inv, heads, kv, d, past, scale)
+    dq, dk, dv = DeviceArray.from_host(qkv), DeviceArray.from_host(kc), DeviceArray.from_host(vc)
+    dinv, ctx = DeviceArray.from_host(inv), DeviceArray((m, heads * d), np.float32)
+    hip.call("nc_rope_append", [dq, dk, dv, dinv], [m, heads, kv, d, past, cap])
+    for slab in (None, 11):
+        work, nbytes = workspace(heads, d, slab or m, past + m)
+        for schedule in range(5):
+            print(f"prefill schedule {schedule} d={d} heads={heads}/{kv} m={m} past={past} slab={slab}", flush=True)
+            ctx.upload(np.full((m, heads * d), np.nan, np.float32))
+            hip.call("nc_attention", [ctx, dq, dk, dv, None, work],
+                     [m, heads, kv, d, past, cap, float_bits(scale), nbytes, schedule])
+            assert np.array_equal(bits(ctx.numpy()), bits(expected)), (schedule, slab)
+
+
 def test_decode_attention_in_a_graph_at_advancing_positions(gpu, host):
     from nanocompile_amd import hip
     from nanocompile_amd.hip import DeviceArray, Graph
