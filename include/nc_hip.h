@@ -265,7 +265,8 @@ int32_t nc_rope_append(void **p, const int64_t *s);
  * cache's table, in one launch on MFMA tiles one head wide.
  * p: [qkv f32[M,W] (out), xq i8[M,K], xs f32[M], q i8[W,K], scales f32[W], bias f32[W] or NULL,
  *     kcache f32[kv,C,D], vcache f32[kv,C,D], rope table f32[2,C,D/2], pos i64[1] or NULL];
- * s: [M, W, K, heads, kv, D, past, C] (W = (heads + 2*kv)*D, D 32 or 64, K a multiple of 16) */
+ * s: [M, W, K, heads, kv, D, past, C, schedule] (W = (heads + 2*kv)*D, D 32 or 64, K a multiple
+ *    of 16; schedule 0 the library's tile, or an MFMA tile 16..24 whose n is one head) */
 int32_t nc_matmul_i8_token_rope(void **p, const int64_t *s);
 
 /* Grouped-query attention of each new row over the cache, causal

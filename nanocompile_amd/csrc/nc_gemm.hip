@@ -54,6 +54,7 @@ struct RopeArgs {
     const int64_t *pos;                // the position of row 0, or NULL: past
     int32_t *error;
     int heads, kv, past, capacity;
+    int head_dim;                      // the tile's n must equal it: the epilogue takes a tile as one head
 };
 
 struct GemmArgs {
@@ -445,6 +446,10 @@ int32_t gemm_i8_token(int tile, int epi, void *out, const int8_t *xq, const floa
 template <int BM, int BN, int BK, int WM, int WN, int NS>
 int32_t launch_rope_tile(const GemmArgs &a) {
     if constexpr (BN == 32 || BN == 64) {
+        if (a.rope.head_dim != BN) {        // the epilogue's head index is n / BN: BN must be the head
+            set_message("nc_matmul_i8_token_rope: the tile is not one head wide");
+            return NC_BAD_ARGS;
+        }
         return launch_tile<BM, BN, BK, WM, WN, NS, kRope>(a);
     } else {
         set_message("nc_matmul_i8_token_rope: the tile is not one head wide");
@@ -482,15 +487,21 @@ int32_t gemm_tile_info(int tile, int64_t *out) {
 
 }  // namespace nc
 
+// The schedule numbers of the MFMA tiles (nc_gemv.hip's space: 16 + tile index).
+constexpr int64_t kGemmFirstSchedule = 16, kGemmTileCount = 9;
+
 // The qkv projection of a prompt with RoPE and the KV-cache append fused into
 // its epilogue: the bits of nc_matmul_i8_token (bias, no residual) followed by
 // nc_rope_append with the cache's table (q rotated in place; k rotated and v
 // copied into the cache at positions past + i; k and v left in qkv as
 // projected), in one launch. The tile is one head wide: 64 x 64 when that
-// gives 144 tiles or more, else 32 x 64 (head_dim 64); 32 x 32 (head_dim 32).
+// gives 576 tiles or more, else 32 x 64 (head_dim 64); 32 x 32 (head_dim 32).
+// (Measured on MI355X, Qwen2.5-0.5B's qkv, 32 x 64 against 64 x 64: M = 128
+// 5.00 / 6.73 us, 512 6.53 / 7.13, 1024 8.37 / 8.66, 2048 11.78 / 11.40.)
 // p: [qkv f32[M,W] (out), xq i8[M,K], xs f32[M], q i8[W,K], scales f32[W], bias f32[W] | NULL,
 //     kcache f32[kv,C,D], vcache f32[kv,C,D], rope table f32[2,C,D/2], pos i64[1] | NULL];
-// s: [M, W, K, heads, kv, D, past, C]  (W = (heads + 2 kv) D, D 32 or 64, K a multiple of 16)
+// s: [M, W, K, heads, kv, D, past, C, schedule]  (W = (heads + 2 kv) D, D 32 or 64, K a multiple of 16;
+//    schedule 0 the library's tile, or an MFMA tile 16..24 one head wide)
 NC_EXPORT int32_t nc_matmul_i8_token_rope(void **p, const int64_t *s) {
     NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3] && p[4] && p[6] && p[7] && p[8],
                "nc_matmul_i8_token_rope: null operand");
@@ -500,12 +511,16 @@ NC_EXPORT int32_t nc_matmul_i8_token_rope(void **p, const int64_t *s) {
                    heads % kv == 0 && (D == 32 || D == 64) && W == (heads + 2 * kv) * D && C > 0 &&
                    C < (1 << 24) && (pos || (past >= 0 && past + M <= C)),
                "nc_matmul_i8_token_rope: bad shape (W = (heads + 2 kv) D, D 32 or 64, past + M <= C)");
+    const int64_t schedule = s[8];
+    NC_REQUIRE(schedule == 0 || (schedule >= kGemmFirstSchedule && schedule < kGemmFirstSchedule + kGemmTileCount),
+               "nc_matmul_i8_token_rope: no such schedule (0, or an MFMA tile 16..24 one head wide)");
     if (M == 0) return NC_OK;
     int tile = 2;
-    if (D == 64) tile = ((M + 63) / 64) * (W / 64) >= 144 ? 5 : 1;
+    if (D == 64) tile = ((M + 63) / 64) * (W / 64) >= 576 ? 5 : 1;
+    if (schedule) tile = (int)(schedule - kGemmFirstSchedule);
     GemmArgs a{p[0], (const int8_t *)p[1], (const float *)p[2], (const int8_t *)p[3], (const float *)p[4],
                (const float *)p[5], nullptr, nullptr, nullptr, (int)M, (int)W, (int)K};
     a.rope = RopeArgs{(float *)p[6], (float *)p[7], (const float *)p[8], pos, nc::error_word(), (int)heads,
-                      (int)kv, pos ? 0 : (int)past, (int)C};
+                      (int)kv, pos ? 0 : (int)past, (int)C, (int)D};
     return nc::gemm_i8_token_rope(tile, a);
 }

@@ -249,7 +249,7 @@ class DeviceArray:
         return DeviceArray(shape, dtype, self.ptr + offset_bytes, owner=self)
 
     def __del__(self) -> None:
-        if self._owner is True and _LIB is not None:
+        if getattr(self, "_owner", None) is True and _LIB is not None:
             _LIB.nc_free(self.ptr)
             self._owner = None
 

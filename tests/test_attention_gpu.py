@@ -270,7 +270,8 @@ def test_prefill_attention_quantizes_ctx_per_token(gpu, host, d, heads, kv, m, p
 def test_qkv_projection_with_rope_is_projection_then_rope_append(gpu, heads, kv, d, k, m, past):
     """nc_matmul_i8_token_rope (RoPE and the cache append in the GEMM's epilogue) leaves qkv and
     both caches bit for bit as nc_matmul_i8_token followed by nc_rope_append with the table does,
-    with the position from the host and from the device."""
+    with the position from the host and from the device, under the library's tile and every MFMA
+    tile one head wide."""
     from nanocompile_amd import hip
     from nanocompile_amd.hip import DeviceArray
     print(f"qkv rope epilogue heads={heads} d={d} m={m} past={past}", flush=True)
@@ -289,23 +290,24 @@ def test_qkv_projection_with_rope_is_projection_then_rope_append(gpu, heads, kv,
     hip.call("nc_rope_table", [table, DeviceArray.from_host(inv)], [cap, d])
     dxq, dxs, dq, dqs, db = (DeviceArray.from_host(a) for a in (xq, xs, q, qs, bias))
     pos = DeviceArray.from_host(np.array([past], np.int64))
+    schedules = [0] + [sch for sch in range(16, 25) if hip.schedule_info(sch)["tile_n"] == d]
     for use_pos in (False, True):
-        outs = []
-        for fused in (False, True):
+        p = pos if use_pos else None
+        host_past = 0 if use_pos else past
+        qkv = DeviceArray((m, w), np.float32)
+        kc, vc = DeviceArray.from_host(kc0), DeviceArray.from_host(vc0)
+        hip.call("nc_matmul_i8_token", [qkv, dxq, dxs, dq, dqs, db, None], [m, w, k, 0])
+        hip.call("nc_rope_append", [qkv, kc, vc, DeviceArray.from_host(inv), p, table],
+                 [m, heads, kv, d, host_past, cap])
+        expected = (qkv.numpy(), kc.numpy(), vc.numpy())
+        for schedule in schedules:
+            print(f"  schedule {schedule} position from the {'device' if use_pos else 'host'}", flush=True)
             qkv = DeviceArray((m, w), np.float32)
             kc, vc = DeviceArray.from_host(kc0), DeviceArray.from_host(vc0)
-            p = pos if use_pos else None
-            host_past = 0 if use_pos else past
-            if fused:
-                hip.call("nc_matmul_i8_token_rope", [qkv, dxq, dxs, dq, dqs, db, kc, vc, table, p],
-                         [m, w, k, heads, kv, d, host_past, cap])
-            else:
-                hip.call("nc_matmul_i8_token", [qkv, dxq, dxs, dq, dqs, db, None], [m, w, k, 0])
-                hip.call("nc_rope_append", [qkv, kc, vc, DeviceArray.from_host(inv), p, table],
-                         [m, heads, kv, d, host_past, cap])
-            outs.append((qkv.numpy(), kc.numpy(), vc.numpy()))
-        for a, b in zip(*outs):
-            assert np.array_equal(bits(a), bits(b)), use_pos
+            hip.call("nc_matmul_i8_token_rope", [qkv, dxq, dxs, dq, dqs, db, kc, vc, table, p],
+                     [m, w, k, heads, kv, d, host_past, cap, schedule])
+            for a, b in zip((qkv.numpy(), kc.numpy(), vc.numpy()), expected):
+                assert np.array_equal(bits(a), bits(b)), (use_pos, schedule)
 
 
 def test_qkv_projection_with_rope_rejects_bad_shapes(gpu):
@@ -320,3 +322,10 @@ def test_qkv_projection_with_rope_rejects_bad_shapes(gpu):
         hip.call("nc_matmul_i8_token_rope", [x, x, x, x, x, None, x, x, x], [4, 1152, 896, 14, 2, 64, 6, 8])
     with pytest.raises(hip.KernelError, match="null operand"):     # no table
         hip.call("nc_matmul_i8_token_rope", [x, x, x, x, x, None, x, x, None], [4, 1152, 896, 14, 2, 64, 0, 8])
+    # tiles whose n is not one head (the epilogue rotates a tile as a head) are refused before launch
+    for schedule, d in ((18, 64), (19, 64), (22, 64), (23, 64), (16, 32), (22, 32)):
+        width = (14 + 2 * 2) * d
+        with pytest.raises(hip.KernelError, match="not one head wide"):
+            hip.call("nc_matmul_i8_token_rope", [x, x, x, x, x, None, x, x, x], [4, width, 896, 14, 2, d, 0, 8, schedule])
+    with pytest.raises(hip.KernelError, match="no such schedule"):
+        hip.call("nc_matmul_i8_token_rope", [x, x, x, x, x, None, x, x, x], [4, 1152, 896, 14, 2, 64, 0, 8, 25])
