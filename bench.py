@@ -54,6 +54,7 @@ import os
 import statistics
 import sys
 import time
+from pathlib import Path
 
 import numpy as np
 
@@ -196,6 +197,73 @@ def cpu_gemv(seconds: float = 6.0, seed: int = 0) -> dict:
             "isa": host.isa(), "cores": cores}
 
 
+def cpu_blocks(seconds: float = 12.0, seed: int = 7) -> dict:
+    """Configs 2-4 on the host C path (oracle/nc_host.c, oracle/nc_model.c: the build's own C, the
+    reference having no per-token int8 mode), on this machine's cores. Config 2: rms_norm -> int8
+    of 512 rows (the host row kernel runs on one thread). Configs 3 and 4: one Qwen2.5-0.5B-shaped
+    decoder block as a one-layer host model whose tied head has 64 rows (0.2 MB beside the block's
+    15 MB), a decode step at past 512 and a 512-token prefill, threads swept."""
+    import dataclasses
+    from oracle import host
+    from oracle.host_model import HostQwen2
+    from nanocompile_amd.models.config import QWEN25_05B, random_weights
+    cores = os.cpu_count() or 1
+    counts = sorted({1, 2, 4, 8, 16, min(cores, 64)} & set(range(1, min(cores, 64) + 1)))
+    rng = np.random.default_rng(seed)
+    c = QWEN25_05B
+    x = rng.standard_normal((512, c.hidden_size)).astype(np.float32)
+    x[rng.random(x.shape) < 0.01] *= 20
+    gamma = (1 + 0.1 * rng.standard_normal(c.hidden_size)).astype(np.float32)
+    t0, reps = time.perf_counter(), 0
+    while reps < 3 or time.perf_counter() - t0 < 1.0:
+        host.rms_norm_quant(x, gamma, c.rms_norm_eps)
+        reps += 1
+    rms_us = (time.perf_counter() - t0) / reps * 1e6
+
+    one = dataclasses.replace(c, num_hidden_layers=1, vocab_size=64)
+    past = 512
+    model = HostQwen2(one, random_weights(one, seed=seed), capacity=past + 8)
+    model.kcache[...] = rng.standard_normal(model.kcache.shape).astype(np.float32)
+    model.vcache[...] = rng.standard_normal(model.vcache.shape).astype(np.float32)
+    prompt = rng.integers(0, one.vocab_size, 512)
+
+    def timed(run, budget: float) -> float:
+        run()                                   # the pool's threads up, caches warm
+        t, n = time.perf_counter(), 0
+        while n < 2 or time.perf_counter() - t < budget:
+            run()
+            n += 1
+        return (time.perf_counter() - t) / n
+
+    decode_us, prefill_us = {}, {}
+    for t in counts:
+        host.set_threads(t)
+
+        def step():
+            model.length = past
+            model.forward([7])
+
+        def prompt_pass():
+            model.length = 0
+            model.forward(prompt)
+
+        decode_us[t] = timed(step, seconds / 3 / len(counts)) * 1e6
+        prefill_us[t] = timed(prompt_pass, seconds / 2 / len(counts)) * 1e6
+    bd, bp = min(decode_us, key=decode_us.get), min(prefill_us, key=prefill_us.get)
+    return {"cores": cores, "isa": host.isa(),
+            "rms_norm_quant_512": {"us": round(rms_us, 2), "threads": 1,
+                                   "gbps": round(rms_row_bytes(512) / (rms_us * 1e-6) / 1e9, 2)},
+            "block_decode": {"past": past, "us": round(decode_us[bd], 1), "threads": bd,
+                             "gbps": round(BLOCK_DECODE_BYTES / (decode_us[bd] * 1e-6) / 1e9, 2),
+                             "by_threads_us": {str(k): round(v, 1) for k, v in decode_us.items()}},
+            "block_prefill": {"seq": 512, "us": round(prefill_us[bp], 1), "threads": bp,
+                              "tok_s": round(512 / (prefill_us[bp] * 1e-6), 1),
+                              "by_threads_us": {str(k): round(v, 1) for k, v in prefill_us.items()}},
+            "sample": "config 2: 512 rows repeated for a second; configs 3 and 4: a one-layer host model "
+                      "(the block, a 64-row head), each thread count timed for a bounded share of "
+                      f"{seconds:.0f} s"}
+
+
 # -- configs 2-4: the fused row kernel, one block's decode step, one block's prefill ----------
 
 MFMA_I8_PEAK_TOPS = 5000.0          # MI355X dense int8 MFMA, 5.0 POP/s
@@ -260,7 +328,27 @@ def block_measurements(model, seed: int = 7) -> dict:
         us = graph_us(lambda i: hip.call("nc_rms_norm_quant", [normed, xq, xs, xd, gamma], [m, H, eps]), 32)
         rows[str(m)] = {"us": round(us, 3), "bytes": rms_row_bytes(m, H),
                         "gbps": round(rms_row_bytes(m, H) / (us * 1e-6) / 1e9, 1)}
-    out["rms_norm_quant"] = {"kernel": "rms_norm_quant (one pass: normed f32, int8 row, scale)", "rows": rows}
+    # the same rows through the reference's own compilation of config 2's graph (rms_norm, then one
+    # int8 scale per row, in its graph ops), recorded from the reference as data
+    # (tests/golden/programs.json.gz) and generated as HIP by codegen_hip: unfused (its lowering with
+    # fuse=False, a kernel per operation, runtime.py:186) and fused (its fusion pass)
+    from nanocompile_amd import lir
+    from nanocompile_amd.compiled import CompiledProgram
+    golden = Path(__file__).resolve().parent / "tests" / "golden"
+    doc = lir.load_programs(golden / "programs.json.gz")
+    with np.load(golden / "programs.npz", allow_pickle=False) as arrays:
+        generated = {variant: CompiledProgram(lir.program_from_json(doc["zoo"]["rms_norm_quant"][key], arrays))
+                     for variant, key in (("unfused", "unfused"), ("fused", "program"))}
+    gamma_host = gamma.numpy()
+    for m in (1, 64, 512):
+        x = rng.standard_normal((m, H)).astype(np.float32)
+        for variant, program in generated.items():
+            launch, _, _ = program.prepare({"x": x}, {"w": gamma_host})
+            us = graph_us(lambda i, launch=launch: launch(), 32)
+            rows[str(m)][f"generated_{variant}"] = {"us": round(us, 3), "kernels": len(program.program.calls)}
+    out["rms_norm_quant"] = {"kernel": "rms_norm_quant (one pass: normed f32, int8 row, scale)", "rows": rows,
+                             "generated": "the reference's program for the same graph, lowered to HIP by "
+                                          "codegen_hip (unfused: a kernel per operation; fused: its fusion)"}
 
     # config 3: one decoder block's decode step at past = 512 (all 24 blocks replayed, per block)
     past = 512
@@ -569,6 +657,7 @@ def main() -> int:
         f"{NEW_TOKENS - 1}; time-dominant kernel {dominant}: {top['step_us']:.1f} us a step")
     cpu = d.get("cpu")
     cpu_g = None if args.no_cpu else cpu_gemv(seconds=8.0)
+    cpu_b = None if args.no_cpu else cpu_blocks()
     step_gbps = d["step_bytes"] * d["tok_s"] / 1e9
     record = {
         "metric": "decode tok/s, Qwen2-0.5B-shape int8 on 1 MI355X",
@@ -618,7 +707,8 @@ def main() -> int:
                 "value": round(cpu_g["gbps"], 2), "unit": "GB/s", "threads": cpu_g["threads"],
                 "by_threads": cpu_g["by_threads"], "isa": cpu_g["isa"],
                 "all_cores_gbps": cpu_g["by_threads"][str(max(map(int, cpu_g["by_threads"])))],
-                "sample": "config 1's GEMV over 240 rotated weight copies (1 GB, past the host's LLC)"}},
+                "sample": "config 1's GEMV over 240 rotated weight copies (1 GB, past the host's LLC)"},
+            "blocks": cpu_b},
     }
     print(json.dumps(record), flush=True)
     return 0

@@ -280,6 +280,25 @@ class CompiledProgram:
                  bindings: Mapping[str, int] | None = None, profile: dict | None = None) -> dict[str, np.ndarray]:
         """Run the program (runtime.py:245-301). ``profile``, if given, accumulates each
         primitive's seconds (each launch then waits for its kernel)."""
+        launch, bound, addresses = self.prepare(inputs, weights, bindings)
+        launch(profile=profile, inputs=inputs)
+        self._wait(inputs, bound)
+        lib = hip.load()
+        outputs = {}
+        for name, buf in self.program.outputs.items():
+            out = np.empty(lir.shape_of(buf.shape, bound), buf.dtype.numpy)
+            if out.nbytes:
+                hip._check(lib.nc_memcpy_d2h(out.ctypes.data, addresses[buf], out.nbytes), "nc_memcpy_d2h")
+            outputs[name] = out
+        return outputs
+
+    def prepare(self, inputs: Mapping[str, np.ndarray], weights: Mapping[str, np.ndarray],
+                bindings: Mapping[str, int] | None = None):
+        """One call's arguments checked, its buffers placed in the arena and its inputs uploaded;
+        returns ``(launch, bound, addresses)``: ``launch()`` enqueues the program's kernels on the
+        library stream and returns without waiting (no copies: it can be replayed, or captured
+        in a graph, to time the kernels alone), ``bound`` the symbols' values, ``addresses`` each
+        buffer's device address (the outputs are read from there)."""
         program = self.program
         bound = self.bind(inputs, weights, bindings)
         syms = (ctypes.c_int64 * max(1, len(self.symbols)))(*[bound[s] for s in self.symbols])
@@ -303,7 +322,7 @@ class CompiledProgram:
             if array.nbytes:
                 hip._check(lib.nc_memcpy_h2d_async(addresses[buf], array.ctypes.data, array.nbytes),
                            "nc_memcpy_h2d_async")
-
+        launches = []
         for c, call in enumerate(program.calls):
             pointers = [addresses[call.output]]
             for i, view in enumerate(call.operands):
@@ -313,24 +332,20 @@ class CompiledProgram:
                     continue
                 offset = lir.evaluate(view.offset, bound) * view.dtype.numpy.itemsize
                 pointers.append(addresses[view.buffer] + offset)
-            args = (ctypes.c_void_p * len(pointers))(*pointers)
-            started = time.perf_counter() if profile is not None else 0.0
-            status = self._launch[call.kernel](args, syms)
-            if status != 0:
-                raise KernelError(f"kernel for node %{call.node} ({call.primitive}) could not be launched "
-                                  f"({status}): {hip.last_error()}")
-            if profile is not None:
-                self._wait(inputs, bound)
-                profile[call.primitive] = profile.get(call.primitive, 0.0) + time.perf_counter() - started
-        self._wait(inputs, bound)
+            launches.append((call, (ctypes.c_void_p * len(pointers))(*pointers)))
 
-        outputs = {}
-        for name, buf in program.outputs.items():
-            out = np.empty(lir.shape_of(buf.shape, bound), buf.dtype.numpy)
-            if out.nbytes:
-                hip._check(lib.nc_memcpy_d2h(out.ctypes.data, addresses[buf], out.nbytes), "nc_memcpy_d2h")
-            outputs[name] = out
-        return outputs
+        def launch(profile: dict | None = None, inputs=inputs) -> None:
+            for call, args in launches:
+                started = time.perf_counter() if profile is not None else 0.0
+                status = self._launch[call.kernel](args, syms)
+                if status != 0:
+                    raise KernelError(f"kernel for node %{call.node} ({call.primitive}) could not be launched "
+                                      f"({status}): {hip.last_error()}")
+                if profile is not None:
+                    self._wait(inputs, bound)
+                    profile[call.primitive] = profile.get(call.primitive, 0.0) + time.perf_counter() - started
+
+        return launch, bound, addresses
 
     def _wait(self, inputs, bound) -> None:
         status = hip.load().nc_sync()
