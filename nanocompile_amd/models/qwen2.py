@@ -28,10 +28,13 @@ is the reference's float32 model (``quantization=None``): every projection
 is its float32 matmul kernel's order (k in order, multiply then add, then +
 bias), which is the LM head's kernel over a packed table (nc_lm_head).
 
-Memory: the weights go into one device arena, made once; activations for up
-to ``max_tokens`` new tokens into a second, also made once; the KV cache is a
-device array per sequence (``new_cache``), so a decode step moves nothing but
-a token id in and (optionally) a row of logits out.
+Memory: one device arena per model (one hipMalloc, made once): the weights,
+then the activations for up to ``max_tokens`` new tokens; and one per sequence
+(``new_cache``, the caller's, as the reference's KVCache is): keys, values,
+RoPE's table, attention's workspace and a device-driven decode's token
+history and position. A decode step moves nothing but a token id in and
+(optionally) a row of logits out. (A checkpoint with an untied LM head is
+uploaded once more, temporarily, to be packed.)
 """
 
 from __future__ import annotations
@@ -102,19 +105,27 @@ class KVCache:
                              f"kernels' limit on keys)")
         self.config, self.capacity, self.length = config, capacity, 0
         shape = (config.num_hidden_layers, config.num_key_value_heads, capacity, config.head_dim)
-        self.keys, self.values = DeviceArray(shape, np.float32), DeviceArray(shape, np.float32)
-        self._layer = config.num_key_value_heads * capacity * config.head_dim * 4
-        # cos and sin of every position's RoPE angles (nc_rope_table), for the
-        # decode attention kernel: the same bits it would compute, one lookup
         D = config.head_dim
-        self.rope = DeviceArray((2, capacity, D // 2), np.float32)
-        inv = DeviceArray.from_host(inverse_frequencies(D, config.rope_theta))
-        hip.call("nc_rope_table", [self.rope, inv], [capacity, D])
         # attention's chunk results (nc_attention, nc_attention_decode): every
         # query row of a prompt up to 64 MiB, longer prompts in slabs
         per_row = attention_workspace_bytes(config.num_attention_heads, D, 1, capacity)
         self.work_bytes = per_row * max(1, min(capacity, WORKSPACE_BYTES // per_row))
-        self.work = DeviceArray((self.work_bytes // 4,), np.float32)
+        # One hipMalloc for the sequence: keys, values, RoPE's table, the attention
+        # workspace, and a device-driven decode's token history and position.
+        parts = [(shape, np.float32), (shape, np.float32), ((2, capacity, D // 2), np.float32),
+                 ((self.work_bytes // 4,), np.float32), ((capacity,), np.int64), ((1,), np.int64),
+                 ((D // 2,), np.float32)]
+        self.arena = Arena(Arena.size(parts))
+        self.keys, self.values = self.arena.take(shape, np.float32), self.arena.take(shape, np.float32)
+        self._layer = config.num_key_value_heads * capacity * D * 4
+        # cos and sin of every position's RoPE angles (nc_rope_table), for the
+        # decode attention kernel: the same bits it would compute, one lookup
+        self.rope = self.arena.take((2, capacity, D // 2), np.float32)
+        self.work = self.arena.take((self.work_bytes // 4,), np.float32)
+        self.tokens, self.position = self.arena.take((capacity,), np.int64), self.arena.take((1,), np.int64)
+        inv = self.arena.take((D // 2,), np.float32)
+        inv.upload(inverse_frequencies(D, config.rope_theta))
+        hip.call("nc_rope_table", [self.rope, inv], [capacity, D])
         hip.sync()
 
     def layer(self, index: int) -> tuple[int, int]:
@@ -166,8 +177,18 @@ class Qwen2:
                           for n, k in ((W, H), (H, Q), (I, H), (I, H), (H, I))]
         shapes = per_layer * L + [((V, H), np.float32), ((vblocks, H), np.float32), ((H,), np.float32),
                                   ((D // 2,), np.float32)]
-        self.weights = Arena(Arena.size(shapes))
-        stage = DeviceArray((max(I * H, W * H, H * Q),), np.float32)     # f32 staging for quantization
+        M = max_tokens
+        act = [((M, H), np.float32), ((M, W), np.float32), ((M, Q), np.float32), ((M, I), np.float32),
+               ((M, max(I, H, Q)), np.int8), ((M,), np.float32), ((M, H), np.float32), ((M,), np.int64),
+               ((argmax_slots(V),), np.uint64), ((1, V), np.float32), ((M,), np.int64), ((M, I), np.float32),
+               ((M, I), np.float32), ((M, -(-max(I, H, Q) // BLOCK)), np.float32), ((M,), np.float32)]
+        # One hipMalloc: the weights, then the activations. While the weights load, the
+        # activation region (not yet in use) holds the float32 rows being quantized.
+        stage_floats = max(I * H, W * H, H * Q)
+        weight_bytes = Arena.size(shapes)
+        self.arena = Arena(weight_bytes + max(Arena.size(act), Arena.size([((stage_floats,), np.float32)])))
+        self.weights = self.arena
+        stage = self.arena.base.view((stage_floats,), np.float32, offset_bytes=weight_bytes)
 
         def upload(name: str, into: DeviceArray) -> DeviceArray:
             into.upload(np.ascontiguousarray(weights[name], np.float32))
@@ -256,14 +277,11 @@ class Qwen2:
         self.fused_decode = (H, I, D) in ((896, 4864, 64), (128, 256, 32)) and Q == H \
             and quantization == "int8-token"
         hip.sync()
-        del stage
-
-        M = max_tokens
-        act = [((M, H), np.float32), ((M, W), np.float32), ((M, Q), np.float32), ((M, I), np.float32),
-               ((M, max(I, H, Q)), np.int8), ((M,), np.float32), ((M, H), np.float32), ((M,), np.int64),
-               ((argmax_slots(V),), np.uint64), ((1, V), np.float32), ((M,), np.int64), ((M, I), np.float32),
-               ((M, I), np.float32), ((M, -(-max(I, H, Q) // BLOCK)), np.float32), ((M,), np.float32)]
-        self.acts = Arena(Arena.size(act))
+        del stage, head
+        if self.arena.top > weight_bytes:
+            raise AssertionError("the weights outgrew their region of the arena")
+        self.arena.top = weight_bytes
+        self.acts = self.arena
         self.x, self.qkv = self.acts.take((M, H), np.float32), self.acts.take((M, W), np.float32)
         self.ctx, self.h = self.acts.take((M, Q), np.float32), self.acts.take((M, I), np.float32)
         self.xq, self.xs = self.acts.take((M, max(I, H, Q)), np.int8), self.acts.take((M,), np.float32)
@@ -512,8 +530,7 @@ class Qwen2:
         H, V = c.hidden_size, c.vocab_size
         capacity = m + max_new_tokens
         cache = self.new_cache(capacity)
-        tokens = DeviceArray((capacity,), np.int64)
-        pos = DeviceArray((1,), np.int64)
+        tokens, pos = cache.tokens, cache.position
         one_id = self.acts.base.view((1,), np.int64, offset_bytes=self.ids.ptr - self.acts.base.ptr)
 
         self.ids.view((m,)).upload(prompt)
