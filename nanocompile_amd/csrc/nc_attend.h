@@ -205,6 +205,43 @@ __device__ __forceinline__ void chunk_scores_n(float (*qp)[kChunk], const Staged
     }
 }
 
+// chunk_scores_n with the queries read from global memory at a wave-uniform
+// address, query u at q + u D (q wave-uniform, the memory unchanged while the
+// kernel runs): scalar loads bring them to SGPRs, so each product reads one
+// operand from LDS (the key, once for the H chains) instead of also a 16-byte
+// broadcast of the query per head. The same chains in the same order; the
+// probabilities go to p[u].
+template <int D, int H>
+__device__ __forceinline__ void chunk_scores_sq(const float *__restrict__ q, float (*p)[kChunk], const Staged<D> &st,
+                                                int n, float scale, float (&m)[H], float (&l)[H]) {
+    const int lane = threadIdx.x & 63;
+    float acc[H];
+#pragma unroll
+    for (int u = 0; u < H; ++u) acc[u] = 0.0f;
+    const float *krow = st.keys + lane * Staged<D>::kKeyStride;
+#pragma unroll 2
+    for (int i = 0; i < D / 4; ++i) {
+        const float4 k = *reinterpret_cast<const float4 *>(krow + 4 * i);
+#pragma unroll
+        for (int u = 0; u < H; ++u) {
+            const float4 qi = *reinterpret_cast<const float4 *>(q + u * D + 4 * i);
+            acc[u] = __builtin_fmaf(qi.x, k.x, acc[u]);
+            acc[u] = __builtin_fmaf(qi.y, k.y, acc[u]);
+            acc[u] = __builtin_fmaf(qi.z, k.z, acc[u]);
+            acc[u] = __builtin_fmaf(qi.w, k.w, acc[u]);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < H; ++u) {
+        const float s = lane < n ? __fadd_rn(__fmul_rn(acc[u], scale), 0.0f) : -__builtin_inff();
+        const float mu = scores_max(s);
+        const float pt = nc_expf(__fsub_rn(s, mu));
+        l[u] = wave_sum_f32(pt);
+        m[u] = mu;
+        p[u][lane] = pt;
+    }
+}
+
 // (keys from n on have p = 0 and leave the accumulators unchanged, so the key
 // loop stops at the first group of four that holds none of the n keys)
 template <int D, int H>

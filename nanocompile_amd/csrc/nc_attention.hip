@@ -157,9 +157,10 @@ __global__ __launch_bounds__(kThreads) void rope_append(float *__restrict__ qkv,
 constexpr int kWaves = 8;              // decode: waves of a chunk workgroup, one query head each
 // Prefill: 4 query rows per workgroup, one per wave. A wave attends its row's
 // heads of the group together, up to 7 at a time (nc_attend.h's
-// chunk_scores_n and chunk_values_n: every key or value element read from LDS
-// once for all the heads' chains, the d and key loops unrolled by two so the
-// compiler does not issue every head's broadcast reads at once): 108 VGPRs,
+// chunk_scores_sq and chunk_values_n: every key or value element read from LDS
+// once for all the heads' chains, the row's queries read with scalar loads
+// into SGPRs (29.7 -> 29.3 us with the combine at 512 rows, where they were
+// 16-byte LDS broadcasts), the d and key loops unrolled by two): 109 VGPRs,
 // and 40 KB of LDS a workgroup (the staged chunk and 7 query/probability rows
 // a wave), so a CU holds four workgroups, four waves a SIMD. Measured on
 // MI355X at 512 rows, chunks + combine: 46 us; 49 us with 8-head batches
@@ -195,11 +196,14 @@ __device__ __forceinline__ F *chunk_result(F *part, int h, int rows, int r, int 
 
 // H heads of one query row attended to a staged chunk (nc_attend.h's two
 // halves for H queries), their chunk results stored head_stride floats apart.
+// The queries are read at q (wave-uniform, in global memory) into SGPRs; qp
+// holds the probabilities between the halves.
 template <int D, int H>
-__device__ __forceinline__ void attend_heads(float (*qp)[nc::kChunk], const nc::Staged<D> &st, int n, float scale,
-                                             float *dst, size_t head_stride) {
+__device__ __forceinline__ void attend_heads(const float *__restrict__ q, float (*qp)[nc::kChunk],
+                                             const nc::Staged<D> &st, int n, float scale, float *dst,
+                                             size_t head_stride) {
     float m[H], l[H], o[H];
-    nc::chunk_scores_n<D, H>(qp, st, n, scale, m, l);
+    nc::chunk_scores_sq<D, H>(q, qp, st, n, scale, m, l);
     nc::chunk_values_n<D, H>(qp, st, n, o);
 #pragma unroll
     for (int u = 0; u < H; ++u) nc::keep_result<D>(dst + u * head_stride, nc::ChunkResult{m[u], l[u], o[u]});
@@ -207,12 +211,13 @@ __device__ __forceinline__ void attend_heads(float (*qp)[nc::kChunk], const nc::
 
 // attend_heads<D, hn> for a run-time hn in 1 .. H.
 template <int D, int H>
-__device__ __forceinline__ void attend_heads_upto(int hn, float (*qp)[nc::kChunk], const nc::Staged<D> &st, int n,
-                                                  float scale, float *dst, size_t head_stride) {
+__device__ __forceinline__ void attend_heads_upto(int hn, const float *__restrict__ q, float (*qp)[nc::kChunk],
+                                                  const nc::Staged<D> &st, int n, float scale, float *dst,
+                                                  size_t head_stride) {
     if constexpr (H > 1) {
-        if (hn < H) return attend_heads_upto<D, H - 1>(hn, qp, st, n, scale, dst, head_stride);
+        if (hn < H) return attend_heads_upto<D, H - 1>(hn, q, qp, st, n, scale, dst, head_stride);
     }
-    attend_heads<D, H>(qp, st, n, scale, dst, head_stride);
+    attend_heads<D, H>(q, qp, st, n, scale, dst, head_stride);
 }
 
 // Prefill: grid (chunks, kv_heads, ceil(rows / ROWS)) over the slab of query
@@ -232,36 +237,25 @@ __global__ __launch_bounds__(64 * ROWS) void attention_rows_chunks(
     const int r_last = min((int)blockIdx.z * ROWS + ROWS, rows) - 1;
     if (past + i0 + r_last + 1 <= t0) return;             // no row of the block sees this chunk
     __shared__ __align__(16) float lds[nc::Staged<D>::kFloats];
-    __shared__ __align__(16) float qp[ROWS][kHeadBatch][nc::kChunk];   // per wave: a head's query, then its p
+    __shared__ __align__(16) float qp[ROWS][kHeadBatch][nc::kChunk];   // per wave: its heads' p
     const nc::Staged<D> st(lds);
     const int group = heads / kv_heads, width = (heads + 2 * kv_heads) * D;
     nc::ChunkLoad<D, 64 * ROWS> load;
     load.issue(kcache + (size_t)g * capacity * D, vcache + (size_t)g * capacity * D, t0, capacity - 1);
-    const int r = blockIdx.z * ROWS + wave, i = i0 + r;
+    // the wave's row, wave-uniform (readfirstlane), so its queries' address is too
+    const int r = blockIdx.z * ROWS + __builtin_amdgcn_readfirstlane(wave), i = i0 + r;
     const bool valid = r < rows && past + i + 1 > t0;
     const float *qrow = qkv + (size_t)(valid ? i : 0) * width + (size_t)g * group * D;
-    float qv[kHeadBatch];
-#pragma unroll
-    for (int u = 0; u < kHeadBatch; ++u) qv[u] = (valid && u < group && lane < D) ? qrow[u * D + lane] : 0.0f;
     load.store(st, -1, past + M - t0);                    // keys past + M and on: not yet in the cache
-#pragma unroll
-    for (int u = 0; u < kHeadBatch; ++u)
-        if (u < group && lane < D) qp[wave][u][lane] = qv[u];
     __syncthreads();
     if (!valid) return;
+    (void)lane;
     const int n = min(nc::kChunk, past + i + 1 - t0);
     for (int h0 = 0; h0 < group; h0 += kHeadBatch) {
-        if (h0 > 0) {                                       // groups of more than 8 heads (wave-local)
-#pragma unroll
-            for (int u = 0; u < kHeadBatch; ++u) qv[u] = (h0 + u < group && lane < D) ? qrow[(h0 + u) * D + lane] : 0.0f;
-#pragma unroll
-            for (int u = 0; u < kHeadBatch; ++u)
-                if (lane < D) qp[wave][u][lane] = qv[u];
-        }
         const int hn = min(kHeadBatch, group - h0);
         float *dst = chunk_result(part, g * group + h0, rows, r, jstride, j, D);
         const size_t head_stride = (size_t)rows * jstride * (D + 2);
-        attend_heads_upto<D, kHeadBatch>(hn, qp[wave], st, n, scale, dst, head_stride);
+        attend_heads_upto<D, kHeadBatch>(hn, qrow + h0 * D, qp[wave], st, n, scale, dst, head_stride);
     }
 }
 
