@@ -237,6 +237,55 @@ class AttentionProblem:
         return checked_output(self, schedule, self.guarded, self.m * self.heads * self.d)
 
 
+class RopeProblem:
+    """A prompt's qkv projection with RoPE and the KV-cache append in its epilogue
+    (nc_matmul_i8_token_rope) over M rows at past 0, W = (heads + 2 kv) D rows of width K: the
+    int8 activations, the weights in rotating copies, the cache and RoPE's table. Its space is
+    the MFMA tiles one head wide (the epilogue rotates a tile as a head)."""
+
+    op = "qkv_rope"
+
+    def __init__(self, m: int, w: int, k: int, heads: int, kv: int, d: int, seed: int = 0,
+                 stream_bytes: int = STREAM_BYTES) -> None:
+        from nanocompile_amd.models.qwen2 import inverse_frequencies
+        self.m, self.w, self.k, self.heads, self.kv, self.d = m, w, k, heads, kv, d
+        self.shape = (m, w, k, heads, kv, d)
+        rng = np.random.default_rng(seed)
+        self.copies = int(min(MAX_COPIES, max(2, -(-stream_bytes // max(w * k, 1)))))
+        self.xq = DeviceArray.from_host(rng.integers(-127, 128, (m, k)).astype(np.int8))
+        self.xs = DeviceArray.from_host((rng.random(m) * 0.05 + 1e-3).astype(np.float32))
+        host = rng.integers(-127, 128, (w, k)).astype(np.int8)
+        self.q = [DeviceArray.from_host(host) for _ in range(self.copies)]
+        self.scales = DeviceArray.from_host((rng.random(w) * 1e-3).astype(np.float32))
+        self.bias = DeviceArray.from_host(rng.standard_normal(w).astype(np.float32))
+        self.kc, self.vc = DeviceArray((kv, m, d), np.float32), DeviceArray((kv, m, d), np.float32)
+        self.table = DeviceArray((2, m, d // 2), np.float32)
+        hip.call("nc_rope_table", [self.table, DeviceArray.from_host(inverse_frequencies(d, 1e6))], [m, d])
+        self.guarded = DeviceArray.from_host(guarded(m * w))
+        self.y = self.guarded.view((m, w), np.float32, offset_bytes=GUARD * 4)
+
+    def space(self) -> list[dict]:
+        out = [{"schedule": 0, "kernel": "default"}]
+        for s in kernels.GEMM_SCHEDULES:
+            shape = hip.schedule_info(s)
+            if shape["tile_n"] == self.d and self.k % 16 == 0:
+                out.append(shape)
+        return out
+
+    def launch(self, schedule: int, copy: int = 0) -> None:
+        hip.call("nc_matmul_i8_token_rope",
+                 [self.y, self.xq, self.xs, self.q[copy % self.copies], self.scales, self.bias, self.kc, self.vc,
+                  self.table, None],
+                 [self.m, self.w, self.k, self.heads, self.kv, self.d, 0, self.m, schedule])
+
+    def output(self, schedule: int) -> np.ndarray:
+        """The rotated qkv rows and both caches' bits; TuningError if qkv's guards were written."""
+        self.guarded.upload(guarded(self.m * self.w))
+        self.launch(schedule, 0)
+        bits = checked_output(self, schedule, self.guarded, self.m * self.w)
+        return np.concatenate([bits, self.kc.numpy().view(np.uint32).ravel(), self.vc.numpy().view(np.uint32).ravel()])
+
+
 def measure(problem: Problem, schedules: list[int], rounds: int, reps: int) -> list[float]:
     """Median seconds per call of each schedule, the candidates alternating round by round."""
     graphs = {}
@@ -415,6 +464,15 @@ class Autotuner:
         if at not in self._chosen:
             self._chosen[at] = self.tune_problem(lambda: AttentionProblem(m, heads, kv, d, self.seed),
                                                  "attention_prefill", (m, heads, kv, d), None).winner
+        return self._chosen[at]
+
+    def rope_schedule(self, m: int, w: int, k: int, heads: int, kv: int, d: int) -> int:
+        """The schedule of a prompt's qkv projection with RoPE in its epilogue (nc_matmul_i8_token_rope)."""
+        at = ("qkv_rope", m, w, k, heads, kv, d)
+        if at not in self._chosen:
+            self._chosen[at] = self.tune_problem(
+                lambda: RopeProblem(m, w, k, heads, kv, d, self.seed, self.stream_bytes), "qkv_rope",
+                (m, w, k, heads, kv, d), None).winner
         return self._chosen[at]
 
     def tune_problem(self, make, op: str, shape: tuple, space: list[dict] | None) -> TuneRecord:

@@ -91,6 +91,15 @@ class Arena:
         return view
 
 
+def _rope_schedule_ok(schedule: int, head_dim: int) -> bool:
+    """Whether nc_matmul_i8_token_rope can run ``schedule``: its own choice (0) or an MFMA tile
+    whose n is one head."""
+    if schedule == 0:
+        return True
+    shape = hip.schedule_info(schedule) if schedule >= 16 else None
+    return shape is not None and shape.get("tile_n") == head_dim
+
+
 class KVCache:
     """Keys and values of one sequence on the device: ``[layers, kv_heads, capacity, head_dim]`` each.
 
@@ -324,11 +333,12 @@ class Qwen2:
             kc, vc = cache.layer(i)
             hip.call("nc_rms_norm_quant", [None, self.xq, self.xs, self.x, w["g1"]], [m, H, eps])
             q, s = w["qkv"]
-            if s_qkv == 0 and D in (32, 64) and cache.rope is not None:
-                # RoPE and the cache append in the projection's epilogue (one launch)
+            if D in (32, 64) and cache.rope is not None and _rope_schedule_ok(s_qkv, D):
+                # RoPE and the cache append in the projection's epilogue (one launch); s_qkv is
+                # this kernel's schedule (0, or a tile one head wide)
                 hip.call("nc_matmul_i8_token_rope",
                          [self.qkv, self.xq, self.xs, q, s, w["qkv_b"], kc, vc, cache.rope, pos],
-                         [m, W, H, heads, kv, D, past, cache.capacity])
+                         [m, W, H, heads, kv, D, past, cache.capacity, s_qkv])
             else:
                 hip.call("nc_matmul_i8_token", [self.qkv, self.xq, self.xs, q, s, w["qkv_b"], None],
                          [m, W, H, s_qkv])
@@ -441,10 +451,15 @@ class Qwen2:
         if self.tuner is None:
             return 0, 0, 0, 0
         c = self.config
-        H, I, Q = c.hidden_size, c.intermediate_size, c.num_attention_heads * c.head_dim
+        H, I, D = c.hidden_size, c.intermediate_size, c.head_dim
+        Q = c.num_attention_heads * D
         t = self.tuner.schedule
-        return (t("matmul_i8_token", m, self.width, H), t("matmul_i8_token", m, H, Q),
-                t("matmul_i8_token_swiglu", m, I, H), t("matmul_i8_token", m, H, I))
+        if D in (32, 64) and self.quantization == "int8-token" and m > 1:
+            # the qkv projection runs with RoPE and the cache append in its epilogue: tune that kernel
+            qkv = self.tuner.rope_schedule(m, self.width, H, c.num_attention_heads, c.num_key_value_heads, D)
+        else:
+            qkv = t("matmul_i8_token", m, self.width, H)
+        return (qkv, t("matmul_i8_token", m, H, Q), t("matmul_i8_token_swiglu", m, I, H), t("matmul_i8_token", m, H, I))
 
     def forward(self, token_ids: Sequence[int] | np.ndarray, cache: KVCache | None = None,
                 last_only: bool = False) -> np.ndarray:

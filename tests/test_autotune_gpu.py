@@ -40,7 +40,8 @@ def test_model_on_tuned_schedules_is_bitwise_the_default(gpu, tmp_path):
     a = default.forward(ids, default.new_cache(64))
     b = tuned.forward(ids, tuned.new_cache(64))
     assert np.array_equal(bits(a), bits(b))
-    assert {r.op for r in tuner.records} == {"matmul_i8_token", "matmul_i8_token_swiglu", "attention_prefill"}
+    assert {r.op for r in tuner.records} == {"matmul_i8_token", "matmul_i8_token_swiglu", "attention_prefill",
+                                            "qkv_rope"}
     assert tuned.generate(list(ids[:8]), 6) == default.generate(list(ids[:8]), 6)
 
 
@@ -66,11 +67,25 @@ def test_every_prefill_attention_schedule_is_the_default_bitwise(gpu, m):
         assert np.array_equal(problem.output(candidate["schedule"]), reference), candidate
 
 
+@pytest.mark.parametrize("m", [16, 130, 512])
+def test_every_qkv_rope_schedule_is_the_default_bitwise(gpu, m):
+    """The fused qkv + RoPE + cache-append GEMM: every tile one head wide leaves qkv and both
+    caches as the library's choice does."""
+    problem = autotune.RopeProblem(m, 1152, 896, 14, 2, 64, seed=m, stream_bytes=4 << 20)
+    space = problem.space()
+    assert [c["schedule"] for c in space] == [0, 16, 17, 20, 21, 24]
+    reference = problem.output(0)
+    for candidate in space[1:]:
+        print(f"qkv rope m={m} schedule {candidate['schedule']}", flush=True)
+        assert np.array_equal(problem.output(candidate["schedule"]), reference), candidate
+
+
 def test_tuner_chooses_decode_and_attention_schedules(gpu, tmp_path):
     tuner = autotune.Autotuner(rounds=2, reps=4, cache=tmp_path / "t.json", stream_bytes=4 << 20)
     legal = [c["schedule"] for c in autotune.DecodeProblem(2, 4864, 896, stream_bytes=1 << 20).space()]
     assert tuner.decode_schedule(2, 4864, 896) in legal
     assert tuner.attention_schedule(130, 14, 2, 64) in range(5)
+    assert tuner.rope_schedule(130, 1152, 896, 14, 2, 64) in (0, 16, 17, 20, 21, 24)
     again = autotune.Autotuner(cache=tmp_path / "t.json")
     assert again.decode_schedule(2, 4864, 896) == tuner.decode_schedule(2, 4864, 896)
     assert again.records[-1].cached
