@@ -336,9 +336,20 @@ def block_measurements(model, seed: int = 7) -> dict:
     from nanocompile_amd.compiled import CompiledProgram
     golden = Path(__file__).resolve().parent / "tests" / "golden"
     doc = lir.load_programs(golden / "programs.json.gz")
+    from nanocompile_amd import autotune
     with np.load(golden / "programs.npz", allow_pickle=False) as arrays:
-        generated = {variant: CompiledProgram(lir.program_from_json(doc["zoo"]["rms_norm_quant"][key], arrays))
-                     for variant, key in (("unfused", "unfused"), ("fused", "program"))}
+        recorded = {variant: lir.program_from_json(doc["zoo"]["rms_norm_quant"][key], arrays)
+                    for variant, key in (("unfused", "unfused"), ("fused", "program"))}
+    generated = {variant: CompiledProgram(program) for variant, program in recorded.items()}
+    # the same programs with each kernel's GPU schedule (threads, LDS staging, workgroup items,
+    # vector width, unroll) chosen by the autotuner on these three row counts, per token
+    tuner = autotune.Autotuner(cache=None, workloads=[(f"m{m}", {"seq": m}, 1.0 / m) for m in (1, 64, 512)])
+    tuned_schedules = {}
+    for variant, program in recorded.items():
+        first = len(tuner.records)
+        generated[f"{variant}_tuned"] = CompiledProgram(program, schedule=tuner)
+        tuned_schedules[variant] = {f"kernel {r.shape[0]} ({r.op})": {
+            "config": r.config, "speedup": round(r.speedup or 1.0, 3)} for r in tuner.records[first:]}
     gamma_host = gamma.numpy()
     for m in (1, 64, 512):
         x = rng.standard_normal((m, H)).astype(np.float32)
@@ -348,7 +359,9 @@ def block_measurements(model, seed: int = 7) -> dict:
             rows[str(m)][f"generated_{variant}"] = {"us": round(us, 3), "kernels": len(program.program.calls)}
     out["rms_norm_quant"] = {"kernel": "rms_norm_quant (one pass: normed f32, int8 row, scale)", "rows": rows,
                              "generated": "the reference's program for the same graph, lowered to HIP by "
-                                          "codegen_hip (unfused: a kernel per operation; fused: its fusion)"}
+                                          "codegen_hip (unfused: a kernel per operation; fused: its fusion; "
+                                          "_tuned: each kernel's GPU schedule chosen by the autotuner)",
+                             "tuned_schedules": tuned_schedules}
 
     # config 3: one decoder block's decode step at past = 512 (all 24 blocks replayed, per block)
     past = 512

@@ -328,6 +328,7 @@ class TuneRecord:
     evaluations: list[Evaluation] = field(default_factory=list)
     seconds: float = 0.0
     cached: bool = False
+    config: dict | None = None          # a generated kernel's winning point of its schedule space
 
     @property
     def speedup(self) -> float | None:
@@ -339,6 +340,7 @@ class TuneRecord:
         return {"key": self.key, "op": self.op, "shape": list(self.shape), "space": self.space_size,
                 "winner": self.winner, "default_cost": self.default_cost, "winner_cost": self.winner_cost,
                 "speedup": self.speedup, "seconds": round(self.seconds, 3), "cached": self.cached,
+                "config": self.config,
                 "evaluations": [{"stage": e.stage, "schedules": e.schedules, "costs": e.costs}
                                 for e in self.evaluations]}
 
@@ -405,6 +407,207 @@ class TuningCache:
         os.replace(scratch, self.path)        # whole file or nothing
 
 
+# -- generated kernels: the code generator's schedule space ------------------------------------
+
+# A workload: (name, symbol values, weight); the weight turns seconds per call into seconds per
+# token, so a decode step and a prefill add up (the reference's DECODE and PREFILL, autotune.py:65-69).
+DECODE = ("decode", {"seq": 1, "past": 64}, 1.0)
+PREFILL = ("prefill", {"seq": 32, "past": 0}, 1.0 / 32)
+WORKLOADS = (DECODE, PREFILL)
+SENTINEL_BYTE = 0xA5             # a candidate's output is filled with it before the candidate runs
+
+
+@dataclass
+class Candidate:
+    """One point of a generated kernel's schedule space (gpu_schedule.space): its configuration,
+    the scheduled kernel and launch, and the kernel's generated text."""
+
+    config: dict
+    kernel: object
+    launch: object
+    source: str
+
+
+def kernel_candidates(kernel, calls) -> list[Candidate]:
+    """The points of ``kernel``'s space that apply, the hand-written default first, one per
+    distinct generated kernel (the reference's legal_space, autotune.py:571-590)."""
+    from nanocompile_amd import codegen_hip, gpu_schedule
+    out, seen = [], set()
+    for config in gpu_schedule.space(kernel):
+        try:
+            scheduled, launch = gpu_schedule.apply(kernel, calls, config)
+        except gpu_schedule.ScheduleError:
+            continue
+        source = codegen_hip.render_kernel(scheduled, launch, 0)
+        if source in seen:
+            continue
+        seen.add(source)
+        out.append(Candidate(config, scheduled, launch, source))
+    return out
+
+
+class CandidateLibrary:
+    """Every candidate of every kernel of a program, generated into one library.
+
+    ``entry[i][c]`` is the launcher (``nc_k<entry>``) of kernel ``i``'s
+    candidate ``c``; candidate 0 is the default schedule. The candidates are
+    measured in this library and the chosen ones run from it, so a tuned
+    program needs no second compile.
+    """
+
+    def __init__(self, program) -> None:
+        from nanocompile_amd import codegen_hip, lir
+        program = lir.adapt(program)
+        calls_of: dict[int, list] = {}
+        for call in program.calls:
+            calls_of.setdefault(call.kernel, []).append(call)
+        self.program = program
+        self.calls_of = calls_of
+        self.candidates = [kernel_candidates(k, calls_of.get(i, [])) for i, k in enumerate(program.kernels)]
+        scheduled, owners, self.entry = [], [], []
+        for i, cands in enumerate(self.candidates):
+            self.entry.append([])
+            for c in cands:
+                self.entry[i].append(len(scheduled))
+                scheduled.append((c.kernel, c.launch))
+                owners.append(i)
+        self.source = codegen_hip.render_library(scheduled, owners)
+
+    def build(self):
+        """(path, was it cached) of the built library (codegen_hip.build_library)."""
+        from nanocompile_amd import codegen_hip
+        return codegen_hip.build_library(self.source)
+
+    def choice(self, chosen) -> tuple:
+        """``(scheduled, source, launcher names)`` with kernel ``i`` at candidate ``chosen[i]``."""
+        from nanocompile_amd import codegen_hip
+        scheduled = [(self.candidates[i][c].kernel, self.candidates[i][c].launch) for i, c in enumerate(chosen)]
+        names = [codegen_hip.kernel_name(self.entry[i][c]) for i, c in enumerate(chosen)]
+        return scheduled, self.source, names
+
+
+class Chosen:
+    """A schedule for CompiledProgram: kernel ``i`` at candidate ``chosen[i]`` of ``library``."""
+
+    def __init__(self, library: CandidateLibrary, chosen) -> None:
+        self.library, self.chosen = library, list(chosen)
+
+    def library_for(self, program) -> tuple:
+        return self.library.choice(self.chosen)
+
+
+def random_arguments(program, bindings, rng) -> tuple[dict, dict, dict]:
+    """Inputs and weights of a program's interface at ``bindings``: floats normal, int8 and bool
+    uniform, wider integers zero (they index: ids, positions), so every gather is in range."""
+    from nanocompile_amd import lir
+
+    def draw(shape, dtype):
+        if dtype.name == "f32":
+            return rng.standard_normal(shape).astype(np.float32)
+        if dtype.name == "i8":
+            return rng.integers(-127, 128, shape).astype(np.int8)
+        if dtype.name == "bool":
+            return rng.integers(0, 2, shape).astype(dtype.numpy)
+        return np.zeros(shape, dtype.numpy)
+
+    bound = {name: int(v) for name, v in bindings.items() if name in program.symbols}
+    missing = [name for name in program.symbols if name not in bound]
+    if missing:
+        raise TuningError(f"the workload {dict(bindings)} gives no value to {missing}")
+    inputs = {name: draw(lir.shape_of(shape, bound), dtype) for name, dtype, shape in program.inputs}
+    weights = {name: draw(lir.shape_of(shape, {}), dtype) for name, (dtype, shape) in program.weights.items()}
+    return inputs, weights, bound
+
+
+class ProgramWorkload:
+    """A program on the device at one workload's symbols, for timing its kernels' candidates:
+    every call's arguments placed in one arena (the default schedules' outputs in place)."""
+
+    def __init__(self, library: CandidateLibrary, bindings, seed: int) -> None:
+        import ctypes
+
+        from nanocompile_amd import compiled
+        self.library = library
+        program = library.program
+        self.compiled = compiled.CompiledProgram(program, Chosen(library, [0] * len(program.kernels)))
+        lib = self.compiled._library
+        self.launchers = [[compiled.KERNEL_TYPE((f"nc_k{n}", lib)) for n in entries] for entries in library.entry]
+        inputs, weights, bound = random_arguments(program, bindings, np.random.default_rng(seed))
+        self.launch, self.bound, self.addresses = self.compiled.prepare(inputs, weights, bound)
+        self.calls = self.launch.calls
+        self.symbols = self.launch.symbols
+        self.inputs = inputs
+        self._ctypes = ctypes
+
+    def _run(self, kernel: int, candidate: int, args) -> None:
+        status = self.launchers[kernel][candidate](args, self.symbols)
+        if status != 0:
+            raise TuningError(f"kernel {kernel} candidate {candidate} could not be launched ({status}): "
+                              f"{hip.last_error()}")
+
+    def gate(self, kernels) -> None:
+        """Run the program's calls in order on the default schedules; at the first call of each
+        kernel in ``kernels``, run every other candidate on the same arguments, its output filled
+        with a sentinel first: the whole arena must then hold exactly what the default left (its
+        output bit for bit, every other byte untouched)."""
+        from nanocompile_amd.compiled import _nbytes
+        pending = set(kernels)
+        arena = self.compiled._arena
+        base = arena.ptr
+        lib = hip.load()
+        for call, args in self.calls:
+            self._run(call.kernel, 0, args)
+            hip.sync()
+            if call.kernel not in pending:
+                continue
+            pending.discard(call.kernel)
+            before = arena.numpy().view(np.uint8).copy()
+            at, n = self.addresses[call.output] - base, _nbytes(call.output, self.bound)
+            fill = np.full(max(n, 1), SENTINEL_BYTE, np.uint8)
+            for c in range(1, len(self.launchers[call.kernel])):
+                if n:
+                    hip._check(lib.nc_memcpy_h2d(base + at, fill.ctypes.data, n), "nc_memcpy_h2d")
+                self._run(call.kernel, c, args)
+                hip.sync()
+                after = arena.numpy().view(np.uint8)
+                if not np.array_equal(after, before):
+                    diff = np.flatnonzero(after != before)
+                    where = "its output" if at <= diff[0] < at + n else "outside its output"
+                    config = self.library.candidates[call.kernel][c].config
+                    raise TuningError(f"kernel {call.kernel} ({call.primitive}) candidate {c} {config} differs "
+                                      f"from the default schedule at byte {int(diff[0]) - at} of {n} ({where})")
+
+    def timer(self, kernel: int):
+        """An object ``measure`` times: ``launch(candidate, copy)`` runs kernel ``kernel``'s calls."""
+        args = [a for call, a in self.calls if call.kernel == kernel]
+        workload = self
+
+        class Calls:
+            def launch(self, candidate: int, copy: int = 0) -> None:
+                for a in args:
+                    workload._run(kernel, candidate, a)
+
+        return Calls()
+
+
+def program_kernel_key(library: CandidateLibrary, kernel: int, workloads) -> str:
+    """A generated kernel's cache key: its candidates' text, what its calls read, the workloads
+    and the compiler (the reference's kernel_key, autotune.py:548-560)."""
+    from nanocompile_amd import codegen_hip
+    calls = library.calls_of.get(kernel, [])
+    operands = [[v.buffer.kind, v.buffer.dtype.name, [str(d) for d in v.buffer.shape], str(v.offset)]
+                for v in calls[0].operands] if calls else []
+    material = json.dumps({
+        "candidates": [c.source for c in library.candidates[kernel]],
+        "operands": operands,
+        "symbols": list(library.program.symbols),
+        "workloads": [[n, sorted(b.items()), w] for n, b, w in workloads],
+        "compiler": codegen_hip.compiler_identity(codegen_hip.hipcc()),
+        "flags": list(codegen_hip.HIPCC_FLAGS),
+    }, sort_keys=True)
+    return hashlib.sha256(material.encode()).hexdigest()[:20]
+
+
 # -- the tuner --------------------------------------------------------------------------------
 
 
@@ -417,8 +620,9 @@ class Autotuner:
 
     def __init__(self, rounds: int = 7, reps: int = 32, margin: float = 0.03, seed: int = 0,
                  cache: TuningCache | Path | str | bool | None = True, verbose: bool = False,
-                 stream_bytes: int = STREAM_BYTES) -> None:
+                 stream_bytes: int = STREAM_BYTES, workloads=None) -> None:
         self.rounds, self.reps, self.margin, self.seed = rounds, reps, margin, seed
+        self.workloads = tuple(WORKLOADS if workloads is None else workloads)
         if cache is True:
             cache = TuningCache()
         elif cache not in (None, False) and not isinstance(cache, TuningCache):
@@ -474,6 +678,86 @@ class Autotuner:
                 lambda: RopeProblem(m, w, k, heads, kv, d, self.seed, self.stream_bytes), "qkv_rope",
                 (m, w, k, heads, kv, d), None).winner
         return self._chosen[at]
+
+    # -- generated programs ------------------------------------------------------------------
+
+    def schedule_program(self, program) -> list:
+        """[(kernel, Launch)] of ``program`` with each kernel at its measured best schedule."""
+        library, chosen = self.tune_program(program)
+        return library.choice(chosen)[0]
+
+    def library_for(self, program) -> tuple:
+        """For CompiledProgram: the tuned kernels, run from the library they were measured in."""
+        library, chosen = self.tune_program(program)
+        return library.choice(chosen)
+
+    def tune_program(self, program) -> tuple[CandidateLibrary, list[int]]:
+        """Choose each kernel's schedule from its space (gpu_schedule.space) by measurement.
+
+        All candidates of all kernels are generated into one library. For each
+        workload (symbol values, weighted per token) the program runs on random
+        inputs; at each kernel's first call every candidate is checked against
+        the default schedule on the same arguments (``ProgramWorkload.gate``),
+        then the candidates of each kernel are timed on all of its calls, in
+        alternation over rounds, and ``choose`` keeps the default unless the
+        best beats it by more than ``margin``. A cached kernel is not measured.
+        """
+        library = CandidateLibrary(program)
+        n = len(library.candidates)
+        chosen = [0] * n
+        keys = [program_kernel_key(library, i, self.workloads) for i in range(n)]
+        machine = machine_key()
+        todo = []
+        for i in range(n):
+            cands = library.candidates[i]
+            if len(cands) <= 1 or not library.calls_of.get(i):
+                continue
+            entry = self.cache.get(machine, keys[i]) if self.cache is not None else None
+            if entry is not None and isinstance(entry.get("config"), dict):
+                hit = [c for c, cand in enumerate(cands)
+                       if sorted(cand.config.items()) == sorted(entry["config"].items())]
+                if hit:
+                    chosen[i] = hit[0]
+                    self.records.append(TuneRecord(keys[i], library.program.kernels[i].primitive, (i,), len(cands),
+                                                   hit[0], entry.get("default_cost"), entry.get("winner_cost"),
+                                                   cached=True, config=entry["config"]))
+                    continue
+            todo.append(i)
+        if not todo:
+            return library, chosen
+        started = time.perf_counter()
+        workloads = [(ProgramWorkload(library, bindings, self.seed + w), weight)
+                     for w, (_, bindings, weight) in enumerate(self.workloads)]
+        for workload, _ in workloads:
+            workload.gate(todo)
+        for i in todo:
+            t0 = time.perf_counter()
+            timers = [(workload.timer(i), weight) for workload, weight in workloads]
+
+            def cost(stage: str, candidates: list[int]) -> list[float]:
+                rounds = self.rounds * 2 if stage == "confirm" else self.rounds
+                total = np.zeros(len(candidates))
+                for timer, weight in timers:
+                    total += weight * np.asarray(measure(timer, candidates, rounds, self.reps))
+                return [float(x) for x in total]
+
+            cands = library.candidates[i]
+            winner, log, default_cost, winner_cost = choose(list(range(len(cands))), cost, self.margin)
+            chosen[i] = winner
+            record = TuneRecord(keys[i], library.program.kernels[i].primitive, (i,), len(cands), winner,
+                                default_cost, winner_cost, log, time.perf_counter() - t0,
+                                config=cands[winner].config)
+            self.records.append(record)
+            if self.cache is not None:
+                self.cache.put(machine, keys[i], {"config": cands[winner].config, "default_cost": default_cost,
+                                                  "winner_cost": winner_cost, "op": record.op})
+            if self.verbose:
+                print(f"tuned kernel {i} ({record.op}): {len(cands)} schedules, "
+                      f"{cands[winner].launch.describe()} at {winner_cost * 1e6:.2f} us per token "
+                      f"({record.speedup:.2f}x the default)", flush=True)
+        if self.verbose:
+            print(f"tuned {len(todo)} generated kernels in {time.perf_counter() - started:.1f} s", flush=True)
+        return library, chosen
 
     def tune_problem(self, make, op: str, shape: tuple, space: list[dict] | None) -> TuneRecord:
         """Measure the candidates of the problem ``make()`` builds (its ``space()`` unless given):

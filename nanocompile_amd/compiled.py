@@ -159,7 +159,10 @@ class CompiledProgram:
     ``program`` is the reference's Program (fusion.fuse's result) or this
     package's reading of one (``lir.program_from_json``). ``schedule`` is
     ``"default"`` (gpu_schedule.default), a function ``(kernel, calls) ->
-    (kernel, Launch)``, or an object with ``schedule_program(program)`` (a tuner).
+    (kernel, Launch)``, an object with ``schedule_program(program)``, or one
+    with ``library_for(program)`` returning ``(scheduled, source, launcher
+    names)``: a library that holds the chosen kernels among others (the
+    autotuner's, whose candidates were measured in that same library).
     """
 
     def __init__(self, program, schedule="default", device: int = 0) -> None:
@@ -167,16 +170,20 @@ class CompiledProgram:
         hip.init(device)
         program = lir.adapt(program)
         self.program = program
-        self.scheduled = schedule_of(program, schedule)
+        if hasattr(schedule, "library_for"):
+            self.scheduled, self.source, names = schedule.library_for(program)
+        else:
+            self.scheduled = schedule_of(program, schedule)
+            self.source = codegen_hip.render_library(self.scheduled)
+            names = [codegen_hip.kernel_name(i) for i in range(len(self.scheduled))]
         self.kernels = [k for k, _ in self.scheduled]
-        self.source = codegen_hip.render_library(self.scheduled)
         self.library_path, self.cached = codegen_hip.build_library(self.source)
         self.compile_seconds = time.perf_counter() - started
         self._library = ctypes.CDLL(str(self.library_path))
         bind = self._library.nc_bind_stream
         bind.argtypes, bind.restype = [ctypes.c_void_p, ctypes.c_void_p], None
         bind(hip.load().nc_stream_handle(), hip.load().nc_error_word())
-        self._launch = [KERNEL_TYPE((codegen_hip.kernel_name(i), self._library)) for i in range(len(self.kernels))]
+        self._launch = [KERNEL_TYPE((name, self._library)) for name in names]
         self._last_use = program.last_uses()
         self.symbols = tuple(program.symbols)
         # operands read in a packed layout: (call, operand) -> rows per block
@@ -298,7 +305,9 @@ class CompiledProgram:
         returns ``(launch, bound, addresses)``: ``launch()`` enqueues the program's kernels on the
         library stream and returns without waiting (no copies: it can be replayed, or captured
         in a graph, to time the kernels alone), ``bound`` the symbols' values, ``addresses`` each
-        buffer's device address (the outputs are read from there)."""
+        buffer's device address (the outputs are read from there). ``launch.calls`` holds each
+        call with its launcher arguments and ``launch.symbols`` the symbol array, for a caller
+        that launches calls one at a time (the autotuner)."""
         program = self.program
         bound = self.bind(inputs, weights, bindings)
         syms = (ctypes.c_int64 * max(1, len(self.symbols)))(*[bound[s] for s in self.symbols])
@@ -345,6 +354,7 @@ class CompiledProgram:
                     self._wait(inputs, bound)
                     profile[call.primitive] = profile.get(call.primitive, 0.0) + time.perf_counter() - started
 
+        launch.calls, launch.symbols = launches, syms
         return launch, bound, addresses
 
     def _wait(self, inputs, bound) -> None:

@@ -16,6 +16,19 @@ space. A GPU launch binds loops to the grid instead of to a thread pool:
   computing the same value in the same order, and ``var``'s independent
   iterations are shared among the threads (a row kernel's write pass across
   a workgroup, with its sums computed once per thread, in order).
+* ``workgroup()``: one workgroup per item without a shared loop: every
+  thread computes the item, thread 0 stores it (an item that only reads and
+  reduces, given a workgroup so that its operands can be staged).
+* ``stage(param)``: LDS staging. Every read of operand ``param`` in an item
+  is ``base + v``, ``base`` fixed for the item and ``v`` one of the item's
+  loops counting up to the same extent ``E``; the workgroup copies the
+  window ``x[base, base + E)`` into LDS with coalesced loads once per item,
+  and the reads go to LDS (a row read by every thread of a workgroup, or by
+  one thread in order, leaves HBM once and at full width).
+* ``vectorize(width)``: each thread takes ``width`` consecutive iterations of
+  the loop spread across threads (the innermost grid loop, or the shared
+  loop), so neighbouring reads and writes sit in one thread and can be
+  issued as one wide access.
 * ``unroll(var, factor)``: a constant-count unroll hint for a serial loop.
 * ``pack(param, rows, cols, block)``: the reference's packed operand layout
   (schedule.py:362-395, loopir.Param.packed): rows in blocks of ``block``,
@@ -29,16 +42,25 @@ None of these changes an arithmetic operation or its order: each output
 element is computed by the same expression sequence as in the unscheduled
 kernel, so every schedule is bitwise the unscheduled kernel, and the tests
 and the autotuner hold every candidate to that.
+
+The space the autotuner searches mirrors the reference's (schedules.py:87-128:
+per kernel class, the knobs and their values; the hand-written defaults;
+``apply`` refusing a point outside the space): here the classes are ``row``
+(an item ends in a loop its workgroup shares) and ``item`` (one thread per
+item), and the knobs are the primitives above.
 """
 
 from __future__ import annotations
 
+import itertools
 from dataclasses import dataclass, field, replace
 
-from nanocompile_amd import lir
+from nanocompile_amd import lir, simplify
 
 WAVE = 64
 MAX_THREADS = 1024
+MAX_STAGE_BYTES = 64 * 1024     # LDS a launch stages; a larger window at run time takes the unstaged kernel
+VECTOR_WIDTHS = (1, 2, 4, 8)
 
 
 class ScheduleError(ValueError):
@@ -108,6 +130,45 @@ def walk(x):
     elif k == "Dp4":
         yield from walk(x.a)
         yield from walk(x.b)
+
+
+def unconditional(x):
+    """The nodes of ``x`` evaluated whenever ``x`` is: C evaluates one arm of ``?:`` and the
+    right side of ``||`` only when the left is false."""
+    yield x
+    k = kind(x)
+    if k == "Select":
+        yield from unconditional(x.cond)
+    elif k == "Binary" and x.op == "or":
+        yield from unconditional(x.a)
+    elif k in ("Load", "Local"):
+        yield from unconditional(x.index)
+    elif k == "Binary":
+        yield from unconditional(x.a)
+        yield from unconditional(x.b)
+    elif k in ("Unary", "Cast"):
+        yield from unconditional(x.a)
+    elif k == "Fma":
+        yield from unconditional(x.a)
+        yield from unconditional(x.b)
+        yield from unconditional(x.c)
+    elif k == "Dp4":
+        yield from unconditional(x.a)
+        yield from unconditional(x.b)
+
+
+def stmt_scalars(s) -> list:
+    """The scalar expressions of one statement itself (not of the statements it holds)."""
+    k = kind(s)
+    if k == "Loop":
+        return [s.extent]
+    if k in ("Store", "ArrayStore"):
+        return [s.index, s.value]
+    if k in ("Let", "Assign"):
+        return [s.value]
+    if k == "Fail":
+        return [s.cond]
+    return []
 
 
 def scalars(stmts):
@@ -210,6 +271,18 @@ def _c(v: int):
 
 
 @dataclass(frozen=True)
+class Staged:
+    """An operand window copied into LDS once per item: ``x{param}[base, base + extent)``, read
+    back as the local array ``name`` (``name[v]`` for the read ``x{param}[base + v]``)."""
+
+    param: int
+    name: str
+    base: object                  # over the grid's loop vars, symbols and constants
+    extent: object                # over symbols and constants: the same for every item
+    dtype: object
+
+
+@dataclass(frozen=True)
 class Launch:
     """How a scheduled kernel runs: its grid loops, workgroup size and the per-item mapping."""
 
@@ -217,11 +290,24 @@ class Launch:
     threads: int = 256
     cooperate: str | None = None           # the loop shared by a workgroup's threads, one item per workgroup
     unroll: tuple[tuple[str, int], ...] = ()
+    workgroup: bool = False                # one workgroup per item with no shared loop; thread 0 stores
+    stage: tuple[Staged, ...] = ()         # operand windows staged in LDS per item
+    vector: int = 1                        # consecutive iterations per thread of the loop spread across threads
+
+    @property
+    def per_workgroup(self) -> bool:
+        """An item is a whole workgroup (else one thread)."""
+        return self.cooperate is not None or self.workgroup
 
     def describe(self) -> str:
         parts = [f"grid({', '.join(self.grid)})", f"block({self.threads})"]
         if self.cooperate:
             parts.append(f"cooperate({self.cooperate})")
+        if self.workgroup:
+            parts.append("workgroup()")
+        parts += [f"stage(x{st.param})" for st in self.stage]
+        if self.vector > 1:
+            parts.append(f"vectorize({self.vector})")
         parts += [f"unroll({v}, {n})" for v, n in self.unroll]
         return ".".join(parts)
 
@@ -284,8 +370,85 @@ class GpuSchedule:
             raise ScheduleError(f"cooperate({name}): an iteration carries a value into the next")
         if any(kind(s) == "Fail" for s in statements(loop.body)):
             raise ScheduleError(f"cooperate({name}): the loop checks its input and may stop early")
+        if self.launch.workgroup:
+            raise ScheduleError(f"cooperate({name}): the item is already a workgroup with no shared loop")
         self.launch = replace(self.launch, cooperate=name)
         self.steps.append(f"cooperate {name}")
+        return self
+
+    def workgroup(self) -> "GpuSchedule":
+        """One workgroup per item with no loop shared: every thread computes the item, thread 0 stores."""
+        if not self.launch.grid:
+            raise ScheduleError("workgroup: bind the grid first")
+        if self.launch.cooperate:
+            raise ScheduleError("workgroup: the item already shares a loop across its workgroup")
+        if self.launch.vector > 1:
+            raise ScheduleError("workgroup: the item is vectorized across threads")
+        self.launch = replace(self.launch, workgroup=True)
+        self.steps.append("workgroup")
+        return self
+
+    def stage(self, param: int) -> "GpuSchedule":
+        """Copy operand ``param``'s window into LDS once per item; its reads go to LDS.
+
+        Legal when every read of the operand in the item is ``base + v``, with
+        ``base`` the same for all of them and built from the grid's vars,
+        symbols and constants, and ``v`` a loop var of the item whose loop
+        counts to the same extent, itself built from symbols and constants;
+        when one of the item's own loops counts to that extent and reads
+        ``base + v`` in every iteration (so the unscheduled kernel reads every
+        element of the window, and the copy reads nothing it would not); and
+        when no ``Fail`` in the item can stop it before that loop.
+        """
+        launch = self.launch
+        params = self.kernel.params
+        if not launch.per_workgroup:
+            raise ScheduleError(f"stage(x{param}): an item must be a workgroup (cooperate or workgroup) "
+                                f"to share a staged window")
+        if not 0 < param < len(params) or params[param].writable:
+            raise ScheduleError(f"stage(x{param}): not an operand")
+        if params[param].packed is not None:
+            raise ScheduleError(f"stage(x{param}): read in a packed layout")
+        if any(st.param == param for st in launch.stage):
+            raise ScheduleError(f"stage(x{param}): already staged")
+        body = self.item_body()
+        if any(kind(x) == "Fail" for x in statements(body)):
+            raise ScheduleError(f"stage(x{param}): the item checks its input and may stop before it has "
+                                f"read the whole window")
+        base, extent, reads = stage_window(body, param)
+        itemsize = params[param].dtype.numpy.itemsize
+        fixed = [st for st in launch.stage if kind(st.extent) == "Const"] + (
+            [Staged(param, "", base, extent, params[param].dtype)] if kind(extent) == "Const" else [])
+        if sum(_align16(int(st.extent.value) * st.dtype.numpy.itemsize) for st in fixed) > MAX_STAGE_BYTES:
+            raise ScheduleError(f"stage(x{param}): {int(extent.value) * itemsize} bytes with the other windows "
+                                f"exceed {MAX_STAGE_BYTES} bytes of LDS")
+        name = f"nc_s{param}"
+        dtype = params[param].dtype
+
+        def rewrite(x):
+            if kind(x) == "Load" and x.param == param:
+                if x not in reads:
+                    raise ScheduleError(f"stage(x{param}): read outside the item")
+                return lir.Local(name, lir.Var(reads[x]), dtype)
+            return x
+
+        body = map_stmts(self.kernel.body, rewrite)
+        self.kernel = lir.Kernel(self.kernel.primitive, tuple(params), body, self.kernel.bytes_read,
+                                 self.kernel.bytes_written)
+        self.launch = replace(launch, stage=launch.stage + (Staged(param, name, base, extent, dtype),))
+        self.steps.append(f"stage x{param}")
+        return self
+
+    def vectorize(self, width: int) -> "GpuSchedule":
+        """Each thread takes ``width`` consecutive iterations of the loop spread across threads."""
+        if width not in VECTOR_WIDTHS:
+            raise ScheduleError(f"vectorize({width}): one of {VECTOR_WIDTHS}")
+        if not self.launch.grid:
+            raise ScheduleError("vectorize: bind the grid first")
+        if self.launch.workgroup:
+            raise ScheduleError("vectorize: a workgroup item spreads no loop across its threads")
+        self.launch = replace(self.launch, vector=width)
+        self.steps.append(f"vectorize {width}")
         return self
 
     def unroll(self, name: str, factor: int) -> "GpuSchedule":
@@ -336,6 +499,99 @@ class GpuSchedule:
         return kernel, self.launch
 
 
+# -- LDS staging -------------------------------------------------------------------------------
+
+
+def _align16(n: int) -> int:
+    return -(-int(n) // 16) * 16
+
+
+def _split_read(index, loops: dict, local: set):
+    """``index`` as ``(base, v)`` with ``index == base + v``, ``v`` one of ``loops``' vars and
+    ``base`` free of item-local names and of loads; None when it is not of that form."""
+    a = simplify.affine(index)
+    hits = [k for k in a.terms if kind(a.atoms[k]) == "Var" and a.atoms[k].name in loops]
+    if len(hits) != 1 or a.terms[hits[0]] != 1:
+        return None
+    rest = simplify.Affine(a.const, {k: c for k, c in a.terms.items() if k != hits[0]}, a.atoms)
+    for k in rest.terms:
+        for n in walk(rest.atoms[k]):
+            if kind(n) in ("Load", "Local") or (kind(n) == "Var" and n.name in local):
+                return None
+    return simplify.expression(rest), a.atoms[hits[0]].name
+
+
+def _reads_every_iteration(loop, param: int, base, loops: dict, local: set) -> bool:
+    """Whether each iteration of ``loop`` reads ``x{param}[base + loop.var]`` unconditionally
+    (in a statement of its own body, not of a nested loop, outside a lazily evaluated operand)."""
+    pending = list(loop.body)
+    while pending:
+        st = pending.pop()
+        if kind(st) == "Block":
+            pending += list(st.body)
+            continue
+        if kind(st) == "Loop":
+            continue
+        for x in stmt_scalars(st):
+            for n in unconditional(x):
+                if kind(n) == "Load" and n.param == param:
+                    split = _split_read(n.index, loops, local)
+                    if split is not None and split[1] == loop.var and repr(split[0]) == repr(base):
+                        return True
+    return False
+
+
+def stage_window(body, param: int) -> tuple:
+    """(base, extent, {read: loop var}) of operand ``param``'s reads in an item's ``body``, or
+    ScheduleError when they do not read one window that the item reads whole."""
+    loops = {}
+    for s in statements(body):
+        if kind(s) == "Loop":
+            if s.var in loops and repr(loops[s.var].extent) != repr(s.extent):
+                raise ScheduleError(f"stage(x{param}): two loops {s.var} of the item count to different extents")
+            loops[s.var] = s
+    local = declared(body)
+    reads = [x for x in scalars(body) if kind(x) == "Load" and x.param == param]
+    if not reads:
+        raise ScheduleError(f"stage(x{param}): the item does not read it")
+    base = extent = None
+    by_read = {}
+    for x in reads:
+        split = _split_read(x.index, loops, local)
+        if split is None:
+            raise ScheduleError(f"stage(x{param}): a read is not a base plus one of the item's loop indices")
+        b, v = split
+        e = loops[v].extent
+        if any(kind(n) in ("Var", "Load", "Local") for n in walk(e)):
+            raise ScheduleError(f"stage(x{param}): loop {v}'s extent changes from item to item")
+        if base is None:
+            base, extent = b, e
+        elif repr(b) != repr(base) or repr(e) != repr(extent):
+            raise ScheduleError(f"stage(x{param}): the reads span more than one window")
+        by_read[x] = v
+    top = [s for s in body if kind(s) == "Loop" and repr(s.extent) == repr(extent)]
+    if not any(_reads_every_iteration(s, param, base, loops, local) for s in top):
+        raise ScheduleError(f"stage(x{param}): no loop of the item reads the whole window")
+    return base, extent, by_read
+
+
+def unstage(kernel, launch) -> tuple:
+    """The same kernel reading its staged operands from memory again: (kernel, launch without
+    staging); a launch whose windows do not fit in LDS at run time takes this kernel."""
+    by_name = {st.name: st for st in launch.stage}
+
+    def rewrite(x):
+        if kind(x) == "Local" and x.name in by_name:
+            st = by_name[x.name]
+            return lir.Load(st.param, lir.Binary("add", st.base, x.index, I64), st.dtype)
+        return x
+
+    params = tuple(kernel.params)
+    body = map_stmts(kernel.body, rewrite)
+    return (lir.Kernel(kernel.primitive, params, body, kernel.bytes_read, kernel.bytes_written),
+            replace(launch, stage=()))
+
+
 # -- the default schedule ----------------------------------------------------------------
 
 
@@ -363,6 +619,145 @@ def _reads_rows_by(kernel, param: int, var: str, cols: int) -> bool:
     return all(simplify.coefficient(x.index, var) == cols for x in loads)
 
 
+def grid_loops(kernel) -> list[str]:
+    """The outermost perfectly nested loops that can be the grid: independent, and each extent
+    free of the loops outside it."""
+    names = []
+    for loop in perfect_nest(kernel.body):
+        if not independent(loop) or any(uses_var(loop.extent, n) for n in names):
+            break
+        names.append(loop.var)
+    return names
+
+
+def shared_loop(kernel, names) -> str | None:
+    """The loop a row kernel's workgroup shares: an item that ends in an independent loop that
+    stores, after statements that only compute (reductions, then the write pass)."""
+    if not names:
+        return None
+    body = tuple(perfect_nest(kernel.body)[len(names) - 1].body)
+    last = body[-1] if body else None
+    if (last is not None and kind(last) == "Loop" and len(body) > 1 and has_store((last,))
+            and not has_store(body[:-1]) and independent(last)
+            and not any(kind(x) == "Fail" for x in statements((last,)))):
+        return last.var
+    return None
+
+
+# -- the space (schedules.py:87-128: SPACES, DEFAULTS, kernel_class, apply) ---------------------
+
+# Each class's knobs and their values; the first value of each is the hand-written default's.
+SPACES: dict[str, dict[str, tuple]] = {
+    # a workgroup per item sharing its write pass: its size, its serial loops' operands staged in
+    # LDS, iterations of the shared loop per thread, the serial loops' unroll
+    "row": {"threads": (256, 64, 128, 512, 1024), "stage": (False, True), "vector": (1, 2, 4),
+            "unroll": (0, 4)},
+    # a thread per item, or (workgroup) a workgroup per item with its loops' operands staged
+    "item": {"threads": (256, 64, 128, 512, 1024), "vector": (1, 2, 4), "workgroup": (False, True),
+             "unroll": (0, 4)},
+    # no loop can be the grid: one thread runs the kernel
+    "serial": {"threads": (256,)},
+}
+DEFAULTS: dict[str, dict] = {cls: {k: v[0] for k, v in knobs.items()} for cls, knobs in SPACES.items()}
+
+
+def kernel_class(kernel) -> str:
+    names = grid_loops(kernel)
+    if not names:
+        return "serial"
+    return "row" if shared_loop(kernel, names) else "item"
+
+
+def canonical(config) -> tuple:
+    """A hashable, order-independent form of ``config``."""
+    return tuple(sorted(config.items()))
+
+
+def space(kernel) -> list[dict]:
+    """Every configuration of ``kernel``'s class, the default first, before asking which apply."""
+    knobs = SPACES[kernel_class(kernel)]
+    return [dict(zip(knobs, values)) for values in itertools.product(*knobs.values())]
+
+
+_POINTS = {cls: {canonical(dict(zip(k, v))) for v in itertools.product(*k.values())} for cls, k in SPACES.items()}
+
+
+def _serial_loops(s: "GpuSchedule") -> list[str]:
+    """The item's loops one thread runs in order, long enough to unroll: constant extent of at
+    least 8, not the shared loop, indexing no register array (those are unrolled whole)."""
+    staged = {st.name for st in s.launch.stage}
+    out = []
+    for st in statements(s.item_body()):
+        if kind(st) != "Loop" or st.var == s.launch.cooperate:
+            continue
+        if kind(st.extent) != "Const" or int(st.extent.value) < 8:
+            continue
+        arrays = any(kind(n) == "Local" and n.name not in staged for x in scalars(st.body) for n in walk(x))
+        if not arrays:
+            out.append(st.var)
+    return out
+
+
+def _reread_operands(s: "GpuSchedule") -> list[int]:
+    """Operands the item reads inside a loop that one thread runs in order (each thread, or the one
+    item thread, reads them element by element): the ones worth a copy in LDS."""
+    out = []
+    for st in statements(s.item_body()):
+        if kind(st) != "Loop" or st.var == s.launch.cooperate:
+            continue
+        for x in scalars(st.body):
+            if kind(x) == "Load" and x.param not in out:
+                out.append(x.param)
+    return sorted(out)
+
+
+def apply(kernel, calls, config) -> tuple:
+    """``kernel`` scheduled by ``config``: (kernel, Launch); ScheduleError if it does not apply.
+
+    A configuration outside its class's space is an error, never rounded to a
+    nearby point (schedules.py:187-197), and so is one whose knob has nothing
+    to act on (staging with no operand to stage, unrolling with no serial
+    loop), so each point of the space is a different kernel.
+    """
+    cls = kernel_class(kernel)
+    config = dict(config)
+    if canonical(config) not in _POINTS[cls]:
+        raise ScheduleError(f"{config} is not a point of the {cls} space")
+    s = GpuSchedule(kernel)
+    names = grid_loops(kernel)
+    if names:
+        s.grid(*names)
+    if cls == "row":
+        s.cooperate(shared_loop(kernel, names))
+    elif config.get("workgroup"):
+        s.workgroup()
+    s.block(config["threads"])
+    if cls == "item" and not config.get("workgroup"):
+        inner = names[-1]
+        for param in range(1, len(kernel.params)):
+            rc = _weight_rows(kernel, calls, param) if calls else None
+            dp4 = any(kind(x) == "Dp4" and param in (x.a.param, x.b.param) for x in scalars(kernel.body))
+            if rc and rc[0] >= WAVE and not dp4 and _reads_rows_by(kernel, param, inner, rc[1]):
+                s.pack(param, rc[0], rc[1], WAVE)
+    if config.get("stage") or config.get("workgroup"):
+        for param in _reread_operands(s):
+            try:
+                s.stage(param)
+            except ScheduleError:
+                continue
+        if not s.launch.stage:
+            raise ScheduleError("no operand of the item can be staged")
+    if config.get("vector", 1) > 1:
+        s.vectorize(config["vector"])
+    if config.get("unroll"):
+        loops = _serial_loops(s)
+        if not loops:
+            raise ScheduleError("no serial loop to unroll")
+        for var in loops:
+            s.unroll(var, config["unroll"])
+    return s.done()
+
+
 def default(kernel, calls=()) -> tuple:
     """The library's schedule for a kernel: (scheduled kernel, Launch).
 
@@ -373,32 +768,7 @@ def default(kernel, calls=()) -> tuple:
     thread per item; weights read row by row by consecutive items are packed
     in blocks of 64 rows so a wavefront's reads coalesce.
     """
-    s = GpuSchedule(kernel)
-    nest = perfect_nest(kernel.body)
-    names = []
-    for loop in nest:
-        if not independent(loop) or any(uses_var(loop.extent, n) for n in names):
-            break
-        names.append(loop.var)
-    if names:
-        s.grid(*names)
-    body = s.item_body()
-    last = body[-1] if body else None
-    if (names and last is not None and kind(last) == "Loop" and len(body) > 1 and has_store((last,))
-            and not has_store(body[:-1]) and independent(last)
-            and not any(kind(x) == "Fail" for x in statements((last,)))):
-        s.cooperate(last.var)
-        s.block(256)
-        return s.done()
-    s.block(256)
-    if names:
-        inner = names[-1]
-        for param in range(1, len(kernel.params)):
-            rc = _weight_rows(kernel, calls, param) if calls else None
-            dp4 = any(kind(x) == "Dp4" and param in (x.a.param, x.b.param) for x in scalars(kernel.body))
-            if rc and rc[0] >= WAVE and not dp4 and _reads_rows_by(kernel, param, inner, rc[1]):
-                s.pack(param, rc[0], rc[1], WAVE)
-    return s.done()
+    return apply(kernel, calls, DEFAULTS[kernel_class(kernel)])
 
 
 def schedule_program(program, fn=default):

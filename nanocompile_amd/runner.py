@@ -209,9 +209,10 @@ class HIPCompiledGraph:
       one (lir.program_from_json); ``lower(graph, fuse)`` may supply the compilation, else the
       reference's own passes are imported (the host framework a drop-in backend runs inside).
 
-    ``schedule`` is ``"default"``, a projection ``autotune.Autotuner`` (the model path), or for
-    generated code a function ``(kernel, calls) -> (kernel, Launch)`` or an object with
-    ``schedule_program(program)`` (a codegen tuner). ``bindings``, when given, must agree with the
+    ``schedule`` is ``"default"``, an ``autotune.Autotuner`` (on the model path it tunes the
+    projections; on generated code each kernel over its GPU schedule space, the reference's
+    ``CompiledGraph(graph, schedule=Autotuner())``), or for generated code a function
+    ``(kernel, calls) -> (kernel, Launch)`` or an object with ``schedule_program(program)``. ``bindings``, when given, must agree with the
     inputs' symbols (``check_arguments``); ``profile`` accumulates seconds per primitive (generated
     code) or under "qwen2_forward" (the model path, one sequence of kernels).
     """
@@ -230,14 +231,12 @@ class HIPCompiledGraph:
             except NotImplementedError:
                 pass
         if self.path == "codegen":
-            from nanocompile_amd import autotune
             from nanocompile_amd.compiled import CompiledProgram
             if program is None:
                 if graph is None:
                     raise ValueError("HIPCompiledGraph needs a graph or a compiled program")
                 program = lower(graph, fuse) if lower is not None else _reference_compile(graph, fuse)
-            codegen_schedule = "default" if isinstance(schedule, autotune.Autotuner) else schedule
-            self.program = CompiledProgram(program, schedule=codegen_schedule, device=device)
+            self.program = CompiledProgram(program, schedule=schedule, device=device)
 
     def __call__(self, inputs: Mapping[str, np.ndarray], weights: Mapping[str, np.ndarray],
                  bindings: Mapping[str, int] | None = None, profile: dict[str, float] | None = None) -> dict:

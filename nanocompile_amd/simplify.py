@@ -153,6 +153,11 @@ def _build(a: Affine):
     return out
 
 
+def expression(a: Affine):
+    """An integer expression with the value of the affine form ``a``."""
+    return _build(a)
+
+
 def _range_of_affine(a: Affine, ranges) -> tuple:
     lo = hi = a.const
     for key, c in a.terms.items():

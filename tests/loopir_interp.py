@@ -180,7 +180,8 @@ class _Py:
                 out.append(f"{pad}if {c}:")
                 out.append(f"{pad}    return {s.code}")
             elif k == "Array":
-                out.append(f"{pad}{s.name} = [{self.const(s.init)}] * {s.size}")
+                size = s.size if isinstance(s.size, int) else f"int({self.x(s.size)[0]})"
+                out.append(f"{pad}{s.name} = [{self.const(s.init)}] * {size}")
             elif k == "ArrayStore":
                 idx, _ = self.x(s.index)
                 val, t = self.x(s.value)
@@ -243,10 +244,33 @@ def compile_kernel(kernel):
     return lambda X, S: fn(X, S, consts)
 
 
+def staged_ir(kernel, launch):
+    """A staged kernel as plain loop IR: each item first copies its windows into local arrays of
+    the windows' extents (``x{param}[base + c]`` for each ``c`` below the extent, every read
+    bounds-checked, as the workgroup's copy into LDS reads them), then runs the item."""
+    if not launch.stage:
+        return kernel
+    prefix = []
+    for st in launch.stage:
+        c = lir.Var("nc_c")
+        prefix.append(lir.Array(st.name, st.extent, lir.Const(0.0 if st.dtype.name == "f32" else 0, st.dtype)))
+        prefix.append(lir.Loop("nc_c", st.extent, (lir.ArrayStore(
+            st.name, c, lir.Load(st.param, lir.Binary("add", st.base, c, lir.DType("i64")), st.dtype)),)))
+
+    def wrap(stmts, depth):
+        if depth == len(launch.grid):
+            return tuple(prefix) + tuple(stmts)
+        loop = stmts[0]
+        return (lir.Loop(loop.var, loop.extent, wrap(loop.body, depth + 1), loop.kind),)
+
+    return lir.Kernel(kernel.primitive, kernel.params, wrap(tuple(kernel.body), 0), kernel.bytes_read,
+                      kernel.bytes_written)
+
+
 def run(program, scheduled, inputs, weights, bound) -> dict:
     """Run ``program`` with its scheduled kernels [(kernel, Launch)] on the CPU; outputs by name.
-    A Fail returns ('fail', call index, code)."""
-    fns = [compile_kernel(k) for k, _ in scheduled]
+    A staged launch runs as ``staged_ir`` writes it. A Fail returns ('fail', call index, code)."""
+    fns = [compile_kernel(staged_ir(k, launch)) for k, launch in scheduled]
     store = {}
     for buf in program.buffers:
         shape = lir.shape_of(buf.shape, bound)

@@ -121,15 +121,29 @@ class Driver:
         return out
 
 
+def candidate_programs() -> list[tuple[str, str]]:
+    """(zoo name, variant) of the programs whose every schedule candidate the GPU tests run and
+    tune: each zoo graph as fused, and config 2's graph unfused (a kernel per operation)."""
+    return [(n, "program") for n in zoo_names()] + [("rms_norm_quant", "unfused")]
+
+
 def prebuild(jobs: int = 8) -> int:
-    """Build every recorded program's library (default GPU schedules) into the codegen cache,
+    """Build every recorded program's library (default GPU schedules), and the candidate
+    libraries of ``candidate_programs`` (every schedule of every kernel), into the codegen cache,
     in parallel, so that GPU runs find them built; returns how many were compiled afresh."""
     from concurrent.futures import ThreadPoolExecutor
 
-    from nanocompile_amd import compiled
+    from nanocompile_amd import autotune, codegen_hip, compiled
     doc, _ = fixture()
     progs = [zoo(n, v) for n in zoo_names() for v in ("program", "unfused", "scheduled")]
     progs += [qwen2(tag, which) for tag, entry in doc["qwen2"].items() for which in entry if which != "weight_names"]
+    libraries = [autotune.CandidateLibrary(zoo(n, v)) for n, v in candidate_programs()]
     with ThreadPoolExecutor(max_workers=jobs) as pool:
         results = list(pool.map(compiled.prebuild, progs))
+        results += list(pool.map(lambda library: library.build(), libraries))
+    # libraries of sources no longer generated would only travel to the GPU with the tree
+    keep = {path.name for path, _ in results}
+    for stale in codegen_hip.cache_dir().glob("nc_hip_*.so"):
+        if stale.name not in keep:
+            stale.unlink()
     return sum(1 for _, cached in results if not cached)

@@ -217,3 +217,164 @@ def test_json_programs_read_back_whole():
     gathers = [call for call in program.calls if call.gather]
     assert gathers and gathers[0].gather["ids_input"] == "token_ids"
     assert lir.evaluate(program.calls[0].operands[0].shape[0], {"seq": 5, "past": 2}) == 5
+
+
+# -- the schedule space: LDS staging, workgroup items, vector width ------------------------------
+
+
+def _calls_of(program):
+    out = {}
+    for call in program.calls:
+        out.setdefault(call.kernel, []).append(call)
+    return out
+
+
+def _staged_everywhere(program):
+    """Each kernel with its operands staged where it can be (a row kernel's serial reads, or an
+    item kernel as a workgroup), else the default; and how many were staged."""
+    calls, out, staged = _calls_of(program), [], 0
+    for i, kernel in enumerate(program.kernels):
+        cls = gpu_schedule.kernel_class(kernel)
+        config = dict(gpu_schedule.DEFAULTS[cls])
+        config.update({"row": {"stage": True, "vector": 4}, "item": {"workgroup": True}}.get(cls, {}))
+        try:
+            out.append(gpu_schedule.apply(kernel, calls.get(i, []), config))
+            staged += 1
+        except gpu_schedule.ScheduleError:
+            out.append(gpu_schedule.default(kernel, calls.get(i, [])))
+    return out, staged
+
+
+@pytest.mark.parametrize("variant", ["program", "unfused", "scheduled"])
+@pytest.mark.parametrize("name", P.zoo_names())
+def test_staged_kernels_compute_the_references_outputs(name, variant):
+    """Staging rewrites reads to LDS windows: run with each window copied first (every copy read
+    bounds-checked), the program still gives the reference C's outputs."""
+    program = P.zoo(name, variant)
+    scheduled, _ = _staged_everywhere(program)
+    cases, weights = P.zoo_cases(name)
+    for inputs, want, error in cases:
+        got = I.run(program, scheduled, inputs, weights, I.bind(program, inputs))
+        if error is not None:
+            assert isinstance(got, tuple) and got[0] == "fail" and got[2] == 1, got
+        else:
+            close(name, got, want)
+
+
+def test_staging_reaches_the_row_and_reduction_kernels():
+    scheduled, staged = _staged_everywhere(P.zoo("rms_norm_quant"))
+    assert staged == 2
+    row, reduce = scheduled[0][1], scheduled[1][1]
+    assert row.cooperate == "j0" and [st.param for st in row.stage] == [1]       # x, not gamma (read once)
+    assert reduce.workgroup and [st.param for st in reduce.stage] == [1]
+    st = row.stage[0]
+    assert st.extent == c(896) and simplify.coefficient(st.base, "i0") == 896
+    reads = [x for x in gpu_schedule.scalars(scheduled[0][0].body) if type(x).__name__ in ("Load", "Local")]
+    assert {(type(x).__name__, getattr(x, "param", getattr(x, "name", None))) for x in reads} == {
+        ("Local", "nc_s1"), ("Load", 2)}
+    plain, launch = gpu_schedule.unstage(*scheduled[0])
+    assert launch.stage == () and not any(type(x).__name__ == "Local" for x in gpu_schedule.scalars(plain.body))
+
+
+def test_stage_refuses_what_would_read_past_the_window():
+    program = P.zoo("rms_norm_quant")
+    row, reduce, quant = program.kernels[0], program.kernels[1], program.kernels[3]
+    with pytest.raises(gpu_schedule.ScheduleError, match="workgroup"):
+        gpu_schedule.GpuSchedule(reduce).grid("i0").stage(1)               # a thread per item
+    s = gpu_schedule.GpuSchedule(row).grid("i0").cooperate("j0")
+    with pytest.raises(gpu_schedule.ScheduleError, match="not an operand"):
+        s.stage(0)
+    s.stage(1)
+    with pytest.raises(gpu_schedule.ScheduleError, match="already"):
+        s.stage(1)
+    # x2[i0], a per-row scale, is read at no loop index of the item
+    with pytest.raises(gpu_schedule.ScheduleError, match="loop indices|does not read"):
+        gpu_schedule.GpuSchedule(quant).grid("i0").workgroup().stage(2)
+    f32 = lir.DType("f32")
+    params = (lir.Param(f32, True), lir.Param(f32, False))
+    # the only read sits in the untaken arm of a select: the unscheduled kernel may read nothing
+    lazy = lir.Kernel("row", params, (lir.Loop("i0", c(4), (
+        lir.Let("acc", lir.Const(0.0, f32)),
+        lir.Loop("r", c(8), (lir.Assign("acc", lir.Select(lir.Binary("lt", v("r"), c(0), lir.DType("bool")),
+                                                          lir.Load(1, b("add", b("mul", v("i0"), c(8)), v("r")), f32),
+                                                          lir.Var("acc", f32), f32)),)),
+        lir.Store(0, v("i0"), lir.Var("acc", f32)))),))
+    s = gpu_schedule.GpuSchedule(lazy).grid("i0").workgroup()
+    with pytest.raises(gpu_schedule.ScheduleError, match="whole window"):
+        s.stage(1)
+    # two windows of one operand
+    two = lir.Kernel("row", params, (lir.Loop("i0", c(4), (
+        lir.Let("acc", lir.Const(0.0, f32)),
+        lir.Loop("r", c(8), (lir.Assign("acc", lir.Binary("add", lir.Load(1, v("r"), f32),
+                                                          lir.Load(1, b("add", v("r"), c(8)), f32), f32)),)),
+        lir.Store(0, v("i0"), lir.Var("acc", f32)))),))
+    with pytest.raises(gpu_schedule.ScheduleError, match="more than one window"):
+        gpu_schedule.GpuSchedule(two).grid("i0").workgroup().stage(1)
+
+
+def test_workgroup_and_vectorize_compose_only_where_they_mean_something():
+    program = P.zoo("rms_norm_quant")
+    row, reduce = program.kernels[0], program.kernels[1]
+    with pytest.raises(gpu_schedule.ScheduleError, match="shares a loop"):
+        gpu_schedule.GpuSchedule(row).grid("i0").cooperate("j0").workgroup()
+    with pytest.raises(gpu_schedule.ScheduleError, match="vectorized"):
+        gpu_schedule.GpuSchedule(reduce).grid("i0").vectorize(4).workgroup()
+    with pytest.raises(gpu_schedule.ScheduleError, match="spreads no loop"):
+        gpu_schedule.GpuSchedule(reduce).grid("i0").workgroup().vectorize(4)
+    with pytest.raises(gpu_schedule.ScheduleError, match="one of"):
+        gpu_schedule.GpuSchedule(reduce).grid("i0").vectorize(3)
+
+
+def test_space_starts_at_the_default_and_refuses_points_outside_it():
+    program = P.zoo("rms_norm_quant")
+    calls = _calls_of(program)
+    for i, kernel in enumerate(program.kernels):
+        cls = gpu_schedule.kernel_class(kernel)
+        points = gpu_schedule.space(kernel)
+        assert points[0] == gpu_schedule.DEFAULTS[cls]
+        assert len({gpu_schedule.canonical(p) for p in points}) == len(points)
+        assert gpu_schedule.apply(kernel, calls[i], points[0]) == gpu_schedule.default(kernel, calls[i])
+    row = program.kernels[0]
+    assert gpu_schedule.kernel_class(row) == "row"
+    with pytest.raises(gpu_schedule.ScheduleError, match="not a point"):
+        gpu_schedule.apply(row, calls[0], {"threads": 96, "stage": False, "vector": 1, "unroll": 0})
+    with pytest.raises(gpu_schedule.ScheduleError, match="not a point"):
+        gpu_schedule.apply(row, calls[0], {"threads": 256, "workgroup": True, "vector": 1, "unroll": 0})
+    elementwise = program.kernels[2]
+    with pytest.raises(gpu_schedule.ScheduleError, match="unroll"):
+        gpu_schedule.apply(elementwise, calls[2], {"threads": 256, "vector": 1, "workgroup": False, "unroll": 4})
+
+
+def test_candidate_library_holds_each_distinct_kernel_once_and_reports_failures_as_its_kernel():
+    from nanocompile_amd import autotune
+    program = P.zoo("gather")
+    library = autotune.CandidateLibrary(program)
+    entries = [n for per in library.entry for n in per]
+    assert entries == list(range(len(entries)))
+    for i, cands in enumerate(library.candidates):
+        assert cands[0].config == gpu_schedule.DEFAULTS[gpu_schedule.kernel_class(program.kernels[i])]
+        assert len({c.source for c in cands}) == len(cands)
+        for n in library.entry[i]:
+            assert f"NC_EXPORT int32_t nc_k{n}(void **p, const int64_t *s)" in library.source
+    gather = next(i for i, k in enumerate(program.kernels) if k.primitive == "gather")
+    codes = {int(x) for x in __import__("re").findall(r"nc_fail\(nc_err, (\d+)\)", library.source)}
+    assert codes and all((code >> 8) - 1 == gather for code in codes)
+    scheduled, source, names = library.choice([len(c) - 1 for c in library.candidates])
+    assert source == library.source and names == [f"nc_k{per[-1]}" for per in library.entry]
+
+
+def test_vectorized_items_are_unrolled_without_checks_only_when_whole():
+    program = P.zoo("rms_norm_quant")
+    calls = _calls_of(program)
+    kernel, launch = gpu_schedule.apply(program.kernels[3], calls[3],
+                                        {"threads": 64, "vector": 4, "workgroup": False, "unroll": 0})
+    text = codegen_hip.render_kernel(kernel, launch, 3)
+    assert "const int64_t nc_q1 = (nc_e1 + 3) / 4;" in text
+    assert "if (nc_i1 * 4 + 4 <= nc_e1) {" in text and "#pragma unroll" in text
+    assert text.count("const int64_t nc_items = nc_e0 * nc_q1;") == 2          # kernel and launcher agree
+    row, rl = gpu_schedule.apply(program.kernels[0], calls[0], {"threads": 128, "stage": True, "vector": 2,
+                                                                 "unroll": 4})
+    text = codegen_hip.render_kernel(row, rl, 0)
+    assert "extern __shared__" in text and text.count("__syncthreads();") == 2      # after the copy, after the item
+    assert "nc_g0_unstaged" in text and f"if (nc_lds > {gpu_schedule.MAX_STAGE_BYTES})" in text
+    assert "#pragma unroll 4" in text
