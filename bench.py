@@ -304,6 +304,55 @@ def graph_us(fn, reps: int, rounds: int = 5) -> float:
     return statistics.median(samples)
 
 
+def generated_config2(cache=None) -> tuple[dict, dict]:
+    """Config 2's graph (rms_norm, then one int8 scale per row, in the reference's graph ops) as
+    the reference compiles it, recorded as data (tests/golden/programs.json.gz) and generated as
+    HIP by codegen_hip: unfused (its lowering with fuse=False, a kernel per operation,
+    runtime.py:186) and fused (its fusion pass), each on the default GPU schedules and with each
+    kernel's schedule (threads, LDS staging, workgroup items, vector width, unroll) chosen by the
+    autotuner on 1, 64 and 512 rows, per token (``cache``: the autotuner's). Both run from the
+    program's candidate library, so every kernel in a trace has its own name. Returns
+    ({variant: CompiledProgram}, the tuned schedules by variant)."""
+    from nanocompile_amd import autotune, lir
+    from nanocompile_amd.compiled import CompiledProgram
+    golden = Path(__file__).resolve().parent / "tests" / "golden"
+    doc = lir.load_programs(golden / "programs.json.gz")
+    with np.load(golden / "programs.npz", allow_pickle=False) as arrays:
+        recorded = {variant: lir.program_from_json(doc["zoo"]["rms_norm_quant"][key], arrays)
+                    for variant, key in (("unfused", "unfused"), ("fused", "program"))}
+    generated = {}
+    for variant, program in recorded.items():
+        library = autotune.CandidateLibrary(program)
+        generated[variant] = CompiledProgram(program, autotune.Chosen(library, [0] * len(library.candidates)))
+    tuner = autotune.Autotuner(cache=cache, workloads=[(f"m{m}", {"seq": m}, 1.0 / m) for m in (1, 64, 512)])
+    tuned_schedules = {}
+    for variant, program in recorded.items():
+        first = len(tuner.records)
+        generated[f"{variant}_tuned"] = CompiledProgram(program, schedule=tuner)
+        tuned_schedules[variant] = {f"kernel {r.shape[0]} ({r.op})": {
+            "config": r.config, "speedup": round(r.speedup or 1.0, 3)} for r in tuner.records[first:]}
+    return generated, tuned_schedules
+
+
+def generated_kernels(rows: int = 512, reps: int = 20, seed: int = 7) -> dict:
+    """Config 2's generated programs (default and tuned) launched eagerly ``reps`` times at
+    ``rows`` rows, for a kernel trace; returns each kernel's launcher and schedule by variant."""
+    from nanocompile_amd import hip
+    generated, tuned = generated_config2(cache=True)
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((rows, 896)).astype(np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(896)).astype(np.float32)
+    out = {}
+    for variant, program in generated.items():
+        launch, _, _ = program.prepare({"x": x}, {"w": gamma})
+        for _ in range(reps):
+            launch()
+        hip.sync()
+        out[variant] = [{"launcher": name, "device": "nc_g" + name[4:], "schedule": launch_.describe()}
+                        for name, (_, launch_) in zip(program.launcher_names, program.scheduled)]
+    return {"rows": rows, "reps": reps, "kernels": out, "tuned": tuned}
+
+
 def block_measurements(model, seed: int = 7) -> dict:
     """Configs 2, 3 and 4 on the decode model's own weights (24 layers, so weights stream as in the model)."""
     from nanocompile_amd import hip
@@ -328,28 +377,8 @@ def block_measurements(model, seed: int = 7) -> dict:
         us = graph_us(lambda i: hip.call("nc_rms_norm_quant", [normed, xq, xs, xd, gamma], [m, H, eps]), 32)
         rows[str(m)] = {"us": round(us, 3), "bytes": rms_row_bytes(m, H),
                         "gbps": round(rms_row_bytes(m, H) / (us * 1e-6) / 1e9, 1)}
-    # the same rows through the reference's own compilation of config 2's graph (rms_norm, then one
-    # int8 scale per row, in its graph ops), recorded from the reference as data
-    # (tests/golden/programs.json.gz) and generated as HIP by codegen_hip: unfused (its lowering with
-    # fuse=False, a kernel per operation, runtime.py:186) and fused (its fusion pass)
-    from nanocompile_amd import lir
-    from nanocompile_amd.compiled import CompiledProgram
-    golden = Path(__file__).resolve().parent / "tests" / "golden"
-    doc = lir.load_programs(golden / "programs.json.gz")
-    from nanocompile_amd import autotune
-    with np.load(golden / "programs.npz", allow_pickle=False) as arrays:
-        recorded = {variant: lir.program_from_json(doc["zoo"]["rms_norm_quant"][key], arrays)
-                    for variant, key in (("unfused", "unfused"), ("fused", "program"))}
-    generated = {variant: CompiledProgram(program) for variant, program in recorded.items()}
-    # the same programs with each kernel's GPU schedule (threads, LDS staging, workgroup items,
-    # vector width, unroll) chosen by the autotuner on these three row counts, per token
-    tuner = autotune.Autotuner(cache=None, workloads=[(f"m{m}", {"seq": m}, 1.0 / m) for m in (1, 64, 512)])
-    tuned_schedules = {}
-    for variant, program in recorded.items():
-        first = len(tuner.records)
-        generated[f"{variant}_tuned"] = CompiledProgram(program, schedule=tuner)
-        tuned_schedules[variant] = {f"kernel {r.shape[0]} ({r.op})": {
-            "config": r.config, "speedup": round(r.speedup or 1.0, 3)} for r in tuner.records[first:]}
+    # the same rows through the reference's own compilation of config 2's graph
+    generated, tuned_schedules = generated_config2()
     gamma_host = gamma.numpy()
     for m in (1, 64, 512):
         x = rng.standard_normal((m, H)).astype(np.float32)
@@ -603,8 +632,9 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=NEW_TOKENS - 1)
     parser.add_argument("--warmup", type=int, default=1)
-    parser.add_argument("--workload", choices=("decode", "gemv", "kernels"), default="decode",
-                        help="kernels: each decode-step kernel launched eagerly at past 383 (for counter passes)")
+    parser.add_argument("--workload", choices=("decode", "gemv", "kernels", "generated"), default="decode",
+                        help="kernels: each decode-step kernel launched eagerly at past 383 (for counter passes); "
+                             "generated: config 2's generated programs, default and tuned, launched eagerly")
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-blocks", action="store_true", help="skip the per-block measurements (configs 2-4)")
     parser.add_argument("--no-graph", action="store_true",
@@ -625,6 +655,10 @@ def main() -> int:
     hip.sync()
     del src, dst
 
+    if args.workload == "generated":
+        print(json.dumps({"workload": "config 2's generated programs at 512 rows, eager",
+                          **generated_kernels()}), flush=True)
+        return 0
     if args.workload == "kernels":
         print(json.dumps({"workload": "config 5's decode-step kernels, eager, past 383",
                           "kernels": decode_kernels()}), flush=True)

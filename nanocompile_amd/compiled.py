@@ -183,6 +183,7 @@ class CompiledProgram:
         bind = self._library.nc_bind_stream
         bind.argtypes, bind.restype = [ctypes.c_void_p, ctypes.c_void_p], None
         bind(hip.load().nc_stream_handle(), hip.load().nc_error_word())
+        self.launcher_names = list(names)
         self._launch = [KERNEL_TYPE((name, self._library)) for name in names]
         self._last_use = program.last_uses()
         self.symbols = tuple(program.symbols)

@@ -25,6 +25,12 @@ space. A GPU launch binds loops to the grid instead of to a thread pool:
   window ``x[base, base + E)`` into LDS with coalesced loads once per item,
   and the reads go to LDS (a row read by every thread of a workgroup, or by
   one thread in order, leaves HBM once and at full width).
+* ``lead()``: in a workgroup item, one wave computes the item's serial part
+  (a row kernel's reductions before the shared loop, or a workgroup item's
+  whole body) and the other waves wait at a barrier, then read the values the
+  shared loop needs from LDS: the same values, computed once per workgroup
+  instead of once per wave, so the waves no longer compete for issue slots
+  with identical chains.
 * ``vectorize(width)``: each thread takes ``width`` consecutive iterations of
   the loop spread across threads (the innermost grid loop, or the shared
   loop), so neighbouring reads and writes sit in one thread and can be
@@ -293,6 +299,7 @@ class Launch:
     workgroup: bool = False                # one workgroup per item with no shared loop; thread 0 stores
     stage: tuple[Staged, ...] = ()         # operand windows staged in LDS per item
     vector: int = 1                        # consecutive iterations per thread of the loop spread across threads
+    lead: bool = False                     # one wave computes the item's serial part, shared through LDS
 
     @property
     def per_workgroup(self) -> bool:
@@ -306,6 +313,8 @@ class Launch:
         if self.workgroup:
             parts.append("workgroup()")
         parts += [f"stage(x{st.param})" for st in self.stage]
+        if self.lead:
+            parts.append("lead()")
         if self.vector > 1:
             parts.append(f"vectorize({self.vector})")
         parts += [f"unroll({v}, {n})" for v, n in self.unroll]
@@ -439,6 +448,23 @@ class GpuSchedule:
         self.steps.append(f"stage x{param}")
         return self
 
+    def lead(self) -> "GpuSchedule":
+        """One wave computes the item's serial part; with a shared loop, the values it reads from
+        that part reach the other waves through LDS after a barrier."""
+        launch = self.launch
+        if not launch.per_workgroup:
+            raise ScheduleError("lead: an item must be a workgroup (cooperate or workgroup)")
+        body = self.item_body()
+        serial = body[:-1] if launch.cooperate else body
+        if any(kind(x) == "Fail" for x in statements(serial)):
+            # a failing wave returns; the others would wait at the barrier for it
+            raise ScheduleError("lead: the serial part checks its input and may stop one wave early")
+        if launch.cooperate and live_ins(body[:-1], body[-1]) is None:
+            raise ScheduleError("lead: the shared loop reads an array the serial part fills")
+        self.launch = replace(launch, lead=True)
+        self.steps.append("lead")
+        return self
+
     def vectorize(self, width: int) -> "GpuSchedule":
         """Each thread takes ``width`` consecutive iterations of the loop spread across threads."""
         if width not in VECTOR_WIDTHS:
@@ -500,6 +526,22 @@ class GpuSchedule:
 
 
 # -- LDS staging -------------------------------------------------------------------------------
+
+
+def live_ins(before, shared) -> list[tuple[str, object]] | None:
+    """The scalars the shared loop reads that the statements before it declare (their top-level
+    Lets, in order), with their types; None if it reads an array they declare."""
+    used = set()
+    for x in scalars((shared,)):
+        for n in walk(x):
+            if kind(n) == "Var":
+                used.add(n.name)
+            elif kind(n) == "Local":
+                used.add(n.name)
+    used |= {s.name for s in statements((shared,)) if kind(s) == "ArrayStore"}
+    if any(kind(s) == "Array" and s.name in used for s in statements(before)):
+        return None
+    return [(s.var, s.value.dtype) for s in before if kind(s) == "Let" and s.var in used]
 
 
 def _align16(n: int) -> int:
@@ -651,10 +693,10 @@ SPACES: dict[str, dict[str, tuple]] = {
     # a workgroup per item sharing its write pass: its size, its serial loops' operands staged in
     # LDS, iterations of the shared loop per thread, the serial loops' unroll
     "row": {"threads": (256, 64, 128, 512, 1024), "stage": (False, True), "vector": (1, 2, 4),
-            "unroll": (0, 4)},
+            "unroll": (0, 4), "lead": (False, True)},
     # a thread per item, or (workgroup) a workgroup per item with its loops' operands staged
     "item": {"threads": (256, 64, 128, 512, 1024), "vector": (1, 2, 4), "workgroup": (False, True),
-             "unroll": (0, 4)},
+             "unroll": (0, 4), "lead": (False, True)},
     # no loop can be the grid: one thread runs the kernel
     "serial": {"threads": (256,)},
 }
@@ -747,6 +789,8 @@ def apply(kernel, calls, config) -> tuple:
                 continue
         if not s.launch.stage:
             raise ScheduleError("no operand of the item can be staged")
+    if config.get("lead"):
+        s.lead()
     if config.get("vector", 1) > 1:
         s.vectorize(config["vector"])
     if config.get("unroll"):

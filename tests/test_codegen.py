@@ -342,7 +342,8 @@ def test_space_starts_at_the_default_and_refuses_points_outside_it():
         gpu_schedule.apply(row, calls[0], {"threads": 256, "workgroup": True, "vector": 1, "unroll": 0})
     elementwise = program.kernels[2]
     with pytest.raises(gpu_schedule.ScheduleError, match="unroll"):
-        gpu_schedule.apply(elementwise, calls[2], {"threads": 256, "vector": 1, "workgroup": False, "unroll": 4})
+        gpu_schedule.apply(elementwise, calls[2], {"threads": 256, "vector": 1, "workgroup": False, "unroll": 4,
+                                                              "lead": False})
 
 
 def test_candidate_library_holds_each_distinct_kernel_once_and_reports_failures_as_its_kernel():
@@ -367,14 +368,39 @@ def test_vectorized_items_are_unrolled_without_checks_only_when_whole():
     program = P.zoo("rms_norm_quant")
     calls = _calls_of(program)
     kernel, launch = gpu_schedule.apply(program.kernels[3], calls[3],
-                                        {"threads": 64, "vector": 4, "workgroup": False, "unroll": 0})
+                                        {"threads": 64, "vector": 4, "workgroup": False, "unroll": 0,
+                                         "lead": False})
     text = codegen_hip.render_kernel(kernel, launch, 3)
     assert "const int64_t nc_q1 = (nc_e1 + 3) / 4;" in text
     assert "if (nc_i1 * 4 + 4 <= nc_e1) {" in text and "#pragma unroll" in text
     assert text.count("const int64_t nc_items = nc_e0 * nc_q1;") == 2          # kernel and launcher agree
     row, rl = gpu_schedule.apply(program.kernels[0], calls[0], {"threads": 128, "stage": True, "vector": 2,
-                                                                 "unroll": 4})
+                                                                 "unroll": 4, "lead": False})
     text = codegen_hip.render_kernel(row, rl, 0)
     assert "extern __shared__" in text and text.count("__syncthreads();") == 2      # after the copy, after the item
     assert "nc_g0_unstaged" in text and f"if (nc_lds > {gpu_schedule.MAX_STAGE_BYTES})" in text
     assert "#pragma unroll 4" in text
+
+
+def test_lead_shares_the_serial_parts_values_and_refuses_a_failing_serial_part():
+    program = P.zoo("rms_norm_quant")
+    calls = _calls_of(program)
+    row, rl = gpu_schedule.apply(program.kernels[0], calls[0], {"threads": 256, "stage": False, "vector": 1,
+                                                                 "unroll": 0, "lead": True})
+    body = gpu_schedule.perfect_nest(row.body)[0].body
+    assert [name for name, _ in gpu_schedule.live_ins(body[:-1], body[-1])] == ["acc0"]
+    text = codegen_hip.render_kernel(row, rl, 0)
+    assert "__shared__ float nc_lead_f32[1];" in text and "const float acc0 = nc_lead_f32[0];" in text
+    assert text.count("__syncthreads();") == 2                   # after the lead wave, after the item
+    with pytest.raises(gpu_schedule.ScheduleError, match="workgroup"):
+        gpu_schedule.GpuSchedule(program.kernels[1]).grid("i0").lead()
+    gather = P.zoo("gather")
+    k = next(k for k in gather.kernels if k.primitive == "gather")
+    s = gpu_schedule.GpuSchedule(k)
+    s.grid(*gpu_schedule.grid_loops(k)[:1])
+    if gpu_schedule.shared_loop(k, s.launch.grid):
+        s.cooperate(gpu_schedule.shared_loop(k, s.launch.grid))
+    else:
+        s.workgroup()
+    with pytest.raises(gpu_schedule.ScheduleError, match="stop one wave"):
+        s.lead()
