@@ -464,6 +464,11 @@ class CandidateLibrary:
         self.program = program
         self.calls_of = calls_of
         self.candidates = [kernel_candidates(k, calls_of.get(i, [])) for i, k in enumerate(program.kernels)]
+        for i, cands in enumerate(self.candidates):
+            layouts = {tuple(p.packed for p in c.kernel.params) for c in cands}
+            if len(layouts) != 1:
+                # the tuner runs every candidate on the default's arguments
+                raise TuningError(f"kernel {i}: candidates read their operands in different layouts {layouts}")
         scheduled, owners, self.entry = [], [], []
         for i, cands in enumerate(self.candidates):
             self.entry.append([])

@@ -774,7 +774,9 @@ def apply(kernel, calls, config) -> tuple:
     elif config.get("workgroup"):
         s.workgroup()
     s.block(config["threads"])
-    if cls == "item" and not config.get("workgroup"):
+    if cls == "item":
+        # the same operands packed at every point of the space, so that one set of arguments
+        # (the default's) serves every candidate of the kernel
         inner = names[-1]
         for param in range(1, len(kernel.params)):
             rc = _weight_rows(kernel, calls, param) if calls else None

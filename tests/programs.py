@@ -127,6 +127,11 @@ def candidate_programs() -> list[tuple[str, str]]:
     return [(n, "program") for n in zoo_names()] + [("rms_norm_quant", "unfused")]
 
 
+def candidate_models() -> list[tuple[str, str]]:
+    """(mode, which) of the tiny Qwen2 programs the GPU tests tune (every kernel's candidates)."""
+    return [("int8", "full"), ("int8", "last")]
+
+
 def prebuild(jobs: int = 8) -> int:
     """Build every recorded program's library (default GPU schedules), and the candidate
     libraries of ``candidate_programs`` (every schedule of every kernel), into the codegen cache,
@@ -138,6 +143,7 @@ def prebuild(jobs: int = 8) -> int:
     progs = [zoo(n, v) for n in zoo_names() for v in ("program", "unfused", "scheduled")]
     progs += [qwen2(tag, which) for tag, entry in doc["qwen2"].items() for which in entry if which != "weight_names"]
     libraries = [autotune.CandidateLibrary(zoo(n, v)) for n, v in candidate_programs()]
+    libraries += [autotune.CandidateLibrary(qwen2(tag, which)) for tag, which in candidate_models()]
     with ThreadPoolExecutor(max_workers=jobs) as pool:
         results = list(pool.map(compiled.prebuild, progs))
         results += list(pool.map(lambda library: library.build(), libraries))

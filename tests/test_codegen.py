@@ -404,3 +404,15 @@ def test_lead_shares_the_serial_parts_values_and_refuses_a_failing_serial_part()
         s.workgroup()
     with pytest.raises(gpu_schedule.ScheduleError, match="stop one wave"):
         s.lead()
+
+
+def test_every_candidate_of_a_kernel_reads_its_operands_in_one_layout():
+    """The tuner runs every candidate on the default's arguments, packed weights included."""
+    from nanocompile_amd import autotune
+    packed = 0
+    for program in (P.qwen2("int8", "full"), P.zoo("mlp_int8_64"), P.zoo("linear")):
+        library = autotune.CandidateLibrary(program)
+        for cands in library.candidates:
+            assert len({tuple(p.packed for p in c.kernel.params) for c in cands}) == 1
+            packed += any(p.packed for p in cands[0].kernel.params)
+    assert packed

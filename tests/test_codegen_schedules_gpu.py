@@ -94,3 +94,24 @@ def test_tuner_checks_every_candidate_and_its_choice_is_the_references_c(gpu, tm
     CompiledProgram(P.zoo(name, variant), schedule=again)
     assert again.records and all(r.cached for r in again.records)
     assert [r.config for r in again.records] == [r.config for r in tuned]
+
+
+def test_tuned_tiny_qwen2_greedy_tokens_and_logits_are_golden(gpu, tmp_path):
+    """The tiny Qwen2 (int8 mode) with every generated kernel tuned over its schedule space on the
+    reference's decode and prefill workloads: golden G5's greedy tokens, and its logits to the
+    same tolerance as the default schedules."""
+    from nanocompile_amd import autotune
+    from nanocompile_amd.compiled import CompiledProgram
+    tuner = autotune.Autotuner(rounds=2, reps=4, cache=tmp_path / "tuning.json")
+    compiled = {which: CompiledProgram(P.qwen2(tag, which), schedule=tuner) for tag, which in P.candidate_models()}
+    assert tuner.records and all(r.config is not None for r in tuner.records)
+    print(f"tuned {len(tuner.records)} kernels, {sum(r.winner != 0 for r in tuner.records)} off their defaults",
+          flush=True)
+    weights = P.qwen2_weights("int8")
+    driver = P.Driver(lambda which, inputs: compiled[which](inputs, weights))
+    golden = np.load(P.GOLDEN / "golden.npz")
+    for i, prompt in enumerate(P.PROMPTS):
+        assert driver.greedy(prompt, 8) == list(golden[f"g5_int8_tokens_{i}"]), prompt
+    ids = P.PROMPTS[3]
+    want = golden["g5_int8_logits"]
+    np.testing.assert_allclose(driver.forward(ids), want, rtol=0, atol=1e-5 * np.abs(want).max())
