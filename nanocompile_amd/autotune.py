@@ -1,4 +1,5 @@
-"""GPU autotuning of the int8 projections: each shape's schedule chosen by measurement.
+"""GPU autotuning: each int8 projection shape's schedule, and each generated kernel's GPU
+schedule, chosen by measurement.
 
 The reference tunes each generated C kernel over a space of CPU schedules
 (autotune.py:1-53): candidates timed in alternation, medians over rounds,
@@ -33,6 +34,12 @@ keeps those rules for the GPU library:
   versions, CU count) and by problem (op, M, N, K, the space, and the
   library's digest of its kernel sources and flags, so a rebuilt kernel is
   measured afresh).
+
+Generated kernels (codegen_hip) are tuned the same way over the code
+generator's schedule space (gpu_schedule.space: workgroup size, LDS staging,
+workgroup items with one lead wave, vector width, unroll), per kernel of a
+program, on weighted workloads of symbol values as the reference does
+(``Autotuner.schedule_program``; see ``tune_program``).
 """
 
 from __future__ import annotations
@@ -529,8 +536,6 @@ class ProgramWorkload:
     every call's arguments placed in one arena (the default schedules' outputs in place)."""
 
     def __init__(self, library: CandidateLibrary, bindings, seed: int) -> None:
-        import ctypes
-
         from nanocompile_amd import compiled
         self.library = library
         program = library.program
@@ -542,7 +547,6 @@ class ProgramWorkload:
         self.calls = self.launch.calls
         self.symbols = self.launch.symbols
         self.inputs = inputs
-        self._ctypes = ctypes
 
     def _run(self, kernel: int, candidate: int, args) -> None:
         status = self.launchers[kernel][candidate](args, self.symbols)
