@@ -416,3 +416,78 @@ def test_every_candidate_of_a_kernel_reads_its_operands_in_one_layout():
             assert len({tuple(p.packed for p in c.kernel.params) for c in cands}) == 1
             packed += any(p.packed for p in cands[0].kernel.params)
     assert packed
+
+
+# -- staging legality as a property: refused, or it reads nothing the kernel would not -----------
+
+_FORMS = ("v", "v+3", "2v", "rev")     # offset of a read within the row, as a function of the loop index
+
+
+def _offset(form: str, var, extent: int):
+    """The lir index offset of ``form`` over loop var ``var`` (extent ``extent``)."""
+    x = v(var)
+    return {"v": x, "v+3": b("add", x, c(3)), "2v": b("mul", x, c(2)),
+            "rev": b("sub", c(extent - 1), x)}[form]
+
+
+def _reads(form: str, extent: int) -> list[int]:
+    return [{"v": k, "v+3": k + 3, "2v": 2 * k, "rev": extent - 1 - k}[form] for k in range(extent)]
+
+
+from hypothesis import given, settings, strategies as hst  # noqa: E402
+
+
+@hst.composite
+def _row_kernels(draw):
+    rows = draw(hst.integers(1, 3))
+    e = draw(hst.integers(1, 9))
+    e2 = draw(hst.sampled_from([e, e + 2]))
+    serial = draw(hst.sampled_from(_FORMS))
+    shared = draw(hst.sampled_from(_FORMS + ("none",)))
+    lazy = draw(hst.booleans())              # the serial read only in a select's untaken arm
+    cooperate = draw(hst.booleans())
+    return rows, e, e2, serial, shared, lazy, cooperate
+
+
+@settings(max_examples=150, deadline=None)
+@given(_row_kernels())
+def test_staging_is_refused_or_reads_only_what_the_kernel_reads(case):
+    rows, e, e2, serial, shared, lazy, cooperate = case
+    f32, boolean = lir.DType("f32"), lir.DType("bool")
+    stride = 2 * max(e, e2) + 4                   # a row of x1 holds every offset any form reads
+    base = b("mul", v("i0"), c(stride))
+    read = lir.Load(1, b("add", base, _offset(serial, "r", e)), f32)
+    acc = lir.Var("acc", f32)
+    step = lir.Binary("add", acc, read, f32)
+    if lazy:
+        step = lir.Select(lir.Binary("lt", v("r"), c(0), boolean), step, acc, f32)
+    body = [lir.Let("acc", lir.Const(0.0, f32)), lir.Loop("r", c(e), (lir.Assign("acc", step),))]
+    if cooperate:
+        value = acc if shared == "none" else lir.Binary(
+            "mul", acc, lir.Load(1, b("add", base, _offset(shared, "j0", e2)), f32), f32)
+        body.append(lir.Loop("j0", c(e2), (lir.Store(0, b("add", b("mul", v("i0"), c(e2)), v("j0")), value),)))
+        out_size = rows * e2
+    else:
+        body.append(lir.Store(0, v("i0"), acc))
+        out_size = rows
+    params = (lir.Param(f32, True), lir.Param(f32, False))
+    kernel = lir.Kernel("row", params, (lir.Loop("i0", c(rows), tuple(body)),))
+    offsets = ([] if lazy else _reads(serial, e)) + (_reads(shared, e2) if cooperate and shared != "none" else [])
+    size = (rows - 1) * stride + max(offsets) + 1 if offsets else 1
+    x1 = np.random.default_rng(rows * 100 + e).standard_normal(size).astype(np.float32)
+    want = np.full(out_size, np.nan, np.float32)
+    assert I.compile_kernel(kernel)([want, x1], []) == 0          # the kernel itself stays in bounds
+
+    s = gpu_schedule.GpuSchedule(kernel).grid("i0")
+    s.cooperate("j0") if cooperate else s.workgroup()
+    try:
+        s.stage(1)
+    except gpu_schedule.ScheduleError:
+        must = (not lazy and serial in ("v", "v+3") and
+                (not cooperate or shared == "none" or (shared == serial and e2 == e)))
+        assert not must, f"refused a legal window: {case}"
+        return
+    staged, launch = s.done()
+    got = np.full(out_size, np.nan, np.float32)
+    assert I.compile_kernel(I.staged_ir(staged, launch))([got, x1], []) == 0   # OutOfBounds would raise
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), case
