@@ -19,7 +19,13 @@ C emitter (runtime.py:182-200), so this script records it for a set of graphs:
   inputs at several symbol bindings and the outputs of the reference's
   compiled C (CompiledGraph, runtime.py:167-301) on them;
 * the seeded tiny Qwen2 (the golden G5 model) in float32, int8 and
-  int8-vnni, both forward graphs, whose tokens and logits G5 already holds.
+  int8-vnni, both forward graphs, whose tokens and logits G5 already holds;
+* config 5's model, Qwen2.5-0.5B-shaped (24 layers, vocabulary 151,936) with
+  BASELINE's seeded N(0, 0.02) weights, in int8: its last-position forward
+  program, a seeded 16-token prompt, the reference's four greedy tokens
+  from it, and the reference's logits of the prompt and of the first decode
+  step at every 97th vocabulary entry and at the argmax (``--add config5``
+  records only this entry, keeping the rest of the fixture as it is).
 
 Each program is recorded fused and unscheduled (what the GPU schedules
 start from); some also unfused (``lower``) and with the reference's CPU
@@ -339,10 +345,43 @@ def record_qwen2(fixture: dict) -> None:
         fixture["qwen2"][tag] = entry
 
 
+CONFIG5_SEED, CONFIG5_PROMPT_SEED, CONFIG5_PROMPT, CONFIG5_NEW = 7, 11, 16, 4
+CONFIG5_STRIDE = 97                     # logits recorded at every 97th vocabulary entry
+
+
+def record_config5(fixture: dict) -> None:
+    from nanocompile.models.qwen2 import greedy
+    c = ours.QWEN25_05B
+    config = Qwen2Config(c.vocab_size, c.hidden_size, c.intermediate_size, c.num_hidden_layers,
+                         c.num_attention_heads, c.num_key_value_heads, c.rms_norm_eps, c.rope_theta,
+                         c.tie_word_embeddings)
+    model = Qwen2(config, ours.random_weights(c, seed=CONFIG5_SEED), quantization="int8")
+    prompt = [int(t) for t in np.random.default_rng(CONFIG5_PROMPT_SEED).integers(0, c.vocab_size, CONFIG5_PROMPT)]
+    fused = fuse(optimize(model.graph_last))
+    entry = {"last": program(fused, "config5/last"), "weight_names": sorted(model.weights),
+             "seed": CONFIG5_SEED, "prompt": prompt, "stride": CONFIG5_STRIDE}
+    cache = model.new_cache(CONFIG5_PROMPT + CONFIG5_NEW)
+    first = model.forward(prompt, cache=cache, last_only=True)[0]
+    step = model.forward([int(np.argmax(first))], cache=cache, last_only=True)[0]
+    for name, logits in (("prompt", first), ("step", step)):
+        ARRAYS[f"config5/logits_{name}"] = np.ascontiguousarray(logits[::CONFIG5_STRIDE])
+        entry[f"argmax_{name}"] = int(np.argmax(logits))
+        entry[f"max_{name}"] = float(np.max(logits)).hex()
+    entry["tokens"] = greedy(model, prompt, CONFIG5_NEW)
+    print(f"config5: {len(fused.kernels)} kernels, {len(fused.calls)} calls, tokens {entry['tokens']}", flush=True)
+    fixture["config5"] = entry
+
+
 def main() -> None:
-    fixture = {"zoo": {}, "qwen2": {}}
-    record_zoo(fixture)
-    record_qwen2(fixture)
+    if sys.argv[1:] == ["--add", "config5"]:
+        with gzip.open(HERE / "programs.json.gz", "rt", encoding="utf-8") as f:
+            fixture = json.load(f)
+        record_config5(fixture)
+    else:
+        fixture = {"zoo": {}, "qwen2": {}}
+        record_zoo(fixture)
+        record_qwen2(fixture)
+        record_config5(fixture)
     with gzip.open(HERE / "programs.json.gz", "wt", encoding="utf-8", compresslevel=9) as f:
         json.dump(fixture, f, sort_keys=True)
     # Arrays already in the fixture are kept: a re-run adds new entries without moving the

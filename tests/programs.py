@@ -89,6 +89,35 @@ def qwen2_weights(tag: str) -> dict[str, np.ndarray]:
     return out
 
 
+def config5() -> tuple[lir.Program, dict]:
+    """Config 5's last-position forward program (Qwen2.5-0.5B-shaped, int8) as the reference
+    compiles it, and what the fixture holds of the reference's run: the prompt, its greedy
+    tokens, and logits of the prompt and of the first decode step at every ``stride``-th entry."""
+    doc, arrays = fixture()
+    entry = doc["config5"]
+    record = {k: v for k, v in entry.items() if k != "last"}
+    record["logits_prompt"] = arrays["config5/logits_prompt"]
+    record["logits_step"] = arrays["config5/logits_step"]
+    return lir.program_from_json(entry["last"], arrays), record
+
+
+def config5_weights(names, seed: int) -> dict[str, np.ndarray]:
+    """Config 5's seeded weights as the reference hands them to its runner: float32 by name, each
+    int8 projection as ``W@int8`` / ``W@scales`` from the per-row quantizer (oracle/reference.py,
+    pinned by golden G1)."""
+    from nanocompile_amd.models.config import QWEN25_05B
+    from oracle import reference as R
+    base = random_weights(QWEN25_05B, seed=seed)
+    out = {}
+    for name in names:
+        if name.endswith("@int8"):
+            w = name.rsplit("@", 1)[0]
+            out[name], out[w + "@scales"] = R.quantize_int8(base[w])
+        elif not name.endswith("@scales"):
+            out[name] = base[name]
+    return out
+
+
 class Driver:
     """The reference's Qwen2 forward and greedy loop over a runner ``run(which, inputs) -> outputs``,
     ``which`` being "full" or "last" (models/qwen2.py:316-368)."""
@@ -142,8 +171,10 @@ def prebuild(jobs: int = 8) -> int:
     doc, _ = fixture()
     progs = [zoo(n, v) for n in zoo_names() for v in ("program", "unfused", "scheduled")]
     progs += [qwen2(tag, which) for tag, entry in doc["qwen2"].items() for which in entry if which != "weight_names"]
+    progs.append(config5()[0])
     libraries = [autotune.CandidateLibrary(zoo(n, v)) for n, v in candidate_programs()]
     libraries += [autotune.CandidateLibrary(qwen2(tag, which)) for tag, which in candidate_models()]
+    libraries.append(autotune.CandidateLibrary(config5()[0]))
     with ThreadPoolExecutor(max_workers=jobs) as pool:
         results = list(pool.map(compiled.prebuild, progs))
         results += list(pool.map(lambda library: library.build(), libraries))
