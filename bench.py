@@ -353,6 +353,50 @@ def generated_kernels(rows: int = 512, reps: int = 20, seed: int = 7) -> dict:
     return {"rows": rows, "reps": reps, "kernels": out, "tuned": tuned}
 
 
+def generated_config5(weights: dict, past: int = PROMPT + NEW_TOKENS - 2, seed: int = 3) -> dict:
+    """Config 5's decode step through the drop-in path: the reference's own compiled program for
+    the model (int8 mode, recorded in tests/golden/programs.json.gz; its tokens and logits are
+    checked against the reference's in tests/test_config5_generated_gpu.py) generated as HIP by
+    codegen_hip, on these weights (the projections quantized per row on the GPU), at one token
+    and ``past`` cached positions; default GPU schedules, then each kernel's schedule chosen by
+    the autotuner on that step. Graph-replayed, like the hand-written step."""
+    from nanocompile_amd import autotune, kernels, lir
+    from nanocompile_amd.compiled import CompiledProgram
+    from nanocompile_amd.models.config import QWEN25_05B as c
+    golden = Path(__file__).resolve().parent / "tests" / "golden"
+    doc = lir.load_programs(golden / "programs.json.gz")
+    with np.load(golden / "programs.npz", allow_pickle=False) as arrays:
+        program = lir.program_from_json(doc["config5"]["last"], arrays)
+    ref_weights = {}
+    for name in program.weights:
+        if name.endswith("@int8"):
+            w = name.rsplit("@", 1)[0]
+            q, scales = kernels.quantize_int8(weights[w])
+            ref_weights[name], ref_weights[w + "@scales"] = q.numpy(), scales.numpy()
+        elif not name.endswith("@scales"):
+            ref_weights[name] = weights[name]
+    rng = np.random.default_rng(seed)
+    cache_shape = (c.num_hidden_layers, c.num_key_value_heads, past, c.head_dim)
+    inputs = {"token_ids": np.array([int(rng.integers(0, c.vocab_size))], np.int64),
+              "past_keys": rng.standard_normal(cache_shape).astype(np.float32),
+              "past_values": rng.standard_normal(cache_shape).astype(np.float32)}
+    out = {"program": f"the reference's int8 program: {len(program.kernels)} kernels, {len(program.calls)} launches "
+                      f"a step", "past": past}
+    t0 = time.perf_counter()
+    tuner = autotune.Autotuner(cache=None, rounds=3, reps=2, verbose=True,
+                               workloads=[("decode", {"seq": 1, "past": past}, 1.0)])
+    for label, schedule in (("default", "default"), ("tuned", tuner)):
+        log(f"generated: config 5's program, {label} schedules")
+        compiled = CompiledProgram(program, schedule=schedule)
+        launch, _, _ = compiled.prepare(inputs, ref_weights)
+        us = graph_us(lambda i, launch=launch: launch(), 1, rounds=5)
+        out[label] = {"us_per_step": round(us, 1), "tok_s": round(1e6 / us, 1)}
+        del compiled
+    out["tuned"]["schedules"] = {f"kernel {r.shape[0]} ({r.op})": r.config for r in tuner.records if r.winner}
+    out["seconds"] = round(time.perf_counter() - t0, 1)
+    return out
+
+
 def block_measurements(model, seed: int = 7) -> dict:
     """Configs 2, 3 and 4 on the decode model's own weights (24 layers, so weights stream as in the model)."""
     from nanocompile_amd import hip
@@ -622,6 +666,10 @@ def decode(steps: int, warmup: int, cpu: bool, seed: int = 0, graph: bool = True
         t0 = time.perf_counter()
         result["blocks"] = block_measurements(model)
         log(f"blocks: configs 2-4 measured in {time.perf_counter() - t0:.1f} s")
+        t0 = time.perf_counter()
+        result["generated"] = generated_config5(weights)
+        log(f"generated: config 5's reference program as HIP, {result['generated']['default']['tok_s']} tok/s "
+            f"default, {result['generated']['tuned']['tok_s']} tuned, in {time.perf_counter() - t0:.1f} s")
     if cpu:
         result["cpu"] = cpu_decode(config, weights, prompt, tokens)
     return result
@@ -730,7 +778,8 @@ def main() -> int:
                                    "tok_s": round(d["all_tok_s"], 2)},
                    "kernels_per_step": kernels,
                    "gemv": gemv_record,
-                   "blocks": d.get("blocks")},
+                   "blocks": d.get("blocks"),
+                   "generated": d.get("generated")},
         "roofline": {"bound": "hbm", "achieved": top["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": top["frac"], "traffic": measured_traffic(KERNEL_SYMBOLS[dominant]),
                      "traffic_source": "profiles/traffic.json (rocprofv3 PMC, calibrated); null when no pass "

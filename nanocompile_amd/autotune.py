@@ -48,6 +48,7 @@ import hashlib
 import json
 import os
 import statistics
+import sys
 import tempfile
 import time
 from dataclasses import dataclass, field
@@ -422,6 +423,8 @@ DECODE = ("decode", {"seq": 1, "past": 64}, 1.0)
 PREFILL = ("prefill", {"seq": 32, "past": 0}, 1.0 / 32)
 WORKLOADS = (DECODE, PREFILL)
 SENTINEL_BYTE = 0xA5             # a candidate's output is filled with it before the candidate runs
+WHOLE_ARENA = 64 * 2**20         # arenas up to this size are compared whole after each candidate
+GUARD_BYTES = 1 * 2**20          # else the output and this much either side of it
 
 
 @dataclass
@@ -515,9 +518,9 @@ def random_arguments(program, bindings, rng) -> tuple[dict, dict, dict]:
 
     def draw(shape, dtype):
         if dtype.name == "f32":
-            return rng.standard_normal(shape).astype(np.float32)
+            return rng.standard_normal(shape, dtype=np.float32)
         if dtype.name == "i8":
-            return rng.integers(-127, 128, shape).astype(np.int8)
+            return rng.integers(-127, 128, shape, dtype=np.int8)
         if dtype.name == "bool":
             return rng.integers(0, 2, shape).astype(dtype.numpy)
         return np.zeros(shape, dtype.numpy)
@@ -557,8 +560,9 @@ class ProgramWorkload:
     def gate(self, kernels) -> None:
         """Run the program's calls in order on the default schedules; at the first call of each
         kernel in ``kernels``, run every other candidate on the same arguments, its output filled
-        with a sentinel first: the whole arena must then hold exactly what the default left (its
-        output bit for bit, every other byte untouched)."""
+        with a sentinel first: the arena must then hold exactly what the default left (its
+        output bit for bit, every other byte untouched). The whole arena is compared up to
+        WHOLE_ARENA bytes; above that, the output and GUARD_BYTES either side of it."""
         from nanocompile_amd.compiled import _nbytes
         pending = set(kernels)
         arena = self.compiled._arena
@@ -570,21 +574,27 @@ class ProgramWorkload:
             if call.kernel not in pending:
                 continue
             pending.discard(call.kernel)
-            before = arena.numpy().view(np.uint8).copy()
             at, n = self.addresses[call.output] - base, _nbytes(call.output, self.bound)
+            if arena.nbytes <= WHOLE_ARENA:
+                lo, hi = 0, arena.nbytes
+            else:
+                lo, hi = max(0, at - GUARD_BYTES), min(arena.nbytes, at + n + GUARD_BYTES)
+            window = arena.view((hi - lo,), np.uint8, offset_bytes=lo)
+            before = window.numpy().copy()
             fill = np.full(max(n, 1), SENTINEL_BYTE, np.uint8)
             for c in range(1, len(self.launchers[call.kernel])):
                 if n:
                     hip._check(lib.nc_memcpy_h2d(base + at, fill.ctypes.data, n), "nc_memcpy_h2d")
                 self._run(call.kernel, c, args)
                 hip.sync()
-                after = arena.numpy().view(np.uint8)
+                after = window.numpy()
                 if not np.array_equal(after, before):
                     diff = np.flatnonzero(after != before)
-                    where = "its output" if at <= diff[0] < at + n else "outside its output"
+                    first = int(diff[0]) + lo
+                    where = "its output" if at <= first < at + n else "outside its output"
                     config = self.library.candidates[call.kernel][c].config
                     raise TuningError(f"kernel {call.kernel} ({call.primitive}) candidate {c} {config} differs "
-                                      f"from the default schedule at byte {int(diff[0]) - at} of {n} ({where})")
+                                      f"from the default schedule at byte {first - at} of {n} ({where})")
 
     def timer(self, kernel: int):
         """An object ``measure`` times: ``launch(candidate, copy)`` runs kernel ``kernel``'s calls."""
@@ -763,9 +773,10 @@ class Autotuner:
             if self.verbose:
                 print(f"tuned kernel {i} ({record.op}): {len(cands)} schedules, "
                       f"{cands[winner].launch.describe()} at {winner_cost * 1e6:.2f} us per token "
-                      f"({record.speedup:.2f}x the default)", flush=True)
+                      f"({record.speedup:.2f}x the default)", file=sys.stderr, flush=True)
         if self.verbose:
-            print(f"tuned {len(todo)} generated kernels in {time.perf_counter() - started:.1f} s", flush=True)
+            print(f"tuned {len(todo)} generated kernels in {time.perf_counter() - started:.1f} s", file=sys.stderr,
+                  flush=True)
         return library, chosen
 
     def tune_problem(self, make, op: str, shape: tuple, space: list[dict] | None) -> TuneRecord:
@@ -810,5 +821,5 @@ class Autotuner:
         if self.verbose:
             print(f"tuned {op} {tuple(shape)}: {len(space)} schedules in {record.seconds:.1f} s, "
                   f"schedule {winner} at {winner_cost * 1e6:.2f} us ({record.speedup:.2f}x the default)",
-                  flush=True)
+                  file=sys.stderr, flush=True)
         return record

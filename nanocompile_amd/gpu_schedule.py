@@ -31,6 +31,13 @@ space. A GPU launch binds loops to the grid instead of to a thread pool:
   shared loop needs from LDS: the same values, computed once per workgroup
   instead of once per wave, so the waves no longer compete for issue slots
   with identical chains.
+* ``lanes(array)``: an item's accumulator array of L independent chains (the
+  reference's L accumulators, written one element per iteration of the
+  innermost loops, whose indices enumerate 0..L-1) held one element per lane:
+  an item becomes L lanes of a wavefront, lane l runs chain l (the loops that
+  enumerated the chains become l's digits), and the statements after the
+  chains read element i from lane i. Each chain is the same sequence of
+  operations in the same order; only where it runs changes.
 * ``vectorize(width)``: each thread takes ``width`` consecutive iterations of
   the loop spread across threads (the innermost grid loop, or the shared
   loop), so neighbouring reads and writes sit in one thread and can be
@@ -289,6 +296,18 @@ class Staged:
 
 
 @dataclass(frozen=True)
+class Lanes:
+    """Accumulator arrays held one element per lane: ``width`` lanes an item; lane l runs the
+    chain of element l, the chain loops' vars given by ``loops`` as (var, extent, coefficient),
+    var = l / coefficient % extent; ``index`` is the element index the chain statements use."""
+
+    width: int
+    arrays: tuple[str, ...]
+    loops: tuple[tuple[str, int, int], ...]
+    index: object
+
+
+@dataclass(frozen=True)
 class Launch:
     """How a scheduled kernel runs: its grid loops, workgroup size and the per-item mapping."""
 
@@ -300,6 +319,7 @@ class Launch:
     stage: tuple[Staged, ...] = ()         # operand windows staged in LDS per item
     vector: int = 1                        # consecutive iterations per thread of the loop spread across threads
     lead: bool = False                     # one wave computes the item's serial part, shared through LDS
+    lanes: Lanes | None = None             # an item's accumulator arrays spread one element a lane
 
     @property
     def per_workgroup(self) -> bool:
@@ -315,6 +335,8 @@ class Launch:
         parts += [f"stage(x{st.param})" for st in self.stage]
         if self.lead:
             parts.append("lead()")
+        if self.lanes:
+            parts.append(f"lanes({', '.join(self.lanes.arrays)})")
         if self.vector > 1:
             parts.append(f"vectorize({self.vector})")
         parts += [f"unroll({v}, {n})" for v, n in self.unroll]
@@ -465,6 +487,21 @@ class GpuSchedule:
         self.steps.append("lead")
         return self
 
+    def lanes(self, name: str) -> "GpuSchedule":
+        """Hold accumulator array ``name`` (and the arrays its chains update alongside it) one
+        element per lane; see ``lane_chains`` for when that is legal."""
+        launch = self.launch
+        if not launch.grid:
+            raise ScheduleError("lanes: bind the grid first")
+        if launch.per_workgroup or launch.vector > 1 or launch.lanes:
+            raise ScheduleError("lanes: an item must be one thread's, not vectorized")
+        lanes = lane_chains(self.item_body(), name)
+        if launch.threads % lanes.width:
+            raise ScheduleError(f"lanes({name}): {lanes.width} lanes an item do not divide block({launch.threads})")
+        self.launch = replace(launch, lanes=lanes)
+        self.steps.append(f"lanes {name}")
+        return self
+
     def vectorize(self, width: int) -> "GpuSchedule":
         """Each thread takes ``width`` consecutive iterations of the loop spread across threads."""
         if width not in VECTOR_WIDTHS:
@@ -473,6 +510,8 @@ class GpuSchedule:
             raise ScheduleError("vectorize: bind the grid first")
         if self.launch.workgroup:
             raise ScheduleError("vectorize: a workgroup item spreads no loop across its threads")
+        if self.launch.lanes:
+            raise ScheduleError("vectorize: the item's lanes hold its accumulators")
         self.launch = replace(self.launch, vector=width)
         self.steps.append(f"vectorize {width}")
         return self
@@ -523,6 +562,84 @@ class GpuSchedule:
         kernel = lir.Kernel(self.kernel.primitive, tuple(self.kernel.params), simplify.simplify_body(self.kernel.body),
                             self.kernel.bytes_read, self.kernel.bytes_written)
         return kernel, self.launch
+
+
+# -- accumulators across lanes ----------------------------------------------------------------
+
+
+def _with_loops(stmts, loops=()):
+    """Every statement with the loops around it (outermost first)."""
+    for s in stmts:
+        yield loops, s
+        if kind(s) == "Loop":
+            yield from _with_loops(s.body, loops + (s,))
+        elif kind(s) == "Block":
+            yield from _with_loops(s.body, loops)
+
+
+def lane_chains(body, name: str) -> Lanes:
+    """The Lanes for accumulator array ``name`` declared at the top of an item's ``body``, or
+    ScheduleError. Legal when: the array's size L is a power of two from 2 to 64; every store
+    to it (and to any array stored beside it) sits in one innermost nest of constant loops
+    whose vars enumerate the element index e = sum(coefficient * var) over 0..L-1 exactly once
+    (mixed radix), the nest holding only Lets and those stores; every read of those arrays in
+    that nest is of element e (so each element's chain touches no other); nothing else in the
+    item stores to them; and the item has no Fail (a lane that stopped would leave the others
+    reading its element)."""
+    arrays = {s.name: s for s in body if kind(s) == "Array"}
+    if name not in arrays:
+        raise ScheduleError(f"lanes({name}): no array {name} at the top of the item")
+    width = int(arrays[name].size)
+    if width < 2 or width > WAVE or width & (width - 1):
+        raise ScheduleError(f"lanes({name}): {width} elements, not a power of two from 2 to {WAVE}")
+    if any(kind(s) == "Fail" for s in statements(body)):
+        raise ScheduleError(f"lanes({name}): the item checks its input and may stop early")
+    stores = [(loops, s) for loops, s in _with_loops(body) if kind(s) == "ArrayStore" and s.name == name]
+    if not stores:
+        raise ScheduleError(f"lanes({name}): nothing stores to it")
+    loops, first = stores[0]
+    index = first.index
+    a = simplify.affine(index)
+    if a.const or not a.terms:
+        raise ScheduleError(f"lanes({name}): the element index is not a sum of loop indices")
+    by_var = {l.var: l for l in loops}
+    digits = []
+    for key, coeff in a.terms.items():
+        atom = a.atoms[key]
+        if kind(atom) != "Var" or atom.name not in by_var or coeff <= 0:
+            raise ScheduleError(f"lanes({name}): the element index is not a sum of loop indices")
+        loop = by_var[atom.name]
+        if kind(loop.extent) != "Const":
+            raise ScheduleError(f"lanes({name}): loop {loop.var} has no constant extent")
+        digits.append((atom.name, int(loop.extent.value), int(coeff)))
+    chain = list(loops[len(loops) - len(digits):])
+    if sorted(l.var for l in chain) != sorted(v for v, _, _ in digits):
+        raise ScheduleError(f"lanes({name}): the loops that enumerate the elements are not the innermost")
+    for outer, inner in zip(chain, chain[1:]):
+        if list(outer.body) != [inner]:
+            raise ScheduleError(f"lanes({name}): the element loops are not perfectly nested")
+    radix = 1
+    for var, extent, coeff in sorted(digits, key=lambda d: d[2]):
+        if coeff != radix:
+            raise ScheduleError(f"lanes({name}): the element index does not enumerate 0..{width - 1} once")
+        radix *= extent
+    if radix != width:
+        raise ScheduleError(f"lanes({name}): the element loops enumerate {radix} elements, not {width}")
+    inner_body = chain[-1].body
+    group = set()
+    for s in inner_body:
+        if kind(s) == "Let":
+            continue
+        if kind(s) != "ArrayStore" or s.name not in arrays or int(arrays[s.name].size) != width or s.index != index:
+            raise ScheduleError(f"lanes({name}): the chains do more than update elements {index!r}")
+        group.add(s.name)
+    for x in scalars(inner_body):
+        if kind(x) == "Local" and (x.name in group or x.name in arrays) and (x.name not in group or x.index != index):
+            raise ScheduleError(f"lanes({name}): a chain reads another element")
+    for loops_of, s in _with_loops(body):
+        if kind(s) == "ArrayStore" and s.name in group and s not in inner_body:
+            raise ScheduleError(f"lanes({name}): {s.name} is stored outside its chains")
+    return Lanes(width, tuple(sorted(group)), tuple(sorted(digits, key=lambda d: -d[2])), index)
 
 
 # -- LDS staging -------------------------------------------------------------------------------
@@ -696,7 +813,7 @@ SPACES: dict[str, dict[str, tuple]] = {
             "unroll": (0, 4), "lead": (False, True)},
     # a thread per item, or (workgroup) a workgroup per item with its loops' operands staged
     "item": {"threads": (256, 64, 128, 512, 1024), "vector": (1, 2, 4), "workgroup": (False, True),
-             "unroll": (0, 4), "lead": (False, True)},
+             "unroll": (0, 4), "lead": (False, True), "lanes": (False, True)},
     # no loop can be the grid: one thread runs the kernel
     "serial": {"threads": (256,)},
 }
@@ -793,6 +910,16 @@ def apply(kernel, calls, config) -> tuple:
             raise ScheduleError("no operand of the item can be staged")
     if config.get("lead"):
         s.lead()
+    if config.get("lanes"):
+        arrays = [st.name for st in s.item_body() if kind(st) == "Array"]
+        for name in arrays:
+            try:
+                s.lanes(name)
+                break
+            except ScheduleError:
+                continue
+        if not s.launch.lanes:
+            raise ScheduleError("no accumulator array of the item can be spread over lanes")
     if config.get("vector", 1) > 1:
         s.vectorize(config["vector"])
     if config.get("unroll"):

@@ -342,8 +342,7 @@ def test_space_starts_at_the_default_and_refuses_points_outside_it():
         gpu_schedule.apply(row, calls[0], {"threads": 256, "workgroup": True, "vector": 1, "unroll": 0})
     elementwise = program.kernels[2]
     with pytest.raises(gpu_schedule.ScheduleError, match="unroll"):
-        gpu_schedule.apply(elementwise, calls[2], {"threads": 256, "vector": 1, "workgroup": False, "unroll": 4,
-                                                              "lead": False})
+        gpu_schedule.apply(elementwise, calls[2], dict(gpu_schedule.DEFAULTS["item"], unroll=4))
 
 
 def test_candidate_library_holds_each_distinct_kernel_once_and_reports_failures_as_its_kernel():
@@ -368,8 +367,7 @@ def test_vectorized_items_are_unrolled_without_checks_only_when_whole():
     program = P.zoo("rms_norm_quant")
     calls = _calls_of(program)
     kernel, launch = gpu_schedule.apply(program.kernels[3], calls[3],
-                                        {"threads": 64, "vector": 4, "workgroup": False, "unroll": 0,
-                                         "lead": False})
+                                        dict(gpu_schedule.DEFAULTS["item"], threads=64, vector=4))
     text = codegen_hip.render_kernel(kernel, launch, 3)
     assert "const int64_t nc_q1 = (nc_e1 + 3) / 4;" in text
     assert "if (nc_i1 * 4 + 4 <= nc_e1) {" in text and "#pragma unroll" in text
@@ -491,3 +489,58 @@ def test_staging_is_refused_or_reads_only_what_the_kernel_reads(case):
     got = np.full(out_size, np.nan, np.float32)
     assert I.compile_kernel(I.staged_ir(staged, launch))([got, x1], []) == 0   # OutOfBounds would raise
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), case
+
+
+# -- accumulators across lanes ----------------------------------------------------------------
+
+
+def test_lanes_spread_the_references_accumulators_one_element_a_lane():
+    """The int8 matmuls' 32 accumulator chains (quantize.py's recipe: element kc * 8 + kl) go one
+    a lane; each lane's digits give back its own element, every element once."""
+    found = 0
+    for name in ("mlp_int8_64", "mlp_int8-vnni_64"):
+        program = P.zoo(name)
+        calls = _calls_of(program)
+        for i, kernel in enumerate(program.kernels):
+            if gpu_schedule.kernel_class(kernel) != "item":
+                continue
+            config = dict(gpu_schedule.DEFAULTS["item"], lanes=True)
+            try:
+                scheduled, launch = gpu_schedule.apply(kernel, calls[i], config)
+            except gpu_schedule.ScheduleError:
+                continue
+            lanes = launch.lanes
+            found += 1
+            elements = []
+            for lane in range(lanes.width):
+                digits = {var: (lane // coeff) % extent for var, extent, coeff in lanes.loops}
+                elements.append(simplify.value_range(lanes.index, {v: (d, d) for v, d in digits.items()})[0])
+            assert elements == list(range(lanes.width)), (name, i)
+            text = codegen_hip.render_kernel(scheduled, launch, i)
+            assert f"const int nc_l = threadIdx.x & {lanes.width - 1};" in text
+            assert "__shfl(" in text and "if (nc_l == 0) x0[" in text
+    assert found
+
+
+def test_lanes_refuses_chains_that_are_not_independent():
+    f32 = lir.DType("f32")
+    params = (lir.Param(f32, True), lir.Param(f32, False))
+
+    def kernel(index, extra=()):
+        chain = lir.Loop("k0", c(4), (lir.Loop("kl", c(8), (lir.ArrayStore("acc", index, lir.Fma(
+            lir.Load(1, b("add", b("mul", v("k0"), c(8)), v("kl")), f32), lir.Const(2.0, f32),
+            lir.Local("acc", index, f32), f32)),) + tuple(extra)),))
+        tail = lir.Store(0, v("i0"), lir.Local("acc", c(0), f32))
+        return lir.Kernel("matmul", params, (lir.Loop("i0", c(3), (
+            lir.Array("acc", 8, lir.Const(0.0, f32)), chain, tail)),))
+
+    s = gpu_schedule.GpuSchedule(kernel(v("kl"))).grid("i0")
+    assert s.lanes("acc").launch.lanes.width == 8
+    with pytest.raises(gpu_schedule.ScheduleError, match="enumerate"):
+        gpu_schedule.GpuSchedule(kernel(b("mul", v("kl"), c(2)))).grid("i0").lanes("acc")
+    with pytest.raises(gpu_schedule.ScheduleError, match="more than update"):
+        gpu_schedule.GpuSchedule(kernel(v("kl"), (lir.Store(0, v("kl"), lir.Const(1.0, f32)),))).grid("i0").lanes("acc")
+    with pytest.raises(gpu_schedule.ScheduleError, match="no array"):
+        gpu_schedule.GpuSchedule(kernel(v("kl"))).grid("i0").lanes("h")
+    with pytest.raises(gpu_schedule.ScheduleError, match="vectorized|thread"):
+        gpu_schedule.GpuSchedule(kernel(v("kl"))).grid("i0").vectorize(2).lanes("acc")

@@ -33,6 +33,7 @@ def config5(gpu):
     weights = P.config5_weights(record["weight_names"], record["seed"])
     compiled = CompiledProgram(program)
     driver = P.Driver(lambda which, inputs: compiled(inputs, weights), config=QWEN25_05B)
+    driver.program, driver.weights = program, weights
     return driver, record
 
 
@@ -59,3 +60,24 @@ def test_config5_greedy_tokens_are_the_references(config5):
     driver, record = config5
     print("config 5 generated: greedy", flush=True)
     assert driver.greedy(record["prompt"], len(record["tokens"])) == record["tokens"]
+
+
+def test_config5_with_its_int8_matmuls_across_lanes_is_the_references(config5):
+    """The same program with every int8 projection's 32 accumulator chains one a lane
+    (gpu_schedule lanes): the reference's tokens and logits."""
+    from nanocompile_amd import autotune
+    from nanocompile_amd.compiled import CompiledProgram
+    from nanocompile_amd.models.config import QWEN25_05B
+    driver, record = config5
+    library = autotune.CandidateLibrary(driver.program)
+    chosen = [next((c for c, cand in enumerate(cands) if cand.config.get("lanes") and cand.config["threads"] == 256
+                    and not cand.config.get("unroll")), 0) for cands in library.candidates]
+    assert sum(1 for c in chosen if c) >= 7
+    compiled = CompiledProgram(driver.program, autotune.Chosen(library, chosen))
+    lanes = P.Driver(lambda which, inputs: compiled(inputs, driver.weights), config=QWEN25_05B)
+    print("config 5 generated, matmuls across lanes", flush=True)
+    cache = list(lanes.empty())
+    first = lanes.forward(record["prompt"], cache, last_only=True)[0]
+    _close(first, record, "prompt")
+    _close(lanes.forward([int(np.argmax(first))], cache, last_only=True)[0], record, "step")
+    assert lanes.greedy(record["prompt"], len(record["tokens"])) == record["tokens"]
