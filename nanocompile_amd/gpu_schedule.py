@@ -31,6 +31,12 @@ space. A GPU launch binds loops to the grid instead of to a thread pool:
   shared loop needs from LDS: the same values, computed once per workgroup
   instead of once per wave, so the waves no longer compete for issue slots
   with identical chains.
+* ``hoist()``: with a lead wave, each serial loop of its part that updates
+  one accumulator from one per-iteration value (the reference's reductions:
+  ``acc = acc + t``, the NaN-propagating maximum over ``t``) has ``t``
+  computed by every thread of the workgroup first, one iteration a thread,
+  into LDS; the lead wave then runs the accumulator's chain over the stored
+  values, in the loop's order. The values and the chain are the loop's own.
 * ``lanes(array)``: an item's accumulator array of L independent chains (the
   reference's L accumulators, written one element per iteration of the
   innermost loops, whose indices enumerate 0..L-1) held one element per lane:
@@ -296,6 +302,20 @@ class Staged:
 
 
 @dataclass(frozen=True)
+class Hoisted:
+    """A serial loop of the lead wave's part (statement ``at`` of it) whose per-iteration value
+    ``value`` (of dtype ``dtype``) every thread computes first into LDS array ``name`` (one
+    element an iteration of ``var`` up to ``extent``); the accumulator's chain then reads it."""
+
+    at: int
+    var: str
+    extent: object
+    value: object                 # the expression stored (a Let's var, or the update's own operand)
+    name: str
+    dtype: object
+
+
+@dataclass(frozen=True)
 class Lanes:
     """Accumulator arrays held one element per lane: ``width`` lanes an item; lane l runs the
     chain of element l, the chain loops' vars given by ``loops`` as (var, extent, coefficient),
@@ -320,6 +340,7 @@ class Launch:
     vector: int = 1                        # consecutive iterations per thread of the loop spread across threads
     lead: bool = False                     # one wave computes the item's serial part, shared through LDS
     lanes: Lanes | None = None             # an item's accumulator arrays spread one element a lane
+    hoist: tuple[Hoisted, ...] = ()        # lead-wave loops whose chain operands all threads compute first
 
     @property
     def per_workgroup(self) -> bool:
@@ -335,6 +356,8 @@ class Launch:
         parts += [f"stage(x{st.param})" for st in self.stage]
         if self.lead:
             parts.append("lead()")
+        if self.hoist:
+            parts.append("hoist()")
         if self.lanes:
             parts.append(f"lanes({', '.join(self.lanes.arrays)})")
         if self.vector > 1:
@@ -487,6 +510,25 @@ class GpuSchedule:
         self.steps.append("lead")
         return self
 
+    def hoist(self) -> "GpuSchedule":
+        """Every hoistable loop of the lead wave's part (``hoistable``) gets its chain operand
+        computed by all threads first; ScheduleError when none is."""
+        launch = self.launch
+        if not launch.lead:
+            raise ScheduleError("hoist: needs a lead wave")
+        body = self.item_body()
+        serial = body[:-1] if launch.cooperate else body
+        found = []
+        for at, st in enumerate(serial):
+            h = hoistable(serial, at, len(found))
+            if h is not None:
+                found.append(h)
+        if not found:
+            raise ScheduleError("hoist: no loop of the lead wave's part updates one accumulator from one value")
+        self.launch = replace(launch, hoist=tuple(found))
+        self.steps.append("hoist")
+        return self
+
     def lanes(self, name: str) -> "GpuSchedule":
         """Hold accumulator array ``name`` (and the arrays its chains update alongside it) one
         element per lane; see ``lane_chains`` for when that is legal."""
@@ -562,6 +604,51 @@ class GpuSchedule:
         kernel = lir.Kernel(self.kernel.primitive, tuple(self.kernel.params), simplify.simplify_body(self.kernel.body),
                             self.kernel.bytes_read, self.kernel.bytes_written)
         return kernel, self.launch
+
+
+# -- chains whose operands are computed first --------------------------------------------------
+
+
+def hoistable(serial, at: int, k: int) -> Hoisted | None:
+    """Statement ``at`` of a lead wave's part as a Hoisted (its LDS array ``nc_h<k>``), when it is
+    a loop whose body is Lets and then one update of an accumulator declared outside it, and
+    the value the update takes each iteration is one expression free of the accumulator:
+    either exactly one of the loop's Lets (the update reading it, the loop var and outer
+    scalars), or, with no Lets, the other operand of ``acc op x``. The Lets and that value read
+    no array but staged windows (another thread would not have it), and the extent is the same
+    for every item (symbols and constants), so the LDS array has one size."""
+    loop = serial[at]
+    if kind(loop) != "Loop" or not loop.body:
+        return None
+    *lets, update = loop.body
+    if any(kind(s) != "Let" for s in lets) or kind(update) != "Assign":
+        return None
+    acc = update.var
+    names = {s.var for s in lets}
+    if acc in names or acc == loop.var:
+        return None
+
+    def private(x) -> bool:
+        return any(kind(n) == "Local" and not n.name.startswith("nc_s") for n in walk(x))
+
+    if any(uses_var(s.value, acc) or private(s.value) for s in lets):
+        return None
+    if any(kind(n) in ("Var", "Load", "Local") for n in walk(loop.extent)):
+        return None
+    read = {n.name for n in walk(update.value) if kind(n) == "Var" and n.name in names}
+    if lets:
+        if len(read) != 1:
+            return None
+        name = read.pop()
+        value = next(lir.Var(s.var, s.value.dtype) for s in lets if s.var == name)
+    else:
+        v = update.value
+        if kind(v) != "Binary" or not any(kind(o) == "Var" and o.name == acc for o in (v.a, v.b)):
+            return None
+        value = v.b if kind(v.a) == "Var" and v.a.name == acc else v.a
+        if uses_var(value, acc) or private(value) or kind(value) in ("Const", "Var"):
+            return None
+    return Hoisted(at, loop.var, loop.extent, value, f"nc_h{k}", value.dtype)
 
 
 # -- accumulators across lanes ----------------------------------------------------------------
@@ -735,8 +822,9 @@ def stage_window(body, param: int) -> tuple:
 
 
 def unstage(kernel, launch) -> tuple:
-    """The same kernel reading its staged operands from memory again: (kernel, launch without
-    staging); a launch whose windows do not fit in LDS at run time takes this kernel."""
+    """The same kernel reading its staged operands from memory again and its lead wave computing
+    its chains' operands itself: (kernel, launch without staging or hoisting); a launch whose
+    LDS arrays do not fit at run time takes this kernel."""
     by_name = {st.name: st for st in launch.stage}
 
     def rewrite(x):
@@ -748,7 +836,7 @@ def unstage(kernel, launch) -> tuple:
     params = tuple(kernel.params)
     body = map_stmts(kernel.body, rewrite)
     return (lir.Kernel(kernel.primitive, params, body, kernel.bytes_read, kernel.bytes_written),
-            replace(launch, stage=()))
+            replace(launch, stage=(), hoist=()))
 
 
 # -- the default schedule ----------------------------------------------------------------
@@ -810,10 +898,10 @@ SPACES: dict[str, dict[str, tuple]] = {
     # a workgroup per item sharing its write pass: its size, its serial loops' operands staged in
     # LDS, iterations of the shared loop per thread, the serial loops' unroll
     "row": {"threads": (256, 64, 128, 512, 1024), "stage": (False, True), "vector": (1, 2, 4),
-            "unroll": (0, 4), "lead": (False, True)},
+            "unroll": (0, 4), "lead": (False, True), "hoist": (False, True)},
     # a thread per item, or (workgroup) a workgroup per item with its loops' operands staged
     "item": {"threads": (256, 64, 128, 512, 1024), "vector": (1, 2, 4), "workgroup": (False, True),
-             "unroll": (0, 4), "lead": (False, True), "lanes": (False, True)},
+             "unroll": (0, 4), "lead": (False, True), "hoist": (False, True), "lanes": (False, True)},
     # no loop can be the grid: one thread runs the kernel
     "serial": {"threads": (256,)},
 }
@@ -910,6 +998,8 @@ def apply(kernel, calls, config) -> tuple:
             raise ScheduleError("no operand of the item can be staged")
     if config.get("lead"):
         s.lead()
+    if config.get("hoist"):
+        s.hoist()
     if config.get("lanes"):
         arrays = [st.name for st in s.item_body() if kind(st) == "Array"]
         for name in arrays:

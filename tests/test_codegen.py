@@ -372,8 +372,8 @@ def test_vectorized_items_are_unrolled_without_checks_only_when_whole():
     assert "const int64_t nc_q1 = (nc_e1 + 3) / 4;" in text
     assert "if (nc_i1 * 4 + 4 <= nc_e1) {" in text and "#pragma unroll" in text
     assert text.count("const int64_t nc_items = nc_e0 * nc_q1;") == 2          # kernel and launcher agree
-    row, rl = gpu_schedule.apply(program.kernels[0], calls[0], {"threads": 128, "stage": True, "vector": 2,
-                                                                 "unroll": 4, "lead": False})
+    row, rl = gpu_schedule.apply(program.kernels[0], calls[0], dict(gpu_schedule.DEFAULTS["row"], threads=128,
+                                                                      stage=True, vector=2, unroll=4))
     text = codegen_hip.render_kernel(row, rl, 0)
     assert "extern __shared__" in text and text.count("__syncthreads();") == 2      # after the copy, after the item
     assert "nc_g0_unstaged" in text and f"if (nc_lds > {gpu_schedule.MAX_STAGE_BYTES})" in text
@@ -383,8 +383,7 @@ def test_vectorized_items_are_unrolled_without_checks_only_when_whole():
 def test_lead_shares_the_serial_parts_values_and_refuses_a_failing_serial_part():
     program = P.zoo("rms_norm_quant")
     calls = _calls_of(program)
-    row, rl = gpu_schedule.apply(program.kernels[0], calls[0], {"threads": 256, "stage": False, "vector": 1,
-                                                                 "unroll": 0, "lead": True})
+    row, rl = gpu_schedule.apply(program.kernels[0], calls[0], dict(gpu_schedule.DEFAULTS["row"], lead=True))
     body = gpu_schedule.perfect_nest(row.body)[0].body
     assert [name for name, _ in gpu_schedule.live_ins(body[:-1], body[-1])] == ["acc0"]
     text = codegen_hip.render_kernel(row, rl, 0)
@@ -544,3 +543,35 @@ def test_lanes_refuses_chains_that_are_not_independent():
         gpu_schedule.GpuSchedule(kernel(v("kl"))).grid("i0").lanes("h")
     with pytest.raises(gpu_schedule.ScheduleError, match="vectorized|thread"):
         gpu_schedule.GpuSchedule(kernel(v("kl"))).grid("i0").vectorize(2).lanes("acc")
+
+
+def test_hoist_computes_the_chains_operands_first_and_refuses_what_depends_on_the_chain():
+    program = P.zoo("softmax_mask")
+    calls = _calls_of(program)
+    row = program.kernels[0]
+    scheduled, launch = gpu_schedule.apply(row, calls[0], dict(gpu_schedule.DEFAULTS["row"], stage=True, lead=True,
+                                                               hoist=True))
+    assert [h.name for h in launch.hoist] == ["nc_h0", "nc_h1"]             # the max, then the sum of exps
+    text = codegen_hip.render_kernel(scheduled, launch, 0)
+    assert "nc_h1[r] = t" in text and "acc1 = (acc1 + nc_h1[r]);" in text
+    assert "nc_g0_unstaged" in text                                    # the fallback when LDS is short
+    with pytest.raises(gpu_schedule.ScheduleError, match="lead"):
+        gpu_schedule.GpuSchedule(row).grid("i0", "i1").cooperate("j0").hoist()
+    f32 = lir.DType("f32")
+    params = (lir.Param(f32, True), lir.Param(f32, False))
+    acc = lir.Var("acc", f32)
+
+    def kernel(lets, update):
+        return lir.Kernel("row", params, (lir.Loop("i0", c(2), (
+            lir.Let("acc", lir.Const(0.0, f32)), lir.Loop("r", c(8), tuple(lets) + (lir.Assign("acc", update),)),
+            lir.Store(0, v("i0"), acc))),))
+
+    x = lir.Load(1, b("add", b("mul", v("i0"), c(8)), v("r")), f32)
+    ok = kernel([lir.Let("t", x)], lir.Binary("add", acc, lir.Var("t", f32), f32))
+    assert gpu_schedule.GpuSchedule(ok).grid("i0").workgroup().lead().hoist().launch.hoist[0].value == lir.Var("t", f32)
+    reads_acc = kernel([lir.Let("t", lir.Binary("mul", x, acc, f32))], lir.Binary("add", acc, lir.Var("t", f32), f32))
+    two = kernel([lir.Let("t", x), lir.Let("u", x)],
+                 lir.Binary("add", lir.Binary("add", acc, lir.Var("t", f32), f32), lir.Var("u", f32), f32))
+    for bad in (reads_acc, two):
+        with pytest.raises(gpu_schedule.ScheduleError, match="no loop"):
+            gpu_schedule.GpuSchedule(bad).grid("i0").workgroup().lead().hoist()
