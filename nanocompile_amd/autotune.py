@@ -37,7 +37,8 @@ keeps those rules for the GPU library:
 
 Generated kernels (codegen_hip) are tuned the same way over the code
 generator's schedule space (gpu_schedule.space: workgroup size, LDS staging,
-workgroup items with one lead wave, vector width, unroll), per kernel of a
+workgroup items with one lead wave and hoisted chain operands, accumulators
+across lanes, weight packing, vector width, unroll), per kernel of a
 program, on weighted workloads of symbol values as the reference does
 (``Autotuner.schedule_program``; see ``tune_program``).
 """
@@ -475,10 +476,12 @@ class CandidateLibrary:
         self.calls_of = calls_of
         self.candidates = [kernel_candidates(k, calls_of.get(i, [])) for i, k in enumerate(program.kernels)]
         for i, cands in enumerate(self.candidates):
-            layouts = {tuple(p.packed for p in c.kernel.params) for c in cands}
-            if len(layouts) != 1:
-                # the tuner runs every candidate on the default's arguments
-                raise TuningError(f"kernel {i}: candidates read their operands in different layouts {layouts}")
+            # the tuner runs a candidate on the default's arguments, an operand the default reads
+            # packed pointed at its row-major copy where the candidate reads it so
+            default = [p.packed for p in cands[0].kernel.params]
+            for c in cands[1:]:
+                if any(p.packed is not None and p.packed != d for p, d in zip(c.kernel.params, default)):
+                    raise TuningError(f"kernel {i}: a candidate packs an operand the default does not")
         scheduled, owners, self.entry = [], [], []
         for i, cands in enumerate(self.candidates):
             self.entry.append([])
@@ -550,8 +553,36 @@ class ProgramWorkload:
         self.calls = self.launch.calls
         self.symbols = self.launch.symbols
         self.inputs = inputs
+        self._args: dict = {}
 
-    def _run(self, kernel: int, candidate: int, args) -> None:
+    def _layout_args(self, call, args, candidate):
+        """The call's launcher arguments for a candidate that reads a weight row-major where the
+        default reads it packed (the row-major copy is always resident): the default's, with those
+        operands pointed at the row-major copy. Packing where the default does not is refused."""
+        import ctypes
+
+        from nanocompile_amd import lir
+        params = candidate.kernel.params
+        default = self.library.candidates[call.kernel][0].kernel.params
+        if all(p.packed == q.packed for p, q in zip(params, default)):
+            return args
+        key = (id(args), tuple(p.packed for p in params))
+        if key not in self._args:
+            pointers = [args[i] for i in range(len(params))]
+            for i, view in enumerate(call.operands):
+                ours, theirs = params[i + 1].packed, default[i + 1].packed
+                if ours == theirs:
+                    continue
+                if ours is not None:
+                    raise TuningError(f"kernel {call.kernel}: a candidate packs an operand the default does not")
+                offset = lir.evaluate(view.offset, self.bound) * view.dtype.numpy.itemsize
+                pointers[i + 1] = self.addresses[view.buffer] + offset
+            self._args[key] = (ctypes.c_void_p * len(pointers))(*pointers)
+        return self._args[key]
+
+    def _run(self, kernel: int, candidate: int, args, call=None) -> None:
+        if call is not None and candidate:
+            args = self._layout_args(call, args, self.library.candidates[kernel][candidate])
         status = self.launchers[kernel][candidate](args, self.symbols)
         if status != 0:
             raise TuningError(f"kernel {kernel} candidate {candidate} could not be launched ({status}): "
@@ -585,7 +616,7 @@ class ProgramWorkload:
             for c in range(1, len(self.launchers[call.kernel])):
                 if n:
                     hip._check(lib.nc_memcpy_h2d(base + at, fill.ctypes.data, n), "nc_memcpy_h2d")
-                self._run(call.kernel, c, args)
+                self._run(call.kernel, c, args, call)
                 hip.sync()
                 after = window.numpy()
                 if not np.array_equal(after, before):
@@ -598,13 +629,13 @@ class ProgramWorkload:
 
     def timer(self, kernel: int):
         """An object ``measure`` times: ``launch(candidate, copy)`` runs kernel ``kernel``'s calls."""
-        args = [a for call, a in self.calls if call.kernel == kernel]
+        calls = [(call, a) for call, a in self.calls if call.kernel == kernel]
         workload = self
 
         class Calls:
             def launch(self, candidate: int, copy: int = 0) -> None:
-                for a in args:
-                    workload._run(kernel, candidate, a)
+                for call, a in calls:
+                    workload._run(kernel, candidate, a, call)
 
         return Calls()
 

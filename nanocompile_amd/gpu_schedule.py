@@ -901,7 +901,8 @@ SPACES: dict[str, dict[str, tuple]] = {
             "unroll": (0, 4), "lead": (False, True), "hoist": (False, True)},
     # a thread per item, or (workgroup) a workgroup per item with its loops' operands staged
     "item": {"threads": (256, 64, 128, 512, 1024), "vector": (1, 2, 4), "workgroup": (False, True),
-             "unroll": (0, 4), "lead": (False, True), "hoist": (False, True), "lanes": (False, True)},
+             "unroll": (0, 4), "lead": (False, True), "hoist": (False, True), "lanes": (False, True),
+             "pack": (True, False)},
     # no loop can be the grid: one thread runs the kernel
     "serial": {"threads": (256,)},
 }
@@ -979,9 +980,7 @@ def apply(kernel, calls, config) -> tuple:
     elif config.get("workgroup"):
         s.workgroup()
     s.block(config["threads"])
-    if cls == "item":
-        # the same operands packed at every point of the space, so that one set of arguments
-        # (the default's) serves every candidate of the kernel
+    if cls == "item" and config.get("pack", True):
         inner = names[-1]
         for param in range(1, len(kernel.params)):
             rc = _weight_rows(kernel, calls, param) if calls else None
