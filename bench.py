@@ -353,14 +353,17 @@ def generated_kernels(rows: int = 512, reps: int = 20, seed: int = 7) -> dict:
     return {"rows": rows, "reps": reps, "kernels": out, "tuned": tuned}
 
 
-def generated_config5(weights: dict, past: int = PROMPT + NEW_TOKENS - 2, seed: int = 3) -> dict:
+def generated_config5(weights: dict, past: int = PROMPT + NEW_TOKENS - 2, seed: int = 3, cache=None,
+                      eager: int = 0) -> dict:
     """Config 5's decode step through the drop-in path: the reference's own compiled program for
     the model (int8 mode, recorded in tests/golden/programs.json.gz; its tokens and logits are
     checked against the reference's in tests/test_config5_generated_gpu.py) generated as HIP by
     codegen_hip, on these weights (the projections quantized per row on the GPU), at one token
     and ``past`` cached positions; default GPU schedules, then each kernel's schedule chosen by
-    the autotuner on that step. Graph-replayed, like the hand-written step."""
-    from nanocompile_amd import autotune, kernels, lir
+    the autotuner on that step (``cache``: the autotuner's). Graph-replayed, like the hand-written
+    step; with ``eager``, each step is then also launched that many times directly (for a kernel
+    trace: both run from the program's candidate library, so every kernel has its own name)."""
+    from nanocompile_amd import autotune, hip, kernels, lir
     from nanocompile_amd.compiled import CompiledProgram
     from nanocompile_amd.models.config import QWEN25_05B as c
     golden = Path(__file__).resolve().parent / "tests" / "golden"
@@ -383,14 +386,22 @@ def generated_config5(weights: dict, past: int = PROMPT + NEW_TOKENS - 2, seed: 
     out = {"program": f"the reference's int8 program: {len(program.kernels)} kernels, {len(program.calls)} launches "
                       f"a step", "past": past}
     t0 = time.perf_counter()
-    tuner = autotune.Autotuner(cache=None, rounds=3, reps=2, verbose=True,
+    tuner = autotune.Autotuner(cache=cache, rounds=3, reps=2, verbose=True,
                                workloads=[("decode", {"seq": 1, "past": past}, 1.0)])
-    for label, schedule in (("default", "default"), ("tuned", tuner)):
+    library = autotune.CandidateLibrary(program)
+    for label, schedule in (("default", autotune.Chosen(library, [0] * len(program.kernels))), ("tuned", tuner)):
         log(f"generated: config 5's program, {label} schedules")
         compiled = CompiledProgram(program, schedule=schedule)
         launch, _, _ = compiled.prepare(inputs, ref_weights)
         us = graph_us(lambda i, launch=launch: launch(), 1, rounds=5)
         out[label] = {"us_per_step": round(us, 1), "tok_s": round(1e6 / us, 1)}
+        if eager:
+            for _ in range(eager):
+                launch()
+            hip.sync()
+            out[label]["kernels"] = [{"device": "nc_g" + name[4:], "schedule": l.describe(),
+                                      "packed": any(p.packed for p in k.params)}
+                                     for name, (k, l) in zip(compiled.launcher_names, compiled.scheduled)]
         del compiled
     out["tuned"]["schedules"] = {f"kernel {r.shape[0]} ({r.op})": r.config for r in tuner.records if r.winner}
     out["seconds"] = round(time.perf_counter() - t0, 1)
@@ -680,9 +691,11 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=NEW_TOKENS - 1)
     parser.add_argument("--warmup", type=int, default=1)
-    parser.add_argument("--workload", choices=("decode", "gemv", "kernels", "generated"), default="decode",
+    parser.add_argument("--workload", choices=("decode", "gemv", "kernels", "generated", "generated5"),
+                        default="decode",
                         help="kernels: each decode-step kernel launched eagerly at past 383 (for counter passes); "
-                             "generated: config 2's generated programs, default and tuned, launched eagerly")
+                             "generated / generated5: config 2's generated programs / config 5's generated "
+                             "decode step, default and tuned, launched eagerly (for kernel traces)")
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-blocks", action="store_true", help="skip the per-block measurements (configs 2-4)")
     parser.add_argument("--no-graph", action="store_true",
@@ -703,6 +716,12 @@ def main() -> int:
     hip.sync()
     del src, dst
 
+    if args.workload == "generated5":
+        from nanocompile_amd.models.config import QWEN25_05B, random_weights
+        print(json.dumps({"workload": "config 5's reference program as HIP, one decode step at past 382, eager",
+                          **generated_config5(random_weights(QWEN25_05B, seed=0), cache=True, eager=10)}),
+              flush=True)
+        return 0
     if args.workload == "generated":
         print(json.dumps({"workload": "config 2's generated programs at 512 rows, eager",
                           **generated_kernels()}), flush=True)
