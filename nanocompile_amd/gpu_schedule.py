@@ -317,14 +317,21 @@ class Hoisted:
 
 @dataclass(frozen=True)
 class Lanes:
-    """Accumulator arrays held one element per lane: ``width`` lanes an item; lane l runs the
-    chain of element l, the chain loops' vars given by ``loops`` as (var, extent, coefficient),
-    var = l / coefficient % extent; ``index`` is the element index the chain statements use."""
+    """Accumulator arrays of ``width`` elements held ``per_lane`` consecutive elements a lane:
+    ``width / per_lane`` lanes an item; lane l runs the chains of elements l * per_lane + j,
+    the chain loops' vars given by ``loops`` as (var, extent, coefficient), var = e /
+    coefficient % extent for element e; ``index`` is the element index the chain statements use."""
 
     width: int
     arrays: tuple[str, ...]
     loops: tuple[tuple[str, int, int], ...]
     index: object
+    per_lane: int = 1
+
+    @property
+    def lanes(self) -> int:
+        """Lanes an item."""
+        return self.width // self.per_lane
 
 
 @dataclass(frozen=True)
@@ -359,7 +366,8 @@ class Launch:
         if self.hoist:
             parts.append("hoist()")
         if self.lanes:
-            parts.append(f"lanes({', '.join(self.lanes.arrays)})")
+            per = f", {self.lanes.per_lane} a lane" if self.lanes.per_lane > 1 else ""
+            parts.append(f"lanes({', '.join(self.lanes.arrays)}{per})")
         if self.vector > 1:
             parts.append(f"vectorize({self.vector})")
         parts += [f"unroll({v}, {n})" for v, n in self.unroll]
@@ -529,19 +537,25 @@ class GpuSchedule:
         self.steps.append("hoist")
         return self
 
-    def lanes(self, name: str) -> "GpuSchedule":
-        """Hold accumulator array ``name`` (and the arrays its chains update alongside it) one
-        element per lane; see ``lane_chains`` for when that is legal."""
+    def lanes(self, name: str, per_lane: int = 1) -> "GpuSchedule":
+        """Hold accumulator array ``name`` (and the arrays its chains update alongside it)
+        ``per_lane`` consecutive elements a lane; see ``lane_chains`` for when that is legal.
+        ``per_lane`` must divide the extent of the element index's unit digit (the innermost
+        element loop), so a lane's elements differ in that digit alone: consecutive."""
         launch = self.launch
         if not launch.grid:
             raise ScheduleError("lanes: bind the grid first")
         if launch.per_workgroup or launch.vector > 1 or launch.lanes:
             raise ScheduleError("lanes: an item must be one thread's, not vectorized")
         lanes = lane_chains(self.item_body(), name)
-        if launch.threads % lanes.width:
-            raise ScheduleError(f"lanes({name}): {lanes.width} lanes an item do not divide block({launch.threads})")
+        unit = next(extent for _, extent, coeff in lanes.loops if coeff == 1)
+        if per_lane < 1 or per_lane & (per_lane - 1) or unit % per_lane:
+            raise ScheduleError(f"lanes({name}, {per_lane}): not a power of two dividing the unit digit's {unit}")
+        lanes = replace(lanes, per_lane=per_lane)
+        if launch.threads % lanes.lanes:
+            raise ScheduleError(f"lanes({name}): {lanes.lanes} lanes an item do not divide block({launch.threads})")
         self.launch = replace(launch, lanes=lanes)
-        self.steps.append(f"lanes {name}")
+        self.steps.append(f"lanes {name} {per_lane}")
         return self
 
     def vectorize(self, width: int) -> "GpuSchedule":
@@ -901,7 +915,7 @@ SPACES: dict[str, dict[str, tuple]] = {
             "unroll": (0, 4), "lead": (False, True), "hoist": (False, True)},
     # a thread per item, or (workgroup) a workgroup per item with its loops' operands staged
     "item": {"threads": (256, 64, 128, 512, 1024), "vector": (1, 2, 4), "workgroup": (False, True),
-             "unroll": (0, 4), "lead": (False, True), "hoist": (False, True), "lanes": (False, True),
+             "unroll": (0, 4), "lead": (False, True), "hoist": (False, True), "lanes": (0, 1, 4),
              "pack": (True, False)},
     # no loop can be the grid: one thread runs the kernel
     "serial": {"threads": (256,)},
@@ -1000,10 +1014,11 @@ def apply(kernel, calls, config) -> tuple:
     if config.get("hoist"):
         s.hoist()
     if config.get("lanes"):
+        # lanes: elements a lane (0: one thread an item)
         arrays = [st.name for st in s.item_body() if kind(st) == "Array"]
         for name in arrays:
             try:
-                s.lanes(name)
+                s.lanes(name, int(config["lanes"]))
                 break
             except ScheduleError:
                 continue

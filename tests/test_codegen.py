@@ -524,6 +524,18 @@ def test_lanes_spread_the_references_accumulators_one_element_a_lane():
             text = codegen_hip.render_kernel(scheduled, launch, i)
             assert f"const int nc_l = threadIdx.x & {lanes.width - 1};" in text
             assert "__shfl(" in text and "if (nc_l == 0) x0[" in text
+            # four consecutive elements a lane: lane l's j-th is element 4 l + j, as the renderer
+            # computes its digits (the others from 4 l, the unit digit 4 l % extent + j)
+            four, fl = gpu_schedule.apply(kernel, calls[i], dict(config, lanes=4))
+            assert fl.lanes.lanes == lanes.width // 4
+            elements = []
+            for lane in range(fl.lanes.lanes):
+                for j in range(4):
+                    digits = {var: ((lane * 4) // coeff) % extent if coeff != 1 else (lane * 4) % extent + j
+                              for var, extent, coeff in fl.lanes.loops}
+                    elements.append(simplify.value_range(fl.lanes.index, {v: (d, d) for v, d in digits.items()})[0])
+            assert elements == list(range(lanes.width)), (name, i)
+            assert "acc_0_l[nc_j] = " in codegen_hip.render_kernel(four, fl, i)
     assert found
 
 
