@@ -386,7 +386,7 @@ def generated_config5(weights: dict, past: int = PROMPT + NEW_TOKENS - 2, seed: 
     out = {"program": f"the reference's int8 program: {len(program.kernels)} kernels, {len(program.calls)} launches "
                       f"a step", "past": past}
     t0 = time.perf_counter()
-    tuner = autotune.Autotuner(cache=cache, rounds=3, reps=2, verbose=True,
+    tuner = autotune.Autotuner(cache=cache, rounds=5, reps=4, verbose=True,
                                workloads=[("decode", {"seq": 1, "past": past}, 1.0)])
     library = autotune.CandidateLibrary(program)
     for label, schedule in (("default", autotune.Chosen(library, [0] * len(program.kernels))), ("tuned", tuner)):

@@ -945,14 +945,15 @@ _POINTS = {cls: {canonical(dict(zip(k, v))) for v in itertools.product(*k.values
 
 
 def _serial_loops(s: "GpuSchedule") -> list[str]:
-    """The item's loops one thread runs in order, long enough to unroll: constant extent of at
-    least 8, not the shared loop, indexing no register array (those are unrolled whole)."""
+    """The item's loops one thread runs in order, long enough to unroll: an extent known to be at
+    least 8 or set at run time, not the shared loop, indexing no register array (those are
+    unrolled whole)."""
     staged = {st.name for st in s.launch.stage}
     out = []
     for st in statements(s.item_body()):
         if kind(st) != "Loop" or st.var == s.launch.cooperate:
             continue
-        if kind(st.extent) != "Const" or int(st.extent.value) < 8:
+        if kind(st.extent) == "Const" and int(st.extent.value) < 8:
             continue
         arrays = any(kind(n) == "Local" and n.name not in staged for x in scalars(st.body) for n in walk(x))
         if not arrays:
