@@ -527,8 +527,9 @@ class GpuSchedule:
         body = self.item_body()
         serial = body[:-1] if launch.cooperate else body
         found = []
+        staged = {st.name for st in launch.stage}
         for at, st in enumerate(serial):
-            h = hoistable(serial, at, len(found))
+            h = hoistable(serial, at, len(found), staged)
             if h is not None:
                 found.append(h)
         if not found:
@@ -623,14 +624,14 @@ class GpuSchedule:
 # -- chains whose operands are computed first --------------------------------------------------
 
 
-def hoistable(serial, at: int, k: int) -> Hoisted | None:
+def hoistable(serial, at: int, k: int, staged=frozenset()) -> Hoisted | None:
     """Statement ``at`` of a lead wave's part as a Hoisted (its LDS array ``nc_h<k>``), when it is
     a loop whose body is Lets and then one update of an accumulator declared outside it, and
     the value the update takes each iteration is one expression free of the accumulator:
     either exactly one of the loop's Lets (the update reading it, the loop var and outer
     scalars), or, with no Lets, the other operand of ``acc op x``. The Lets and that value read
-    no array but staged windows (another thread would not have it), and the extent is the same
-    for every item (symbols and constants), so the LDS array has one size."""
+    no array but the ``staged`` windows (another thread would not have it), and the extent is
+    the same for every item (symbols and constants), so the LDS array has one size."""
     loop = serial[at]
     if kind(loop) != "Loop" or not loop.body:
         return None
@@ -643,7 +644,7 @@ def hoistable(serial, at: int, k: int) -> Hoisted | None:
         return None
 
     def private(x) -> bool:
-        return any(kind(n) == "Local" and not n.name.startswith("nc_s") for n in walk(x))
+        return any(kind(n) == "Local" and n.name not in staged for n in walk(x))
 
     if any(uses_var(s.value, acc) or private(s.value) for s in lets):
         return None
