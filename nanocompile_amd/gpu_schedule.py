@@ -526,6 +526,10 @@ class GpuSchedule:
             raise ScheduleError("hoist: needs a lead wave")
         body = self.item_body()
         serial = body[:-1] if launch.cooperate else body
+        if any(kind(st) == "Array" for st in serial):
+            # the phases split the lead wave's part into blocks; an array declared in one would
+            # not be visible in the next
+            raise ScheduleError("hoist: the lead wave's part declares an array")
         found = []
         staged = {st.name for st in launch.stage}
         for at, st in enumerate(serial):
