@@ -964,7 +964,7 @@ def _serial_loops(s: "GpuSchedule") -> list[str]:
         if kind(st.extent) == "Const" and int(st.extent.value) < 8:
             continue
         arrays = any(kind(n) == "Local" and n.name not in staged for x in scalars(st.body) for n in walk(x))
-        if not arrays:
+        if not arrays and st.var not in out:          # (two loops may share a name: one hint covers both)
             out.append(st.var)
     return out
 
