@@ -15,10 +15,12 @@ namespace {
 
 constexpr int kThreads = 256;
 
+// The workgroup's maximum and sum through four LDS words. Each scratch array
+// serves one reduction of a launch (every kernel here takes one row a
+// workgroup), so no barrier is needed before it is written.
 __device__ float block_max(float v, float *scratch) {
     v = nc::wave_max_f32(v);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();
     if (lane == 0) scratch[wave] = v;
     __syncthreads();
     return nc::nan_max(nc::nan_max(scratch[0], scratch[1]), nc::nan_max(scratch[2], scratch[3]));
@@ -27,7 +29,6 @@ __device__ float block_max(float v, float *scratch) {
 __device__ float block_sum(float v, float *scratch) {
     v = nc::wave_sum_f32(v);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();
     if (lane == 0) scratch[wave] = v;
     __syncthreads();
     return __fadd_rn(__fadd_rn(scratch[0], scratch[1]), __fadd_rn(scratch[2], scratch[3]));
@@ -144,7 +145,7 @@ template <int PER_THREAD>
 __global__ __launch_bounds__(kThreads) void rms_norm_quant(float *__restrict__ normed, int8_t *__restrict__ xq,
                                                            float *__restrict__ xs, const float *__restrict__ x,
                                                            const float *__restrict__ gamma, int K, float eps) {
-    __shared__ float scratch[4];
+    __shared__ float scratch[4], scratch_max[4];      // one array a reduction
     const float *row = x + (size_t)blockIdx.x * K;
     float v[PER_THREAD];
     float ss = 0.0f;
@@ -163,7 +164,7 @@ __global__ __launch_bounds__(kThreads) void rms_norm_quant(float *__restrict__ n
         v[i] = k < K ? __fmul_rn(__fmul_rn(v[i], rcp), gamma[k]) : 0.0f;
         mag = nc::nan_max(mag, fabsf(v[i]));
     }
-    const float scale = nc::token_scale(block_max(mag, scratch));
+    const float scale = nc::token_scale(block_max(mag, scratch_max));
 #pragma unroll
     for (int i = 0; i < PER_THREAD; ++i) {
         const int k = threadIdx.x + i * kThreads;
