@@ -354,7 +354,7 @@ def generated_kernels(rows: int = 512, reps: int = 20, seed: int = 7) -> dict:
 
 
 def generated_config5(weights: dict, past: int = PROMPT + NEW_TOKENS - 2, seed: int = 3, cache=None,
-                      eager: int = 0) -> dict:
+                      eager: int = 0, seq: int = 1, rounds: int = 5, reps: int = 4) -> dict:
     """Config 5's decode step through the drop-in path: the reference's own compiled program for
     the model (int8 mode, recorded in tests/golden/programs.json.gz; its tokens and logits are
     checked against the reference's in tests/test_config5_generated_gpu.py) generated as HIP by
@@ -362,7 +362,8 @@ def generated_config5(weights: dict, past: int = PROMPT + NEW_TOKENS - 2, seed: 
     and ``past`` cached positions; default GPU schedules, then each kernel's schedule chosen by
     the autotuner on that step (``cache``: the autotuner's). Graph-replayed, like the hand-written
     step; with ``eager``, each step is then also launched that many times directly (for a kernel
-    trace: both run from the program's candidate library, so every kernel has its own name)."""
+    trace: both run from the program's candidate library, so every kernel has its own name).
+    ``seq`` > 1 with ``past`` 0 is a prompt's prefill instead (config 4: 512 tokens)."""
     from nanocompile_amd import autotune, hip, kernels, lir
     from nanocompile_amd.compiled import CompiledProgram
     from nanocompile_amd.models.config import QWEN25_05B as c
@@ -380,21 +381,21 @@ def generated_config5(weights: dict, past: int = PROMPT + NEW_TOKENS - 2, seed: 
             ref_weights[name] = weights[name]
     rng = np.random.default_rng(seed)
     cache_shape = (c.num_hidden_layers, c.num_key_value_heads, past, c.head_dim)
-    inputs = {"token_ids": np.array([int(rng.integers(0, c.vocab_size))], np.int64),
+    inputs = {"token_ids": rng.integers(0, c.vocab_size, seq).astype(np.int64),
               "past_keys": rng.standard_normal(cache_shape).astype(np.float32),
               "past_values": rng.standard_normal(cache_shape).astype(np.float32)}
     out = {"program": f"the reference's int8 program: {len(program.kernels)} kernels, {len(program.calls)} launches "
-                      f"a step", "past": past}
+                      f"a step", "seq": seq, "past": past}
     t0 = time.perf_counter()
-    tuner = autotune.Autotuner(cache=cache, rounds=5, reps=4, verbose=True,
-                               workloads=[("decode", {"seq": 1, "past": past}, 1.0)])
+    tuner = autotune.Autotuner(cache=cache, rounds=rounds, reps=reps, verbose=True,
+                               workloads=[("decode" if seq == 1 else "prefill", {"seq": seq, "past": past}, 1.0 / seq)])
     library = autotune.CandidateLibrary(program)
     for label, schedule in (("default", autotune.Chosen(library, [0] * len(program.kernels))), ("tuned", tuner)):
         log(f"generated: config 5's program, {label} schedules")
         compiled = CompiledProgram(program, schedule=schedule)
         launch, _, _ = compiled.prepare(inputs, ref_weights)
         us = graph_us(lambda i, launch=launch: launch(), 1, rounds=5)
-        out[label] = {"us_per_step": round(us, 1), "tok_s": round(1e6 / us, 1)}
+        out[label] = {"us_per_step": round(us, 1), "tok_s": round(seq * 1e6 / us, 1)}
         if eager:
             for _ in range(eager):
                 launch()
@@ -691,10 +692,10 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=NEW_TOKENS - 1)
     parser.add_argument("--warmup", type=int, default=1)
-    parser.add_argument("--workload", choices=("decode", "gemv", "kernels", "generated", "generated5"),
+    parser.add_argument("--workload", choices=("decode", "gemv", "kernels", "generated", "generated5", "generated4"),
                         default="decode",
                         help="kernels: each decode-step kernel launched eagerly at past 383 (for counter passes); "
-                             "generated / generated5: config 2's generated programs / config 5's generated "
+                             "generated / generated5 / generated4: config 2's generated programs / config 5's generated "
                              "decode step, default and tuned, launched eagerly (for kernel traces)")
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-blocks", action="store_true", help="skip the per-block measurements (configs 2-4)")
@@ -716,6 +717,13 @@ def main() -> int:
     hip.sync()
     del src, dst
 
+    if args.workload == "generated4":
+        from nanocompile_amd.models.config import QWEN25_05B, random_weights
+        print(json.dumps({"workload": "config 4 through the reference's program as HIP: a 512-token prompt's "
+                                      "prefill, 24 layers, past 0",
+                          **generated_config5(random_weights(QWEN25_05B, seed=0), past=0, seq=512, cache=True,
+                                              eager=3, rounds=3, reps=2)}), flush=True)
+        return 0
     if args.workload == "generated5":
         from nanocompile_amd.models.config import QWEN25_05B, random_weights
         print(json.dumps({"workload": "config 5's reference program as HIP, one decode step at past 382, eager",
