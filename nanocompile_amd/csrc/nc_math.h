@@ -9,7 +9,8 @@
 // kernel bit for bit.
 //
 // Method (Cody and Waite's argument reduction, then a Taylor polynomial):
-//   exp(x) = 2^k * exp(r),   k = nearest(x / ln 2),     |r| <= ln(2) / 2
+//   exp(x) = 2^m * 2^(j / 64) * exp(r),  64 m + j = nearest(64 x / ln 2),
+//            |r| <= ln(2) / 128, 2^(j / 64) from a table of 64 doubles
 //   sin/cos(x): k = nearest(x * 2 / pi), r = x - k * pi / 2 (two-part pi / 2),
 //   then sin(r) or cos(r) by quadrant, |r| <= pi / 4.
 // Everything runs in double, so the result before the final rounding to
@@ -23,8 +24,10 @@
 
 #if defined(__HIPCC__)
 #define NC_MATH_FN __host__ __device__ __forceinline__
+#define NC_MATH_TABLE static __device__ __constant__ const
 #else
 #define NC_MATH_FN static inline
+#define NC_MATH_TABLE static const
 #endif
 
 NC_MATH_FN double nc_pow2i(int k) {
@@ -42,6 +45,27 @@ NC_MATH_FN double nc_nearest(double x) {
     return __builtin_trunc(x + (x >= 0.0 ? 0.5 : -0.5));
 }
 
+// 2^(j / 64) for j = 0 .. 63, each the double nearest the exact value (written
+// as hexadecimal literals so no decimal conversion intervenes).
+NC_MATH_TABLE double nc_exp2_64ths[64] = {
+    0x1.0000000000000p+0, 0x1.02c9a3e778061p+0, 0x1.059b0d3158574p+0, 0x1.0874518759bc8p+0,
+    0x1.0b5586cf9890fp+0, 0x1.0e3ec32d3d1a2p+0, 0x1.11301d0125b51p+0, 0x1.1429aaea92de0p+0,
+    0x1.172b83c7d517bp+0, 0x1.1a35beb6fcb75p+0, 0x1.1d4873168b9aap+0, 0x1.2063b88628cd6p+0,
+    0x1.2387a6e756238p+0, 0x1.26b4565e27cddp+0, 0x1.29e9df51fdee1p+0, 0x1.2d285a6e4030bp+0,
+    0x1.306fe0a31b715p+0, 0x1.33c08b26416ffp+0, 0x1.371a7373aa9cbp+0, 0x1.3a7db34e59ff7p+0,
+    0x1.3dea64c123422p+0, 0x1.4160a21f72e2ap+0, 0x1.44e086061892dp+0, 0x1.486a2b5c13cd0p+0,
+    0x1.4bfdad5362a27p+0, 0x1.4f9b2769d2ca7p+0, 0x1.5342b569d4f82p+0, 0x1.56f4736b527dap+0,
+    0x1.5ab07dd485429p+0, 0x1.5e76f15ad2148p+0, 0x1.6247eb03a5585p+0, 0x1.6623882552225p+0,
+    0x1.6a09e667f3bcdp+0, 0x1.6dfb23c651a2fp+0, 0x1.71f75e8ec5f74p+0, 0x1.75feb564267c9p+0,
+    0x1.7a11473eb0187p+0, 0x1.7e2f336cf4e62p+0, 0x1.82589994cce13p+0, 0x1.868d99b4492edp+0,
+    0x1.8ace5422aa0dbp+0, 0x1.8f1ae99157736p+0, 0x1.93737b0cdc5e5p+0, 0x1.97d829fde4e50p+0,
+    0x1.9c49182a3f090p+0, 0x1.a0c667b5de565p+0, 0x1.a5503b23e255dp+0, 0x1.a9e6b5579fdbfp+0,
+    0x1.ae89f995ad3adp+0, 0x1.b33a2b84f15fbp+0, 0x1.b7f76f2fb5e47p+0, 0x1.bcc1e904bc1d2p+0,
+    0x1.c199bdd85529cp+0, 0x1.c67f12e57d14bp+0, 0x1.cb720dcef9069p+0, 0x1.d072d4a07897cp+0,
+    0x1.d5818dcfba487p+0, 0x1.da9e603db3285p+0, 0x1.dfc97337b9b5fp+0, 0x1.e502ee78b3ff6p+0,
+    0x1.ea4afa2a490dap+0, 0x1.efa1bee615a27p+0, 0x1.f50765b6e4540p+0, 0x1.fa7c1819e90d8p+0,
+};
+
 NC_MATH_FN float nc_expf(float xf) {
     // The special cases are chosen at the end, so the GPU runs one straight
     // path with no divergent branch; their operand is replaced by 0 first.
@@ -50,32 +74,27 @@ NC_MATH_FN float nc_expf(float xf) {
                                                    // double result rounds to inf itself)
     const int tiny = xf < -104.0f;                 // below half the least subnormal: 0
     const double x = (nan | big | tiny) ? 0.0 : (double)xf;
-    const double inv_ln2 = 1.4426950408889634;
-    const double ln2_hi = 6.93147180369123816490e-01;   // 33 significant bits: k * ln2_hi is exact
-    const double ln2_lo = 1.90821492927058770002e-10;
-    const double k = nc_nearest(x * inv_ln2);
-    const double r = (x - k * ln2_hi) - k * ln2_lo;
-    // exp(r), |r| <= 0.3466: Taylor to r^13 (truncation < 3e-17 relative),
-    // Horner's steps as a multiply and an add each (measured on MI355X: the
-    // fused double multiply-add form made the prefill attention kernel, where
-    // 7 of these chains run side by side, 6% slower)
-    double p = 1.0 / 6227020800.0;                 // 1/13!
-    p = p * r + 1.0 / 479001600.0;                 // 1/12!
-    p = p * r + 1.0 / 39916800.0;
-    p = p * r + 1.0 / 3628800.0;
-    p = p * r + 1.0 / 362880.0;
-    p = p * r + 1.0 / 40320.0;
-    p = p * r + 1.0 / 5040.0;
-    p = p * r + 1.0 / 720.0;
-    p = p * r + 1.0 / 120.0;
+    const double inv = 0x1.71547652b82fep+6;       // 64 / ln 2
+    const double l_hi = 0x1.62e42ffp-7;            // ln 2 / 64 to 29 significant bits: k * l_hi is exact
+    const double l_lo = -0x1.718432a1b0e26p-41;    // ln 2 / 64 - l_hi
+    const double k = nc_nearest(x * inv);          // |k| <= 9601
+    const double r = (x - k * l_hi) - k * l_lo;
+    // exp(r), |r| <= ln 2 / 128 = 0.0054: Taylor to r^5 (truncation < 4e-17
+    // relative), Horner's steps as a multiply and an add each (measured on
+    // MI355X: the fused double multiply-add form made the prefill attention
+    // kernel, where 7 of these chains run side by side, 6% slower)
+    double p = 1.0 / 120.0;
     p = p * r + 1.0 / 24.0;
     p = p * r + 1.0 / 6.0;
     p = p * r + 0.5;
     p = p * r + 1.0;
     p = p * r + 1.0;
+    // k = 64 m + j, 0 <= j < 64: exp(x) = 2^m * 2^(j / 64) * exp(r); 2^m may be
+    // subnormal in float but never in double (m >= -151)
     const int ki = (int)k;
-    // 2^k may be subnormal in float but never in double (k >= -150)
-    const float y = (float)(p * nc_pow2i(ki));
+    const int j = ki & 63;
+    const int m = (ki - j) / 64;
+    const float y = (float)(nc_exp2_64ths[j] * p * nc_pow2i(m));
     return nan ? xf : big ? (float)(1e300 * 1e300) : tiny ? 0.0f : y;
 }
 

@@ -120,6 +120,32 @@ def test_nc_math_against_the_c_library(host):
     assert s[0] == 0 and np.signbit(s[1]) and np.isnan(s[2]) and np.isnan(s[3]) and s[7] == np.float32(1e-30)
 
 
+
+def test_nc_math_exp_constants():
+    """nc_expf's table holds the double nearest 2^(j / 64) for every j, its
+    reduction constants split ln 2 / 64 exactly enough (the high part short
+    enough (29 bits) that k * l_hi is exact for every |k| <= 9601) and 64 / ln 2 is the
+    nearest double: checked against 50-digit decimal arithmetic."""
+    import math
+    import re
+    from decimal import Decimal, getcontext
+
+    getcontext().prec = 50
+    text = (Path(__file__).resolve().parents[1] / "nanocompile_amd" / "csrc" / "nc_math.h").read_text()
+    body = text[text.index("nc_exp2_64ths[64] = {"):]
+    table = [float.fromhex(h) for h in re.findall(r"0x[0-9a-f.]+p[-+]\d+", body[:body.index("};")])]
+    ln2 = Decimal(2).ln()
+    assert table == [float((ln2 * j / 64).exp()) for j in range(64)]
+
+    def constant(name):
+        return float.fromhex(re.search(rf"const double {name} = (-?0x[0-9a-f.]+p[-+]\d+);", text).group(1))
+
+    inv, hi, lo = constant("inv"), constant("l_hi"), constant("l_lo")
+    assert inv == float(64 / ln2)
+    assert abs(Decimal(hi) + Decimal(lo) - ln2 / 64) < Decimal(2) ** -95
+    mantissa = int(math.frexp(hi)[0] * 2 ** 53)
+    assert mantissa % 2 ** (53 - 29) == 0 and 9601 * 2 ** 29 < 2 ** 53
+
 WIDTHS = [(896, 72), (4864, 24), (77, 40), (40, 16), (160, 40), (96, 24)]
 
 
