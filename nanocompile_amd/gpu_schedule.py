@@ -921,9 +921,10 @@ SPACES: dict[str, dict[str, tuple]] = {
             "unroll": (0, 4), "lead": (False, True), "hoist": (False, True)},
     # a thread per item, or (workgroup) a workgroup per item with its loops' operands staged (a
     # lead wave, hoisting, as for rows), or (lanes) an item's accumulator chains 1 or 4 elements
-    # a lane; weights packed in 64-row blocks or read row-major
+    # a lane; weights packed in 64-row blocks or read row-major; serial loops unrolled up to 32
+    # steps (a lane's chain then issues that many steps' loads before its multiply-adds need them)
     "item": {"threads": (256, 64, 128, 512, 1024), "vector": (1, 2, 4), "workgroup": (False, True),
-             "unroll": (0, 4), "lead": (False, True), "hoist": (False, True), "lanes": (0, 1, 4),
+             "unroll": (0, 4, 16, 32), "lead": (False, True), "hoist": (False, True), "lanes": (0, 1, 4),
              "pack": (True, False)},
     # no loop can be the grid: one thread runs the kernel
     "serial": {"threads": (256,)},
@@ -957,13 +958,19 @@ def _serial_loops(s: "GpuSchedule") -> list[str]:
     least 8 or set at run time, not the shared loop, indexing no register array (those are
     unrolled whole)."""
     staged = {st.name for st in s.launch.stage}
+    # arrays held across lanes are a register (or a few) a lane, indexed by nothing that varies;
+    # the loops that enumerate their elements become the lane mapping
+    held = set(s.launch.lanes.arrays) if s.launch.lanes else set()
+    element_loops = {var for var, _, _ in s.launch.lanes.loops} if s.launch.lanes else set()
     out = []
     for st in statements(s.item_body()):
-        if kind(st) != "Loop" or st.var == s.launch.cooperate:
+        if kind(st) != "Loop" or st.var == s.launch.cooperate or st.var in element_loops:
             continue
         if kind(st.extent) == "Const" and int(st.extent.value) < 8:
             continue
-        arrays = any(kind(n) == "Local" and n.name not in staged for x in scalars(st.body) for n in walk(x))
+        arrays = any(kind(n) == "Local" and n.name not in staged and n.name not in held
+                     for x in scalars(st.body) for n in walk(x))
+        arrays = arrays or any(kind(t) == "ArrayStore" and t.name not in held for t in statements(st.body))
         if not arrays and st.var not in out:          # (two loops may share a name: one hint covers both)
             out.append(st.var)
     return out
