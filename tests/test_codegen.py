@@ -593,3 +593,25 @@ def test_hoist_computes_the_chains_operands_first_and_refuses_what_depends_on_th
     for bad in (reads_acc, two):
         with pytest.raises(gpu_schedule.ScheduleError, match="no loop"):
             gpu_schedule.GpuSchedule(bad).grid("i0").workgroup().lead().hoist()
+
+
+def test_unroll_reaches_the_loop_around_lane_held_chains_but_not_register_array_stores():
+    """With an item's accumulators held across lanes, its k loop updates one register a lane and
+    may be unrolled (its loads then issue ahead of the chain); the tree after it, which stores
+    into a register array, is never given a partial unroll hint (it would move the array to
+    memory). Config 5's down projection, as the reference compiles it."""
+    prog = P.config5()[0]
+    kernel = prog.kernels[14]
+    assert kernel.primitive == "matmul_i8+epilogue" and gpu_schedule.kernel_class(kernel) == "item"
+    config = dict(gpu_schedule.DEFAULTS["item"], threads=128, lanes=1, unroll=16, pack=False)
+    sched, launch = gpu_schedule.apply(kernel, (), config)
+    unrolled = dict(launch.unroll)
+    # one loop: the k loop (the tree's loop over the register array h stays without a hint)
+    assert launch.lanes is not None and len(unrolled) == 1 and set(unrolled.values()) == {16}
+    source = codegen_hip.render_kernel(sched, launch, 0, None)
+    for var in unrolled:
+        loop_at = source.index(f"for (int64_t {var} = 0;")
+        assert source.rfind("#pragma unroll 16", 0, loop_at) > source.rfind("\n", 0, loop_at) - 80
+    # without lanes the same loop indexes the accumulator array: nothing to unroll
+    with pytest.raises(gpu_schedule.ScheduleError):
+        gpu_schedule.apply(kernel, (), dict(gpu_schedule.DEFAULTS["item"], threads=128, unroll=16, pack=False))
