@@ -662,10 +662,13 @@ def program_kernel_key(library: CandidateLibrary, kernel: int, workloads) -> str
 
 
 class Autotuner:
-    """Chooses the schedule of each projection problem (op, M, N, K) on this GPU.
+    """Finds, by timing on the GPU in use, the fastest schedule of each problem it is asked
+    about: a projection (op, M, N, K), a prompt's attention, a generated program's kernels.
 
-    ``cache`` is a TuningCache, a path, True for the default file, or None to
-    measure every time. ``records`` holds what each tuning did.
+    Winners persist through ``cache``: a TuningCache; a file path; True for the file that
+    NANOCOMPILE_AMD_TUNING names, else one under the user's cache directory; or None, which
+    keeps nothing across processes, so each new tuner times each problem again. ``records``
+    lists every tuning this tuner ran or read back.
     """
 
     def __init__(self, rounds: int = 7, reps: int = 32, margin: float = 0.03, seed: int = 0,
