@@ -507,6 +507,66 @@ def block_measurements(model, seed: int = 7) -> dict:
     return out
 
 
+def prefill_gemms_vs_library(m: int = 512, copies: int = 8) -> dict:
+    """Config 4's int8 GEMMs at M = ``m``: this library's MFMA kernel (its default tile, and every
+    tile of its table, with the int32-only epilogue beside the dequantizing one) against the
+    vendor library's int8 GEMM (torch._int_mm, int32 out), each graph-replayed over ``copies``
+    rotating weight copies. Microseconds a call."""
+    import torch
+    torch.cuda.init()               # torch's runtime first: it finds no device once ours holds it
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import DeviceArray
+    hip.init(0)
+    rng = np.random.default_rng(0)
+    shapes = dict(PREFILL_SHAPES, **{"gate+up as one (9728,896)": (9728, 896)})
+    out = {}
+    for name, (n, k) in shapes.items():
+        xq = DeviceArray.from_host(rng.integers(-127, 128, (m, k)).astype(np.int8))
+        xs = DeviceArray.from_host((rng.random(m) * 0.05).astype(np.float32))
+        ws = [(DeviceArray.from_host(rng.integers(-127, 128, (n, k)).astype(np.int8)),
+               DeviceArray.from_host((rng.random(n) * 0.01).astype(np.float32))) for _ in range(copies)]
+        y = DeviceArray((m, n), np.float32)
+        acc = DeviceArray((m, n), np.int32)
+
+        def ours(schedule, entry="dequant"):
+            if entry == "dequant":
+                return graph_us(lambda i: hip.call("nc_matmul_i8_token", [y, xq, xs, ws[i % copies][0],
+                                                                          ws[i % copies][1], None, None],
+                                                   [m, n, k, schedule]), 2 * copies)
+            return graph_us(lambda i: hip.call("nc_matmul_i8_token_acc", [acc, xq, ws[i % copies][0]],
+                                               [m, n, k, schedule]), 2 * copies)
+
+        tiles = [t for t in range(16, 32) if (hip.schedule_info(t) or {}).get("kernel") == "mfma"]
+        row = {"ours_default": round(ours(0), 2),
+               "ours_by_tile": {str(t): round(ours(t), 2) for t in tiles},
+               "ours_int32_by_tile": {str(t): round(ours(t, "acc"), 2) for t in tiles}}
+        a = torch.from_numpy(rng.integers(-127, 128, (m, k)).astype(np.int8)).cuda()
+        bs = [torch.from_numpy(rng.integers(-127, 128, (n, k)).astype(np.int8)).cuda() for _ in range(copies)]
+        side = torch.cuda.Stream()
+        with torch.cuda.stream(side):
+            for b in bs:
+                torch._int_mm(a, b.t())
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for r in range(2 * copies):
+                    torch._int_mm(a, bs[r % copies].t())
+        graph.replay()
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        samples = []
+        for _ in range(5):
+            start.record()
+            graph.replay()
+            stop.record()
+            torch.cuda.synchronize()
+            samples.append(start.elapsed_time(stop) * 1e3 / (2 * copies))
+        row["vendor_int_mm"] = round(statistics.median(samples), 2)
+        out[name] = row
+        log(f"gemms {name}: ours {row['ours_default']} us, torch._int_mm {row['vendor_int_mm']} us")
+    return out
+
+
 # -- config 5: the whole model, greedy decode ----------------------------------------
 
 LM_HEAD_BYTES = 4 * 151936 * 896 + 4 * 896 + 8
@@ -692,11 +752,13 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=NEW_TOKENS - 1)
     parser.add_argument("--warmup", type=int, default=1)
-    parser.add_argument("--workload", choices=("decode", "gemv", "kernels", "generated", "generated5", "generated4"),
+    parser.add_argument("--workload", choices=("decode", "gemv", "kernels", "generated", "generated5", "generated4",
+                                               "gemms"),
                         default="decode",
                         help="kernels: each decode-step kernel launched eagerly at past 383 (for counter passes); "
                              "generated / generated5 / generated4: config 2's generated programs / config 5's generated "
-                             "decode step, default and tuned, launched eagerly (for kernel traces)")
+                             "decode step, default and tuned, launched eagerly (for kernel traces); gemms: config 4's "
+                             "int8 GEMMs, every MFMA tile, against the vendor library's int8 GEMM")
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-blocks", action="store_true", help="skip the per-block measurements (configs 2-4)")
     parser.add_argument("--no-graph", action="store_true",
@@ -707,6 +769,10 @@ def main() -> int:
         print(f"bench.py runs on one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)
         return 2
+    if args.workload == "gemms":
+        print(json.dumps({"workload": "config 4's int8 GEMMs at 512 rows against torch._int_mm, graph-replayed",
+                          "us": prefill_gemms_vs_library()}), flush=True)
+        return 0
     from nanocompile_amd import hip
     from nanocompile_amd.hip import DeviceArray
     hip.init(0)
