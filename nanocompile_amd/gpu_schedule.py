@@ -955,8 +955,9 @@ _POINTS = {cls: {canonical(dict(zip(k, v))) for v in itertools.product(*k.values
 
 def _serial_loops(s: "GpuSchedule") -> list[str]:
     """The item's loops one thread runs in order, long enough to unroll: an extent known to be at
-    least 8 or set at run time, not the shared loop, indexing no register array (those are
-    unrolled whole)."""
+    least 8 or set at run time, not the shared loop, neither reading nor storing a register
+    array (loops over those are unrolled whole; an array held across lanes is a register or a
+    few a lane and does not count), and not a loop that enumerates such an array's elements."""
     staged = {st.name for st in s.launch.stage}
     # arrays held across lanes are a register (or a few) a lane, indexed by nothing that varies;
     # the loops that enumerate their elements become the lane mapping
