@@ -62,20 +62,22 @@ def test_config5_greedy_tokens_are_the_references(config5):
     assert driver.greedy(record["prompt"], len(record["tokens"])) == record["tokens"]
 
 
-def test_config5_with_its_int8_matmuls_across_lanes_is_the_references(config5):
+@pytest.mark.parametrize("unroll", [0, 32])
+def test_config5_with_its_int8_matmuls_across_lanes_is_the_references(config5, unroll):
     """The same program with every int8 projection's 32 accumulator chains one a lane
-    (gpu_schedule lanes): the reference's tokens and logits."""
+    (gpu_schedule lanes), their k loops as written or unrolled 32 steps (152 steps at
+    K = 4864, so a remainder): the reference's tokens and logits."""
     from nanocompile_amd import autotune
     from nanocompile_amd.compiled import CompiledProgram
     from nanocompile_amd.models.config import QWEN25_05B
     driver, record = config5
     library = autotune.CandidateLibrary(driver.program)
     chosen = [next((c for c, cand in enumerate(cands) if cand.config.get("lanes") and cand.config["threads"] == 256
-                    and not cand.config.get("unroll")), 0) for cands in library.candidates]
+                    and cand.config.get("unroll", 0) == unroll), 0) for cands in library.candidates]
     assert sum(1 for c in chosen if c) >= 7
     compiled = CompiledProgram(driver.program, autotune.Chosen(library, chosen))
     lanes = P.Driver(lambda which, inputs: compiled(inputs, driver.weights), config=QWEN25_05B)
-    print("config 5 generated, matmuls across lanes", flush=True)
+    print(f"config 5 generated, matmuls across lanes, unroll {unroll}", flush=True)
     cache = list(lanes.empty())
     first = lanes.forward(record["prompt"], cache, last_only=True)[0]
     _close(first, record, "prompt")
