@@ -214,11 +214,17 @@ def cpu_blocks(seconds: float = 12.0, seed: int = 7) -> dict:
     x = rng.standard_normal((512, c.hidden_size)).astype(np.float32)
     x[rng.random(x.shape) < 0.01] *= 20
     gamma = (1 + 0.1 * rng.standard_normal(c.hidden_size)).astype(np.float32)
-    t0, reps = time.perf_counter(), 0
-    while reps < 3 or time.perf_counter() - t0 < 1.0:
-        host.rms_norm_quant(x, gamma, c.rms_norm_eps)
-        reps += 1
-    rms_us = (time.perf_counter() - t0) / reps * 1e6
+    rms_by_threads = {}
+    for t in counts:                               # config 2's rows spread over the pool, threads swept
+        host.set_threads(t)
+        host.rms_norm_quant_pool(x, gamma, c.rms_norm_eps)
+        t0, reps = time.perf_counter(), 0
+        while reps < 3 or time.perf_counter() - t0 < 1.0 / len(counts) + 0.2:
+            host.rms_norm_quant_pool(x, gamma, c.rms_norm_eps)
+            reps += 1
+        rms_by_threads[t] = (time.perf_counter() - t0) / reps * 1e6
+    rms_threads = min(rms_by_threads, key=rms_by_threads.get)
+    rms_us = rms_by_threads[rms_threads]
 
     one = dataclasses.replace(c, num_hidden_layers=1, vocab_size=64)
     past = 512
@@ -251,15 +257,17 @@ def cpu_blocks(seconds: float = 12.0, seed: int = 7) -> dict:
         prefill_us[t] = timed(prompt_pass, seconds / 2 / len(counts)) * 1e6
     bd, bp = min(decode_us, key=decode_us.get), min(prefill_us, key=prefill_us.get)
     return {"cores": cores, "isa": host.isa(),
-            "rms_norm_quant_512": {"us": round(rms_us, 2), "threads": 1,
-                                   "gbps": round(rms_row_bytes(512) / (rms_us * 1e-6) / 1e9, 2)},
+            "rms_norm_quant_512": {"us": round(rms_us, 2), "threads": rms_threads,
+                                   "gbps": round(rms_row_bytes(512) / (rms_us * 1e-6) / 1e9, 2),
+                                   "by_threads_us": {str(k): round(v, 2) for k, v in rms_by_threads.items()}},
             "block_decode": {"past": past, "us": round(decode_us[bd], 1), "threads": bd,
                              "gbps": round(BLOCK_DECODE_BYTES / (decode_us[bd] * 1e-6) / 1e9, 2),
                              "by_threads_us": {str(k): round(v, 1) for k, v in decode_us.items()}},
             "block_prefill": {"seq": 512, "us": round(prefill_us[bp], 1), "threads": bp,
                               "tok_s": round(512 / (prefill_us[bp] * 1e-6), 1),
                               "by_threads_us": {str(k): round(v, 1) for k, v in prefill_us.items()}},
-            "sample": "config 2: 512 rows repeated for a second; configs 3 and 4: a one-layer host model "
+            "sample": "config 2: 512 rows on the pool, each thread count repeated for a bounded share of a "
+                      "second; configs 3 and 4: a one-layer host model "
                       "(the block, a 64-row head), each thread count timed for a bounded share of "
                       f"{seconds:.0f} s"}
 
@@ -693,6 +701,101 @@ def cpu_decode(config, weights, prompt, gpu_tokens, seconds: float = 16.0) -> di
             "tokens_identical": tokens == gpu_tokens}
 
 
+REFERENCE_PUBLISHED_TOK_S = {"int8": 21.22, "int8-vnni": 19.77}     # README.md:718-719, i7-12700H, 6 threads
+
+
+def reference_modes(weights, prompt, seed: int, graph: bool = True) -> dict:
+    """Config 5 in the reference's own int8 modes on the hand-written model: ``int8`` (float32
+    activations into matmul_i8's 32-chain order) and ``int8-vnni`` (32-wide int8 activation
+    blocks into matmul_i8_vnni's order), each decoding the 256 greedy tokens with one graph
+    replay a token. Timed over all 255 replays with HIP events; the tokens are compared with the
+    reference's own run of this workload (golden G6, tests/golden/g6.json, seed 0) and set beside
+    the reference's published CPU figures for these modes."""
+    from nanocompile_amd.hip import Event
+    from nanocompile_amd.models.config import QWEN25_05B
+    from nanocompile_amd.models.qwen2 import Qwen2
+    g6 = json.loads((Path(__file__).resolve().parent / "tests" / "golden" / "g6.json").read_text())
+    comparable = seed == g6["seed"] and prompt == g6["prompt"]
+    replays = NEW_TOKENS - 1
+    out = {}
+    for mode, tag in (("int8", "int8"), ("int8-vnni", "vnni")):
+        t0 = time.perf_counter()
+        model = Qwen2(QWEN25_05B, weights, quantization=mode, max_tokens=PROMPT)
+        built = time.perf_counter() - t0
+        marks = {0: Event(), replays: Event()}
+        tokens = model.generate(prompt, NEW_TOKENS, timer=lambda i: marks[i].record() if i in marks else None,
+                                graph=graph)
+        ms = marks[0].elapsed_ms(marks[replays])
+        out[mode] = {"tok_s": round(replays / (ms * 1e-3), 2), "ms_per_step": round(ms / replays, 4),
+                     "tokens_identical_to_reference": (tokens == g6[tag]["tokens"][:NEW_TOKENS]) if comparable else None,
+                     "reference_published_cpu_tok_s": REFERENCE_PUBLISHED_TOK_S[mode], "model_build_s": round(built, 1)}
+        log(f"reference modes: {mode} {out[mode]['tok_s']} tok/s, tokens identical to the reference's run: "
+            f"{out[mode]['tokens_identical_to_reference']}")
+        del model
+    out["note"] = ("all 255 decode replays after the 128-token prompt, events on the library stream; the reference's "
+                   "published figures are its own CPU runs (README.md:718-719), a different machine and real weights")
+    return out
+
+
+def qwen2_graph_interface(config, mode: str, last_only: bool = True):
+    """What HIPBackend reads of the reference's Qwen2 graph (models/qwen2.py:167-224 after
+    quantize.quantize): its name, inputs, outputs, the weights it reads and its int8 primitive.
+    The reference's graphs at the tiny model's size are recorded in tests/golden/runner_graphs.json
+    (the backend is tested on those); this is the same interface at config 5's size."""
+    from types import SimpleNamespace
+
+    from nanocompile_amd.runner import HIPBackend
+    weights = HIPBackend(config).expected_weights(mode)
+    op = {"int8": "matmul_i8", "int8-vnni": "matmul_i8_vnni"}.get(mode)
+    nodes = [SimpleNamespace(op=op, attrs={"block": 32} if mode == "int8-vnni" else {})] if op else []
+    return SimpleNamespace(
+        name="qwen2_last" if last_only else "qwen2",
+        inputs=[SimpleNamespace(attrs={"name": n}) for n in ("token_ids", "past_keys", "past_values")],
+        outputs={"logits": None, "keys": None, "values": None},
+        weights={name: SimpleNamespace(dtype=dtype, shape=list(shape)) for name, (dtype, shape) in weights.items()},
+        nodes=nodes)
+
+
+def runner_decode(weights, prompt, expected: list[int], activations: str) -> dict:
+    """Config 5 through the reference's Runner protocol (models/qwen2.py:229, 316-368): the
+    reference's greedy loop restated over ``HIPBackend`` and a host cache kept the reference's way
+    (one buffer sized for the sequence, a view of its filled rows handed over each call, the new
+    keys and values appended after them). Each call uploads the token, runs the model, and
+    downloads the logits row and the new keys and values; argmax on the host. Host wall time of
+    the 255 decode calls (every call ends in a wait for its results)."""
+    from nanocompile_amd import hip, kernels
+    from nanocompile_amd.models.config import QWEN25_05B as c
+    from nanocompile_amd.runner import HIPBackend
+    graph = qwen2_graph_interface(c, "int8")
+    passed = {}
+    for name in HIPBackend(c).expected_weights("int8"):
+        if name.endswith("@int8"):
+            w = name.rsplit("@", 1)[0]
+            q, scales = kernels.quantize_int8(weights[w])          # quantize.py:55-70, on the GPU
+            passed[name], passed[w + "@scales"] = q.numpy(), scales.numpy()
+        elif not name.endswith("@scales"):
+            passed[name] = weights[name]
+    backend = HIPBackend(c, max_tokens=PROMPT, activations=activations)
+    shape = (c.num_hidden_layers, c.num_key_value_heads, PROMPT + NEW_TOKENS, c.head_dim)
+    keys, values, length = np.zeros(shape, np.float32), np.zeros(shape, np.float32), 0
+    pending, tokens, started = list(prompt), [], None
+    before = None
+    for i in range(NEW_TOKENS):
+        if i == 1:
+            started, before = time.perf_counter(), hip.allocations()
+        out = backend(graph, {"token_ids": np.asarray(pending, np.int64), "past_keys": keys[:, :, :length],
+                              "past_values": values[:, :, :length]}, passed)
+        n = out["keys"].shape[2]
+        keys[:, :, length:length + n], values[:, :, length:length + n] = out["keys"], out["values"]
+        length += n
+        tokens.append(int(np.argmax(out["logits"][0])))
+        pending = [tokens[-1]]
+    seconds = time.perf_counter() - started
+    return {"tok_s": round((NEW_TOKENS - 1) / seconds, 2), "ms_per_step": round(seconds * 1e3 / (NEW_TOKENS - 1), 3),
+            "activations": activations, "device_allocations_after_first_call": hip.allocations() - before,
+            "tokens_identical_to_device_loop": tokens == expected if expected is not None else None}
+
+
 def decode(steps: int, warmup: int, cpu: bool, seed: int = 0, graph: bool = True, blocks: bool = True) -> dict:
     """Config 5 as stated: 256 greedy tokens after the 128-token prompt, whatever ``steps`` is;
     the last ``steps`` of the 255 replays (ending at past 383, the config's expensive end) are
@@ -742,6 +845,12 @@ def decode(steps: int, warmup: int, cpu: bool, seed: int = 0, graph: bool = True
         result["generated"] = generated_config5(weights)
         log(f"generated: config 5's reference program as HIP, {result['generated']['default']['tok_s']} tok/s "
             f"default, {result['generated']['tuned']['tok_s']} tuned, in {time.perf_counter() - t0:.1f} s")
+    if blocks:
+        t0 = time.perf_counter()
+        result["reference_modes"] = reference_modes(weights, prompt, seed, graph=graph)
+        result["runner"] = {"token": runner_decode(weights, prompt, tokens, "token")}
+        log(f"runner: config 5 through the reference's Runner protocol, per-token activations: "
+            f"{result['runner']['token']['tok_s']} tok/s; reference modes and runner in {time.perf_counter() - t0:.1f} s")
     if cpu:
         result["cpu"] = cpu_decode(config, weights, prompt, tokens)
     return result
@@ -846,6 +955,7 @@ def main() -> int:
     cpu = d.get("cpu")
     cpu_g = None if args.no_cpu else cpu_gemv(seconds=8.0)
     cpu_b = None if args.no_cpu else cpu_blocks()
+    read = None if args.no_cpu else host_read_bandwidth()
     step_gbps = d["step_bytes"] * d["tok_s"] / 1e9
     record = {
         "metric": "decode tok/s, Qwen2-0.5B-shape int8 on 1 MI355X",
@@ -872,7 +982,9 @@ def main() -> int:
                    "kernels_per_step": kernels,
                    "gemv": gemv_record,
                    "blocks": d.get("blocks"),
-                   "generated": d.get("generated")},
+                   "generated": d.get("generated"),
+                   "reference_modes": d.get("reference_modes"),
+                   "runner": d.get("runner")},
         "roofline": {"bound": "hbm", "achieved": top["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": top["frac"], "traffic": measured_traffic(KERNEL_SYMBOLS[dominant]),
                      "traffic_source": "profiles/traffic.json (rocprofv3 PMC, calibrated); null when no pass "
@@ -897,10 +1009,41 @@ def main() -> int:
                 "by_threads": cpu_g["by_threads"], "isa": cpu_g["isa"],
                 "all_cores_gbps": cpu_g["by_threads"][str(max(map(int, cpu_g["by_threads"])))],
                 "sample": "config 1's GEMV over 240 rotated weight copies (1 GB, past the host's LLC)"},
-            "blocks": cpu_b},
+            "blocks": cpu_b,
+            "host_read_gbps": None if read is None else read["gbps"],
+            "host_read": read,
+            "fraction_of_host_read": None if read is None else host_fractions(read["gbps"], cpu, cpu_g, cpu_b, d)},
     }
     print(json.dumps(record), flush=True)
     return 0
+
+
+def host_read_bandwidth() -> dict:
+    """The host's measured read bandwidth (oracle/nc_host.c nc_host_read_gbps: every core summing
+    its share of a 1 GiB buffer, the reference's bench/probe.c:47-72 idea), the denominator of
+    each CPU figure's fraction."""
+    from oracle import host
+    cores = os.cpu_count() or 1
+    threads = min(cores, 64)
+    host.set_threads(threads)
+    host.read_gbps(1 << 30, 1)                     # pages touched, threads up
+    gbps = max(host.read_gbps(1 << 30, 3) for _ in range(3))
+    log(f"cpu: host read bandwidth {gbps:.1f} GB/s on {threads} threads")
+    return {"gbps": round(gbps, 2), "threads": threads, "buffer_bytes": 1 << 30,
+            "method": "int64 sums over 256 chunks of a 1 GiB buffer on the host pool, best of 3 x 3 passes"}
+
+
+def host_fractions(read: float, cpu, cpu_g, cpu_b, d) -> dict:
+    """Each host figure's bytes per second over the host's read bandwidth."""
+    out = {}
+    if cpu is not None:
+        out["decode"] = round(d["step_bytes"] * cpu["tok_s"] / 1e9 / read, 4)
+    if cpu_g is not None:
+        out["gemv"] = round(cpu_g["gbps"] / read, 4)
+    if cpu_b is not None:
+        out["rms_norm_quant_512"] = round(cpu_b["rms_norm_quant_512"]["gbps"] / read, 4)
+        out["block_decode"] = round(cpu_b["block_decode"]["gbps"] / read, 4)
+    return out
 
 
 if __name__ == "__main__":

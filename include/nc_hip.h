@@ -63,6 +63,14 @@ int32_t nc_memcpy_d2h(void *dst, const void *src, int64_t bytes);      /* waits 
 int32_t nc_memcpy_h2d_async(void *dst, const void *src, int64_t bytes);
 int32_t nc_memcpy_d2h_async(void *dst, const void *src, int64_t bytes);
 int32_t nc_memcpy_d2d(void *dst, const void *src, int64_t bytes);
+/* height rows of width bytes, each side with its own pitch; kind 1 = host to
+ * device, 2 = device to host; waits. The Runner path moves the rows of the
+ * KV cache it does not hold on either side: the reference hands its cache
+ * over as a view of one host buffer per call (models/qwen2.py:232-271,
+ * 337-342), [layers, kv_heads, capacity, head_dim], whose (layer, head)
+ * blocks are rows of a uniform pitch. */
+int32_t nc_memcpy_rows(void *dst, int64_t dst_pitch, const void *src, int64_t src_pitch, int64_t width,
+                       int64_t height, int32_t kind);
 
 /* Wait for the stream; returns the first kernel failure code since the last
  * call (clearing it), NC_LAUNCH_FAILED, or 0 (runtime.py:298-299). */

@@ -50,9 +50,8 @@ import json
 import os
 import statistics
 import sys
-import tempfile
 import time
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 from pathlib import Path
 
 import numpy as np
@@ -315,43 +314,52 @@ def measure(problem: Problem, schedules: list[int], rounds: int, reps: int) -> l
     return [statistics.median(samples[s]) for s in schedules]
 
 
-# -- records and the cache ----------------------------------------------------------------------
+# -- decisions, their log, and the cache ----------------------------------------------------------
 
 
-@dataclass
+@dataclass(frozen=True)
 class Evaluation:
+    """One timing pass of ``choose``: the candidates it ran and their seconds per call."""
+
     stage: str
     schedules: list[int]
     costs: list[float]
 
 
-@dataclass
+@dataclass(frozen=True)
 class TuneRecord:
+    """The answer to one tuning question, measured now or read back from the cache.
+
+    ``winner`` is a schedule number (a library problem) or a candidate index
+    whose point of the schedule space is ``config`` (a generated kernel).
+    ``costs`` holds (incumbent, winner) in seconds per call, or per token for a
+    generated kernel's weighted workloads; ``None`` where they are unknown.
+    ``evaluations`` is what ``choose`` timed, empty for a cached answer.
+    """
+
     key: str
     op: str
     shape: tuple
     space_size: int
     winner: int = 0
-    default_cost: float | None = None
-    winner_cost: float | None = None
-    evaluations: list[Evaluation] = field(default_factory=list)
-    seconds: float = 0.0
+    costs: tuple = (None, None)
     cached: bool = False
-    config: dict | None = None          # a generated kernel's winning point of its schedule space
+    config: dict | None = None
+    evaluations: tuple = ()
+    seconds: float = 0.0
+
+    @property
+    def default_cost(self) -> float | None:
+        return self.costs[0]
+
+    @property
+    def winner_cost(self) -> float | None:
+        return self.costs[1]
 
     @property
     def speedup(self) -> float | None:
-        if not self.default_cost or not self.winner_cost:
-            return None
-        return self.default_cost / self.winner_cost
-
-    def as_json(self) -> dict:
-        return {"key": self.key, "op": self.op, "shape": list(self.shape), "space": self.space_size,
-                "winner": self.winner, "default_cost": self.default_cost, "winner_cost": self.winner_cost,
-                "speedup": self.speedup, "seconds": round(self.seconds, 3), "cached": self.cached,
-                "config": self.config,
-                "evaluations": [{"stage": e.stage, "schedules": e.schedules, "costs": e.costs}
-                                for e in self.evaluations]}
+        before, after = self.costs
+        return before / after if before and after else None
 
 
 def choose(space: list[int], cost, margin: float) -> tuple[int, list[Evaluation], float, float]:
@@ -375,6 +383,11 @@ def choose(space: list[int], cost, margin: float) -> tuple[int, list[Evaluation]
     return incumbent, log, confirm[0], confirm[0]
 
 
+# how many of the tuner's rounds each stage of ``choose`` runs: the confirmation decides, so it
+# gets more samples than the first pass over every candidate
+ROUNDS_FACTOR = {"sample": 1, "confirm": 2}
+
+
 def machine_key() -> str:
     """Arch, HIP runtime and driver, CU count: a schedule tuned on one need not suit another."""
     info = hip.device_info()
@@ -384,36 +397,54 @@ def machine_key() -> str:
 
 
 class TuningCache:
-    """Winning schedules on disk: ``{"machines": {machine: {problem: entry}}}``, in JSON."""
+    """Tuning answers on disk, as an append-only log of JSON lines.
+
+    Each ``put`` appends one line, ``{"v": CACHE_VERSION, "machine": ..., "key":
+    ..., "entry": {...}}``, in a single write to a file opened for appending, so
+    tuners in several processes never overwrite each other's answers and a crash
+    loses at most the line being written. ``get`` scans the log and returns the
+    newest entry for (machine, key). Lines of another version, torn lines and
+    anything that is not such an object are skipped, so a damaged or foreign
+    file reads as fewer answers, never as an error.
+    """
 
     def __init__(self, path: Path | str | None = None) -> None:
         if path is None:
             path = os.environ.get("NANOCOMPILE_AMD_TUNING") or (
-                Path.home() / ".cache" / "nanocompile_amd" / "tuning.json")
+                Path.home() / ".cache" / "nanocompile_amd" / "tuning.jsonl")
         self.path = Path(path)
 
-    def _load(self) -> dict:
+    def _answers(self):
         try:
-            data = json.loads(self.path.read_text(encoding="utf-8"))
-        except (FileNotFoundError, json.JSONDecodeError, UnicodeDecodeError):
-            return {"version": CACHE_VERSION, "machines": {}}
-        if (not isinstance(data, dict) or data.get("version") != CACHE_VERSION
-                or not isinstance(data.get("machines"), dict)
-                or not all(isinstance(v, dict) for v in data["machines"].values())):
-            return {"version": CACHE_VERSION, "machines": {}}       # another version, or not ours: start over
-        return data
+            raw = self.path.read_bytes()
+        except (FileNotFoundError, IsADirectoryError):
+            return
+        for line in raw.split(b"\n"):
+            try:
+                item = json.loads(line)
+            except (ValueError, RecursionError):
+                continue
+            if isinstance(item, dict) and item.get("v") == CACHE_VERSION and isinstance(item.get("entry"), dict):
+                yield item
 
     def get(self, machine: str, key: str) -> dict | None:
-        return self._load()["machines"].get(machine, {}).get(key)
+        newest = None
+        for item in self._answers():
+            if item.get("machine") == machine and item.get("key") == key:
+                newest = item["entry"]
+        return newest
 
     def put(self, machine: str, key: str, entry: dict) -> None:
-        data = self._load()
-        data["machines"].setdefault(machine, {})[key] = entry
+        line = json.dumps({"v": CACHE_VERSION, "machine": machine, "key": key, "entry": entry}, sort_keys=True)
         self.path.parent.mkdir(parents=True, exist_ok=True)
-        fd, scratch = tempfile.mkstemp(dir=self.path.parent, suffix=".tmp")
-        with os.fdopen(fd, "w", encoding="utf-8") as f:
-            json.dump(data, f, indent=1, sort_keys=True)
-        os.replace(scratch, self.path)        # whole file or nothing
+        fd = os.open(self.path, os.O_RDWR | os.O_CREAT | os.O_APPEND, 0o644)
+        try:
+            size = os.fstat(fd).st_size
+            # a torn last line (no newline) is closed first, so this answer starts a line of its own
+            torn = size > 0 and os.pread(fd, 1, size - 1) != b"\n"
+            os.write(fd, (b"\n" if torn else b"") + line.encode() + b"\n")
+        finally:
+            os.close(fd)
 
 
 # -- generated kernels: the code generator's schedule space ------------------------------------
@@ -756,104 +787,109 @@ class Autotuner:
         best beats it by more than ``margin``. A cached kernel is not measured.
         """
         library = CandidateLibrary(program)
-        n = len(library.candidates)
-        chosen = [0] * n
-        keys = [program_kernel_key(library, i, self.workloads) for i in range(n)]
+        chosen = [0] * len(library.candidates)
+        keys = [program_kernel_key(library, i, self.workloads) for i in range(len(chosen))]
         machine = machine_key()
         todo = []
-        for i in range(n):
-            cands = library.candidates[i]
+        for i, cands in enumerate(library.candidates):
             if len(cands) <= 1 or not library.calls_of.get(i):
+                continue                               # nothing to choose, or never called
+            answer = self._recall(machine, keys[i])
+            stored = answer.get("config") if answer is not None else None
+            match = next((c for c, cand in enumerate(cands) if isinstance(stored, dict)
+                          and sorted(cand.config.items()) == sorted(stored.items())), None)
+            if match is None:
+                todo.append(i)                         # never tuned here, or its point left the space
                 continue
-            entry = self.cache.get(machine, keys[i]) if self.cache is not None else None
-            if entry is not None and isinstance(entry.get("config"), dict):
-                hit = [c for c, cand in enumerate(cands)
-                       if sorted(cand.config.items()) == sorted(entry["config"].items())]
-                if hit:
-                    chosen[i] = hit[0]
-                    self.records.append(TuneRecord(keys[i], library.program.kernels[i].primitive, (i,), len(cands),
-                                                   hit[0], entry.get("default_cost"), entry.get("winner_cost"),
-                                                   cached=True, config=entry["config"]))
-                    continue
-            todo.append(i)
+            chosen[i] = match
+            self._log(TuneRecord(keys[i], library.program.kernels[i].primitive, (i,), len(cands), match,
+                                 (answer.get("default_cost"), answer.get("winner_cost")), cached=True,
+                                 config=stored))
         if not todo:
             return library, chosen
-        started = time.perf_counter()
+        clock = time.perf_counter()
         workloads = [(ProgramWorkload(library, bindings, self.seed + w), weight)
                      for w, (_, bindings, weight) in enumerate(self.workloads)]
         for workload, _ in workloads:
             workload.gate(todo)
         for i in todo:
-            t0 = time.perf_counter()
-            timers = [(workload.timer(i), weight) for workload, weight in workloads]
-
-            def cost(stage: str, candidates: list[int]) -> list[float]:
-                rounds = self.rounds * 2 if stage == "confirm" else self.rounds
-                total = np.zeros(len(candidates))
-                for timer, weight in timers:
-                    total += weight * np.asarray(measure(timer, candidates, rounds, self.reps))
-                return [float(x) for x in total]
-
+            began = time.perf_counter()
             cands = library.candidates[i]
-            winner, log, default_cost, winner_cost = choose(list(range(len(cands))), cost, self.margin)
+            cost = self._cost([(workload.timer(i), weight) for workload, weight in workloads])
+            winner, trail, before, after = choose(list(range(len(cands))), cost, self.margin)
             chosen[i] = winner
-            record = TuneRecord(keys[i], library.program.kernels[i].primitive, (i,), len(cands), winner,
-                                default_cost, winner_cost, log, time.perf_counter() - t0,
-                                config=cands[winner].config)
-            self.records.append(record)
-            if self.cache is not None:
-                self.cache.put(machine, keys[i], {"config": cands[winner].config, "default_cost": default_cost,
-                                                  "winner_cost": winner_cost, "op": record.op})
+            record = self._log(TuneRecord(keys[i], library.program.kernels[i].primitive, (i,), len(cands), winner,
+                                          (before, after), config=cands[winner].config, evaluations=tuple(trail),
+                                          seconds=time.perf_counter() - began))
+            self._remember(machine, keys[i], {"config": record.config, "default_cost": before,
+                                              "winner_cost": after, "op": record.op})
             if self.verbose:
                 print(f"tuned kernel {i} ({record.op}): {len(cands)} schedules, "
-                      f"{cands[winner].launch.describe()} at {winner_cost * 1e6:.2f} us per token "
+                      f"{cands[winner].launch.describe()} at {after * 1e6:.2f} us per token "
                       f"({record.speedup:.2f}x the default)", file=sys.stderr, flush=True)
         if self.verbose:
-            print(f"tuned {len(todo)} generated kernels in {time.perf_counter() - started:.1f} s", file=sys.stderr,
+            print(f"tuned {len(todo)} generated kernels in {time.perf_counter() - clock:.1f} s", file=sys.stderr,
                   flush=True)
         return library, chosen
 
-    def tune_problem(self, make, op: str, shape: tuple, space: list[dict] | None) -> TuneRecord:
-        """Measure the candidates of the problem ``make()`` builds (its ``space()`` unless given):
-        each checked bit for bit against schedule 0 inside guard regions, then timed."""
-        started = time.perf_counter()
-        problem = None
-        if space is None:
-            problem = make()
-            space = problem.space()
-        key = self.problem_key(op, *((list(shape) + [0, 0, 0])[:3]), space, extra=tuple(shape[3:]))
-        record = TuneRecord(key, op, tuple(shape), len(space))
-        machine = machine_key()
-        if self.cache is not None:
-            entry = self.cache.get(machine, key)
-            if entry is not None and isinstance(entry.get("winner"), int):
-                record.winner, record.cached = entry["winner"], True
-                record.default_cost, record.winner_cost = entry.get("default_cost"), entry.get("winner_cost")
-                record.seconds = time.perf_counter() - started
-                self.records.append(record)
-                return record
+    # -- shared steps ----------------------------------------------------------------------------
 
-        problem = problem or make()
-        schedules = [c["schedule"] for c in space]
-        reference = problem.output(0)
-        for s in schedules[1:]:
-            if not np.array_equal(problem.output(s), reference):
-                raise TuningError(f"{op} schedule {s} on {tuple(shape)} differs from the default's bits")
-
-        def cost(stage: str, candidates: list[int]) -> list[float]:
-            rounds = self.rounds * 2 if stage == "confirm" else self.rounds
-            return measure(problem, candidates, rounds, self.reps)
-
-        winner, log, default_cost, winner_cost = choose(schedules, cost, self.margin)
-        record.winner, record.evaluations = winner, log
-        record.default_cost, record.winner_cost = default_cost, winner_cost
-        record.seconds = time.perf_counter() - started
+    def _log(self, record: TuneRecord) -> TuneRecord:
         self.records.append(record)
+        return record
+
+    def _recall(self, machine: str, key: str) -> dict | None:
+        """This machine's stored answer for ``key``; None without a cache or an answer."""
+        return self.cache.get(machine, key) if self.cache is not None else None
+
+    def _remember(self, machine: str, key: str, entry: dict) -> None:
         if self.cache is not None:
-            self.cache.put(machine, key, {"winner": winner, "default_cost": default_cost,
-                                          "winner_cost": winner_cost, "op": op, "shape": list(shape)})
+            self.cache.put(machine, key, entry)
+
+    def _cost(self, timers):
+        """``choose``'s cost function over ``timers`` [(timer, weight)]: each candidate's
+        seconds per call under every timer, weighted and added (a generated kernel's decode
+        and prefill workloads), over the stage's share of the tuner's rounds."""
+        def cost(stage: str, candidates: list[int]) -> list[float]:
+            rounds = self.rounds * ROUNDS_FACTOR[stage]
+            total = np.zeros(len(candidates))
+            for timer, weight in timers:
+                total += weight * np.asarray(measure(timer, candidates, rounds, self.reps))
+            return [float(x) for x in total]
+        return cost
+
+    def tune_problem(self, make, op: str, shape: tuple, space: list[dict] | None) -> TuneRecord:
+        """Answer one library problem: the schedule ``make()``'s problem should launch with.
+
+        The candidates are ``space``, or the problem's own ``space()``. A stored
+        answer for this machine is used as it is; otherwise every candidate's
+        output is first compared bit for bit with schedule 0's inside guard
+        regions (``problem.output``), and only then are they timed and chosen
+        between (``choose``), the answer stored for next time.
+        """
+        began = time.perf_counter()
+        problem = make() if space is None else None
+        space = problem.space() if problem is not None else space
+        key = self.problem_key(op, *((list(shape) + [0, 0, 0])[:3]), space, extra=tuple(shape[3:]))
+        machine = machine_key()
+        answer = self._recall(machine, key)
+        if answer is not None and isinstance(answer.get("winner"), int):
+            return self._log(TuneRecord(key, op, tuple(shape), len(space), answer["winner"],
+                                        (answer.get("default_cost"), answer.get("winner_cost")), cached=True,
+                                        seconds=time.perf_counter() - began))
+        problem = problem if problem is not None else make()
+        numbers = [c["schedule"] for c in space]
+        incumbent = problem.output(numbers[0])
+        for number in numbers[1:]:
+            if not np.array_equal(problem.output(number), incumbent):
+                raise TuningError(f"{op} schedule {number} on {tuple(shape)} differs from the default's bits")
+        winner, trail, before, after = choose(numbers, self._cost([(problem, 1.0)]), self.margin)
+        record = self._log(TuneRecord(key, op, tuple(shape), len(space), winner, (before, after),
+                                      evaluations=tuple(trail), seconds=time.perf_counter() - began))
+        self._remember(machine, key, {"winner": winner, "default_cost": before, "winner_cost": after,
+                                      "op": op, "shape": list(shape)})
         if self.verbose:
             print(f"tuned {op} {tuple(shape)}: {len(space)} schedules in {record.seconds:.1f} s, "
-                  f"schedule {winner} at {winner_cost * 1e6:.2f} us ({record.speedup:.2f}x the default)",
+                  f"schedule {winner} at {after * 1e6:.2f} us ({record.speedup:.2f}x the default)",
                   file=sys.stderr, flush=True)
         return record

@@ -192,13 +192,16 @@ class CompiledProgram:
                         for c, call in enumerate(program.calls)
                         for i in range(len(call.operands))
                         if self.kernels[call.kernel].params[i + 1].packed is not None}
+        # a packed copy is made once, at upload, so it must cover a whole matrix that never changes
         for (c, i), block in self._packed.items():
-            view = program.calls[c].operands[i]
-            if view.buffer.kind != "weight" or len(view.buffer.shape) != 2 or view.offset != 0:
-                raise ValueError(f"call {c} reads {view.buffer!r} packed; only whole 2-D weights can be")
+            operand = program.calls[c].operands[i]
+            buf = operand.buffer
+            if not (buf.kind == "weight" and len(buf.shape) == 2 and operand.offset == 0):
+                raise ValueError(f"packed operand {i} of call {c} is {buf!r}: a packed layout is made "
+                                 f"for an unsliced two-dimensional weight and nothing else")
         self._arena: hip.DeviceArray | None = None
         self._resident: dict = {}          # (buffer name or id, packing) -> offset in the weight region
-        self._weights_of = None            # the weights mapping the region holds, and its arrays' ids
+        self._held: dict | None = None     # name -> the very array uploaded (kept alive, compared by identity)
         self._region = 0                   # bytes of the weight region
         self.last_plan: Plan | None = None
 
@@ -254,9 +257,18 @@ class CompiledProgram:
             items.append(((name, block), pack_rows(np.asarray(weights[name]), block)))
         return items
 
+    def _is_resident(self, weights: Mapping[str, np.ndarray]) -> bool:
+        """Whether the weight region already holds these arrays: the same objects, not equal ids.
+
+        The uploaded arrays are held (``self._held``), so none of them can be
+        freed and its id handed to a new array while it is resident. An array
+        changed in place after its upload is not noticed: weights are constants.
+        """
+        held = self._held
+        return held is not None and all(weights[name] is held[name] for name in self.program.weights)
+
     def _ensure(self, weights: Mapping[str, np.ndarray], call_bytes: int) -> None:
-        ids = {name: id(weights[name]) for name in self.program.weights}
-        fresh = self._weights_of != ids
+        fresh = not self._is_resident(weights)
         if fresh:
             items = self._constants(weights)
             region = sum(_align(a.nbytes) for _, a in items)
@@ -280,7 +292,7 @@ class CompiledProgram:
                 self._resident[key] = at
                 at += _align(array.nbytes)
             self._region = region
-            self._weights_of = ids
+            self._held = {name: weights[name] for name in self.program.weights}
 
     # -- a call -------------------------------------------------------------------------------
 
@@ -308,7 +320,13 @@ class CompiledProgram:
         in a graph, to time the kernels alone), ``bound`` the symbols' values, ``addresses`` each
         buffer's device address (the outputs are read from there). ``launch.calls`` holds each
         call with its launcher arguments and ``launch.symbols`` the symbol array, for a caller
-        that launches calls one at a time (the autotuner)."""
+        that launches calls one at a time (the autotuner).
+
+        Lifetime: the addresses point into the arena current at this call. A later call that
+        needs a larger arena, or gets new weights, moves to a new one; ``launch.arena`` keeps
+        the old one allocated for as long as the launch object lives, so replaying it (or a
+        graph captured from it) stays within memory it owns. Keep the launch object alive as
+        long as such a graph is replayed."""
         program = self.program
         bound = self.bind(inputs, weights, bindings)
         syms = (ctypes.c_int64 * max(1, len(self.symbols)))(*[bound[s] for s in self.symbols])
@@ -356,6 +374,7 @@ class CompiledProgram:
                     profile[call.primitive] = profile.get(call.primitive, 0.0) + time.perf_counter() - started
 
         launch.calls, launch.symbols = launches, syms
+        launch.arena = self._arena          # the memory its pointers address stays allocated with it
         return launch, bound, addresses
 
     def _wait(self, inputs, bound) -> None:

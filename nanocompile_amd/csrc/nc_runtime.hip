@@ -139,6 +139,22 @@ NC_EXPORT int32_t nc_memcpy_d2d(void *dst, const void *src, int64_t n) {
     return record(hipMemcpyAsync(dst, src, (size_t)n, hipMemcpyDeviceToDevice, g_stream), "hipMemcpyAsync(d2d)");
 }
 
+// height rows of width bytes, each with its own pitch on either side (the KV
+// cache's [layer, head] blocks): kind 1 host to device, 2 device to host.
+// Ordered on the library stream; waits.
+NC_EXPORT int32_t nc_memcpy_rows(void *dst, int64_t dst_pitch, const void *src, int64_t src_pitch, int64_t width,
+                                 int64_t height, int32_t kind) {
+    if (!dst || !src || width < 0 || height < 0 || width > dst_pitch || width > src_pitch || (kind != 1 && kind != 2)) {
+        nc::set_message("nc_memcpy_rows: bad arguments");
+        return NC_BAD_ARGS;
+    }
+    if (width == 0 || height == 0) return NC_OK;
+    const hipMemcpyKind direction = kind == 1 ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost;
+    int32_t rc = record(hipMemcpy2DAsync(dst, (size_t)dst_pitch, src, (size_t)src_pitch, (size_t)width,
+                                         (size_t)height, direction, g_stream), "hipMemcpy2DAsync");
+    return rc ? rc : record(hipStreamSynchronize(g_stream), "hipStreamSynchronize");
+}
+
 // Wait for the stream. Returns the first kernel failure code recorded since
 // the last call (and clears it), NC_LAUNCH_FAILED on a runtime error, or 0.
 NC_EXPORT int32_t nc_sync(void) {

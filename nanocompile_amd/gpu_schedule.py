@@ -724,6 +724,13 @@ def lane_chains(body, name: str) -> Lanes:
     for outer, inner in zip(chain, chain[1:]):
         if list(outer.body) != [inner]:
             raise ScheduleError(f"lanes({name}): the element loops are not perfectly nested")
+    # the renderer maps a lane to its digits starting at the outermost loop of the nest, which
+    # must therefore carry the largest coefficient, each inner loop a smaller one
+    coefficient = {var: coeff for var, _, coeff in digits}
+    nested = [coefficient[l.var] for l in chain]
+    if any(outer <= inner for outer, inner in zip(nested, nested[1:])):
+        raise ScheduleError(f"lanes({name}): the element loops are not nested from the largest "
+                            f"coefficient inwards ({[l.var for l in chain]} have {nested})")
     radix = 1
     for var, extent, coeff in sorted(digits, key=lambda d: d[2]):
         if coeff != radix:

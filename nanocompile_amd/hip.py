@@ -58,6 +58,8 @@ _RUNTIME = {
     "nc_memcpy_h2d_async": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]),
     "nc_memcpy_d2h_async": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]),
     "nc_memcpy_d2d": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]),
+    "nc_memcpy_rows": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
+                                        ctypes.c_int64, ctypes.c_int64, ctypes.c_int32]),
     "nc_sync": (ctypes.c_int32, []),
     "nc_stream_handle": (ctypes.c_void_p, []),
     "nc_error_word": (ctypes.c_void_p, []),
@@ -202,6 +204,26 @@ def _address(x) -> int | None:
     return x.ptr
 
 
+_ALLOCATIONS = 0
+
+
+def allocations() -> int:
+    """How many device allocations this process's DeviceArrays have made (each one ``hipMalloc``)."""
+    return _ALLOCATIONS
+
+
+def copy_rows(dst: int, dst_pitch: int, src: int, src_pitch: int, width: int, height: int,
+              to_device: bool) -> None:
+    """``height`` rows of ``width`` bytes between host and device memory, each side with its own
+    pitch (bytes from one row's start to the next's); waits for the copy."""
+    if width <= 0 or height <= 0:
+        return
+    if width > dst_pitch or width > src_pitch:
+        raise ValueError(f"rows of {width} bytes do not fit pitches {dst_pitch} / {src_pitch}")
+    _check(load().nc_memcpy_rows(dst, dst_pitch, src, src_pitch, width, height, 1 if to_device else 2),
+           "nc_memcpy_rows")
+
+
 class DeviceArray:
     """A device allocation with a dtype and shape. Freed when dropped, unless it is a view."""
 
@@ -213,9 +235,11 @@ class DeviceArray:
         self.dtype = np.dtype(dtype)
         self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
         if ptr is None:
+            global _ALLOCATIONS
             ptr = load().nc_malloc(max(self.nbytes, 1))
             if not ptr:
                 raise MemoryError(f"nc_malloc({self.nbytes}) failed: {last_error()}")
+            _ALLOCATIONS += 1
             owner = True
         self.ptr = int(ptr)
         self._owner = owner

@@ -25,10 +25,30 @@ reference's compiled program for it, lowered by codegen_hip with GPU
 schedules and run from one device arena (compiled.py), the reference's own
 kernels' arithmetic in the reference's order.
 
-On the model path each call uploads the past keys and values it is given
-(the reference keeps its cache on the host and hands it over every step);
-the model, with its weights uploaded and packed, is made once per mode and
-kept for the weights mapping it was last called with.
+On the model path the model, with its weights uploaded and packed, is made
+once per mode and kept for the weights mapping it was last called with. The
+reference keeps its cache on the host and hands the filled part over every
+call, a view of one buffer that its KVCache grows by doubling
+(models/qwen2.py:232-271); the backend keeps one device cache per mode for
+the sequence it was last called with, identified by the host buffer those
+views come from. The rows the device produced itself (the keys and values it
+returned, which the caller appends at the rows after ``past``) are not
+uploaded again: a call uploads only the rows the device does not hold, and
+downloads only the new rows. A new buffer (another sequence, or the host
+cache grown into a fresh buffer) uploads its filled part once. The device
+cache is allocated when a sequence needs more rows than it has, sized to the
+host buffer's capacity, so a sequence whose host cache is made for its whole
+length (as the reference's ``greedy`` makes it) allocates nothing after its
+first call. Rows are trusted by position, as weights are by identity: a
+caller that rewrites rows of its cache in place, rather than appending, must
+hand over a fresh buffer (or call ``forget``).
+
+``activations="token"`` is an opt-in numeric deviation: graphs the reference
+built in its ``int8`` or ``int8-vnni`` mode run on the per-token model
+(``quantization="int8-token"``: the same per-row int8 weights, each token's
+activations quantized with one scale, exact int32 accumulation), which is
+this package's fast decode path. Its logits differ from the reference mode's
+by the activations' quantization error; its tokens are the per-token model's.
 ``HIPCompiledGraph`` is the per-graph form, the reference's
 ``CompiledGraph(graph, ...)(inputs, weights, bindings, profile)``
 (runtime.py:167-301), which ``HIPBackend.compiled`` makes once per graph as
@@ -63,13 +83,18 @@ class HIPBackend:
     """
 
     def __init__(self, config=None, max_tokens: int = 512, device: int = 0, schedule="default",
-                 fuse: bool = True, lower=None) -> None:
+                 fuse: bool = True, lower=None, activations: str = "reference") -> None:
+        if activations not in ("reference", "token"):
+            raise ValueError("activations must be 'reference' (the graph's own int8 mode) or 'token' "
+                             "(per-token int8 activations, a numeric deviation)")
         self.config = None if config is None else Qwen2Config.coerce(config)
         self.max_tokens, self.device, self.schedule = max_tokens, device, schedule
-        self.fuse, self.lower = fuse, lower
+        self.fuse, self.lower, self.activations = fuse, lower, activations
         # one model per mode, for the weights mapping it was last called with: a new
         # mapping replaces (and frees) the model made for the old one
         self._models: dict[str, tuple[Mapping, object]] = {}
+        # one device cache per mode, for the sequence last run in it
+        self._sequences: dict[str, _Sequence] = {}
         self._compiled: list[tuple[object, "HIPCompiledGraph"]] = []
 
     # -- recognising a graph ----------------------------------------------------------------
@@ -138,16 +163,54 @@ class HIPBackend:
 
     # -- running it -----------------------------------------------------------------------------
 
+    def model_quantization(self, mode: str) -> str:
+        """The GPU model's quantization for a graph of ``mode``: the mode itself, or with
+        ``activations="token"`` the per-token model for either int8 mode."""
+        if self.activations == "token" and mode in ("int8", "int8-vnni"):
+            return "int8-token"
+        return mode
+
     def _model(self, mode: str, weights: Mapping):
         held = self._models.get(mode)
         if held is not None and held[0] is weights:
             return held[1]
         self._models.pop(mode, None)          # drop the old weights' device arena before uploading new ones
+        self._sequences.pop(mode, None)
         from nanocompile_amd.models.qwen2 import Qwen2
-        model = Qwen2(self.config, weights, quantization=mode, max_tokens=self.max_tokens, device=self.device,
-                      schedule=self.schedule)
+        model = Qwen2(self.config, weights, quantization=self.model_quantization(mode), max_tokens=self.max_tokens,
+                      device=self.device, schedule=self.schedule)
         self._models[mode] = (weights, model)
         return model
+
+    def forget(self) -> None:
+        """Drop the device caches, so the next call of every mode uploads its past rows afresh."""
+        self._sequences.clear()
+
+    def _cache_for(self, mode: str, model, past_keys: np.ndarray, past_values: np.ndarray, need: int):
+        """The device cache for this call's sequence, holding the rows [0, past) of the host's;
+        only rows it did not already hold are uploaded."""
+        from nanocompile_amd.models.qwen2 import KVCache
+        past = int(past_keys.shape[2])
+        kbuf, vbuf = _owner(past_keys), _owner(past_values)
+        seq = self._sequences.get(mode)
+        if seq is None or seq.cache.capacity < need:
+            # sized for the whole host buffer when it is the reference's preallocated one, and at
+            # least doubling, so a growing sequence allocates O(log length) times
+            old = seq.cache.capacity if seq is not None else 0
+            capacity = min(max(need, _rows_of(kbuf, past_keys), 2 * old), MAX_CACHE_ROWS)
+            if capacity < need:
+                raise ValueError(f"{need} tokens exceed the device cache's limit of {MAX_CACHE_ROWS}")
+            seq = _Sequence(KVCache(self.config, capacity))
+            self._sequences[mode] = seq
+        if seq.keys_buffer is not kbuf or seq.values_buffer is not vbuf:
+            seq.keys_buffer, seq.values_buffer, seq.held = kbuf, vbuf, 0     # another sequence: nothing held
+        seq.held = min(seq.held, past)         # a shorter view: the rows past it are not the caller's now
+        if seq.held < past:
+            _upload_rows(seq.cache.keys, past_keys, seq.held, past)
+            _upload_rows(seq.cache.values, past_values, seq.held, past)
+        seq.held = past
+        seq.cache.length = past
+        return seq
 
     def compiled(self, graph) -> "HIPCompiledGraph":
         """The graph bound once, on first use (the reference's CBackend.compiled, runtime.py:321-333)."""
@@ -179,17 +242,73 @@ class HIPBackend:
         if m > self.max_tokens:
             raise ValueError(f"{m} tokens in one call; this backend was made with max_tokens={self.max_tokens}")
         model = self._model(mode, weights)
-        cache = model.new_cache(past + m)
-        if past:
-            for host, device in ((past_keys, cache.keys), (past_values, cache.values)):
-                full = np.zeros(device.shape, np.float32)
-                full[:, :, :past] = host
-                device.upload(full)
-        cache.length = past
-        logits = model.forward(ids, cache, last_only=last_only)
-        keys = np.ascontiguousarray(cache.keys.numpy()[:, :, past:past + m])
-        values = np.ascontiguousarray(cache.values.numpy()[:, :, past:past + m])
+        seq = self._cache_for(mode, model, past_keys, past_values, past + m)
+        logits = model.forward(ids, seq.cache, last_only=last_only)
+        keys = _download_rows(seq.cache.keys, past, past + m)
+        values = _download_rows(seq.cache.values, past, past + m)
+        # the caller appends these at rows past .. past + m of the same buffer (models/qwen2.py:263-271)
+        seq.held = past + m
         return {"logits": logits, "keys": keys, "values": values}
+
+
+MAX_CACHE_ROWS = 16384          # the attention kernels' limit on keys (kernels.MAX_KEYS)
+
+
+class _Sequence:
+    """A device cache and which host buffers its rows [0, held) mirror."""
+
+    def __init__(self, cache) -> None:
+        self.cache = cache
+        self.keys_buffer = self.values_buffer = None
+        self.held = 0
+
+
+def _owner(view: np.ndarray) -> np.ndarray:
+    """The array whose memory ``view`` starts, when it is a leading slice of it along the rows
+    (the reference's ``_keys[:, :, :length]``); else the view itself. Identity of this array
+    names the sequence."""
+    root = view
+    while isinstance(root.base, np.ndarray):
+        root = root.base
+    if (root is not view and root.ndim == 4 and root.shape[:2] == view.shape[:2] and root.shape[3] == view.shape[3]
+            and root.strides == view.strides and root.ctypes.data == view.ctypes.data):
+        return root
+    return view
+
+
+def _rows_of(buffer: np.ndarray, view: np.ndarray) -> int:
+    """The host buffer's capacity in rows when ``view`` is its leading slice, else the view's rows."""
+    return int(buffer.shape[2]) if buffer is not view else int(view.shape[2])
+
+
+def _upload_rows(device, host: np.ndarray, start: int, stop: int) -> None:
+    """Rows [start, stop) of every (layer, head) of ``host`` [L, kv, past, D] into the device cache
+    [L, kv, capacity, D]: one strided copy when the host rows have a uniform pitch."""
+    from nanocompile_amd import hip
+    layers, heads, _, width = host.shape
+    capacity = device.shape[2]
+    row = width * 4
+    if not (host.strides[3] == 4 and host.strides[2] == row and host.strides[0] == heads * host.strides[1]):
+        host = np.ascontiguousarray(host[:, :, start:stop])
+        start, stop = 0, host.shape[2]
+        src = host.ctypes.data
+    else:
+        src = host.ctypes.data + start * row
+    pitch = host.strides[1]
+    hip.copy_rows(device.ptr + start * row, capacity * row, src, pitch, (stop - start) * row, layers * heads,
+                  to_device=True)
+
+
+def _download_rows(device, start: int, stop: int) -> np.ndarray:
+    """Rows [start, stop) of every (layer, head) of the device cache, as a host [L, kv, n, D] array."""
+    from nanocompile_amd import hip
+    layers, heads, capacity, width = device.shape
+    row = width * 4
+    out = np.empty((layers, heads, stop - start, width), np.float32)
+    if out.size:
+        hip.copy_rows(out.ctypes.data, (stop - start) * row, device.ptr + start * row, capacity * row,
+                      (stop - start) * row, layers * heads, to_device=False)
+    return out
 
 
 class HIPCompiledGraph:

@@ -136,6 +136,16 @@ def rms_norm_quant(x, gamma, eps: float):
     return normed, xq, xs
 
 
+def rms_norm_quant_pool(x, gamma, eps: float):
+    """``rms_norm_quant`` with the rows spread over the host pool (the same bits)."""
+    x = np.ascontiguousarray(x, np.float32)
+    m, k = x.shape
+    normed, xq, xs = np.empty_like(x), np.empty((m, k), np.int8), np.empty(m, np.float32)
+    _sig("nc_host_rms_norm_quant_pool", 5, 2, [ctypes.c_float])(
+        _ptr(normed), _ptr(xq), _ptr(xs), _ptr(x), _ptr(np.ascontiguousarray(gamma, np.float32)), m, k, eps)
+    return normed, xq, xs
+
+
 def rope_append_attention(qkv, kcache, vcache, inv_freq, heads: int, kv: int, d: int, past: int, scale: float):
     """RoPE + cache append (in place on qkv and the caches), then attention; returns the context."""
     m = qkv.shape[0]

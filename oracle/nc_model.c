@@ -97,6 +97,24 @@ EXPORT void nc_host_rms_norm_quant(float *normed, int8_t *xq, float *xs, const f
     free(tmp);
 }
 
+/* The same rows spread over the host pool, ROWS_A_TASK rows a task (each row is independent, so
+ * the bits are the serial function's): the CPU baseline's config 2 with its threads swept. */
+#define ROWS_A_TASK 8
+typedef struct { float *normed; int8_t *xq; float *xs; const float *x; const float *gamma; int64_t m, k; float eps; } rnq_ctx;
+
+static void rnq_task(void *arg, int64_t t) {
+    const rnq_ctx *c = (const rnq_ctx *)arg;
+    const int64_t r0 = t * ROWS_A_TASK, n = c->m - r0 < ROWS_A_TASK ? c->m - r0 : ROWS_A_TASK;
+    nc_host_rms_norm_quant(c->normed ? c->normed + r0 * c->k : NULL, c->xq + r0 * c->k, c->xs + r0, c->x + r0 * c->k,
+                           c->gamma, n, c->k, c->eps);
+}
+
+EXPORT void nc_host_rms_norm_quant_pool(float *normed, int8_t *xq, float *xs, const float *x, const float *gamma,
+                                        int64_t m, int64_t k, float eps) {
+    rnq_ctx c = {normed, xq, xs, x, gamma, m, k, eps};
+    nc_pool_run(rnq_task, &c, (m + ROWS_A_TASK - 1) / ROWS_A_TASK);
+}
+
 EXPORT void nc_host_quantize_token(int8_t *xq, float *xs, const float *x, int64_t m, int64_t k) {
     for (int64_t r = 0; r < m; ++r) xs[r] = quantize_row(xq + r * k, x + r * k, k);
 }

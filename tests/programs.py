@@ -177,6 +177,8 @@ def prebuild(jobs: int = 8) -> int:
     libraries.append(autotune.CandidateLibrary(config5()[0]))
     with ThreadPoolExecutor(max_workers=jobs) as pool:
         results = list(pool.map(compiled.prebuild, progs))
+        results.append(compiled.prebuild(lane_store_program(), lane_store_lanes))
+        results.append(compiled.prebuild(lane_store_program()))
         results += list(pool.map(lambda library: library.build(), libraries))
     # libraries of sources no longer generated would only travel to the GPU with the tree
     keep = {path.name for path, _ in results}
@@ -184,3 +186,52 @@ def prebuild(jobs: int = 8) -> int:
         if stale.name not in keep:
             stale.unlink()
     return sum(1 for _, cached in results if not cached)
+
+
+def lane_store_program(rows: int = 3, width: int = 8, steps: int = 4) -> lir.Program:
+    """A hand-built program whose item stores its accumulators directly, ``y[i, e] = acc[e]``:
+    ``acc[e] = fma(x[i, s * width + e], 2, acc[e])`` over ``steps``, then one store per element.
+    Held across lanes, element e lives in lane e, so the store's value is a shuffle that every
+    lane must take part in while only lane 0 stores. Returns the program; its input is ``x``
+    [rows, steps * width] float32 and its output ``y`` [rows, width]."""
+    f32, i64 = lir.DType("f32"), lir.DType("i64")
+
+    def c(x):
+        return lir.Const(x, i64)
+
+    def add(a, b):
+        return lir.Binary("add", a, b, i64)
+
+    def mul(a, b):
+        return lir.Binary("mul", a, b, i64)
+
+    k = steps * width
+    i, s, e = lir.Var("i0"), lir.Var("k0"), lir.Var("e0")
+    chain = lir.Loop("k0", c(steps), (lir.Loop("kl", c(width), (lir.ArrayStore("acc", lir.Var("kl"), lir.Fma(
+        lir.Load(1, add(add(mul(i, c(k)), mul(s, c(width))), lir.Var("kl")), f32), lir.Const(2.0, f32),
+        lir.Local("acc", lir.Var("kl"), f32), f32)),), "serial"),), "serial")
+    store = lir.Loop("e0", c(width), (lir.Store(0, add(mul(i, c(width)), e), lir.Local("acc", e, f32)),), "serial")
+    kernel = lir.Kernel("lane_store", (lir.Param(f32, True), lir.Param(f32, False)), (lir.Loop("i0", c(rows), (
+        lir.Array("acc", width, lir.Const(0.0, f32)), chain, store), "parallel"),))
+    x = lir.Buffer("input", f32, (rows, k), "x")
+    y = lir.Buffer("output", f32, (rows, width), "y")
+    call = lir.Call(0, y, (lir.View(x, (rows, k), (k, 1), 0),), "lane_store", 0)
+    return lir.Program("lane_store", (), [("x", f32, (rows, k))], {}, [kernel], [call], [x, y], {"y": y})
+
+
+def lane_store_lanes(kernel, calls):
+    """``lane_store_program``'s kernel with its accumulators one element a lane."""
+    from nanocompile_amd import gpu_schedule
+    s = gpu_schedule.GpuSchedule(kernel).grid("i0").lanes("acc")
+    return s.kernel, s.launch
+
+
+def lane_store_expected(x: np.ndarray, width: int = 8) -> np.ndarray:
+    """``lane_store_program``'s output computed directly: each element's chain of fused
+    multiply-adds in order. For float32 x and acc of normal magnitudes, 2 x + acc is exact in
+    float64, so rounding it to float32 once is what the fused multiply-add gives."""
+    rows, k = x.shape
+    acc = np.zeros((rows, width), np.float32)
+    for s in range(k // width):
+        acc = (x[:, s * width:(s + 1) * width].astype(np.float64) * 2.0 + acc.astype(np.float64)).astype(np.float32)
+    return acc

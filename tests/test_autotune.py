@@ -85,28 +85,40 @@ def test_choose_stops_when_the_incumbent_is_best():
     assert winner == 0 and len(log) == 1 and d == w == 1.0
 
 
-def test_cache_roundtrip_and_version(tmp_path):
-    path = tmp_path / "sub" / "tuning.json"
+def test_cache_log_roundtrip_versions_and_damage(tmp_path):
+    """The cache is a log of JSON lines: the newest answer for (machine, key) wins, lines of
+    another version and damaged lines are skipped, and an answer appended after a torn line
+    still reads back."""
+    path = tmp_path / "sub" / "tuning.jsonl"
     cache = autotune.TuningCache(path)
     assert cache.get("m", "k") is None
     cache.put("m", "k", {"winner": 17})
     cache.put("m", "k2", {"winner": 0})
     cache.put("other", "k", {"winner": 5})
     assert cache.get("m", "k") == {"winner": 17} and cache.get("other", "k") == {"winner": 5}
-    assert list(path.parent.glob("*.tmp")) == []
-    data = json.loads(path.read_text())
-    data["version"] = autotune.CACHE_VERSION + 1
-    path.write_text(json.dumps(data))
-    assert cache.get("m", "k") is None                          # another version: ignored
-    path.write_text("{not json")
-    assert cache.get("m", "k") is None
-    for junk in ("[1, 2]", '{"version": 1, "machines": [3]}', '{"version": 1, "machines": {"m": 4}}'):
-        path.write_text(junk)                                   # valid JSON, not a cache: ignored
-        assert cache.get("m", "k") is None
-    path.write_bytes(b"\xff\xfe\x00")
-    assert cache.get("m", "k") is None
-    cache.put("m", "k", {"winner": 3})                          # and a put starts it over
+    cache.put("m", "k", {"winner": 16})                         # a newer answer replaces it
+    assert cache.get("m", "k") == {"winner": 16} and cache.get("m", "k2") == {"winner": 0}
+    assert len(path.read_text().splitlines()) == 4 and list(path.parent.iterdir()) == [path]
+    with open(path, "a") as f:
+        f.write(json.dumps({"v": autotune.CACHE_VERSION + 1, "machine": "m", "key": "k",
+                            "entry": {"winner": 9}}) + "\n")   # another version: ignored
+        f.write("[1, 2]\n{not json\n" + '{"v": 1, "machine": "m", "key": "k", "entry": 4}\n')
+    assert cache.get("m", "k") == {"winner": 16}
+    with open(path, "ab") as f:
+        f.write(b'{"v": 1, "machine": "m", "key": "k", "ent')      # a write cut short
+    assert cache.get("m", "k") == {"winner": 16}
+    cache.put("m", "k", {"winner": 3})
     assert cache.get("m", "k") == {"winner": 3}
+    path.write_bytes(b"\xff\xfe\x00")                          # not text at all
+    assert cache.get("m", "k") is None
+    cache.put("m", "k", {"winner": 2})
+    assert cache.get("m", "k") == {"winner": 2}
+
+
+def test_records_report_costs_and_speedup():
+    r = autotune.TuneRecord("key", "op", (1, 2, 3), 5, 3, (2.0, 1.0))
+    assert (r.default_cost, r.winner_cost, r.speedup) == (2.0, 1.0, 2.0)
+    assert autotune.TuneRecord("key", "op", (), 1).speedup is None
 
 
 def test_guard_regions_catch_writes_outside_the_output():

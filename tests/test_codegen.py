@@ -615,3 +615,65 @@ def test_unroll_reaches_the_loop_around_lane_held_chains_but_not_register_array_
     # without lanes the same loop indexes the accumulator array: nothing to unroll
     with pytest.raises(gpu_schedule.ScheduleError):
         gpu_schedule.apply(kernel, (), dict(gpu_schedule.DEFAULTS["item"], threads=128, unroll=16, pack=False))
+
+
+def test_lane_held_values_are_read_by_every_lane_and_only_the_store_is_guarded():
+    """An item that stores its lane-held accumulators directly: the shuffle that fetches element
+    e from lane e is evaluated by all of the item's lanes (outside ``if (nc_l == 0)``), and the
+    scheduled program computes the unscheduled one's bits."""
+    import re
+    program = P.lane_store_program()
+    kernel = program.kernels[0]
+    s = gpu_schedule.GpuSchedule(kernel).grid("i0").lanes("acc")
+    text = codegen_hip.render_kernel(s.kernel, s.launch, 0)
+    assert "__shfl(" in text
+    for line in text.splitlines():
+        if "nc_l == 0" in line:
+            assert "__shfl" not in line, line
+    guarded = [m.group(0) for m in re.finditer(r"if \(nc_l == 0\)[^;]*;", text)]
+    assert guarded and all("__shfl" not in g for g in guarded)
+    x = np.random.default_rng(3).standard_normal((3, 32)).astype(np.float32)
+    got = I.run(program, [(s.kernel, s.launch)], {"x": x}, {}, {})["y"]
+    assert np.array_equal(got.view(np.uint32), P.lane_store_expected(x).view(np.uint32))
+
+
+def test_lanes_refuses_element_loops_nested_from_the_smallest_coefficient():
+    """acc[i + 2 j] with i outer: the lane's digits start at the outermost loop, which must carry
+    the largest coefficient; the reversed nest is refused, not rendered wrongly."""
+    f32 = lir.DType("f32")
+    params = (lir.Param(f32, True), lir.Param(f32, False))
+
+    def kernel(outer, inner, index):
+        chain = lir.Loop(outer, c(2), (lir.Loop(inner, c(2), (lir.ArrayStore("acc", index, lir.Fma(
+            lir.Load(1, index, f32), lir.Const(2.0, f32), lir.Local("acc", index, f32), f32)),)),))
+        tail = lir.Store(0, v("i0"), lir.Local("acc", c(0), f32))
+        return lir.Kernel("matmul", params, (lir.Loop("i0", c(3), (
+            lir.Array("acc", 4, lir.Const(0.0, f32)), chain, tail)),))
+
+    index = b("add", v("i"), b("mul", v("j"), c(2)))
+    assert gpu_schedule.GpuSchedule(kernel("j", "i", index)).grid("i0").lanes("acc").launch.lanes.width == 4
+    with pytest.raises(gpu_schedule.ScheduleError, match="largest coefficient"):
+        gpu_schedule.GpuSchedule(kernel("i", "j", index)).grid("i0").lanes("acc")
+
+
+def test_weights_are_resident_by_identity_not_by_id():
+    """A compiled program keeps the arrays it uploaded and compares the next call's with ``is``:
+    a fresh array that happens to get a freed array's id is not taken for the resident one."""
+    prog = compiled.CompiledProgram.__new__(compiled.CompiledProgram)
+    f32 = lir.DType("f32")
+    prog.program = lir.Program("w", (), [], {"w": (f32, (4,))}, [], [], [], {})
+    prog._held = None
+    first = {"w": np.zeros(4, np.float32)}
+    assert not prog._is_resident(first)
+    prog._held = dict(first)
+    assert prog._is_resident(first) and prog._is_resident({"w": first["w"]})
+    assert not prog._is_resident({"w": first["w"].copy()})
+    # the reused-id case: while held, the first array cannot be freed, so no new array shares
+    # its id; an equal-valued new array is still a different object and is uploaded afresh
+    ids = set()
+    for _ in range(5):
+        fresh = {"w": np.ones(4, np.float32)}
+        ids.add(id(fresh["w"]))
+        assert not prog._is_resident(fresh)
+        del fresh
+    assert id(first["w"]) not in ids

@@ -115,3 +115,17 @@ def test_tuned_tiny_qwen2_greedy_tokens_and_logits_are_golden(gpu, tmp_path):
     ids = P.PROMPTS[3]
     want = golden["g5_int8_logits"]
     np.testing.assert_allclose(driver.forward(ids), want, rtol=0, atol=1e-5 * np.abs(want).max())
+
+
+def test_an_item_storing_its_lane_held_accumulators_directly(gpu):
+    """``y[i, e] = acc[e]`` with acc held one element a lane: each stored value is a shuffle from
+    lane e that every lane of the item evaluates, lane 0 alone storing. Bitwise the direct
+    chain of fused multiply-adds, and the unscheduled (default) kernel's output."""
+    from nanocompile_amd.compiled import CompiledProgram
+    program = P.lane_store_program()
+    x = np.random.default_rng(3).standard_normal((3, 32)).astype(np.float32)
+    want = P.lane_store_expected(x)
+    print("lane_store: lanes and default schedules", flush=True)
+    for schedule in (P.lane_store_lanes, "default"):
+        got = CompiledProgram(program, schedule)({"x": x}, {})["y"]
+        assert np.array_equal(bits(got), bits(want)), schedule

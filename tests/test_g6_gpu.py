@@ -1,0 +1,144 @@
+"""Config 5's workload in the reference's own int8 modes, against the reference's own run (golden G6).
+
+tests/golden/make_g6.py ran the reference's Qwen2 through its compiled C
+(models/qwen2.py with CBackend) on exactly config 5's workload: the 24-layer
+Qwen2.5-0.5B-shaped model with ``random_weights(QWEN25_05B, seed=0)``, the
+128-token prompt drawn from ``default_rng(1)``, greedy decoding for 257 new
+tokens, in ``int8`` (float32 activations into matmul_i8's 32-chain order) and
+``int8-vnni`` (32-wide int8 activation blocks into matmul_i8_vnni's order).
+It recorded the tokens, and at cache lengths 0 (the prompt), 255 and 383 the
+argmax, the largest logit and the logits at every 97th vocabulary entry.
+
+Held to it here, on the GPU:
+* the hand-written model in each mode (``Qwen2(..., quantization=mode)``):
+  its device loop's 256 greedy tokens are the reference's, and its logits at
+  the three positions are within 1e-4 of the largest (the bar the north star
+  states for logits; its projections are the reference's kernels bit for bit,
+  only the float reductions around them are summed in a tree);
+* the reference's own compiled program for this model in int8, generated as
+  HIP by codegen_hip (the drop-in path): the same tokens and logits.
+"""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from tests import programs as P
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+TOLERANCE = 1e-4          # max |ours - reference| over max |reference|, per sampled logits row
+NEW_TOKENS = 256
+MODES = [("int8", "int8"), ("int8-vnni", "vnni")]
+
+
+@pytest.fixture(scope="module")
+def g6():
+    meta = json.loads((GOLDEN / "g6.json").read_text())
+    with np.load(GOLDEN / "g6.npz", allow_pickle=False) as z:
+        arrays = {k: z[k] for k in z.files}
+    return meta, arrays
+
+
+@pytest.fixture(scope="module")
+def weights(g6):
+    from nanocompile_amd.models.config import QWEN25_05B, random_weights
+    meta, _ = g6
+    print("G6: drawing the 24-layer model's weights", flush=True)
+    w = random_weights(QWEN25_05B, seed=meta["seed"])
+    prompt = [int(t) for t in np.random.default_rng(meta["prompt_seed"]).integers(0, QWEN25_05B.vocab_size, 128)]
+    assert prompt == meta["prompt"]
+    return w
+
+
+def chunks(meta, tag):
+    """The prompt, then the reference's greedy tokens fed back so that single-token calls land
+    at cache lengths 255 and 383: [(cache length before, ids)]."""
+    fed = meta[tag]["tokens"][:NEW_TOKENS]
+    parts = [meta["prompt"], fed[:127], fed[127:128], fed[128:255], fed[255:256]]
+    out, past = [], 0
+    for ids in parts:
+        out.append((past, ids))
+        past += len(ids)
+    assert [p for p, ids in out if p in (0, 255, 383)] == [0, 255, 383]
+    return out
+
+
+def check_logits(got: np.ndarray, meta, arrays, tag: str, past: int) -> float:
+    want = arrays[f"{tag}_logits_{past}"]
+    sampled = np.asarray(got, np.float32)[::meta["stride"]]
+    assert sampled.shape == want.shape
+    rel = float(np.max(np.abs(sampled.astype(np.float64) - want)) / np.max(np.abs(want)))
+    assert rel <= TOLERANCE, (tag, past, rel)
+    assert int(np.argmax(got)) == meta[tag][f"argmax_{past}"], (tag, past)
+    top = float.fromhex(meta[tag][f"max_{past}"])
+    assert abs(float(np.max(got)) - top) <= TOLERANCE * abs(top), (tag, past)
+    return rel
+
+
+@pytest.fixture(scope="module", params=MODES, ids=[m for m, _ in MODES])
+def model(gpu, weights, request):
+    from nanocompile_amd.models.config import QWEN25_05B
+    from nanocompile_amd.models.qwen2 import Qwen2
+    mode, tag = request.param
+    print(f"G6 {mode}: building the hand-written model", flush=True)
+    return Qwen2(QWEN25_05B, weights, quantization=mode, max_tokens=128), tag
+
+
+def test_hand_written_reference_modes_decode_the_references_tokens(model, g6):
+    m, tag = model
+    meta, _ = g6
+    print(f"G6 {tag}: device loop, {NEW_TOKENS} tokens", flush=True)
+    assert m.generate(meta["prompt"], NEW_TOKENS) == meta[tag]["tokens"][:NEW_TOKENS]
+
+
+def test_hand_written_reference_modes_logits_at_past_0_255_383(model, g6):
+    m, tag = model
+    meta, arrays = g6
+    cache = m.new_cache(128 + NEW_TOKENS + 1)
+    for past, ids in chunks(meta, tag):
+        assert cache.length == past
+        got = m.forward(ids, cache=cache, last_only=True)[0]
+        if past in (0, 255, 383):
+            rel = check_logits(got, meta, arrays, tag, past)
+            print(f"G6 {tag} logits at past {past}: {rel:.2e} of the largest", flush=True)
+
+
+def test_the_two_modes_are_told_apart(g6):
+    """The fixture's modes disagree well beyond the tolerance, so passing is not a coincidence."""
+    meta, arrays = g6
+    a, b = arrays["int8_logits_0"], arrays["vnni_logits_0"]
+    assert np.max(np.abs(a - b)) / np.max(np.abs(a)) > 10 * TOLERANCE
+    assert meta["int8"]["tokens"] != meta["vnni"]["tokens"]
+
+
+def test_generated_program_in_int8_gives_the_references_tokens_and_logits(gpu, weights, g6):
+    """The reference's compiled last-position program for this model (the fixture's config 5
+    program, which does not depend on the weights' values), generated as HIP, on the seed-0
+    weights: G6's int8 logits at the three positions and its 256 greedy tokens."""
+    from nanocompile_amd.compiled import CompiledProgram
+    from nanocompile_amd.models.config import QWEN25_05B
+    from oracle import reference as R
+    meta, arrays = g6
+    program, record = P.config5()
+    named = {}
+    for name in record["weight_names"]:
+        if name.endswith("@int8"):
+            base = name.rsplit("@", 1)[0]
+            named[name], named[base + "@scales"] = R.quantize_int8(weights[base])
+        elif not name.endswith("@scales"):
+            named[name] = weights[name]
+    compiled = CompiledProgram(program)
+    driver = P.Driver(lambda which, inputs: compiled(inputs, named), config=QWEN25_05B)
+    cache = list(driver.empty())
+    for past, ids in chunks(meta, "int8"):
+        print(f"G6 generated int8: {len(ids)} tokens at past {past}", flush=True)
+        got = driver.forward(ids, cache, last_only=True)[0]
+        if past in (0, 255, 383):
+            check_logits(got, meta, arrays, "int8", past)
+    print("G6 generated int8: greedy", flush=True)
+    assert driver.greedy(meta["prompt"], NEW_TOKENS) == meta["int8"]["tokens"][:NEW_TOKENS]

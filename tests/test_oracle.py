@@ -243,3 +243,23 @@ def test_host_c_is_bitwise_the_numpy_oracle_on_every_isa(host, isa):
                                   bits(R.matmul_i8_token(xq, xs, q, ws, b, r)))
     finally:
         host.limit_isa(3)
+
+
+def test_host_rows_on_the_pool_are_the_serial_rows(host):
+    """Config 2's host baseline with its rows spread over threads computes the serial bits, and
+    the GPU-order oracle's (rows independent; 1, 8 and 13 rows cover partial and whole tasks)."""
+    rng = np.random.default_rng(12)
+    g = (1 + 0.1 * rng.standard_normal(896)).astype(np.float32)
+    before = host.load().nc_host_threads()
+    host.set_threads(4)
+    try:
+        for m in (1, 8, 13, 512):
+            x = rng.standard_normal((m, 896)).astype(np.float32)
+            x[rng.random(x.shape) < 0.01] *= 20
+            serial, pooled = host.rms_norm_quant(x, g, 1e-6), host.rms_norm_quant_pool(x, g, 1e-6)
+            for a, b in zip(serial, pooled):
+                assert np.array_equal(np.asarray(a).view(np.uint8), np.asarray(b).view(np.uint8)), m
+            _, xq, xs = R.rms_norm_quant_gpu_order(x, g, 1e-6)
+            assert np.array_equal(pooled[1], xq) and np.array_equal(bits(pooled[2]), bits(xs))
+    finally:
+        host.set_threads(before)

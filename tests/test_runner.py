@@ -104,3 +104,32 @@ def test_a_graph_nothing_can_lower_is_refused_with_the_way_out():
     from nanocompile_amd.runner import HIPCompiledGraph
     with pytest.raises(NotImplementedError, match="program= or lower="):
         HIPCompiledGraph(SimpleNamespace(name="mystery", nodes=[]))
+
+
+def test_a_cache_view_names_its_host_buffer():
+    """The reference hands over ``_keys[:, :, :length]`` (models/qwen2.py:257-258): the backend
+    names the sequence by that buffer, whose capacity sizes the device cache. Any other array
+    (a fresh one, or a slice that does not start the buffer's rows) names only itself."""
+    import numpy as np
+
+    from nanocompile_amd.runner import _owner, _rows_of
+    buffer = np.zeros((2, 2, 16, 32), np.float32)
+    view = buffer[:, :, :5]
+    assert _owner(view) is buffer and _rows_of(buffer, view) == 16
+    assert _owner(buffer[:, :, :0]) is buffer
+    fresh = np.zeros((2, 2, 5, 32), np.float32)
+    assert _owner(fresh) is fresh and _rows_of(fresh, fresh) == 5
+    inner = buffer[:, :, 3:8]                      # does not start at the buffer's first row
+    assert _owner(inner) is inner and _rows_of(inner, inner) == 5
+    heads = buffer[:, :1, :5]                      # a different block shape
+    assert _owner(heads) is heads
+
+
+def test_token_activations_are_an_opt_in_for_the_int8_graphs():
+    from nanocompile_amd.models.config import TINY
+    from nanocompile_amd.runner import HIPBackend
+    assert HIPBackend(TINY).model_quantization("int8") == "int8"
+    token = HIPBackend(TINY, activations="token")
+    assert [token.model_quantization(m) for m in ("int8", "int8-vnni", "f32")] == ["int8-token", "int8-token", "f32"]
+    with pytest.raises(ValueError, match="activations"):
+        HIPBackend(TINY, activations="int4")

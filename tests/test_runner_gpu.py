@@ -36,6 +36,39 @@ class HostCache:
         self.values = np.concatenate([self.values, values], axis=2)
 
 
+class ReferenceCache:
+    """The reference's KVCache as its driver uses it (models/qwen2.py:232-271): one preallocated
+    buffer per side, grown by doubling; each call is handed a view of the filled rows."""
+
+    def __init__(self, config, capacity: int) -> None:
+        self.config, self.length = config, 0
+        self._keys, self._values = self._allocate(capacity), self._allocate(capacity)
+
+    def _allocate(self, capacity: int) -> np.ndarray:
+        c = self.config
+        return np.zeros((c.num_hidden_layers, c.num_key_value_heads, capacity, c.head_dim), np.float32)
+
+    @property
+    def keys(self) -> np.ndarray:
+        return self._keys[:, :, :self.length]
+
+    @property
+    def values(self) -> np.ndarray:
+        return self._values[:, :, :self.length]
+
+    def append(self, keys, values) -> None:
+        n = keys.shape[2]
+        if self.length + n > self._keys.shape[2]:
+            capacity = max(self.length + n, 2 * self._keys.shape[2])
+            for name in ("_keys", "_values"):
+                grown = self._allocate(capacity)
+                grown[:, :, :self.length] = getattr(self, name)[:, :, :self.length]
+                setattr(self, name, grown)
+        self._keys[:, :, self.length:self.length + n] = keys
+        self._values[:, :, self.length:self.length + n] = values
+        self.length += n
+
+
 class Driver:
     """models/qwen2.py:316-368 over a Runner, recording each call."""
 
@@ -59,8 +92,9 @@ class Driver:
             cache.append(out["keys"], out["values"])
         return out["logits"]
 
-    def greedy(self, prompt, n):
-        cache, pending, out = HostCache(self.config), list(prompt), []
+    def greedy(self, prompt, n, cache=None):
+        cache = HostCache(self.config) if cache is None else cache
+        pending, out = list(prompt), []
         for _ in range(n):
             token = int(np.argmax(self.forward(pending, cache, last_only=True)[0]))
             out.append(token)
@@ -126,3 +160,68 @@ def test_logits_keys_and_values_through_the_runner(setup, mode):
     assert np.max(np.abs(step - ref)) / np.max(np.abs(ref)) <= 1e-4
     assert cache.keys.shape == (config.num_hidden_layers, config.num_key_value_heads, 7, config.head_dim)
     assert np.isfinite(cache.keys).all() and np.isfinite(cache.values).all()
+
+
+@pytest.mark.parametrize("mode", ["int8", "int8-vnni", "f32"])
+def test_the_references_cache_is_held_on_the_device_and_nothing_is_allocated_after_the_first_call(setup, mode):
+    """With the reference's own cache (one buffer sized for the sequence, views of its filled
+    rows), the first call allocates the device cache and every later call of the sequence
+    allocates nothing, uploading none of the rows the device produced; the tokens are G5's."""
+    from nanocompile_amd import hip
+    config, golden = setup[0], setup[5]
+    d = driver(setup, mode)
+    for i, prompt in enumerate(PROMPTS):
+        cache = ReferenceCache(config, len(prompt) + 8)
+        first = d.forward(prompt, cache, last_only=True)
+        before = hip.allocations()
+        tokens = [int(np.argmax(first[0]))]
+        for _ in range(7):
+            tokens.append(int(np.argmax(d.forward([tokens[-1]], cache, last_only=True)[0])))
+        assert hip.allocations() == before, (mode, i)
+        assert tokens == [int(t) for t in golden[f"g5_{TAGS[mode]}_tokens_{i}"]], (mode, i)
+
+
+def test_a_growing_or_rewound_host_cache_gives_the_same_results(setup):
+    """A cache that starts too small and doubles (each growth a new host buffer, uploaded once),
+    and a cache rewound and refilled with other tokens (the device's rows past the new length
+    no longer count): the same logits as a fresh run."""
+    config, golden = setup[0], setup[5]
+    d = driver(setup, "int8")
+    prompt = PROMPTS[3]
+    grown = ReferenceCache(config, 2)
+    assert d.greedy(prompt, 8, cache=grown) == [int(t) for t in golden["g5_int8_tokens_3"]]
+    assert grown._keys.shape[2] >= len(prompt) + 7
+    ids = np.array(PROMPTS[3])
+    cache = ReferenceCache(config, 16)
+    d.forward(ids[:6], cache)
+    d.forward(ids[6:9], cache)
+    cache.length = 6                          # rewind: rows 6.. are refilled with other tokens
+    d.forward(ids[8:9], cache)
+    step = d.forward(ids[6:7], cache, last_only=True)
+    fresh = ReferenceCache(config, 16)
+    d.forward(ids[:6], fresh)
+    d.forward(ids[8:9], fresh)
+    want = d.forward(ids[6:7], fresh, last_only=True)
+    assert np.array_equal(step.view(np.uint32), want.view(np.uint32))
+
+
+def test_token_activations_through_the_runner_are_the_per_token_model(setup):
+    """``HIPBackend(config, activations="token")`` runs the reference's int8 graphs on the
+    per-token model: its greedy tokens and logits are Qwen2(..., "int8-token")'s, bit for bit."""
+    from nanocompile_amd.models.qwen2 import Qwen2, greedy
+    from nanocompile_amd.runner import HIPBackend
+    config, _, _, quantized, fixture, _ = setup
+    backend = HIPBackend(config, max_tokens=64, activations="token")
+    for mode in ("int8", "int8-vnni"):
+        graphs = {k: runner_graphs.stand_in(fixture["modes"][mode][k]) for k in ("graph", "graph_last")}
+        passed = {n: quantized[n] for n in fixture["modes"][mode]["weights_passed"]}
+        d = Driver(config, backend, graphs, passed)
+        model = Qwen2(config, passed, quantization="int8-token", max_tokens=64)
+        for prompt in PROMPTS:
+            want = greedy(model, prompt, 8)
+            assert d.greedy(prompt, 8, cache=ReferenceCache(config, len(prompt) + 8)) == want, (mode, prompt)
+            assert model.generate(prompt, 8) == want
+        ids = np.array(PROMPTS[3])
+        got = d.forward(ids, ReferenceCache(config, 16), last_only=True)
+        want = model.forward(ids, model.new_cache(16), last_only=True)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), mode
