@@ -189,6 +189,23 @@ int32_t nc_matmul_i8_vnni(void **p, const int64_t *s);
  * p: [xq i8[M,K], xs f32[M,K/block], offset f32[M], x f32[M,K]];  s: [M, K, block] */
 int32_t nc_quantize_blocks(void **p, const int64_t *s);
 
+/* The reference's rms_norm in its own order (nn.py:34-38 as fusion.py:631-650
+ * emits it: the row's sum of squares in index order), for the reference modes,
+ * whose int8-vnni activations round after every norm and so need its bits.
+ * p: [normed f32[M,K], x f32[M,K], gamma f32[K]];  s: [M, K, eps as float32 bits] */
+int32_t nc_rms_norm_index_order(void **p, const int64_t *s);
+
+/* The reference's attention in its own order (models/qwen2.py:143-147 with
+ * nn.py:57-66 and the causal mask nn.py:123-135): each score a dot product in
+ * order of d, times scale, plus the mask; exp(z - max); the sum in order of
+ * position; p = e / sum; the context summed in order of position. One
+ * workgroup a (query row, head); after nc_rope_append has rotated q and
+ * appended the rows' keys and values. For the reference modes.
+ * p: [ctx f32[M, heads*D], qkv f32[M, (heads+2kv)*D], kcache f32[kv, capacity, D],
+ *     vcache f32[kv, capacity, D], pos i64[1] | NULL (past read on the device)];
+ * s: [M, heads, kv, D, past, capacity (at most 16000), scale as float32 bits] */
+int32_t nc_attention_index_order(void **p, const int64_t *s);
+
 /* -- one decode token, fused ---------------------------------------------------- */
 
 /* One projection of a single token with its activation prologue fused

@@ -19,6 +19,7 @@
 // Elements past the last whole 32-block (or 128-block) are read from the
 // plain row-major weights, in the reference's order.
 #include "nc_common.h"
+#include "nc_math.h"
 
 namespace {
 
@@ -166,7 +167,131 @@ __global__ __launch_bounds__(256) void quantize_blocks(int8_t *__restrict__ xq, 
     }
 }
 
+// The reference's rms_norm row kernel in its own order (nn.py:34-38, fusion.py:631-650): the
+// sum of squares in index order, one multiply and one add a step from 0, then
+// (x * (1 / sqrt(ss / K + eps))) * gamma. The row is staged in LDS and the one
+// chain runs in lane 0; every thread then writes its share of the row.
+__global__ __launch_bounds__(256) void rms_norm_index_order(float *__restrict__ normed, const float *__restrict__ x,
+                                                            const float *__restrict__ gamma, int K, float eps) {
+    extern __shared__ float srow[];
+    __shared__ float rcp_shared;
+    const float *row = x + (size_t)blockIdx.x * K;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) srow[k] = row[k];
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float ss = 0.0f;
+        for (int k = 0; k < K; ++k) ss = __fadd_rn(ss, __fmul_rn(srow[k], srow[k]));
+        rcp_shared = nc::div_rn(1.0f, nc::sqrt_rn(__fadd_rn(nc::div_rn(ss, (float)K), eps)));
+    }
+    __syncthreads();
+    const float rcp = rcp_shared;
+    for (int k = threadIdx.x; k < K; k += blockDim.x)
+        normed[(size_t)blockIdx.x * K + k] = __fmul_rn(__fmul_rn(srow[k], rcp), gamma[k]);
+}
+
+// The reference's attention for one query row and one head, in the order its graph states it
+// (models/qwen2.py:143-147, nn.py:57-66, 109-135): each score a dot product over d in order,
+// one multiply and one add a step from 0, times scale, plus the mask's 0; the row's maximum;
+// e_t = exp(z_t - max); their sum in order of t from 0; p_t = e_t / sum; the context
+// sum over t in order of p_t * v_t[d]. The key of row i at absolute position past + i sees
+// positions 0 .. past + i; the masked positions after them would add exp(-inf) = 0 to the sum
+// and 0 * v to each context sum, neither of which changes a float, so they are skipped.
+// Keys and values come from the cache (RoPE'd keys; this call's rows already appended), the
+// KV head of query head h being h / (heads / kv) (repeat_kv's consecutive groups).
+// LDS: one float per visible position (the scores, then the exponentials, then p).
+__global__ __launch_bounds__(256) void attention_index_order(float *__restrict__ ctx, const float *__restrict__ qkv,
+                                                             const float *__restrict__ kcache,
+                                                             const float *__restrict__ vcache,
+                                                             const int64_t *__restrict__ pos, int heads, int kv,
+                                                             int D, int past_arg, int M, int capacity, float scale,
+                                                             int32_t *__restrict__ error) {
+    extern __shared__ float sp[];
+    __shared__ float sq[128];
+    __shared__ float shared_max[4];
+    __shared__ float shared_sum;
+    const int i = blockIdx.x, h = blockIdx.y, g = h / (heads / kv);
+    int past = past_arg;
+    if (pos) {
+        // a position read on the device (a captured decode step) must leave room for the M rows;
+        // every thread reads the same word and takes the same branch
+        const int64_t at = pos[0];
+        if (at < 0 || at + M > capacity) {
+            if (i == 0 && h == 0 && threadIdx.x == 0) atomicCAS(error, 0, NC_FAIL_CAPACITY);
+            return;
+        }
+        past = (int)at;
+    }
+    const int T = past + i + 1;
+    const int W = (heads + 2 * kv) * D;
+    for (int d = threadIdx.x; d < D; d += blockDim.x) sq[d] = qkv[(size_t)i * W + (size_t)h * D + d];
+    __syncthreads();
+    const float *kh = kcache + (size_t)g * capacity * D;
+    const float *vh = vcache + (size_t)g * capacity * D;
+    float mx = -__builtin_inff();
+    for (int t = threadIdx.x; t < T; t += blockDim.x) {
+        const float *kt = kh + (size_t)t * D;
+        float acc = 0.0f;
+        for (int d = 0; d < D; ++d) acc = __fadd_rn(acc, __fmul_rn(sq[d], kt[d]));
+        const float z = __fadd_rn(__fmul_rn(acc, scale), 0.0f);
+        sp[t] = z;
+        mx = nc::nan_max(mx, z);
+    }
+    // the maximum is exact in any order; NaN from any score wins, as the reference's does
+    mx = nc::wave_max_f32(mx);
+    if ((threadIdx.x & 63) == 0) shared_max[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = shared_max[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) mx = nc::nan_max(mx, shared_max[w]);
+    for (int t = threadIdx.x; t < T; t += blockDim.x) sp[t] = nc_expf(__fsub_rn(sp[t], mx));
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float total = 0.0f;
+        for (int t = 0; t < T; ++t) total = __fadd_rn(total, sp[t]);
+        shared_sum = total;
+    }
+    __syncthreads();
+    const float total = shared_sum;
+    for (int t = threadIdx.x; t < T; t += blockDim.x) sp[t] = nc::div_rn(sp[t], total);
+    __syncthreads();
+    for (int d = threadIdx.x; d < D; d += blockDim.x) {
+        float acc = 0.0f;
+        for (int t = 0; t < T; ++t) acc = __fadd_rn(acc, __fmul_rn(sp[t], vh[(size_t)t * D + d]));
+        ctx[(size_t)i * heads * D + (size_t)h * D + d] = acc;
+    }
+}
+
 }  // namespace
+
+// The reference's rms_norm in its index order (reference modes), normed rows only.
+// p: [normed f32[M,K], x f32[M,K], gamma f32[K]];  s: [M, K, eps as float32 bits]
+NC_EXPORT int32_t nc_rms_norm_index_order(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2], "nc_rms_norm_index_order: null operand");
+    NC_REQUIRE(s[0] >= 0 && s[0] < (1 << 26) && s[1] > 0 && s[1] <= 16384, "nc_rms_norm_index_order: bad shape");
+    if (s[0] == 0) return NC_OK;
+    hipLaunchKernelGGL(rms_norm_index_order, dim3((unsigned)s[0]), dim3(256), (size_t)s[1] * sizeof(float),
+                       nc::stream(), (float *)p[0], (const float *)p[1], (const float *)p[2], (int)s[1],
+                       nc::bits_to_float(s[2]));
+    return nc::launched("rms_norm_index_order");
+}
+
+// The reference's attention in its own order (reference modes), after nc_rope_append.
+// p: [ctx f32[M, heads*D], qkv f32[M, (heads+2kv)*D] (q rotated), kcache f32[kv, capacity, D],
+//     vcache f32[kv, capacity, D] (rows 0 .. past+M-1 filled), pos i64[1] | NULL (past read on the device)];
+// s: [M, heads, kv, D, past, capacity, scale as float32 bits]
+NC_EXPORT int32_t nc_attention_index_order(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3], "nc_attention_index_order: null operand");
+    const int64_t M = s[0], heads = s[1], kv = s[2], D = s[3], past = s[4], capacity = s[5];
+    // one float of LDS per position the rows can see, beside 0.5 KB of the kernel's own: within 64 KB
+    NC_REQUIRE(M >= 0 && M < 65536 && heads > 0 && heads < 65536 && kv > 0 && heads % kv == 0 && D > 0 &&
+                   D <= 128 && past >= 0 && capacity > 0 && capacity <= 16000 && past + M <= capacity,
+               "nc_attention_index_order: bad shape (head_dim at most 128, at most 16000 positions)");
+    if (M == 0) return NC_OK;
+    hipLaunchKernelGGL(attention_index_order, dim3((unsigned)M, (unsigned)heads), dim3(256),
+                       (size_t)capacity * sizeof(float), nc::stream(), (float *)p[0], (const float *)p[1],
+                       (const float *)p[2], (const float *)p[3], (const int64_t *)p[4], (int)heads, (int)kv, (int)D,
+                       (int)past, (int)M, (int)capacity, nc::bits_to_float(s[6]), nc::error_word());
+    return nc::launched("attention_index_order");
+}
 
 // The reference's matmul_i8: y = x @ (q * scales).T in its 32-chain order, then
 // + bias, then residual +.

@@ -62,6 +62,7 @@ def _packed_bytes(quantization: str, n: int, k: int) -> int:
 
 
 WORKSPACE_BYTES = 64 << 20     # attention chunk results held at once (longer prompts go in slabs)
+REFERENCE_ORDER_KEYS = 16000   # nc_attention_index_order: a float of LDS per position
 
 
 def inverse_frequencies(head_dim: int, theta: float) -> np.ndarray:
@@ -307,6 +308,9 @@ class Qwen2:
     # -- running ---------------------------------------------------------------------
 
     def new_cache(self, capacity: int = 256) -> KVCache:
+        if self.quantization != "int8-token" and capacity > REFERENCE_ORDER_KEYS:
+            raise ValueError(f"capacity {capacity}: the reference modes' attention holds at most "
+                             f"{REFERENCE_ORDER_KEYS} positions")
         return KVCache(self.config, capacity)
 
     def _layers(self, m: int, past: int, cache: KVCache, pos: DeviceArray | None = None) -> None:
@@ -388,8 +392,12 @@ class Qwen2:
     def _layers_reference_modes(self, m: int, past: int, cache: KVCache, pos: DeviceArray | None) -> None:
         """The layers with the reference's own modes (quantize.py:127-164): float32 activations
         into matmul_i8 ("int8"), 32-wide int8 blocks into matmul_i8_vnni ("int8-vnni"), or float32
-        weights ("f32"), each in the reference's k order; rms_norm, RoPE, attention and the LM head
-        as in "int8-token"."""
+        weights ("f32"), each in the reference's k order; rms_norm and attention in the reference's
+        own order too (nc_rms_norm_index_order, nc_attention_index_order: sums in index order), RoPE
+        and the LM head as in "int8-token". The int8-vnni mode needs the reference's orders: its
+        activations are rounded to int8 at every projection, and a last-bit difference in one of
+        them can move a rounding and with it the logits by a few percent (a one-ulp change of every
+        norm's gamma in the reference's own C moves its logits by 2.1% of the largest)."""
         c = self.config
         H, I, D = c.hidden_size, c.intermediate_size, c.head_dim
         heads, kv, W = c.num_attention_heads, c.num_key_value_heads, self.width
@@ -397,14 +405,14 @@ class Qwen2:
         eps = float_bits(c.rms_norm_eps)
         for i, w in enumerate(self.layers):
             kc, vc = cache.layer(i)
-            hip.call("nc_rms_norm_quant", [self.normed, self.xq, self.xs, self.x, w["g1"]], [m, H, eps])
+            hip.call("nc_rms_norm_index_order", [self.normed, self.x, w["g1"]], [m, H, eps])
             self._project(w["qkv"], self.normed, self.qkv, m, W, H, bias=w["qkv_b"])
             hip.call("nc_rope_append", [self.qkv, kc, vc, self.inv_freq, pos, cache.rope],
                      [m, heads, kv, D, past, cache.capacity])
-            hip.call("nc_attention", [self.ctx, self.qkv, kc, vc, pos, cache.work],
-                     [m, heads, kv, D, past, cache.capacity, float_bits(self.scale), cache.work_bytes])
+            hip.call("nc_attention_index_order", [self.ctx, self.qkv, kc, vc, pos],
+                     [m, heads, kv, D, past, cache.capacity, float_bits(self.scale)])
             self._project(w["o"], self.ctx, self.x, m, H, Q, residual=self.x)
-            hip.call("nc_rms_norm_quant", [self.normed, self.xq, self.xs, self.x, w["g2"]], [m, H, eps])
+            hip.call("nc_rms_norm_index_order", [self.normed, self.x, w["g2"]], [m, H, eps])
             self._project(w["gate"], self.normed, self.gate, m, I, H)
             self._project(w["up"], self.normed, self.up, m, I, H)
             hip.call("nc_silu_mul", [self.h, self.gate, self.up], [m * I])
@@ -483,8 +491,7 @@ class Qwen2:
         rows = 1 if last_only else m
         first = m - rows
         x_rows = self.x.ptr + first * H * 4
-        hip.call("nc_rms_norm_quant", [self.normed, self.xq, self.xs, x_rows, self.norm],
-                 [rows, H, float_bits(c.rms_norm_eps)])
+        self._final_norm(x_rows, rows)
         logits = self.logits_row if rows == 1 else DeviceArray((rows, V), np.float32)
         hip.call("nc_lm_head", [logits, None, self.normed, self.head], [rows, V, H])
         hip.sync()
@@ -503,8 +510,7 @@ class Qwen2:
         self.ids.view((m,)).upload(ids)
         hip.call("nc_embed", [self.x, self.embed, self.ids], [m, H, V])
         self._layers(m, past, cache)
-        hip.call("nc_rms_norm_quant", [self.normed, self.xq, self.xs, self.x.ptr + (m - 1) * H * 4, self.norm],
-                 [1, H, float_bits(c.rms_norm_eps)])
+        self._final_norm(self.x.ptr + (m - 1) * H * 4, 1)
         hip.call("nc_lm_head", [None, self.best, self.normed, self.head], [1, V, H, 0, 1])
         hip.call("nc_argmax_index", [self.argmax, self.best], [1, self.slots])
         token = int(self.argmax.view((1,)).numpy()[0])      # waits for the stream; a failed copy raises
@@ -515,11 +521,26 @@ class Qwen2:
 
     # -- greedy decoding on the device -------------------------------------------------
 
+    def _final_norm(self, rows_ptr: int, rows: int) -> None:
+        """The final rms_norm of ``rows`` rows into ``normed``: the reference's index order in its
+        own modes, the row kernels' order in "int8-token"."""
+        c = self.config
+        eps = float_bits(c.rms_norm_eps)
+        if self.quantization == "int8-token":
+            hip.call("nc_rms_norm_quant", [self.normed, self.xq, self.xs, rows_ptr, self.norm],
+                     [rows, c.hidden_size, eps])
+        else:
+            hip.call("nc_rms_norm_index_order", [self.normed, rows_ptr, self.norm], [rows, c.hidden_size, eps])
+
     def _head_argmax(self, row_ptr: int) -> None:
-        """Final rms_norm of one row and the LM head (one kernel), its argmax keys (one per
-        workgroup) into ``best``."""
+        """Final rms_norm of one row and the LM head (one kernel in "int8-token"; the norm in the
+        reference's order first in its own modes), its argmax keys (one per workgroup) into ``best``."""
         c = self.config
         H, V = c.hidden_size, c.vocab_size
+        if self.quantization != "int8-token":
+            self._final_norm(row_ptr, 1)
+            hip.call("nc_lm_head", [None, self.best, self.normed, self.head], [1, V, H, 0, 1])
+            return
         hip.call("nc_lm_head", [None, self.best, row_ptr, self.head, self.norm],
                  [1, V, H, float_bits(c.rms_norm_eps), 1])
 

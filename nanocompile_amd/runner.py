@@ -189,7 +189,6 @@ class HIPBackend:
     def _cache_for(self, mode: str, model, past_keys: np.ndarray, past_values: np.ndarray, need: int):
         """The device cache for this call's sequence, holding the rows [0, past) of the host's;
         only rows it did not already hold are uploaded."""
-        from nanocompile_amd.models.qwen2 import KVCache
         past = int(past_keys.shape[2])
         kbuf, vbuf = _owner(past_keys), _owner(past_values)
         seq = self._sequences.get(mode)
@@ -200,7 +199,7 @@ class HIPBackend:
             capacity = min(max(need, _rows_of(kbuf, past_keys), 2 * old), MAX_CACHE_ROWS)
             if capacity < need:
                 raise ValueError(f"{need} tokens exceed the device cache's limit of {MAX_CACHE_ROWS}")
-            seq = _Sequence(KVCache(self.config, capacity))
+            seq = _Sequence(model.new_cache(capacity))
             self._sequences[mode] = seq
         if seq.keys_buffer is not kbuf or seq.values_buffer is not vbuf:
             seq.keys_buffer, seq.values_buffer, seq.held = kbuf, vbuf, 0     # another sequence: nothing held
@@ -251,7 +250,7 @@ class HIPBackend:
         return {"logits": logits, "keys": keys, "values": values}
 
 
-MAX_CACHE_ROWS = 16384          # the attention kernels' limit on keys (kernels.MAX_KEYS)
+MAX_CACHE_ROWS = 16000          # the attention kernels' limit on positions, in every mode
 
 
 class _Sequence:

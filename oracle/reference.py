@@ -25,6 +25,11 @@ How each function is pinned (tests/test_oracle.py and tests/golden/):
   rms_norm_gpu_order   the same function as rms_norm_reference up to the
                        order of one sum (bounded), and exact on rows whose
                        squares sum exactly (powers of two)
+  attention_index_order  float64 attention (within rounding), golden G4's
+                       softmax with the mask (the reference's row kernel) for
+                       its softmax step, a planted dropped max failing the
+                       first; end to end, golden G6's int8-vnni tokens, which
+                       move with any last-bit difference in the activations
 """
 
 from __future__ import annotations
@@ -192,3 +197,50 @@ def rms_norm_quant_gpu_order(x, gamma, eps):
     normed = rms_norm_gpu_order(x, gamma, eps)
     xq, xs = quantize_token(normed)
     return normed, xq, xs
+
+
+# -- the reference's attention in its own order ----------------------------------
+
+
+def softmax_index_order(z: np.ndarray, exp) -> np.ndarray:
+    """The reference's softmax over the last axis (nn.py:57-66): shifted = exp(z - max z); the
+    sum of shifted in index order from 0; shifted / sum. ``exp`` is the float32 exponential to
+    use (the reference's C calls the C library's expf, codegen_c.py:58)."""
+    z = np.asarray(z, F32)
+    m = z.max(axis=-1, keepdims=True)
+    shifted = np.asarray(exp((z - m).astype(F32)), F32).reshape(z.shape)
+    total = np.zeros(z.shape[:-1] + (1,), F32)
+    for t in range(z.shape[-1]):
+        total = (total + shifted[..., t:t + 1]).astype(F32)
+    return (shifted / total).astype(F32)
+
+
+def attention_index_order(q: np.ndarray, kcache: np.ndarray, vcache: np.ndarray, past: int, scale: float,
+                          exp) -> np.ndarray:
+    """The reference's grouped-query attention for M new rows (models/qwen2.py:143-147 with
+    nn.py:57-66, 109-135), each sum in its order: ``q`` [M, heads, D] (rotated), ``kcache`` /
+    ``vcache`` [kv, >= past + M, D] holding the rows' own keys and values at past .. past + M - 1.
+    Scores: for each position a dot product over d in order (one multiply and one add a step,
+    from 0), times scale, plus the mask (0 where visible). Row i sees positions 0 .. past + i;
+    the masked rest would add exp(-inf) = 0 to the softmax's sum and 0 * v to each context sum,
+    changing no float, so only the visible ones are summed. Context: the sum over positions in
+    order of p_t * v_t. Returns [M, heads, D]."""
+    q = np.asarray(q, F32)
+    m_rows, heads, d = q.shape
+    kv = kcache.shape[0]
+    group = heads // kv
+    out = np.zeros((m_rows, heads, d), F32)
+    for i in range(m_rows):
+        t_end = past + i + 1
+        k = np.repeat(np.asarray(kcache[:, :t_end], F32), group, axis=0)        # [heads, T, D]
+        v = np.repeat(np.asarray(vcache[:, :t_end], F32), group, axis=0)
+        acc = np.zeros((heads, t_end), F32)
+        for j in range(d):
+            acc = (acc + (q[i, :, j:j + 1] * k[:, :, j]).astype(F32)).astype(F32)
+        z = ((acc * F32(scale)).astype(F32) + F32(0.0)).astype(F32)
+        p = softmax_index_order(z, exp)
+        ctx = np.zeros((heads, d), F32)
+        for t in range(t_end):
+            ctx = (ctx + (p[:, t:t + 1] * v[:, t, :]).astype(F32)).astype(F32)
+        out[i] = ctx
+    return out

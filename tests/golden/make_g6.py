@@ -19,12 +19,25 @@ Recorded per mode: the 257 tokens; for the calls at cache length 0 (the
 prompt), 255 and 383, the argmax, the largest logit, and the logits at every
 97th vocabulary entry. A recording wrapper around the reference's runner keeps
 each call's logits; nothing of the reference is copied, only its outputs.
+
+``--math nc`` records the same runs again, under the tags ``int8_ncmath`` and
+``vnni_ncmath``, with the reference's compiled C calling this package's expf,
+sinf and cosf (csrc/nc_math.h, the functions the GPU kernels use) in place of
+the C library's: nc_math_shim.c is built with gcc and preloaded into a child
+process. The int8-vnni mode rounds its activations to int8 at every
+projection, so a last-bit difference anywhere moves roundings downstream: the
+reference's own logits move by 2.1% of the largest when every norm weight
+moves by one ulp, and by 2.4% between the C library's functions and these
+(their results differ in the last bit on a small fraction of inputs). With the
+same functions on both sides the whole model can be held bit for bit.
 """
 
 from __future__ import annotations
 
+import ctypes
 import json
 import os
+import subprocess
 import sys
 import tempfile
 import time
@@ -62,7 +75,29 @@ class Recording:
         return out
 
 
+def preloaded_math() -> bool:
+    """Whether nc_math_shim.c's functions are the process's expf, sinf and cosf."""
+    return hasattr(ctypes.CDLL(None), "nc_g6_math_shim")
+
+
+def rerun_with_nc_math(modes: list[str]) -> None:
+    """Build nc_math_shim.c and run this script again with it preloaded."""
+    with tempfile.TemporaryDirectory() as scratch:
+        shim = Path(scratch) / "nc_math_shim.so"
+        subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-fPIC", "-shared", "-o", str(shim),
+                        str(HERE / "nc_math_shim.c"), "-lm"], check=True)
+        env = dict(os.environ, LD_PRELOAD=str(shim))
+        subprocess.run([sys.executable, __file__, "--math", "nc", *modes], env=env, check=True)
+
+
 def main() -> None:
+    args = sys.argv[1:]
+    nc_math = args[:2] == ["--math", "nc"]
+    if nc_math:
+        args = args[2:]
+        if not preloaded_math():
+            rerun_with_nc_math(args)
+            return
     c = ours.QWEN25_05B
     config = Qwen2Config(c.vocab_size, c.hidden_size, c.intermediate_size, c.num_hidden_layers,
                          c.num_attention_heads, c.num_key_value_heads, c.rms_norm_eps, c.rope_theta,
@@ -72,9 +107,9 @@ def main() -> None:
     meta: dict[str, object] = {"seed": SEED, "prompt_seed": SEED + 1, "prompt": prompt, "new_tokens": NEW,
                                "stride": STRIDE, "checked_past": sorted(CHECKED)}
     arrays: dict[str, np.ndarray] = {}
-    modes = sys.argv[1:] or ["int8", "int8-vnni"]
+    modes = args or ["int8", "int8-vnni"]
     for mode in modes:
-        tag = {"int8": "int8", "int8-vnni": "vnni"}[mode]
+        tag = {"int8": "int8", "int8-vnni": "vnni"}[mode] + ("_ncmath" if nc_math else "")
         recorder = Recording(CBackend())
         model = Qwen2(config, weights, run=recorder, quantization=mode)
         start = time.time()

@@ -9,14 +9,26 @@ tokens, in ``int8`` (float32 activations into matmul_i8's 32-chain order) and
 It recorded the tokens, and at cache lengths 0 (the prompt), 255 and 383 the
 argmax, the largest logit and the logits at every 97th vocabulary entry.
 
+It recorded the same runs again with the reference's compiled C calling this
+package's expf, sinf and cosf (``make_g6.py --math nc``; tags ``int8_ncmath``
+and ``vnni_ncmath``): the GPU kernels use those functions, which differ from the
+C library's in the last bit on a small fraction of inputs.
+
 Held to it here, on the GPU:
-* the hand-written model in each mode (``Qwen2(..., quantization=mode)``):
-  its device loop's 256 greedy tokens are the reference's, and its logits at
-  the three positions are within 1e-4 of the largest (the bar the north star
-  states for logits; its projections are the reference's kernels bit for bit,
-  only the float reductions around them are summed in a tree);
+* the hand-written model in each mode (``Qwen2(..., quantization=mode)``), whose
+  projections are the reference's kernels bit for bit and whose norms and
+  attention sum in the reference's order: against the reference run with the
+  same math functions, the 256 greedy tokens and the sampled logits at the three
+  positions bit for bit; against the run with the C library's, in int8 the same
+  tokens and logits within 1e-4 of the largest (the north star's bar);
+* in int8-vnni against the C library's run, the tokens up to where the two
+  reference runs themselves part (the 10th token): int8-vnni rounds its
+  activations to int8 at every projection, so the C library's last-bit
+  differences move roundings and the logits by 2.4% of the largest in the
+  reference's own C (test_golden.py holds the fixture to that);
 * the reference's own compiled program for this model in int8, generated as
-  HIP by codegen_hip (the drop-in path): the same tokens and logits.
+  HIP by codegen_hip (the drop-in path): the same, bit for bit against the
+  run with the same math functions.
 """
 
 from __future__ import annotations
@@ -68,15 +80,19 @@ def chunks(meta, tag):
     return out
 
 
-def check_logits(got: np.ndarray, meta, arrays, tag: str, past: int) -> float:
+def check_logits(got: np.ndarray, meta, arrays, tag: str, past: int, bitwise: bool = False) -> float:
     want = arrays[f"{tag}_logits_{past}"]
     sampled = np.asarray(got, np.float32)[::meta["stride"]]
     assert sampled.shape == want.shape
     rel = float(np.max(np.abs(sampled.astype(np.float64) - want)) / np.max(np.abs(want)))
-    assert rel <= TOLERANCE, (tag, past, rel)
     assert int(np.argmax(got)) == meta[tag][f"argmax_{past}"], (tag, past)
     top = float.fromhex(meta[tag][f"max_{past}"])
-    assert abs(float(np.max(got)) - top) <= TOLERANCE * abs(top), (tag, past)
+    if bitwise:
+        assert np.array_equal(sampled.view(np.uint32), want.view(np.uint32)), (tag, past, rel)
+        assert float(np.max(got)) == top, (tag, past)
+    else:
+        assert rel <= TOLERANCE, (tag, past, rel)
+        assert abs(float(np.max(got)) - top) <= TOLERANCE * abs(top), (tag, past)
     return rel
 
 
@@ -93,27 +109,27 @@ def test_hand_written_reference_modes_decode_the_references_tokens(model, g6):
     m, tag = model
     meta, _ = g6
     print(f"G6 {tag}: device loop, {NEW_TOKENS} tokens", flush=True)
-    assert m.generate(meta["prompt"], NEW_TOKENS) == meta[tag]["tokens"][:NEW_TOKENS]
+    tokens = m.generate(meta["prompt"], NEW_TOKENS)
+    assert tokens == meta[f"{tag}_ncmath"]["tokens"][:NEW_TOKENS]
+    if tag == "int8":
+        assert tokens == meta[tag]["tokens"][:NEW_TOKENS]
+    else:
+        assert tokens[:9] == meta[tag]["tokens"][:9]           # where the two reference runs part
 
 
 def test_hand_written_reference_modes_logits_at_past_0_255_383(model, g6):
     m, tag = model
     meta, arrays = g6
     cache = m.new_cache(128 + NEW_TOKENS + 1)
-    for past, ids in chunks(meta, tag):
+    for past, ids in chunks(meta, f"{tag}_ncmath"):
         assert cache.length == past
         got = m.forward(ids, cache=cache, last_only=True)[0]
         if past in (0, 255, 383):
-            rel = check_logits(got, meta, arrays, tag, past)
-            print(f"G6 {tag} logits at past {past}: {rel:.2e} of the largest", flush=True)
-
-
-def test_the_two_modes_are_told_apart(g6):
-    """The fixture's modes disagree well beyond the tolerance, so passing is not a coincidence."""
-    meta, arrays = g6
-    a, b = arrays["int8_logits_0"], arrays["vnni_logits_0"]
-    assert np.max(np.abs(a - b)) / np.max(np.abs(a)) > 10 * TOLERANCE
-    assert meta["int8"]["tokens"] != meta["vnni"]["tokens"]
+            check_logits(got, meta, arrays, f"{tag}_ncmath", past, bitwise=True)
+            if tag == "int8":
+                rel = check_logits(got, meta, arrays, tag, past)
+                print(f"G6 {tag} logits at past {past}: {rel:.2e} of the largest from the C library's run",
+                      flush=True)
 
 
 def test_generated_program_in_int8_gives_the_references_tokens_and_logits(gpu, weights, g6):
@@ -140,5 +156,6 @@ def test_generated_program_in_int8_gives_the_references_tokens_and_logits(gpu, w
         got = driver.forward(ids, cache, last_only=True)[0]
         if past in (0, 255, 383):
             check_logits(got, meta, arrays, "int8", past)
+            check_logits(got, meta, arrays, "int8_ncmath", past, bitwise=True)
     print("G6 generated int8: greedy", flush=True)
     assert driver.greedy(meta["prompt"], NEW_TOKENS) == meta["int8"]["tokens"][:NEW_TOKENS]

@@ -181,3 +181,98 @@ def test_the_interpreter_meanings_agree_with_the_orders_to_rounding(golden):
     for key in [k for k in golden.files if (k.startswith("g2_") or k.startswith("g3_")) and not k.endswith("_interp")
                 and not k.startswith("g3_quant")]:
         np.testing.assert_allclose(golden[key], golden[key + "_interp"], rtol=1e-4, atol=1e-3)
+
+
+def _causal(s: np.ndarray, past: int) -> np.ndarray:
+    """scores + the causal mask (nn.py:123-135): row i sees columns 0 .. past + i."""
+    seq, total = s.shape[-2], s.shape[-1]
+    allowed = np.arange(total)[None, :] <= np.arange(seq)[:, None] + past
+    return (s + np.where(allowed, np.float32(0.0), np.float32(-np.inf))).astype(np.float32)
+
+
+@pytest.mark.parametrize("seq,past", [(1, 12), (5, 3)])
+def test_g4_softmax_in_index_order_is_the_references(golden, host, seq, past):
+    """The reference's softmax row kernel with the causal mask, bit for bit, given the C
+    library's expf (the reference's): the order of its sum and its divide are pinned."""
+    s = golden[f"g4_softmax_{seq}_{past}_s"]
+    y = R.softmax_index_order(_causal(s, past), lambda v: host.math("exp", v))
+    assert np.array_equal(bits(y), bits(golden[f"g4_softmax_{seq}_{past}_y"]))
+
+
+def test_attention_index_order_is_attention_and_a_dropped_max_is_caught(host):
+    """Against float64 softmax attention (within float32 rounding) on Qwen2.5-0.5B's heads,
+    prefill rows and decode at several positions; a restatement that forgot to subtract the
+    maximum overflows exp on large scores and fails the same check."""
+    rng = np.random.default_rng(9)
+    heads, kv, d = 14, 2, 64
+    exp = lambda v: host.math("nc_exp", v)                     # noqa: E731
+
+    def float64_attention(q, kc, vc, past):
+        out = np.zeros(q.shape, np.float64)
+        for i in range(q.shape[0]):
+            t = past + i + 1
+            for h in range(heads):
+                k, v = kc[h // (heads // kv), :t].astype(np.float64), vc[h // (heads // kv), :t].astype(np.float64)
+                z = k @ q[i, h].astype(np.float64) * 0.125
+                p = np.exp(z - z.max())
+                out[i, h] = (p / p.sum()) @ v
+        return out
+
+    for m, past, spread in [(1, 0, 1.0), (1, 70, 1.0), (5, 3, 1.0), (3, 40, 60.0)]:
+        q = (rng.standard_normal((m, heads, d)) * spread).astype(np.float32)
+        kc = rng.standard_normal((kv, past + m, d)).astype(np.float32)
+        vc = rng.standard_normal((kv, past + m, d)).astype(np.float32)
+        got = R.attention_index_order(q, kc, vc, past, 0.125, exp)
+        # scores of magnitude ~spread * 8 carry float32 rounding of that size into the softmax
+        tol = dict(rtol=1e-5 * spread, atol=2e-6 * spread)
+        np.testing.assert_allclose(got, float64_attention(q, kc, vc, past), **tol)
+        if spread > 10:
+            def no_max(z, ex):
+                e = np.asarray(ex(z.astype(np.float32)), np.float32)
+                return (e / e.sum(axis=-1, keepdims=True)).astype(np.float32)
+            original = R.softmax_index_order
+            R.softmax_index_order = no_max
+            try:
+                with np.errstate(all="ignore"):
+                    bad = R.attention_index_order(q, kc, vc, past, 0.125, exp)
+            finally:
+                R.softmax_index_order = original
+            assert not np.allclose(bad, float64_attention(q, kc, vc, past), equal_nan=False, **tol)
+
+
+def test_g6_fixture_is_the_workload_and_consistent():
+    """G6 (make_g6.py) is config 5's exact workload: seed-0 weights, the seed-1 128-token
+    prompt; in each mode the recorded argmax at each checked call is that call's token."""
+    from nanocompile_amd.models.config import QWEN25_05B
+    meta = json.loads((HERE / "g6.json").read_text())
+    prompt = [int(t) for t in np.random.default_rng(meta["prompt_seed"]).integers(0, QWEN25_05B.vocab_size, 128)]
+    assert meta["seed"] == 0 and prompt == meta["prompt"] and meta["checked_past"] == [0, 255, 383]
+    with np.load(HERE / "g6.npz", allow_pickle=False) as z:
+        for tag in ("int8", "vnni", "int8_ncmath", "vnni_ncmath"):
+            tokens = meta[tag]["tokens"]
+            assert len(tokens) == meta["new_tokens"] == 257
+            for past, call in ((0, 0), (255, 128), (383, 256)):
+                assert tokens[call] == meta[tag][f"argmax_{past}"]
+                sampled = z[f"{tag}_logits_{past}"]
+                assert sampled.shape == (-(-QWEN25_05B.vocab_size // meta["stride"]),)
+                assert float(sampled.max()) <= float.fromhex(meta[tag][f"max_{past}"])
+
+
+def test_g6_modes_differ_and_vnni_moves_with_the_math_library():
+    """The two modes' logits differ well beyond the logits bar, so passing one is no accident of
+    the other. int8 is insensitive to the math library (the same 257 tokens with the C library's
+    exp/sin/cos and with this package's, logits within 1e-5); int8-vnni is not: the reference's
+    own runs part at the 10th token and their prompt logits differ by more than 1% of the
+    largest, the size of the difference a one-ulp change of the norm weights makes."""
+    meta = json.loads((HERE / "g6.json").read_text())
+    with np.load(HERE / "g6.npz", allow_pickle=False) as z:
+        a, b = z["int8_logits_0"], z["vnni_logits_0"]
+        assert np.max(np.abs(a - b)) / np.max(np.abs(a)) > 1e-3
+        assert meta["int8"]["tokens"] == meta["int8_ncmath"]["tokens"]
+        for past in (0, 255, 383):
+            x, y = z[f"int8_logits_{past}"], z[f"int8_ncmath_logits_{past}"]
+            assert np.max(np.abs(x - y)) / np.max(np.abs(x)) < 1e-5
+        x, y = z["vnni_logits_0"], z["vnni_ncmath_logits_0"]
+        assert np.max(np.abs(x - y)) / np.max(np.abs(x)) > 1e-2
+    glibc, ours = meta["vnni"]["tokens"], meta["vnni_ncmath"]["tokens"]
+    assert glibc[:9] == ours[:9] and glibc[9] != ours[9]

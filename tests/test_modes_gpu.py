@@ -89,3 +89,47 @@ def test_vnni_rejects_blocks_that_are_not_powers_of_two(gpu):
     with pytest.raises(kernels.ShapeError, match="power of two"):
         kernels.matmul_i8_vnni(xq, np.ones((1, 2), np.float32), np.zeros(1, np.float32),
                                np.zeros((4, 96), np.int8), np.ones(4, np.float32), block=48)
+
+
+@pytest.mark.parametrize("m,k", [(1, 896), (3, 4864), (128, 896), (2, 128)])
+def test_rms_norm_index_order_is_the_references_order(gpu, m, k):
+    """The reference modes' rms_norm: its row sum in index order (golden G4 pins the oracle)."""
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import DeviceArray
+    from nanocompile_amd.kernels import float_bits
+    print(f"rms_norm_index_order m={m} k={k}", flush=True)
+    rng = np.random.default_rng(m * k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[rng.random(x.shape) < 0.01] *= 20
+    g = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    dx, dg, out = DeviceArray.from_host(x), DeviceArray.from_host(g), DeviceArray((m, k), np.float32)
+    hip.call("nc_rms_norm_index_order", [out, dx, dg], [m, k, float_bits(1e-6)])
+    hip.sync()
+    assert np.array_equal(bits(out.numpy()), bits(R.rms_norm_reference(x, g, 1e-6)))
+
+
+@pytest.mark.parametrize("m,past,heads,kv,d", [(1, 0, 14, 2, 64), (1, 383, 14, 2, 64), (7, 0, 14, 2, 64),
+                                               (5, 3, 4, 2, 32), (1, 12, 4, 2, 32), (128, 0, 14, 2, 64)])
+def test_attention_index_order_is_the_oracle(gpu, host, m, past, heads, kv, d):
+    """The reference modes' attention (every sum in the reference's order) bit for bit against the
+    oracle, with the position given on the host and read from the device."""
+    from nanocompile_amd import hip
+    from nanocompile_amd.hip import DeviceArray
+    from nanocompile_amd.kernels import float_bits
+    print(f"attention_index_order m={m} past={past} heads={heads}/{kv} d={d}", flush=True)
+    rng = np.random.default_rng(m + past + heads + d)
+    capacity = past + m + 3
+    qkv = rng.standard_normal((m, (heads + 2 * kv) * d)).astype(np.float32)
+    kc = rng.standard_normal((kv, capacity, d)).astype(np.float32)
+    vc = rng.standard_normal((kv, capacity, d)).astype(np.float32)
+    scale = float(np.float32(d ** -0.5))
+    q = qkv[:, :heads * d].reshape(m, heads, d)
+    want = R.attention_index_order(q, kc, vc, past, scale, lambda v: host.math("nc_exp", v)).reshape(m, heads * d)
+    dq, dk, dv = DeviceArray.from_host(qkv), DeviceArray.from_host(kc), DeviceArray.from_host(vc)
+    pos = DeviceArray.from_host(np.array([past], np.int64))
+    for where in (None, pos):
+        ctx = DeviceArray((m, heads * d), np.float32)
+        hip.call("nc_attention_index_order", [ctx, dq, dk, dv, where],
+                 [m, heads, kv, d, 0 if where is not None else past, capacity, float_bits(scale)])
+        hip.sync()
+        assert np.array_equal(bits(ctx.numpy()), bits(want)), where is not None
