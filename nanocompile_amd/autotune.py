@@ -471,14 +471,23 @@ class Candidate:
 
 
 def kernel_candidates(kernel, calls) -> list[Candidate]:
-    """The points of ``kernel``'s space that apply, the hand-written default first, one per
-    distinct generated kernel (the reference's legal_space, autotune.py:571-590)."""
+    """The points of ``kernel``'s space that apply, the default schedule first, one per distinct
+    generated kernel (the reference's legal_space, autotune.py:571-590). A candidate runs on the
+    default's arguments, so points that would read packed an operand the default reads row-major
+    are left out (the packed copy would not be there); the other way round is allowed, the
+    row-major copy of every weight being resident."""
     from nanocompile_amd import codegen_hip, gpu_schedule
-    out, seen = [], set()
-    for config in gpu_schedule.space(kernel):
+    first = gpu_schedule.default_config(kernel, calls)
+    out, seen, base = [], set(), None
+    for config in [first] + [c for c in gpu_schedule.space(kernel) if c != first]:
         try:
             scheduled, launch = gpu_schedule.apply(kernel, calls, config)
         except gpu_schedule.ScheduleError:
+            continue
+        packs = [p.packed for p in scheduled.params]
+        if base is None:
+            base = packs
+        elif any(p is not None and p != b for p, b in zip(packs, base)):
             continue
         source = codegen_hip.render_kernel(scheduled, launch, 0)
         if source in seen:

@@ -1059,17 +1059,81 @@ def apply(kernel, calls, config) -> tuple:
     return s.done()
 
 
+def _reduces_over_run_time_extent(kernel) -> bool:
+    """Whether the item runs a serial loop whose extent is set at run time (a symbol): a reduction
+    as long as the context, like attention's P.V over past + seq positions."""
+    grid = set(grid_loops(kernel))
+    for st in statements(kernel.body):
+        if kind(st) == "Loop" and st.var not in grid and any(kind(n) == "Sym" for n in walk(st.extent)):
+            return True
+    return False
+
+
+# The default schedule of each class: the first of these points that applies to the kernel. They
+# are what the tuner chose on the reference's own programs (config 5's decode step, the zoo) on
+# MI355X, most specific first, each falling back to the next where a knob has nothing to act on,
+# and last the space's base point, which applies to every kernel of its class.
+PREFERRED: dict[str, tuple] = {
+    "item": (
+        # int8 projections: the 32 accumulator chains one a lane, the weights read row-major so an
+        # item's lanes read consecutive bytes, the k loop unrolled so its loads issue ahead
+        dict(DEFAULTS["item"], threads=64, lanes=1, pack=False, unroll=16),
+        dict(DEFAULTS["item"], threads=64, lanes=1, pack=False),
+        # a reduction as long as the context (P.V): a workgroup an item, its operands staged and
+        # computed by every thread, one wave on the chain
+        ("run-time reduction", dict(DEFAULTS["item"], threads=128, workgroup=True, lead=True, hoist=True,
+                                    unroll=16)),
+        ("run-time reduction", dict(DEFAULTS["item"], threads=128, workgroup=True, lead=True)),
+        # anything else with a serial loop: unrolled, small blocks
+        dict(DEFAULTS["item"], threads=64, unroll=16),
+        DEFAULTS["item"],
+    ),
+    "row": (
+        # row kernels: one lead wave on the row's reductions, their operands computed by every
+        # thread first (hoisted), the row staged in LDS
+        dict(DEFAULTS["row"], threads=512, stage=True, lead=True, hoist=True),
+        dict(DEFAULTS["row"], threads=1024, lead=True, hoist=True, vector=4),
+        dict(DEFAULTS["row"], threads=512, lead=True, hoist=True),
+        dict(DEFAULTS["row"], threads=1024, stage=True, lead=True, vector=4),
+        dict(DEFAULTS["row"], threads=512, lead=True),
+        DEFAULTS["row"],
+    ),
+    "serial": (DEFAULTS["serial"],),
+}
+
+
+def default_config(kernel, calls=()) -> dict:
+    """The point of ``kernel``'s space that its default schedule is (``PREFERRED``)."""
+    run_time = None
+    for entry in PREFERRED[kernel_class(kernel)]:
+        if isinstance(entry, tuple):
+            if run_time is None:
+                run_time = _reduces_over_run_time_extent(kernel)
+            if not run_time:
+                continue
+            entry = entry[1]
+        try:
+            apply(kernel, calls, entry)
+        except ScheduleError:
+            continue
+        return dict(entry)
+    raise ScheduleError(f"no default applies to this {kernel_class(kernel)} kernel")
+
+
 def default(kernel, calls=()) -> tuple:
     """The library's schedule for a kernel: (scheduled kernel, Launch).
 
     Every top-level independent loop binds to the grid. An item whose body
     ends in an independent loop that stores, after statements that only
     compute (a row kernel: reductions, then the write pass), runs as one
-    workgroup per item with the write pass across its threads. Otherwise one
-    thread per item; weights read row by row by consecutive items are packed
-    in blocks of 64 rows so a wavefront's reads coalesce.
+    workgroup per item with the write pass across its threads, one wave on
+    its reductions. Otherwise an item is a thread, its int8 accumulators
+    spread over lanes where it has them, or (a reduction over the context) a
+    workgroup; weights an item reads row by row are packed in blocks of 64
+    rows, except where lanes read them row-major. ``default_config`` names the
+    point; ``DEFAULTS`` is the space's base point, which applies everywhere.
     """
-    return apply(kernel, calls, DEFAULTS[kernel_class(kernel)])
+    return apply(kernel, calls, default_config(kernel, calls))
 
 
 def schedule_program(program, fn=default):

@@ -146,17 +146,26 @@ def test_cooperate_refuses_stores_before_the_shared_loop():
         s.cooperate("j0")
 
 
-def test_default_schedule_cooperates_on_row_kernels_and_packs_matmul_weights():
+def test_default_schedule_leads_row_kernels_and_spreads_int8_chains_over_lanes():
+    """The defaults are what the tuner chose on the reference's programs: a row kernel's
+    reductions in one lead wave; an int8 projection's 32 chains one a lane over row-major
+    weights; a float matmul's weights packed; a reduction over the context (P.V) a workgroup."""
     rms = gpu_schedule.schedule_program(P.zoo("rms_norm"))
-    assert rms[0][1].cooperate == "j0"
+    assert rms[0][1].cooperate == "j0" and rms[0][1].lead
     q = P.qwen2("int8", "last")
     scheduled = gpu_schedule.schedule_program(q)
+    int8 = [(k, l) for k, l in scheduled if k.primitive.startswith("matmul_i8")]
+    assert int8 and all(l.lanes is not None and not any(p.packed for p in k.params) for k, l in int8)
     packed = [k.primitive for k, _ in scheduled if any(p.packed for p in k.params)]
-    assert packed and all(p.startswith("matmul") for p in packed)
+    assert packed and all(p == "matmul" for p in packed)
+    assert any(l.workgroup and l.lead for k, l in scheduled if k.primitive == "matmul")
     vnni = gpu_schedule.schedule_program(P.qwen2("vnni", "last"))
     for kernel, _ in vnni:                       # Dp4 reads four consecutive bytes: never packed
         if "vnni" in kernel.primitive:
             assert not any(p.packed for p in kernel.params)
+    for i, kernel in enumerate(q.kernels):       # every default is a point of its class's space
+        config = gpu_schedule.default_config(kernel, [c for c in q.calls if c.kernel == i])
+        assert config in gpu_schedule.space(kernel)
 
 
 def test_pack_refuses_operands_a_dp4_reads():
@@ -333,7 +342,9 @@ def test_space_starts_at_the_default_and_refuses_points_outside_it():
         points = gpu_schedule.space(kernel)
         assert points[0] == gpu_schedule.DEFAULTS[cls]
         assert len({gpu_schedule.canonical(p) for p in points}) == len(points)
-        assert gpu_schedule.apply(kernel, calls[i], points[0]) == gpu_schedule.default(kernel, calls[i])
+        chosen = gpu_schedule.default_config(kernel, calls[i])
+        assert chosen in points
+        assert gpu_schedule.apply(kernel, calls[i], chosen) == gpu_schedule.default(kernel, calls[i])
     row = program.kernels[0]
     assert gpu_schedule.kernel_class(row) == "row"
     with pytest.raises(gpu_schedule.ScheduleError, match="not a point"):
@@ -352,7 +363,7 @@ def test_candidate_library_holds_each_distinct_kernel_once_and_reports_failures_
     entries = [n for per in library.entry for n in per]
     assert entries == list(range(len(entries)))
     for i, cands in enumerate(library.candidates):
-        assert cands[0].config == gpu_schedule.DEFAULTS[gpu_schedule.kernel_class(program.kernels[i])]
+        assert cands[0].config == gpu_schedule.default_config(program.kernels[i], library.calls_of.get(i, []))
         assert len({c.source for c in cands}) == len(cands)
         for n in library.entry[i]:
             assert f"NC_EXPORT int32_t nc_k{n}(void **p, const int64_t *s)" in library.source
