@@ -726,14 +726,19 @@ def reference_modes(weights, prompt, seed: int, graph: bool = True) -> dict:
         tokens = model.generate(prompt, NEW_TOKENS, timer=lambda i: marks[i].record() if i in marks else None,
                                 graph=graph)
         ms = marks[0].elapsed_ms(marks[replays])
+        same = {key: (tokens == g6[key]["tokens"][:NEW_TOKENS]) if comparable else None
+                for key in (tag, f"{tag}_ncmath")}
         out[mode] = {"tok_s": round(replays / (ms * 1e-3), 2), "ms_per_step": round(ms / replays, 4),
-                     "tokens_identical_to_reference": (tokens == g6[tag]["tokens"][:NEW_TOKENS]) if comparable else None,
+                     "tokens_identical_to_reference": same[tag],
+                     "tokens_identical_to_reference_same_math": same[f"{tag}_ncmath"],
                      "reference_published_cpu_tok_s": REFERENCE_PUBLISHED_TOK_S[mode], "model_build_s": round(built, 1)}
         log(f"reference modes: {mode} {out[mode]['tok_s']} tok/s, tokens identical to the reference's run: "
-            f"{out[mode]['tokens_identical_to_reference']}")
+            f"{same[tag]} (with the C library's exp/sin/cos), {same[f'{tag}_ncmath']} (with this package's)")
         del model
     out["note"] = ("all 255 decode replays after the 128-token prompt, events on the library stream; the reference's "
-                   "published figures are its own CPU runs (README.md:718-719), a different machine and real weights")
+                   "published figures are its own CPU runs (README.md:718-719), a different machine and real weights; "
+                   "int8-vnni's tokens follow the reference's run with the same exp/sin/cos (the mode rounds its "
+                   "activations at every projection, so the C library's last-bit differences move its tokens)")
     return out
 
 
