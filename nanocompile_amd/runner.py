@@ -192,17 +192,21 @@ class HIPBackend:
         past = int(past_keys.shape[2])
         kbuf, vbuf = _owner(past_keys), _owner(past_values)
         seq = self._sequences.get(mode)
-        if seq is None or seq.cache.capacity < need:
-            # sized for the whole host buffer when it is the reference's preallocated one, and at
-            # least doubling, so a growing sequence allocates O(log length) times
+        fresh = seq is None or seq.keys_buffer is not kbuf or seq.values_buffer is not vbuf
+        # a sequence's first call sizes the device cache for the whole host buffer (the reference's
+        # preallocated one), so its later calls allocate nothing; a cache that must grow at least
+        # doubles, so a growing sequence allocates O(log length) times
+        want = max(need, _rows_of(kbuf, past_keys)) if fresh else need
+        if seq is None or seq.cache.capacity < want:
             old = seq.cache.capacity if seq is not None else 0
-            capacity = min(max(need, _rows_of(kbuf, past_keys), 2 * old), MAX_CACHE_ROWS)
+            capacity = min(max(want, 2 * old if old < need else 0), MAX_CACHE_ROWS)
             if capacity < need:
                 raise ValueError(f"{need} tokens exceed the device cache's limit of {MAX_CACHE_ROWS}")
             seq = _Sequence(model.new_cache(capacity))
             self._sequences[mode] = seq
-        if seq.keys_buffer is not kbuf or seq.values_buffer is not vbuf:
-            seq.keys_buffer, seq.values_buffer, seq.held = kbuf, vbuf, 0     # another sequence: nothing held
+            fresh = True                       # a new device cache holds nothing yet
+        if fresh:
+            seq.keys_buffer, seq.values_buffer, seq.held = kbuf, vbuf, 0
         seq.held = min(seq.held, past)         # a shorter view: the rows past it are not the caller's now
         if seq.held < past:
             _upload_rows(seq.cache.keys, past_keys, seq.held, past)

@@ -133,3 +133,66 @@ def test_token_activations_are_an_opt_in_for_the_int8_graphs():
     assert [token.model_quantization(m) for m in ("int8", "int8-vnni", "f32")] == ["int8-token", "int8-token", "f32"]
     with pytest.raises(ValueError, match="activations"):
         HIPBackend(TINY, activations="int4")
+
+
+def test_device_cache_bookkeeping_allocates_once_a_sequence_and_uploads_only_missing_rows(monkeypatch):
+    """The Runner's device cache, with the device calls replaced by records: a sequence's first
+    call sizes the cache for the host buffer and uploads its filled rows; the calls after it
+    allocate nothing and upload nothing the device produced; a new buffer uploads its rows once
+    (reusing a cache that is large enough); growth doubles and uploads the rows again; a
+    rewound view uploads only rows past what the device still holds."""
+    import numpy as np
+
+    from nanocompile_amd import runner
+    from nanocompile_amd.models.config import TINY
+    made, uploads = [], []
+
+    class FakeCache:
+        def __init__(self, capacity):
+            self.capacity, self.length, self.keys, self.values = capacity, 0, "k", "v"
+
+    class FakeModel:
+        def new_cache(self, capacity):
+            made.append(capacity)
+            return FakeCache(capacity)
+
+    monkeypatch.setattr(runner, "_upload_rows", lambda device, host, start, stop: uploads.append((device, start, stop)))
+    backend = runner.HIPBackend(TINY)
+    model = FakeModel()
+    shape = (TINY.num_hidden_layers, TINY.num_key_value_heads)
+
+    def buffer(capacity):
+        return np.zeros(shape + (capacity, TINY.head_dim), np.float32), np.zeros(shape + (capacity, TINY.head_dim),
+                                                                               np.float32)
+
+    def call(kb, vb, past, m):
+        seq = backend._cache_for("int8", model, kb[:, :, :past], vb[:, :, :past], past + m)
+        seq.held = past + m                    # what run() records after the forward
+        return seq
+
+    kb, vb = buffer(19)
+    call(kb, vb, 0, 11)
+    assert made == [19] and uploads == []
+    for past in range(11, 18):
+        call(kb, vb, past, 1)
+    assert made == [19] and uploads == []
+    k2, v2 = buffer(10)                         # another sequence: the cache is large enough
+    call(k2, v2, 4, 1)
+    assert made == [19] and uploads == [("k", 0, 4), ("v", 0, 4)]
+    uploads.clear()
+    k3, v3 = buffer(40)                         # a larger buffer: sized for it at once
+    call(k3, v3, 30, 1)
+    assert made == [19, 40] and uploads == [("k", 0, 30), ("v", 0, 30)]
+    uploads.clear()
+    k4 = np.zeros(shape + (45, TINY.head_dim), np.float32)   # a view of a fresh array each call: grows
+    call(k4, k4.copy(), 44, 1)
+    assert made[-1] == 80 and uploads == [("k", 0, 44), ("v", 0, 44)]
+    uploads.clear()
+    kb, vb = buffer(100)
+    call(kb, vb, 0, 20)
+    assert made[-1] == 100
+    uploads.clear()
+    call(kb, vb, 10, 1)                         # rewound to 10: the device still holds 0 .. 9
+    assert uploads == []
+    call(kb, vb, 15, 1)                         # the caller appended 11 .. 14 itself
+    assert uploads == [("k", 11, 15), ("v", 11, 15)]
