@@ -478,6 +478,7 @@ class Qwen2:
         m = int(ids.size)
         if m > self.max_tokens:
             raise ValueError(f"{m} tokens in one forward; this model was made for at most {self.max_tokens}")
+        held = cache is not None
         if cache is None:
             cache = self.new_cache(m)
         past = cache.length
@@ -485,6 +486,16 @@ class Qwen2:
             raise ValueError(f"the cache holds {cache.capacity} tokens; {past} + {m} do not fit")
         c = self.config
         H, V = c.hidden_size, c.vocab_size
+        if m == 1 and held:
+            # one token into a caller's cache: the step replayed from a graph captured for this
+            # cache, the position read on the device (the same kernels, the same bits as
+            # launching them one by one)
+            self.ids.view((1,)).upload(ids)
+            cache.position.upload(np.array([past], np.int64))
+            self._step_graph(cache).launch()
+            hip.sync()
+            cache.length = past + 1
+            return self.logits_row.numpy()[:1]
         self.ids.view((m,)).upload(ids)
         hip.call("nc_embed", [self.x, self.embed, self.ids], [m, H, V])
         self._layers(m, past, cache)
@@ -497,6 +508,31 @@ class Qwen2:
         hip.sync()
         cache.length = past + m
         return logits.numpy()[:rows]
+
+    def _step_graph(self, cache: KVCache):
+        """A one-token forward for ``cache`` captured as a HIP graph: the embedding of ``ids``, every
+        layer at the position ``cache.position`` holds, the final rms_norm and the LM head's logits
+        row. Made on a cache's first one-token call and kept, with a reference to the cache, for
+        the latest cache only (a caller's sequence of steps replays it; switching between caches
+        captures again); any tuning happens before the capture."""
+        held = getattr(self, "_held_step", None)
+        if held is not None and held[0] is cache:
+            return held[1]
+        c = self.config
+        H, V = c.hidden_size, c.vocab_size
+        self._projection_schedules(1)
+        self.decode_schedules()
+        hip.sync()
+
+        def step() -> None:
+            hip.call("nc_embed", [self.x, self.embed, self.ids], [1, H, V])
+            self._layers(1, 0, cache, pos=cache.position)
+            self._final_norm(self.x.ptr, 1)
+            hip.call("nc_lm_head", [self.logits_row, None, self.normed, self.head], [1, V, H])
+
+        graph = hip.Graph.capture(step)
+        self._held_step = (cache, graph)
+        return graph
 
     def next_token(self, token_ids, cache: KVCache) -> int:
         """Greedy's step on the device: forward the new tokens, return the argmax of the last row."""
