@@ -922,14 +922,15 @@ def shared_loop(kernel, names) -> str | None:
 # Each class's knobs and their values; the first value of each is the hand-written default's.
 SPACES: dict[str, dict[str, tuple]] = {
     # a workgroup per item sharing its write pass: its size, its serial loops' operands staged in
-    # LDS, iterations of the shared loop per thread, the serial loops' unroll, one lead wave on
-    # the serial part, its reductions' operands computed by every thread first
+    # LDS, iterations of the shared loop per thread, the serial loops' unroll (64: their operands
+    # read in batches of 64 iterations ahead of the chain), one lead wave on the serial part, its
+    # reductions' operands computed by every thread first
     "row": {"threads": (256, 64, 128, 512, 1024), "stage": (False, True), "vector": (1, 2, 4),
-            "unroll": (0, 4), "lead": (False, True), "hoist": (False, True)},
+            "unroll": (0, 4, 64), "lead": (False, True), "hoist": (False, True)},
     # a thread per item, or (workgroup) a workgroup per item with its loops' operands staged (a
     # lead wave, hoisting, as for rows), or (lanes) an item's accumulator chains 1 or 4 elements
     # a lane; weights packed in 64-row blocks or read row-major; serial loops unrolled up to 32
-    # steps (a lane's chain then issues that many steps' loads before its multiply-adds need them)
+    # steps (a chain then reads that many steps' operands, in a batch, before its multiply-adds)
     "item": {"threads": (256, 64, 128, 512, 1024), "vector": (1, 2, 4), "workgroup": (False, True),
              "unroll": (0, 4, 16, 32), "lead": (False, True), "hoist": (False, True), "lanes": (0, 1, 4),
              "pack": (True, False)},

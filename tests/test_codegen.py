@@ -388,7 +388,9 @@ def test_vectorized_items_are_unrolled_without_checks_only_when_whole():
     text = codegen_hip.render_kernel(row, rl, 0)
     assert "extern __shared__" in text and text.count("__syncthreads();") == 2      # after the copy, after the item
     assert "nc_g0_unstaged" in text and f"if (nc_lds > {gpu_schedule.MAX_STAGE_BYTES})" in text
-    assert "#pragma unroll 4" in text
+    # the serial loop, unrolled by 4: batches of 4 staged values read ahead of the sum's chain
+    assert "for (int64_t nc_base = 0; nc_base < 896; nc_base += 4) {" in text
+    assert "nc_pf1_0[nc_u] = nc_s1[r];" in text and "float t1 = (nc_pf1_0[nc_u] * nc_pf1_0[nc_u]);" in text
 
 
 def test_lead_shares_the_serial_parts_values_and_refuses_a_failing_serial_part():
@@ -582,7 +584,12 @@ def test_hoist_computes_the_chains_operands_first_and_refuses_what_depends_on_th
                                                                hoist=True))
     assert [h.name for h in launch.hoist] == ["nc_h0", "nc_h1"]             # the max, then the sum of exps
     text = codegen_hip.render_kernel(scheduled, launch, 0)
-    assert "nc_h1[r] = t" in text and "acc1 = (acc1 + nc_h1[r]);" in text
+    assert "nc_h1[r] = t" in text
+    # the lead wave's chain over the stored values: read in batches ahead of it, then in order
+    import re
+    batch = re.search(r"(nc_pf\d+_0)\[nc_u\] = nc_h1\[r\];", text)
+    assert batch and f"acc1 = (acc1 + {batch.group(1)}[nc_u]);" in text
+    assert text.index(batch.group(0)) < text.index(f"acc1 = (acc1 + {batch.group(1)}[nc_u]);")
     assert "nc_g0_unstaged" in text                                    # the fallback when LDS is short
     with pytest.raises(gpu_schedule.ScheduleError, match="lead"):
         gpu_schedule.GpuSchedule(row).grid("i0", "i1").cooperate("j0").hoist()
@@ -606,11 +613,13 @@ def test_hoist_computes_the_chains_operands_first_and_refuses_what_depends_on_th
             gpu_schedule.GpuSchedule(bad).grid("i0").workgroup().lead().hoist()
 
 
-def test_unroll_reaches_the_loop_around_lane_held_chains_but_not_register_array_stores():
+def test_unroll_batches_the_loop_around_lane_held_chains_but_not_register_array_stores():
     """With an item's accumulators held across lanes, its k loop updates one register a lane and
-    may be unrolled (its loads then issue ahead of the chain); the tree after it, which stores
-    into a register array, is never given a partial unroll hint (it would move the array to
-    memory). Config 5's down projection, as the reference compiles it."""
+    may be unrolled: it runs in batches of the unroll factor, each batch loading its iterations'
+    weight bytes and activations into register arrays before its multiply-adds (152 = 9 x 16 + 8:
+    nine batches of 16, then one of 8), so a chain has 16 iterations' loads in flight. The tree
+    after it, which stores into a register array, is never given a partial unroll hint (it would
+    move the array to memory). Config 5's down projection, as the reference compiles it."""
     prog = P.config5()[0]
     kernel = prog.kernels[14]
     assert kernel.primitive == "matmul_i8+epilogue" and gpu_schedule.kernel_class(kernel) == "item"
@@ -620,9 +629,14 @@ def test_unroll_reaches_the_loop_around_lane_held_chains_but_not_register_array_
     # one loop: the k loop (the tree's loop over the register array h stays without a hint)
     assert launch.lanes is not None and len(unrolled) == 1 and set(unrolled.values()) == {16}
     source = codegen_hip.render_kernel(sched, launch, 0, None)
-    for var in unrolled:
-        loop_at = source.index(f"for (int64_t {var} = 0;")
-        assert source.rfind("#pragma unroll 16", 0, loop_at) > source.rfind("\n", 0, loop_at) - 80
+    assert "#pragma unroll 16" not in source
+    assert "for (int64_t nc_base = 0; nc_base < 144; nc_base += 16) {" in source
+    assert "int8_t nc_pf1_0[16];" in source and "float nc_pf1_1[16];" in source
+    assert "int8_t nc_pf1_0[8];" in source and "const int64_t k0 = 144 + nc_u;" in source
+    # in each batch every load comes before the first multiply-add, which reads the arrays
+    first = source.index("nc_pf1_0[nc_u] = x1[")
+    assert first < source.index("nc_pf1_1[nc_u] = x2[") < source.index("acc_0_l = __builtin_fmaf(((float)(nc_pf1_0[nc_u]))")
+    assert source.count("= x1[") == 2 and source.count("= x2[") == 2      # the batches' and the tail's
     # without lanes the same loop indexes the accumulator array: nothing to unroll
     with pytest.raises(gpu_schedule.ScheduleError):
         gpu_schedule.apply(kernel, (), dict(gpu_schedule.DEFAULTS["item"], threads=128, unroll=16, pack=False))
