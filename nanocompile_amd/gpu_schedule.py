@@ -1090,6 +1090,10 @@ PREFERRED: dict[str, tuple] = {
         DEFAULTS["item"],
     ),
     "row": (
+        # a reduction of fixed length (rms_norm's sum of squares over the hidden size): one lead
+        # wave on it, its operands computed by every thread first (hoisted) and read back in
+        # batches of 64 ahead of the chain
+        ("fixed-length reduction", dict(DEFAULTS["row"], threads=512, vector=4, unroll=64, lead=True, hoist=True)),
         # row kernels: one lead wave on the row's reductions, their operands computed by every
         # thread first (hoisted), the row staged in LDS
         dict(DEFAULTS["row"], threads=512, stage=True, lead=True, hoist=True),
@@ -1110,7 +1114,7 @@ def default_config(kernel, calls=()) -> dict:
         if isinstance(entry, tuple):
             if run_time is None:
                 run_time = _reduces_over_run_time_extent(kernel)
-            if not run_time:
+            if run_time != (entry[0] == "run-time reduction"):
                 continue
             entry = entry[1]
         try:

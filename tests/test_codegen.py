@@ -584,13 +584,19 @@ def test_hoist_computes_the_chains_operands_first_and_refuses_what_depends_on_th
                                                                hoist=True))
     assert [h.name for h in launch.hoist] == ["nc_h0", "nc_h1"]             # the max, then the sum of exps
     text = codegen_hip.render_kernel(scheduled, launch, 0)
-    assert "nc_h1[r] = t" in text
-    # the lead wave's chain over the stored values: read in batches ahead of it, then in order
+    assert "nc_h1[r] = t" in text and "acc1 = (acc1 + nc_h1[r]);" in text
+    assert "nc_g0_unstaged" in text                                    # the fallback when LDS is short
+    # unrolled by 64, the lead wave's chain over the stored values reads them in batches ahead of
+    # it (the context's length set at run time: whole batches, then one whose reads repeat the
+    # last position and whose steps stop at the length)
     import re
+    scheduled, launch = gpu_schedule.apply(row, calls[0], dict(gpu_schedule.DEFAULTS["row"], stage=True, lead=True,
+                                                               hoist=True, unroll=64))
+    text = codegen_hip.render_kernel(scheduled, launch, 0)
     batch = re.search(r"(nc_pf\d+_0)\[nc_u\] = nc_h1\[r\];", text)
     assert batch and f"acc1 = (acc1 + {batch.group(1)}[nc_u]);" in text
     assert text.index(batch.group(0)) < text.index(f"acc1 = (acc1 + {batch.group(1)}[nc_u]);")
-    assert "nc_g0_unstaged" in text                                    # the fallback when LDS is short
+    assert re.search(r"const int64_t r = nc_last \+ nc_u < (nc_n\d+) \? nc_last \+ nc_u : \1 - 1;", text)
     with pytest.raises(gpu_schedule.ScheduleError, match="lead"):
         gpu_schedule.GpuSchedule(row).grid("i0", "i1").cooperate("j0").hoist()
     f32 = lir.DType("f32")
