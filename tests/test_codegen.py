@@ -619,6 +619,73 @@ def test_hoist_computes_the_chains_operands_first_and_refuses_what_depends_on_th
             gpu_schedule.GpuSchedule(bad).grid("i0").workgroup().lead().hoist()
 
 
+def _nan_max_step(a, b):
+    """One step of the reference's NaN-propagating maximum, as C evaluates it on float32."""
+    return b if (a < b or b != b) else a
+
+
+def _ordered_tree(values, threads: int, wave: int):
+    """The grouping the generated ordered tree uses: each of ``threads`` threads folds a
+    contiguous run in order from -inf, lanes of a ``wave``-wide wave combine by xor butterfly
+    with the lower lanes' block on the left, then the waves' results are folded in wave order."""
+    ninf = np.float32(-np.inf)
+    run = -(-len(values) // threads) if values else 0
+    m = []
+    for t in range(threads):
+        acc = ninf
+        for v in values[t * run:min((t + 1) * run, len(values))]:
+            acc = _nan_max_step(acc, v)
+        m.append(acc)
+    off = 1
+    while off < wave:
+        m = [_nan_max_step(m[i], m[i ^ off]) if (i & off) == 0 else _nan_max_step(m[i ^ off], m[i])
+             for i in range(threads)]
+        off <<= 1
+    total = m[0]
+    for w in range(1, threads // wave):
+        total = _nan_max_step(total, m[w * wave])
+    return total
+
+
+def test_ordered_max_tree_is_the_serial_chain_bit_for_bit():
+    """The NaN-propagating maximum's chain and the ordered tree codegen renders for it agree bit
+    for bit on sequences built to separate them: NaNs of different payloads and signs (the chain
+    keeps the last), +0 against -0 and equal values (the chain keeps the first), infinities,
+    any length, any thread and wave count. A grouping that swapped a pair's sides, or dropped
+    the accumulator's step, fails here."""
+    bits_of = lambda x: np.float32(x).view(np.uint32)
+    pool = [np.uint32(u).view(np.float32) for u in (0x7FC00000, 0x7FC00001, 0xFFC00002, 0x7F800001)]
+    pool += [np.float32(v) for v in (0.0, -0.0, np.inf, -np.inf, 1.0, 1.0, 2.0, -3.5, 7.0, 7.0, -0.0)]
+    rng = np.random.default_rng(5)
+    for trial in range(3000):
+        n = int(rng.integers(0, 40))
+        values = [pool[int(i)] for i in rng.integers(0, len(pool), n)]
+        init = pool[int(rng.integers(0, len(pool)))] if trial % 3 else np.float32(-np.inf)
+        serial = init
+        for v in values:
+            serial = _nan_max_step(serial, v)
+        for threads, wave in ((1, 1), (4, 2), (8, 4), (16, 4), (64, 8), (16, 16)):
+            tree = _nan_max_step(init, _ordered_tree(values, threads, wave))
+            assert bits_of(tree) == bits_of(serial), (values, init, threads, wave)
+    # what the test would catch: a butterfly with its operands' sides swapped
+    a, b = pool[0], pool[1]                                          # two NaNs: the chain keeps the last
+    assert bits_of(_nan_max_step(a, b)) != bits_of(_nan_max_step(b, a))
+    zero, negzero = np.float32(0.0), np.float32(-0.0)                # a tie: the chain keeps the first
+    assert bits_of(_nan_max_step(zero, negzero)) != bits_of(_nan_max_step(negzero, zero))
+
+
+def test_hoisted_nan_max_chain_renders_as_an_ordered_tree():
+    program = P.zoo("softmax_mask")
+    calls = _calls_of(program)
+    scheduled, launch = gpu_schedule.apply(program.kernels[0], calls[0],
+                                           dict(gpu_schedule.DEFAULTS["row"], stage=True, lead=True, hoist=True))
+    text = codegen_hip.render_kernel(scheduled, launch, 0)
+    # the maximum (nc_h0) as a tree over every thread; the sum of exps (nc_h1) stays the lead's chain
+    assert "__shfl_xor(nc_m, nc_off, 64)" in text and "nc_h0_waves[threadIdx.x >> 6] = nc_m;" in text
+    assert "acc0 = ((acc0 < nc_m) || (nc_m != nc_m)) ? nc_m : acc0;" in text
+    assert "acc1 = (acc1 + nc_h1[r]);" in text
+
+
 def test_unroll_batches_the_loop_around_lane_held_chains_but_not_register_array_stores():
     """With an item's accumulators held across lanes, its k loop updates one register a lane and
     may be unrolled: it runs in batches of the unroll factor, each batch loading its iterations'
