@@ -674,6 +674,23 @@ def test_ordered_max_tree_is_the_serial_chain_bit_for_bit():
     assert bits_of(_nan_max_step(zero, negzero)) != bits_of(_nan_max_step(negzero, zero))
 
 
+def test_batches_never_read_what_the_statement_would_skip():
+    """A batch reads every iteration's operands before running the iterations, so a read under
+    one arm of ?: (P.V's products, which read the past cache or the new rows by position: the
+    other arm's index is out of its array there) must keep its loop unbatched; a chain whose
+    reads are all unconditional (the norm's sum of squares) is batched."""
+    prog = P.config5()[0]
+    calls = _calls_of(prog)
+    pv = prog.kernels[11]
+    config = dict(gpu_schedule.default_config(pv, calls[11]), hoist=False, unroll=16)
+    text = codegen_hip.render_kernel(*gpu_schedule.apply(pv, calls[11], config), 11)
+    assert "? x2[" in text and "nc_pf" not in text
+    norm = prog.kernels[1]
+    config = dict(gpu_schedule.DEFAULTS["row"], threads=512, stage=True, unroll=64, lead=True)
+    text = codegen_hip.render_kernel(*gpu_schedule.apply(norm, calls[1], config), 1)
+    assert "nc_pf1_0[nc_u] = nc_s1[r];" in text
+
+
 def test_hoisted_nan_max_chain_renders_as_an_ordered_tree():
     program = P.zoo("softmax_mask")
     calls = _calls_of(program)
