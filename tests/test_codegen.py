@@ -675,20 +675,34 @@ def test_ordered_max_tree_is_the_serial_chain_bit_for_bit():
 
 
 def test_batches_never_read_what_the_statement_would_skip():
-    """A batch reads every iteration's operands before running the iterations, so a read under
-    one arm of ?: (P.V's products, which read the past cache or the new rows by position: the
-    other arm's index is out of its array there) must keep its loop unbatched; a chain whose
-    reads are all unconditional (the norm's sum of squares) is batched."""
+    """A batch reads its iterations' operands before running them, so a read under one arm of ?:
+    is read ahead only as the whole ?: (evaluated as C does: the arm the statement would take;
+    P.V's products read the past cache or the new rows by position, the other arm's index out
+    of its array), and not at all when the condition depends on the iteration's own values."""
     prog = P.config5()[0]
     calls = _calls_of(prog)
     pv = prog.kernels[11]
     config = dict(gpu_schedule.default_config(pv, calls[11]), hoist=False, unroll=16)
     text = codegen_hip.render_kernel(*gpu_schedule.apply(pv, calls[11], config), 11)
-    assert "? x2[" in text and "nc_pf" not in text
+    assert "nc_pf1_1[nc_u] = ((k < s1) ? x2[" in text
+    assert "= x3[" not in text and "= x2[" not in text            # never read outside its ?:
     norm = prog.kernels[1]
     config = dict(gpu_schedule.DEFAULTS["row"], threads=512, stage=True, unroll=64, lead=True)
     text = codegen_hip.render_kernel(*gpu_schedule.apply(norm, calls[1], config), 1)
     assert "nc_pf1_0[nc_u] = nc_s1[r];" in text
+    # the units of a statement, directly: a condition on the loop index takes the ?: whole; one on
+    # the accumulator cannot be read ahead
+    f32, i64 = lir.DType("f32"), lir.DType("i64")
+    acc, r = lir.Var("acc", f32), lir.Var("r", i64)
+    pick = lambda cond: lir.Select(cond, lir.Load(1, r, f32), lir.Load(2, b("sub", r, c(8)), f32), f32)
+    by_index = pick(lir.Binary("lt", r, c(8), lir.DType("bool")))
+    units: list = []
+    st = lir.Assign("acc", lir.Binary("add", acc, by_index, f32))
+    assert codegen_hip._prefetch_units(st, frozenset({"acc"}), frozenset(), {1, 2}, set(), units)
+    assert units == [by_index]
+    by_chain = pick(lir.Binary("lt", acc, lir.Const(0.0, f32), lir.DType("bool")))
+    st = lir.Assign("acc", lir.Binary("add", acc, by_chain, f32))
+    assert not codegen_hip._prefetch_units(st, frozenset({"acc"}), frozenset(), {1, 2}, set(), [])
 
 
 def test_hoisted_nan_max_chain_renders_as_an_ordered_tree():
