@@ -1093,7 +1093,7 @@ PREFERRED: dict[str, tuple] = {
         # a reduction of fixed length (rms_norm's sum of squares over the hidden size): one lead
         # wave on it, its operands computed by every thread first (hoisted) and read back in
         # batches of 64 ahead of the chain
-        ("fixed-length reduction", dict(DEFAULTS["row"], threads=1024, unroll=64, lead=True, hoist=True)),
+        ("fixed-length reduction", dict(DEFAULTS["row"], threads=512, vector=4, unroll=64, lead=True, hoist=True)),
         # row kernels: one lead wave on the row's reductions, their operands computed by every
         # thread first (hoisted), the row staged in LDS
         dict(DEFAULTS["row"], threads=512, stage=True, lead=True, hoist=True),
