@@ -294,8 +294,9 @@ class RopeProblem:
         return np.concatenate([bits, self.kc.numpy().view(np.uint32).ravel(), self.vc.numpy().view(np.uint32).ravel()])
 
 
-def measure(problem: Problem, schedules: list[int], rounds: int, reps: int) -> list[float]:
-    """Median seconds per call of each schedule, the candidates alternating round by round."""
+def measure(problem: Problem, schedules: list[int], rounds: int, reps: int, progress=None) -> list[float]:
+    """Median seconds per call of each schedule, the candidates alternating round by round
+    (``progress()``, when given, after each sample)."""
     graphs = {}
     for s in schedules:
         graphs[s] = Graph.capture(lambda s=s: [problem.launch(s, i) for i in range(reps)])
@@ -311,6 +312,8 @@ def measure(problem: Problem, schedules: list[int], rounds: int, reps: int) -> l
             stop.record()
             hip.sync()
             samples[s].append(start.elapsed_ms(stop) * 1e-3 / reps)
+            if progress is not None:
+                progress()
     return [statistics.median(samples[s]) for s in schedules]
 
 
@@ -824,7 +827,8 @@ class Autotuner:
         for i in todo:
             began = time.perf_counter()
             cands = library.candidates[i]
-            cost = self._cost([(workload.timer(i), weight) for workload, weight in workloads])
+            progress = self._progress(i, len(cands)) if self.verbose else None
+            cost = self._cost([(workload.timer(i), weight) for workload, weight in workloads], progress)
             winner, trail, before, after = choose(list(range(len(cands))), cost, self.margin)
             chosen[i] = winner
             record = self._log(TuneRecord(keys[i], library.program.kernels[i].primitive, (i,), len(cands), winner,
@@ -841,6 +845,19 @@ class Autotuner:
                   flush=True)
         return library, chosen
 
+    @staticmethod
+    def _progress(kernel: int, total: int, every: int = 16):
+        """A ``measure`` progress callback that prints a line after every ``every`` samples (a
+        kernel whose candidates run for milliseconds each takes minutes to tune)."""
+        done = [0]
+
+        def sampled() -> None:
+            done[0] += 1
+            if done[0] % every == 0:
+                print(f"tuning kernel {kernel}: {done[0]} samples taken ({total} schedules)", file=sys.stderr,
+                      flush=True)
+        return sampled
+
     # -- shared steps ----------------------------------------------------------------------------
 
     def _log(self, record: TuneRecord) -> TuneRecord:
@@ -855,7 +872,7 @@ class Autotuner:
         if self.cache is not None:
             self.cache.put(machine, key, entry)
 
-    def _cost(self, timers):
+    def _cost(self, timers, progress=None):
         """``choose``'s cost function over ``timers`` [(timer, weight)]: each candidate's
         seconds per call under every timer, weighted and added (a generated kernel's decode
         and prefill workloads), over the stage's share of the tuner's rounds."""
@@ -863,7 +880,7 @@ class Autotuner:
             rounds = self.rounds * ROUNDS_FACTOR[stage]
             total = np.zeros(len(candidates))
             for timer, weight in timers:
-                total += weight * np.asarray(measure(timer, candidates, rounds, self.reps))
+                total += weight * np.asarray(measure(timer, candidates, rounds, self.reps, progress))
             return [float(x) for x in total]
         return cost
 
