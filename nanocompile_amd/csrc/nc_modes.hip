@@ -40,6 +40,10 @@ __device__ __forceinline__ int8_t byte_of(const i8x16 &v, int i) {
 }
 
 // y[m, n] = tree(acc) (+ tail) * scales[n], float activations x[m, :] staged in LDS.
+// QUADS > 0: K = 128 QUADS (the model's widths), a lane's whole packed row loaded before its
+// chains run (one memory round trip, where the run-time loop waits on each quad's load in
+// turn); 0: any K. The chains' order is the same either way.
+template <int QUADS>
 __global__ __launch_bounds__(64) void matmul_i8_f32(float *__restrict__ y, const float *__restrict__ x,
                                                     const int8_t *__restrict__ packed, const int8_t *__restrict__ q,
                                                     const float *__restrict__ scales, const float *__restrict__ bias,
@@ -52,18 +56,34 @@ __global__ __launch_bounds__(64) void matmul_i8_f32(float *__restrict__ y, const
     const int n = blockIdx.x * 8 + lane / 8;
     const bool valid = n < N;
     const int nr = valid ? n : 0;
-    const int blocks = K / 32, quads = (blocks + 3) / 4;
+    const int blocks = K / 32, quads = QUADS > 0 ? QUADS : (blocks + 3) / 4;
     const int8_t *prow = packed + (size_t)nr * quads * 128 + l * 16;
     float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int j = 0; j < quads; ++j) {
-        const i8x16 w = nc::load16(prow + (size_t)j * 128);
+    if constexpr (QUADS > 0) {
+        i8x16 w[QUADS];
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            const int k0 = 4 * j + kk;
-            if (k0 < blocks) {
+        for (int j = 0; j < QUADS; ++j) w[j] = nc::load16(prow + (size_t)j * 128);
+#pragma unroll
+        for (int j = 0; j < QUADS; ++j) {
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const int k0 = 4 * j + kk;
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
-                    a[c] = __builtin_fmaf((float)byte_of(w, kk * 4 + c), sx[32 * k0 + 8 * c + l], a[c]);
+                    a[c] = __builtin_fmaf((float)byte_of(w[j], kk * 4 + c), sx[32 * k0 + 8 * c + l], a[c]);
+            }
+        }
+    } else {
+        for (int j = 0; j < quads; ++j) {
+            const i8x16 w = nc::load16(prow + (size_t)j * 128);
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const int k0 = 4 * j + kk;
+                if (k0 < blocks) {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        a[c] = __builtin_fmaf((float)byte_of(w, kk * 4 + c), sx[32 * k0 + 8 * c + l], a[c]);
+                }
             }
         }
     }
@@ -89,6 +109,9 @@ __device__ __forceinline__ int32_t dp4_offset(int32_t w, int32_t x) {
     return nc::dot4(w, x, 0) + 128 * nc::dot4(x, 0x01010101, 0);
 }
 
+// STRIDES > 0: K = 128 STRIDES, a lane's whole packed row loaded before its chains (as
+// matmul_i8_f32); 0: any K.
+template <int STRIDES>
 __global__ __launch_bounds__(64) void matmul_i8_vnni(float *__restrict__ y, const int8_t *__restrict__ xq,
                                                      const float *__restrict__ xs, const float *__restrict__ offset,
                                                      const int8_t *__restrict__ packed, const int8_t *__restrict__ q,
@@ -106,16 +129,31 @@ __global__ __launch_bounds__(64) void matmul_i8_vnni(float *__restrict__ y, cons
     const int n = blockIdx.x * 8 + lane / 8;
     const bool valid = n < N;
     const int nr = valid ? n : 0;
-    const int strides = K / 128;
+    const int strides = STRIDES > 0 ? STRIDES : K / 128;
     const int8_t *prow = packed + (size_t)nr * strides * 128 + l * 16;
     float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int k0 = 0; k0 < strides; ++k0) {
-        const i8x16 w = nc::load16(prow + (size_t)k0 * 128);
+    if constexpr (STRIDES > 0) {
+        i8x16 w[STRIDES];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int g = 128 * k0 + 32 * c;
-            const int32_t xd = *reinterpret_cast<const int32_t *>(sxq + g + 4 * l);
-            a[c] = __builtin_fmaf((float)dp4_offset(w.w[c], xd), sxs[g / block], a[c]);
+        for (int k0 = 0; k0 < STRIDES; ++k0) w[k0] = nc::load16(prow + (size_t)k0 * 128);
+#pragma unroll
+        for (int k0 = 0; k0 < STRIDES; ++k0) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int g = 128 * k0 + 32 * c;
+                const int32_t xd = *reinterpret_cast<const int32_t *>(sxq + g + 4 * l);
+                a[c] = __builtin_fmaf((float)dp4_offset(w[k0].w[c], xd), sxs[g / block], a[c]);
+            }
+        }
+    } else {
+        for (int k0 = 0; k0 < strides; ++k0) {
+            const i8x16 w = nc::load16(prow + (size_t)k0 * 128);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int g = 128 * k0 + 32 * c;
+                const int32_t xd = *reinterpret_cast<const int32_t *>(sxq + g + 4 * l);
+                a[c] = __builtin_fmaf((float)dp4_offset(w.w[c], xd), sxs[g / block], a[c]);
+            }
         }
     }
     const int groups = (K % 128) / 32;
@@ -171,6 +209,10 @@ __global__ __launch_bounds__(256) void quantize_blocks(int8_t *__restrict__ xq, 
 // sum of squares in index order, one multiply and one add a step from 0, then
 // (x * (1 / sqrt(ss / K + eps))) * gamma. The row is staged in LDS and the one
 // chain runs in lane 0; every thread then writes its share of the row.
+// A serial chain over LDS (one thread's sum in index order) reads this many values ahead of its
+// steps, so it waits on LDS once a batch rather than once a step.
+constexpr int kChainBatch = 64;
+
 __global__ __launch_bounds__(256) void rms_norm_index_order(float *__restrict__ normed, const float *__restrict__ x,
                                                             const float *__restrict__ gamma, int K, float eps) {
     extern __shared__ float srow[];
@@ -180,7 +222,15 @@ __global__ __launch_bounds__(256) void rms_norm_index_order(float *__restrict__ 
     __syncthreads();
     if (threadIdx.x == 0) {
         float ss = 0.0f;
-        for (int k = 0; k < K; ++k) ss = __fadd_rn(ss, __fmul_rn(srow[k], srow[k]));
+        int k = 0;
+        for (; k + kChainBatch <= K; k += kChainBatch) {       // a batch's reads ahead of its steps
+            float v[kChainBatch];
+#pragma unroll
+            for (int u = 0; u < kChainBatch; ++u) v[u] = srow[k + u];
+#pragma unroll
+            for (int u = 0; u < kChainBatch; ++u) ss = __fadd_rn(ss, __fmul_rn(v[u], v[u]));
+        }
+        for (; k < K; ++k) ss = __fadd_rn(ss, __fmul_rn(srow[k], srow[k]));
         rcp_shared = nc::div_rn(1.0f, nc::sqrt_rn(__fadd_rn(nc::div_rn(ss, (float)K), eps)));
     }
     __syncthreads();
@@ -231,7 +281,15 @@ __global__ __launch_bounds__(256) void attention_index_order(float *__restrict__
     for (int t = threadIdx.x; t < T; t += blockDim.x) {
         const float *kt = kh + (size_t)t * D;
         float acc = 0.0f;
-        for (int d = 0; d < D; ++d) acc = __fadd_rn(acc, __fmul_rn(sq[d], kt[d]));
+        int d = 0;
+        for (; d + 16 <= D; d += 16) {                        // the key's values ahead of the chain
+            float kv[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) kv[u] = kt[d + u];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) acc = __fadd_rn(acc, __fmul_rn(sq[d + u], kv[u]));
+        }
+        for (; d < D; ++d) acc = __fadd_rn(acc, __fmul_rn(sq[d], kt[d]));
         const float z = __fadd_rn(__fmul_rn(acc, scale), 0.0f);
         sp[t] = z;
         mx = nc::nan_max(mx, z);
@@ -246,7 +304,15 @@ __global__ __launch_bounds__(256) void attention_index_order(float *__restrict__
     __syncthreads();
     if (threadIdx.x == 0) {
         float total = 0.0f;
-        for (int t = 0; t < T; ++t) total = __fadd_rn(total, sp[t]);
+        int t = 0;
+        for (; t + kChainBatch <= T; t += kChainBatch) {
+            float e[kChainBatch];
+#pragma unroll
+            for (int u = 0; u < kChainBatch; ++u) e[u] = sp[t + u];
+#pragma unroll
+            for (int u = 0; u < kChainBatch; ++u) total = __fadd_rn(total, e[u]);
+        }
+        for (; t < T; ++t) total = __fadd_rn(total, sp[t]);
         shared_sum = total;
     }
     __syncthreads();
@@ -255,7 +321,18 @@ __global__ __launch_bounds__(256) void attention_index_order(float *__restrict__
     __syncthreads();
     for (int d = threadIdx.x; d < D; d += blockDim.x) {
         float acc = 0.0f;
-        for (int t = 0; t < T; ++t) acc = __fadd_rn(acc, __fmul_rn(sp[t], vh[(size_t)t * D + d]));
+        int t = 0;
+        for (; t + 32 <= T; t += 32) {                        // 32 positions' p and v ahead of the chain
+            float pv[32], vv[32];
+#pragma unroll
+            for (int u = 0; u < 32; ++u) {
+                pv[u] = sp[t + u];
+                vv[u] = vh[(size_t)(t + u) * D + d];
+            }
+#pragma unroll
+            for (int u = 0; u < 32; ++u) acc = __fadd_rn(acc, __fmul_rn(pv[u], vv[u]));
+        }
+        for (; t < T; ++t) acc = __fadd_rn(acc, __fmul_rn(sp[t], vh[(size_t)t * D + d]));
         ctx[(size_t)i * heads * D + (size_t)h * D + d] = acc;
     }
 }
@@ -302,7 +379,8 @@ NC_EXPORT int32_t nc_matmul_i8(void **p, const int64_t *s) {
     NC_REQUIRE(s[0] >= 0 && s[0] < 65536 && s[1] >= 0 && s[1] < (1 << 24) && s[2] > 0 && s[2] <= 16384,
                "nc_matmul_i8: bad shape (K at most 16384)");
     if (s[0] == 0 || s[1] == 0) return NC_OK;
-    hipLaunchKernelGGL(matmul_i8_f32, dim3((unsigned)((s[1] + 7) / 8), (unsigned)s[0]), dim3(64),
+    const auto kernel = s[2] == 896 ? matmul_i8_f32<7> : s[2] == 4864 ? matmul_i8_f32<38> : matmul_i8_f32<0>;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)((s[1] + 7) / 8), (unsigned)s[0]), dim3(64),
                        (size_t)s[2] * sizeof(float), nc::stream(), (float *)p[0], (const float *)p[1],
                        (const int8_t *)p[2], (const int8_t *)p[3], (const float *)p[4], (const float *)p[5],
                        (const float *)p[6], (int)s[0], (int)s[1], (int)s[2]);
@@ -320,7 +398,8 @@ NC_EXPORT int32_t nc_matmul_i8_vnni(void **p, const int64_t *s) {
                "nc_matmul_i8_vnni: bad shape (block a power of two >= 32 dividing K)");
     if (M == 0 || N == 0) return NC_OK;
     const size_t lds = (size_t)((K + 15) / 16) * 16 + (size_t)(K / block) * sizeof(float);
-    hipLaunchKernelGGL(matmul_i8_vnni, dim3((unsigned)((N + 7) / 8), (unsigned)M), dim3(64), lds, nc::stream(),
+    const auto kernel = K == 896 ? matmul_i8_vnni<7> : K == 4864 ? matmul_i8_vnni<38> : matmul_i8_vnni<0>;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)((N + 7) / 8), (unsigned)M), dim3(64), lds, nc::stream(),
                        (float *)p[0], (const int8_t *)p[1], (const float *)p[2], (const float *)p[3],
                        (const int8_t *)p[4], (const int8_t *)p[5], (const float *)p[6], (const float *)p[7],
                        (const float *)p[8], (int)M, (int)N, (int)K, (int)block);
