@@ -48,9 +48,27 @@ __global__ __launch_bounds__(64) void matmul_i8_f32(float *__restrict__ y, const
                                                     const int8_t *__restrict__ packed, const int8_t *__restrict__ q,
                                                     const float *__restrict__ scales, const float *__restrict__ bias,
                                                     const float *__restrict__ residual, int M, int N, int K) {
-    extern __shared__ float sx[];
+    extern __shared__ __align__(16) float sx[];
     const int m = blockIdx.y;
-    for (int i = threadIdx.x; i < K; i += 64) sx[i] = x[(size_t)m * K + i];
+    if constexpr (QUADS > 0) {
+        // K = 128 QUADS: the row in 16-byte pieces, QUADS / 2 a thread, all in flight at once
+        // (rows of x start at multiples of 512 bytes)
+        const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)m * K);
+        float4 *s4 = reinterpret_cast<float4 *>(sx);
+        float4 v[(32 * QUADS + 63) / 64];
+#pragma unroll
+        for (int u = 0; u < (32 * QUADS + 63) / 64; ++u) {
+            const int i = threadIdx.x + 64 * u;
+            if (i < 32 * QUADS) v[u] = x4[i];
+        }
+#pragma unroll
+        for (int u = 0; u < (32 * QUADS + 63) / 64; ++u) {
+            const int i = threadIdx.x + 64 * u;
+            if (i < 32 * QUADS) s4[i] = v[u];
+        }
+    } else {
+        for (int i = threadIdx.x; i < K; i += 64) sx[i] = x[(size_t)m * K + i];
+    }
     __syncthreads();
     const int lane = threadIdx.x, l = lane & 7;
     const int n = blockIdx.x * 8 + lane / 8;
@@ -207,18 +225,24 @@ __global__ __launch_bounds__(256) void quantize_blocks(int8_t *__restrict__ xq, 
 
 // The reference's rms_norm row kernel in its own order (nn.py:34-38, fusion.py:631-650): the
 // sum of squares in index order, one multiply and one add a step from 0, then
-// (x * (1 / sqrt(ss / K + eps))) * gamma. The row is staged in LDS and the one
-// chain runs in lane 0; every thread then writes its share of the row.
+// (x * (1 / sqrt(ss / K + eps))) * gamma. The row and its squares are staged in
+// LDS (every thread squaring its share: the same products), the one chain of adds
+// runs in lane 0, and every thread then writes its share of the row.
 // A serial chain over LDS (one thread's sum in index order) reads this many values ahead of its
 // steps, so it waits on LDS once a batch rather than once a step.
 constexpr int kChainBatch = 64;
 
 __global__ __launch_bounds__(256) void rms_norm_index_order(float *__restrict__ normed, const float *__restrict__ x,
                                                             const float *__restrict__ gamma, int K, float eps) {
-    extern __shared__ float srow[];
+    extern __shared__ float srow[];          // the row, then (from K on) its squares
     __shared__ float rcp_shared;
+    float *sq = srow + K;
     const float *row = x + (size_t)blockIdx.x * K;
-    for (int k = threadIdx.x; k < K; k += blockDim.x) srow[k] = row[k];
+    for (int k = threadIdx.x; k < K; k += blockDim.x) {
+        const float v = row[k];
+        srow[k] = v;
+        sq[k] = __fmul_rn(v, v);                 // every thread its squares; the chain only adds
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
         float ss = 0.0f;
@@ -226,11 +250,11 @@ __global__ __launch_bounds__(256) void rms_norm_index_order(float *__restrict__ 
         for (; k + kChainBatch <= K; k += kChainBatch) {       // a batch's reads ahead of its steps
             float v[kChainBatch];
 #pragma unroll
-            for (int u = 0; u < kChainBatch; ++u) v[u] = srow[k + u];
+            for (int u = 0; u < kChainBatch; ++u) v[u] = sq[k + u];
 #pragma unroll
-            for (int u = 0; u < kChainBatch; ++u) ss = __fadd_rn(ss, __fmul_rn(v[u], v[u]));
+            for (int u = 0; u < kChainBatch; ++u) ss = __fadd_rn(ss, v[u]);
         }
-        for (; k < K; ++k) ss = __fadd_rn(ss, __fmul_rn(srow[k], srow[k]));
+        for (; k < K; ++k) ss = __fadd_rn(ss, sq[k]);
         rcp_shared = nc::div_rn(1.0f, nc::sqrt_rn(__fadd_rn(nc::div_rn(ss, (float)K), eps)));
     }
     __syncthreads();
@@ -345,7 +369,16 @@ NC_EXPORT int32_t nc_rms_norm_index_order(void **p, const int64_t *s) {
     NC_REQUIRE(p && s && p[0] && p[1] && p[2], "nc_rms_norm_index_order: null operand");
     NC_REQUIRE(s[0] >= 0 && s[0] < (1 << 26) && s[1] > 0 && s[1] <= 16384, "nc_rms_norm_index_order: bad shape");
     if (s[0] == 0) return NC_OK;
-    hipLaunchKernelGGL(rms_norm_index_order, dim3((unsigned)s[0]), dim3(256), (size_t)s[1] * sizeof(float),
+    static bool raised = false;                  // the row and its squares: up to 128 KB of LDS
+    if (!raised) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&rms_norm_index_order),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 2 * 16384 * sizeof(float)) != hipSuccess) {
+            nc::set_message("nc_rms_norm_index_order: could not raise the LDS limit");
+            return NC_LAUNCH_FAILED;
+        }
+        raised = true;
+    }
+    hipLaunchKernelGGL(rms_norm_index_order, dim3((unsigned)s[0]), dim3(256), 2 * (size_t)s[1] * sizeof(float),
                        nc::stream(), (float *)p[0], (const float *)p[1], (const float *)p[2], (int)s[1],
                        nc::bits_to_float(s[2]));
     return nc::launched("rms_norm_index_order");
@@ -379,7 +412,11 @@ NC_EXPORT int32_t nc_matmul_i8(void **p, const int64_t *s) {
     NC_REQUIRE(s[0] >= 0 && s[0] < 65536 && s[1] >= 0 && s[1] < (1 << 24) && s[2] > 0 && s[2] <= 16384,
                "nc_matmul_i8: bad shape (K at most 16384)");
     if (s[0] == 0 || s[1] == 0) return NC_OK;
-    const auto kernel = s[2] == 896 ? matmul_i8_f32<7> : s[2] == 4864 ? matmul_i8_f32<38> : matmul_i8_f32<0>;
+    // the model's widths, x 16-byte aligned: the row staged in 16-byte pieces, each lane's weights ahead
+    const bool whole = ((uintptr_t)p[1] & 15) == 0;
+    const auto kernel = whole && s[2] == 896    ? matmul_i8_f32<7>
+                        : whole && s[2] == 4864 ? matmul_i8_f32<38>
+                                                : matmul_i8_f32<0>;
     hipLaunchKernelGGL(kernel, dim3((unsigned)((s[1] + 7) / 8), (unsigned)s[0]), dim3(64),
                        (size_t)s[2] * sizeof(float), nc::stream(), (float *)p[0], (const float *)p[1],
                        (const int8_t *)p[2], (const int8_t *)p[3], (const float *)p[4], (const float *)p[5],
