@@ -846,14 +846,17 @@ class Autotuner:
         return library, chosen
 
     @staticmethod
-    def _progress(kernel: int, total: int, every: int = 16):
-        """A ``measure`` progress callback that prints a line after every ``every`` samples (a
-        kernel whose candidates run for milliseconds each takes minutes to tune)."""
-        done = [0]
+    def _progress(kernel: int, total: int, seconds: float = 20.0):
+        """A ``measure`` progress callback that prints a line when a sample completes at least
+        ``seconds`` after the last line (a kernel whose candidates run for milliseconds each
+        takes minutes to tune; one that tunes in seconds prints nothing)."""
+        done, last = [0], [time.perf_counter()]
 
         def sampled() -> None:
             done[0] += 1
-            if done[0] % every == 0:
+            now = time.perf_counter()
+            if now - last[0] >= seconds:
+                last[0] = now
                 print(f"tuning kernel {kernel}: {done[0]} samples taken ({total} schedules)", file=sys.stderr,
                       flush=True)
         return sampled

@@ -192,6 +192,10 @@ __global__ __launch_bounds__(64) void matmul_i8_vnni(float *__restrict__ y, cons
     }
 }
 
+// A serial chain over LDS (one thread's sum in index order) reads this many values ahead of its
+// steps, so it waits on LDS once a batch rather than once a step.
+constexpr int kChainBatch = 64;
+
 // quantize.py:102-124: per block of `block` values, scale = max|x| / 127 (1 if
 // zero), xq = clamp(round(x / scale)); offset = 128 * sum over blocks, in
 // order, of f32(sum of the block's xq) * scale.
@@ -201,24 +205,63 @@ __global__ __launch_bounds__(256) void quantize_blocks(int8_t *__restrict__ xq, 
     extern __shared__ float terms[];                              // one per block
     const int m = blockIdx.x, nb = K / block;
     const float *row = x + (size_t)m * K;
-    for (int b = threadIdx.x; b < nb; b += 256) {
-        const float *v = row + (size_t)b * block;
-        float mag = 0.0f;
-        for (int i = 0; i < block; ++i) mag = nc::nan_max(mag, fabsf(v[i]));
-        const float scale = nc::token_scale(mag);
-        int32_t sum = 0;
-        for (int i = 0; i < block; ++i) {
-            const int8_t qv = nc::quantize_value(v[i], scale);
-            xq[(size_t)m * K + (size_t)b * block + i] = qv;
-            sum += qv;
+    if (block == 32) {
+        // a block of 32 on 32 lanes, an element a lane. The chain's maximum, mag = nan_max(mag,
+        // |v_i|) from 0 in index order, as an ordered tree: its step is associative (a NaN on
+        // the right wins, else one on the left, else the leftmost maximum), so lanes combined
+        // by xor butterfly with the lower lanes' block on the left, then one step from 0, give
+        // the chain's bits. Each lane quantizes its own element; the int32 sum is exact in any
+        // order.
+        const int lane = threadIdx.x & 31, group = threadIdx.x >> 5;
+        for (int b = group; b < nb; b += 8) {
+            const float v = row[(size_t)b * 32 + lane];
+            float mag = fabsf(v);
+#pragma unroll
+            for (int off = 1; off < 32; off <<= 1) {
+                const float other = __shfl_xor(mag, off, 32);
+                const bool left = (lane & off) == 0;
+                mag = nc::nan_max(left ? mag : other, left ? other : mag);
+            }
+            mag = nc::nan_max(0.0f, mag);
+            const float scale = nc::token_scale(mag);
+            const int8_t qv = nc::quantize_value(v, scale);
+            xq[(size_t)m * K + (size_t)b * 32 + lane] = qv;
+            int32_t sum = qv;
+#pragma unroll
+            for (int off = 1; off < 32; off <<= 1) sum += __shfl_xor(sum, off, 32);
+            if (lane == 0) {
+                xs[(size_t)m * nb + b] = scale;
+                terms[b] = __fmul_rn((float)sum, scale);
+            }
         }
-        xs[(size_t)m * nb + b] = scale;
-        terms[b] = __fmul_rn((float)sum, scale);
+    } else {
+        for (int b = threadIdx.x; b < nb; b += 256) {
+            const float *v = row + (size_t)b * block;
+            float mag = 0.0f;
+            for (int i = 0; i < block; ++i) mag = nc::nan_max(mag, fabsf(v[i]));
+            const float scale = nc::token_scale(mag);
+            int32_t sum = 0;
+            for (int i = 0; i < block; ++i) {
+                const int8_t qv = nc::quantize_value(v[i], scale);
+                xq[(size_t)m * K + (size_t)b * block + i] = qv;
+                sum += qv;
+            }
+            xs[(size_t)m * nb + b] = scale;
+            terms[b] = __fmul_rn((float)sum, scale);
+        }
     }
     __syncthreads();
     if (threadIdx.x == 0) {
         float total = 0.0f;
-        for (int b = 0; b < nb; ++b) total = __fadd_rn(total, terms[b]);
+        int b = 0;
+        for (; b + kChainBatch <= nb; b += kChainBatch) {
+            float t[kChainBatch];
+#pragma unroll
+            for (int u = 0; u < kChainBatch; ++u) t[u] = terms[b + u];
+#pragma unroll
+            for (int u = 0; u < kChainBatch; ++u) total = __fadd_rn(total, t[u]);
+        }
+        for (; b < nb; ++b) total = __fadd_rn(total, terms[b]);
         offset[m] = __fmul_rn(total, 128.0f);
     }
 }
@@ -228,10 +271,6 @@ __global__ __launch_bounds__(256) void quantize_blocks(int8_t *__restrict__ xq, 
 // (x * (1 / sqrt(ss / K + eps))) * gamma. The row and its squares are staged in
 // LDS (every thread squaring its share: the same products), the one chain of adds
 // runs in lane 0, and every thread then writes its share of the row.
-// A serial chain over LDS (one thread's sum in index order) reads this many values ahead of its
-// steps, so it waits on LDS once a batch rather than once a step.
-constexpr int kChainBatch = 64;
-
 __global__ __launch_bounds__(256) void rms_norm_index_order(float *__restrict__ normed, const float *__restrict__ x,
                                                             const float *__restrict__ gamma, int K, float eps) {
     extern __shared__ float srow[];          // the row, then (from K on) its squares

@@ -65,6 +65,31 @@ def test_block_quantizer_is_the_references(gpu, golden):
     assert np.array_equal(bits(off.numpy()), bits(golden["g3_quant_offset"][:, 0]))
 
 
+def test_block_quantizer_on_special_values(gpu):
+    """Blocks of 32 built to separate a block's maximum taken in another grouping or order:
+    +0 against -0, tied magnitudes of both signs, an infinity, subnormals, and (in the first
+    row) NaNs of two payloads and signs. The row without NaN is the oracle's bit for bit; in
+    the NaN row every other block is too, and the NaN block's scale is NaN and its values 127
+    (the grouping that keeps the NaN's bits is held by test_codegen.py's ordered-tree test)."""
+    from nanocompile_amd import kernels
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal((2, 32 * 6)).astype(np.float32)
+    blocks = x.reshape(2, 6, 32)
+    blocks[:, 1] = np.where(rng.random(32) < 0.5, np.float32(0.0), np.float32(-0.0))
+    blocks[:, 2, ::5] = 3.0
+    blocks[:, 2, 2::7] = -3.0
+    blocks[:, 3, 9] = np.inf
+    blocks[:, 4] = (rng.standard_normal(32) * 1e-39).astype(np.float32)        # subnormals
+    blocks[0, 5, 4] = np.uint32(0x7FC00001).view(np.float32)
+    blocks[0, 5, 20] = np.uint32(0xFFC00002).view(np.float32)
+    xq, xs, off = (a.numpy() for a in kernels.quantize_blocks(x, 32))
+    exq, exs, eoff = R.quantize_blocks(x, 32)
+    assert np.array_equal(xq[1], exq[1]) and np.array_equal(bits(xs[1]), bits(exs[1]))
+    assert np.array_equal(bits(off[1:]), bits(eoff[1:, 0]))
+    assert np.array_equal(xq[0, :160], exq[0, :160]) and np.array_equal(bits(xs[0, :5]), bits(exs[0, :5]))
+    assert np.isnan(xs[0, 5]) and np.all(xq[0, 160:] == 127) and np.isnan(off[0])
+
+
 @pytest.mark.parametrize("k,n,m", [(896, 896, 1), (4864, 896, 2), (896, 4864, 5), (128, 40, 3), (64, 8, 2)])
 def test_modes_at_model_shapes_match_the_host_restatement(gpu, host, k, n, m):
     """Model widths the golden set does not cover, with bias and residual epilogues."""
