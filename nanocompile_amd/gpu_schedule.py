@@ -998,6 +998,22 @@ def _reread_operands(s: "GpuSchedule") -> list[int]:
     return sorted(out)
 
 
+def _read_outside_hoisted(s: "GpuSchedule", param: int) -> bool:
+    """Whether operand ``param`` is read by a statement of the item that hoisting ``s`` (a lead
+    wave) leaves to the lead wave: outside every loop whose values all threads compute first.
+    True when nothing can be hoisted (the lead wave then reads everything)."""
+    trial = GpuSchedule(s.kernel, s.launch, list(s.steps))
+    try:
+        trial.lead().hoist()
+    except ScheduleError:
+        return True
+    body = trial.item_body()
+    serial = body[:-1] if trial.launch.cooperate else body
+    hoisted = {h.at for h in trial.launch.hoist}
+    rest = [st for at, st in enumerate(serial) if at not in hoisted] + list(body[len(serial):])
+    return any(kind(x) == "Load" and x.param == param for x in scalars(tuple(rest)))
+
+
 def apply(kernel, calls, config) -> tuple:
     """``kernel`` scheduled by ``config``: (kernel, Launch); ScheduleError if it does not apply.
 
@@ -1027,12 +1043,18 @@ def apply(kernel, calls, config) -> tuple:
             if rc and rc[0] >= WAVE and not dp4 and _reads_rows_by(kernel, param, inner, rc[1]):
                 s.pack(param, rc[0], rc[1], WAVE)
     if config.get("stage") or config.get("workgroup"):
-        for param in _reread_operands(s):
+        operands = _reread_operands(s)
+        # a workgroup item whose serial loops are all hoisted reads each operand once an element,
+        # in the pass every thread runs: a copy in LDS would only add a pass and a barrier
+        hoisted_only = cls == "item" and config.get("lead") and config.get("hoist")
+        if hoisted_only:
+            operands = [param for param in operands if _read_outside_hoisted(s, param)]
+        for param in operands:
             try:
                 s.stage(param)
             except ScheduleError:
                 continue
-        if not s.launch.stage:
+        if not s.launch.stage and not hoisted_only:
             raise ScheduleError("no operand of the item can be staged")
     if config.get("lead"):
         s.lead()

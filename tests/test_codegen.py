@@ -285,6 +285,24 @@ def test_staging_reaches_the_row_and_reduction_kernels():
     assert launch.stage == () and not any(type(x).__name__ == "Local" for x in gpu_schedule.scalars(plain.body))
 
 
+def test_hoisted_workgroup_item_stages_nothing_only_its_hoisted_pass_reads():
+    """P.V as a workgroup item with a lead wave and hoisting: the probabilities are read once an
+    element, in the pass every thread runs, so no window is copied to LDS first (a pass and a
+    barrier fewer); without hoisting the lead wave rereads them and they are staged."""
+    q = P.qwen2("int8", "last")
+    calls = _calls_of(q)
+    pv = next(i for i, k in enumerate(q.kernels)
+              if k.primitive == "matmul" and gpu_schedule._reduces_over_run_time_extent(k))
+    base = dict(gpu_schedule.DEFAULTS["item"], threads=128, workgroup=True, lead=True, unroll=16)
+    kernel, launch = gpu_schedule.apply(q.kernels[pv], calls[pv], dict(base, hoist=True))
+    assert launch.hoist and launch.stage == ()
+    src = codegen_hip.render_kernel(kernel, launch, pv)
+    body = src[:src.index("_unstaged")]
+    assert "nc_s1" not in body and body.count("__syncthreads();") == 3
+    _, unhoisted = gpu_schedule.apply(q.kernels[pv], calls[pv], base)
+    assert [st.param for st in unhoisted.stage] == [1]
+
+
 def test_stage_refuses_what_would_read_past_the_window():
     program = P.zoo("rms_norm_quant")
     row, reduce, quant = program.kernels[0], program.kernels[1], program.kernels[3]
