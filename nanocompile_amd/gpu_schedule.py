@@ -922,11 +922,11 @@ def shared_loop(kernel, names) -> str | None:
 # Each class's knobs and their values; the first value of each is the hand-written default's.
 SPACES: dict[str, dict[str, tuple]] = {
     # a workgroup per item sharing its write pass: its size, its serial loops' operands staged in
-    # LDS, iterations of the shared loop per thread, the serial loops' unroll (64: their operands
-    # read in batches of 64 iterations ahead of the chain), one lead wave on the serial part, its
-    # reductions' operands computed by every thread first
+    # LDS, iterations of the shared loop per thread, the serial loops' unroll (16, 64: their
+    # operands read in batches of that many iterations ahead of the chain), one lead wave on the
+    # serial part, its reductions' operands computed by every thread first
     "row": {"threads": (256, 64, 128, 512, 1024), "stage": (False, True), "vector": (1, 2, 4),
-            "unroll": (0, 4, 64), "lead": (False, True), "hoist": (False, True)},
+            "unroll": (0, 4, 16, 64), "lead": (False, True), "hoist": (False, True)},
     # a thread per item, or (workgroup) a workgroup per item with its loops' operands staged (a
     # lead wave, hoisting, as for rows), or (lanes) an item's accumulator chains 1 or 4 elements
     # a lane; weights packed in 64-row blocks or read row-major; serial loops unrolled up to 32
@@ -1116,6 +1116,9 @@ PREFERRED: dict[str, tuple] = {
         # wave on it, its operands computed by every thread first (hoisted) and read back in
         # batches of 64 ahead of the chain
         ("fixed-length reduction", dict(DEFAULTS["row"], threads=512, vector=4, unroll=64, lead=True, hoist=True)),
+        # one over a run-time length (softmax's sums over the context): the same, the row read from
+        # HBM by each pass (no staging) and the chain's operands read back in batches of 16
+        ("run-time reduction", dict(DEFAULTS["row"], threads=512, unroll=16, lead=True, hoist=True)),
         # row kernels: one lead wave on the row's reductions, their operands computed by every
         # thread first (hoisted), the row staged in LDS
         dict(DEFAULTS["row"], threads=512, stage=True, lead=True, hoist=True),
