@@ -273,15 +273,23 @@ __global__ __launch_bounds__(256) void quantize_blocks(int8_t *__restrict__ xq, 
 // runs in lane 0, and every thread then writes its share of the row.
 __global__ __launch_bounds__(256) void rms_norm_index_order(float *__restrict__ normed, const float *__restrict__ x,
                                                             const float *__restrict__ gamma, int K, float eps) {
-    extern __shared__ float srow[];          // the row, then (from K on) its squares
+    extern __shared__ __align__(16) float sq[];  // the row's squares
     __shared__ float rcp_shared;
-    float *sq = srow + K;
+    constexpr int kHeld = 4;                     // values a thread holds in registers (the rest re-read)
     const float *row = x + (size_t)blockIdx.x * K;
-    for (int k = threadIdx.x; k < K; k += blockDim.x) {
-        const float v = row[k];
-        srow[k] = v;
-        sq[k] = __fmul_rn(v, v);                 // every thread its squares; the chain only adds
+    float xv[kHeld], gv[kHeld];                  // every load issued before the first is waited on
+#pragma unroll
+    for (int j = 0; j < kHeld; ++j) {
+        const int k = threadIdx.x + j * blockDim.x;
+        xv[j] = k < K ? row[k] : 0.0f;
+        gv[j] = k < K ? gamma[k] : 0.0f;
     }
+#pragma unroll
+    for (int j = 0; j < kHeld; ++j) {
+        const int k = threadIdx.x + j * blockDim.x;
+        if (k < K) sq[k] = __fmul_rn(xv[j], xv[j]);   // every thread its squares; the chain only adds
+    }
+    for (int k = threadIdx.x + kHeld * blockDim.x; k < K; k += blockDim.x) sq[k] = __fmul_rn(row[k], row[k]);
     __syncthreads();
     if (threadIdx.x == 0) {
         float ss = 0.0f;
@@ -298,8 +306,14 @@ __global__ __launch_bounds__(256) void rms_norm_index_order(float *__restrict__ 
     }
     __syncthreads();
     const float rcp = rcp_shared;
-    for (int k = threadIdx.x; k < K; k += blockDim.x)
-        normed[(size_t)blockIdx.x * K + k] = __fmul_rn(__fmul_rn(srow[k], rcp), gamma[k]);
+    float *out = normed + (size_t)blockIdx.x * K;
+#pragma unroll
+    for (int j = 0; j < kHeld; ++j) {
+        const int k = threadIdx.x + j * blockDim.x;
+        if (k < K) out[k] = __fmul_rn(__fmul_rn(xv[j], rcp), gv[j]);
+    }
+    for (int k = threadIdx.x + kHeld * blockDim.x; k < K; k += blockDim.x)
+        out[k] = __fmul_rn(__fmul_rn(row[k], rcp), gamma[k]);
 }
 
 // The reference's attention for one query row and one head, in the order its graph states it
@@ -385,15 +399,25 @@ __global__ __launch_bounds__(256) void attention_index_order(float *__restrict__
     for (int d = threadIdx.x; d < D; d += blockDim.x) {
         float acc = 0.0f;
         int t = 0;
-        for (; t + 32 <= T; t += 32) {                        // 32 positions' p and v ahead of the chain
-            float pv[32], vv[32];
+        for (; t + 64 <= T; t += 64) {                        // 64 positions' p and v ahead of the chain
+            float pv[64], vv[64];
 #pragma unroll
-            for (int u = 0; u < 32; ++u) {
+            for (int u = 0; u < 64; ++u) {
                 pv[u] = sp[t + u];
                 vv[u] = vh[(size_t)(t + u) * D + d];
             }
 #pragma unroll
-            for (int u = 0; u < 32; ++u) acc = __fadd_rn(acc, __fmul_rn(pv[u], vv[u]));
+            for (int u = 0; u < 64; ++u) acc = __fadd_rn(acc, __fmul_rn(pv[u], vv[u]));
+        }
+        for (; t + 16 <= T; t += 16) {
+            float pv[16], vv[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                pv[u] = sp[t + u];
+                vv[u] = vh[(size_t)(t + u) * D + d];
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) acc = __fadd_rn(acc, __fmul_rn(pv[u], vv[u]));
         }
         for (; t < T; ++t) acc = __fadd_rn(acc, __fmul_rn(sp[t], vh[(size_t)t * D + d]));
         ctx[(size_t)i * heads * D + (size_t)h * D + d] = acc;
@@ -408,16 +432,16 @@ NC_EXPORT int32_t nc_rms_norm_index_order(void **p, const int64_t *s) {
     NC_REQUIRE(p && s && p[0] && p[1] && p[2], "nc_rms_norm_index_order: null operand");
     NC_REQUIRE(s[0] >= 0 && s[0] < (1 << 26) && s[1] > 0 && s[1] <= 16384, "nc_rms_norm_index_order: bad shape");
     if (s[0] == 0) return NC_OK;
-    static bool raised = false;                  // the row and its squares: up to 128 KB of LDS
+    static bool raised = false;                  // the row's squares: up to 64 KB of LDS beside the static
     if (!raised) {
         if (hipFuncSetAttribute(reinterpret_cast<const void *>(&rms_norm_index_order),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 2 * 16384 * sizeof(float)) != hipSuccess) {
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 16384 * sizeof(float)) != hipSuccess) {
             nc::set_message("nc_rms_norm_index_order: could not raise the LDS limit");
             return NC_LAUNCH_FAILED;
         }
         raised = true;
     }
-    hipLaunchKernelGGL(rms_norm_index_order, dim3((unsigned)s[0]), dim3(256), 2 * (size_t)s[1] * sizeof(float),
+    hipLaunchKernelGGL(rms_norm_index_order, dim3((unsigned)s[0]), dim3(256), (size_t)s[1] * sizeof(float),
                        nc::stream(), (float *)p[0], (const float *)p[1], (const float *)p[2], (int)s[1],
                        nc::bits_to_float(s[2]));
     return nc::launched("rms_norm_index_order");

@@ -116,7 +116,7 @@ def test_vnni_rejects_blocks_that_are_not_powers_of_two(gpu):
                                np.zeros((4, 96), np.int8), np.ones(4, np.float32), block=48)
 
 
-@pytest.mark.parametrize("m,k", [(1, 896), (3, 4864), (128, 896), (2, 128)])
+@pytest.mark.parametrize("m,k", [(1, 896), (3, 4864), (128, 896), (2, 128), (2, 1030), (1, 16384)])
 def test_rms_norm_index_order_is_the_references_order(gpu, m, k):
     """The reference modes' rms_norm: its row sum in index order (golden G4 pins the oracle)."""
     from nanocompile_amd import hip
@@ -134,7 +134,9 @@ def test_rms_norm_index_order_is_the_references_order(gpu, m, k):
 
 
 @pytest.mark.parametrize("m,past,heads,kv,d", [(1, 0, 14, 2, 64), (1, 383, 14, 2, 64), (7, 0, 14, 2, 64),
-                                               (5, 3, 4, 2, 32), (1, 12, 4, 2, 32), (128, 0, 14, 2, 64)])
+                                               (5, 3, 4, 2, 32), (1, 12, 4, 2, 32), (128, 0, 14, 2, 64),
+                                               (3, 300, 14, 2, 64), (2, 200, 4, 2, 128), (2, 700, 4, 2, 32),
+                                               (2, 40, 4, 2, 48)])
 def test_attention_index_order_is_the_oracle(gpu, host, m, past, heads, kv, d):
     """The reference modes' attention (every sum in the reference's order) bit for bit against the
     oracle, with the position given on the host and read from the device."""
