@@ -5,10 +5,12 @@
 // the reference's IR: 32 float accumulators, accumulator 8c + l fed by FMA
 // with element 32*k0 + 8c + l (or, for vnni, the Dp4 of bytes
 // 128*k0 + 32c + 4l .. +3 scaled by its block's scale), then one fixed tree.
-// Here a group of 8 lanes owns a weight row and lane l owns the four chains
-// 8c + l (c = 0..3), so every chain runs in its own order in one lane and the
-// tree's first level, (acc[l] + acc[8+l]) + (acc[16+l] + acc[24+l]), is local;
-// its last two levels are lane shuffles in the tree's order.
+// At the model's widths (K = 896, 4864) 32 lanes own a weight row and lane
+// 8c + l runs chain 8c + l alone, four waves a workgroup of 8 rows; at any
+// other K a group of 8 lanes owns a row and lane l the four chains 8c + l
+// (c = 0..3). Either way every chain runs in its own order in one lane and
+// the tree, (acc[l] + acc[8+l]) + (acc[16+l] + acc[24+l]), then h[j] + h[j+4],
+// then (u0 + u1) + (u2 + u3), is taken in its order through lane shuffles.
 //
 // Coalescing takes a repacked weight layout (the reference's pack idea,
 // schedule.py:362-395), made once per weight on the host side of the library:
@@ -39,69 +41,92 @@ __device__ __forceinline__ int8_t byte_of(const i8x16 &v, int i) {
     return (int8_t)((v.w[i >> 2] >> (8 * (i & 3))) & 0xff);
 }
 
-// y[m, n] = tree(acc) (+ tail) * scales[n], float activations x[m, :] staged in LDS.
-// QUADS > 0: K = 128 QUADS (the model's widths), a lane's whole packed row loaded before its
-// chains run (one memory round trip, where the run-time loop waits on each quad's load in
-// turn); 0: any K. The chains' order is the same either way.
+// The model's widths (K = 128 QUADS) with a chain a lane: 32 lanes a row, lane 8c + l running
+// accumulator 8c + l alone (elements 32 k0 + 8c + l, k0 in order), so a workgroup of 8 rows has
+// four waves where the four-chains-a-lane form has one; lane 8c + l takes byte 4 kk + c of group
+// l's 16-byte pieces (the four lanes of a group read the same piece). The tree's levels are
+// shuffles in the tree's order: h[l] = (acc[l] + acc[8+l]) + (acc[16+l] + acc[24+l]),
+// u[j] = h[j] + h[j+4], total = (u0 + u1) + (u2 + u3).
 template <int QUADS>
+__global__ __launch_bounds__(256) void matmul_i8_lanes(float *__restrict__ y, const float *__restrict__ x,
+                                                       const int8_t *__restrict__ packed,
+                                                       const float *__restrict__ scales, const float *__restrict__ bias,
+                                                       const float *__restrict__ residual, int N) {
+    constexpr int K = 128 * QUADS, PIECES = 32 * QUADS, PER = (PIECES + 255) / 256;
+    __shared__ __align__(16) float sx[K];
+    const int m = blockIdx.y;
+    {   // the row in 16-byte pieces, all in flight at once (rows of x start at multiples of 512 bytes)
+        const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)m * K);
+        float4 *s4 = reinterpret_cast<float4 *>(sx);
+        float4 v[PER];
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int i = threadIdx.x + 256 * u;
+            if (i < PIECES) v[u] = x4[i];
+        }
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int i = threadIdx.x + 256 * u;
+            if (i < PIECES) s4[i] = v[u];
+        }
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 31, c = lane >> 3, l = lane & 7;
+    const int n = blockIdx.x * 8 + (int)(threadIdx.x >> 5);
+    const bool valid = n < N;
+    const int8_t *prow = packed + (size_t)(valid ? n : 0) * QUADS * 128 + l * 16;
+    i8x16 w[QUADS];
+#pragma unroll
+    for (int j = 0; j < QUADS; ++j) w[j] = nc::load16(prow + (size_t)j * 128);
+    float a = 0.0f;
+#pragma unroll
+    for (int j = 0; j < QUADS; ++j) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const int8_t b = (int8_t)((w[j].w[kk] >> (8 * c)) & 0xff);
+            a = __builtin_fmaf((float)b, sx[32 * (4 * j + kk) + lane], a);
+        }
+    }
+    const float a8 = __shfl_down(a, 8, 32), a16 = __shfl_down(a, 16, 32), a24 = __shfl_down(a, 24, 32);
+    const float h = __fadd_rn(__fadd_rn(a, a8), __fadd_rn(a16, a24));       // lanes 0..7
+    const float u = __fadd_rn(h, __shfl_down(h, 4, 32));                     // lanes 0..3
+    const float u1 = __shfl_down(u, 1, 32), u2 = __shfl_down(u, 2, 32), u3 = __shfl_down(u, 3, 32);
+    const float sum = __fadd_rn(__fadd_rn(u, u1), __fadd_rn(u2, u3));        // lane 0
+    if (lane == 0 && valid) {
+        float v = __fmul_rn(sum, scales[n]);
+        const size_t o = (size_t)m * N + n;
+        if (bias) v = __fadd_rn(v, bias[n]);
+        if (residual) v = __fadd_rn(residual[o], v);
+        y[o] = v;
+    }
+}
+
+// y[m, n] = tree(acc) (+ tail) * scales[n], float activations x[m, :] staged in LDS: any K (the
+// model's widths take matmul_i8_lanes). The chains' order is the same either way.
 __global__ __launch_bounds__(64) void matmul_i8_f32(float *__restrict__ y, const float *__restrict__ x,
                                                     const int8_t *__restrict__ packed, const int8_t *__restrict__ q,
                                                     const float *__restrict__ scales, const float *__restrict__ bias,
                                                     const float *__restrict__ residual, int M, int N, int K) {
     extern __shared__ __align__(16) float sx[];
     const int m = blockIdx.y;
-    if constexpr (QUADS > 0) {
-        // K = 128 QUADS: the row in 16-byte pieces, QUADS / 2 a thread, all in flight at once
-        // (rows of x start at multiples of 512 bytes)
-        const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)m * K);
-        float4 *s4 = reinterpret_cast<float4 *>(sx);
-        float4 v[(32 * QUADS + 63) / 64];
-#pragma unroll
-        for (int u = 0; u < (32 * QUADS + 63) / 64; ++u) {
-            const int i = threadIdx.x + 64 * u;
-            if (i < 32 * QUADS) v[u] = x4[i];
-        }
-#pragma unroll
-        for (int u = 0; u < (32 * QUADS + 63) / 64; ++u) {
-            const int i = threadIdx.x + 64 * u;
-            if (i < 32 * QUADS) s4[i] = v[u];
-        }
-    } else {
-        for (int i = threadIdx.x; i < K; i += 64) sx[i] = x[(size_t)m * K + i];
-    }
+    for (int i = threadIdx.x; i < K; i += 64) sx[i] = x[(size_t)m * K + i];
     __syncthreads();
     const int lane = threadIdx.x, l = lane & 7;
     const int n = blockIdx.x * 8 + lane / 8;
     const bool valid = n < N;
     const int nr = valid ? n : 0;
-    const int blocks = K / 32, quads = QUADS > 0 ? QUADS : (blocks + 3) / 4;
+    const int blocks = K / 32, quads = (blocks + 3) / 4;
     const int8_t *prow = packed + (size_t)nr * quads * 128 + l * 16;
     float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if constexpr (QUADS > 0) {
-        i8x16 w[QUADS];
+    for (int j = 0; j < quads; ++j) {
+        const i8x16 w = nc::load16(prow + (size_t)j * 128);
 #pragma unroll
-        for (int j = 0; j < QUADS; ++j) w[j] = nc::load16(prow + (size_t)j * 128);
-#pragma unroll
-        for (int j = 0; j < QUADS; ++j) {
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                const int k0 = 4 * j + kk;
+        for (int kk = 0; kk < 4; ++kk) {
+            const int k0 = 4 * j + kk;
+            if (k0 < blocks) {
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
-                    a[c] = __builtin_fmaf((float)byte_of(w[j], kk * 4 + c), sx[32 * k0 + 8 * c + l], a[c]);
-            }
-        }
-    } else {
-        for (int j = 0; j < quads; ++j) {
-            const i8x16 w = nc::load16(prow + (size_t)j * 128);
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                const int k0 = 4 * j + kk;
-                if (k0 < blocks) {
-#pragma unroll
-                    for (int c = 0; c < 4; ++c)
-                        a[c] = __builtin_fmaf((float)byte_of(w, kk * 4 + c), sx[32 * k0 + 8 * c + l], a[c]);
-                }
+                    a[c] = __builtin_fmaf((float)byte_of(w, kk * 4 + c), sx[32 * k0 + 8 * c + l], a[c]);
             }
         }
     }
@@ -127,9 +152,7 @@ __device__ __forceinline__ int32_t dp4_offset(int32_t w, int32_t x) {
     return nc::dot4(w, x, 0) + 128 * nc::dot4(x, 0x01010101, 0);
 }
 
-// STRIDES > 0: K = 128 STRIDES, a lane's whole packed row loaded before its chains (as
-// matmul_i8_f32); 0: any K.
-template <int STRIDES>
+// Any K (the model's widths take matmul_i8_vnni_lanes).
 __global__ __launch_bounds__(64) void matmul_i8_vnni(float *__restrict__ y, const int8_t *__restrict__ xq,
                                                      const float *__restrict__ xs, const float *__restrict__ offset,
                                                      const int8_t *__restrict__ packed, const int8_t *__restrict__ q,
@@ -147,31 +170,16 @@ __global__ __launch_bounds__(64) void matmul_i8_vnni(float *__restrict__ y, cons
     const int n = blockIdx.x * 8 + lane / 8;
     const bool valid = n < N;
     const int nr = valid ? n : 0;
-    const int strides = STRIDES > 0 ? STRIDES : K / 128;
+    const int strides = K / 128;
     const int8_t *prow = packed + (size_t)nr * strides * 128 + l * 16;
     float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if constexpr (STRIDES > 0) {
-        i8x16 w[STRIDES];
+    for (int k0 = 0; k0 < strides; ++k0) {
+        const i8x16 w = nc::load16(prow + (size_t)k0 * 128);
 #pragma unroll
-        for (int k0 = 0; k0 < STRIDES; ++k0) w[k0] = nc::load16(prow + (size_t)k0 * 128);
-#pragma unroll
-        for (int k0 = 0; k0 < STRIDES; ++k0) {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int g = 128 * k0 + 32 * c;
-                const int32_t xd = *reinterpret_cast<const int32_t *>(sxq + g + 4 * l);
-                a[c] = __builtin_fmaf((float)dp4_offset(w[k0].w[c], xd), sxs[g / block], a[c]);
-            }
-        }
-    } else {
-        for (int k0 = 0; k0 < strides; ++k0) {
-            const i8x16 w = nc::load16(prow + (size_t)k0 * 128);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int g = 128 * k0 + 32 * c;
-                const int32_t xd = *reinterpret_cast<const int32_t *>(sxq + g + 4 * l);
-                a[c] = __builtin_fmaf((float)dp4_offset(w.w[c], xd), sxs[g / block], a[c]);
-            }
+        for (int c = 0; c < 4; ++c) {
+            const int g = 128 * k0 + 32 * c;
+            const int32_t xd = *reinterpret_cast<const int32_t *>(sxq + g + 4 * l);
+            a[c] = __builtin_fmaf((float)dp4_offset(w.w[c], xd), sxs[g / block], a[c]);
         }
     }
     const int groups = (K % 128) / 32;
@@ -184,6 +192,67 @@ __global__ __launch_bounds__(64) void matmul_i8_vnni(float *__restrict__ y, cons
     }
     const float sum = tree_of_chains(a[0], a[1], a[2], a[3]);
     if (l == 0 && valid) {
+        float v = __fmul_rn(__fsub_rn(sum, offset[m]), scales[n]);
+        const size_t o = (size_t)m * N + n;
+        if (bias) v = __fadd_rn(v, bias[n]);
+        if (residual) v = __fadd_rn(residual[o], v);
+        y[o] = v;
+    }
+}
+
+// The model's widths (K = 128 STRIDES) with a chain a lane, as matmul_i8_lanes: lane 8c + l runs
+// accumulator 8c + l (the Dp4 of bytes 128 k0 + 32c + 4l .. +3, k0 in order), reading its own
+// dword of each 128-byte packed piece, so a row's 32 lanes read the piece whole.
+template <int STRIDES>
+__global__ __launch_bounds__(256) void matmul_i8_vnni_lanes(float *__restrict__ y, const int8_t *__restrict__ xq,
+                                                            const float *__restrict__ xs,
+                                                            const float *__restrict__ offset,
+                                                            const int8_t *__restrict__ packed,
+                                                            const float *__restrict__ scales,
+                                                            const float *__restrict__ bias,
+                                                            const float *__restrict__ residual, int N, int shift) {
+    constexpr int K = 128 * STRIDES, PIECES = K / 16, PER = (PIECES + 255) / 256;
+    const int block = 1 << shift;                                // a power of two: g / block = g >> shift
+    __shared__ __align__(16) int8_t sxq[K];
+    __shared__ float sxs[K / 32];
+    const int m = blockIdx.y, nb = K / block;
+    {   // the row's bytes in 16-byte pieces, all in flight at once, and its block scales
+        const int4 *x16 = reinterpret_cast<const int4 *>(xq + (size_t)m * K);
+        int4 *s16 = reinterpret_cast<int4 *>(sxq);
+        int4 v[PER];
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int i = threadIdx.x + 256 * u;
+            if (i < PIECES) v[u] = x16[i];
+        }
+        for (int i = threadIdx.x; i < nb; i += 256) sxs[i] = xs[(size_t)m * nb + i];
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int i = threadIdx.x + 256 * u;
+            if (i < PIECES) s16[i] = v[u];
+        }
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 31, c = lane >> 3, l = lane & 7;
+    const int n = blockIdx.x * 8 + (int)(threadIdx.x >> 5);
+    const bool valid = n < N;
+    const int8_t *prow = packed + (size_t)(valid ? n : 0) * STRIDES * 128 + l * 16 + c * 4;
+    int32_t w[STRIDES];
+#pragma unroll
+    for (int k0 = 0; k0 < STRIDES; ++k0) w[k0] = *reinterpret_cast<const int32_t *>(prow + (size_t)k0 * 128);
+    float a = 0.0f;
+#pragma unroll
+    for (int k0 = 0; k0 < STRIDES; ++k0) {
+        const int g = 128 * k0 + 32 * c;
+        const int32_t xd = *reinterpret_cast<const int32_t *>(sxq + g + 4 * l);
+        a = __builtin_fmaf((float)dp4_offset(w[k0], xd), sxs[g >> shift], a);
+    }
+    const float a8 = __shfl_down(a, 8, 32), a16 = __shfl_down(a, 16, 32), a24 = __shfl_down(a, 24, 32);
+    const float h = __fadd_rn(__fadd_rn(a, a8), __fadd_rn(a16, a24));       // lanes 0..7
+    const float u = __fadd_rn(h, __shfl_down(h, 4, 32));                     // lanes 0..3
+    const float u1 = __shfl_down(u, 1, 32), u2 = __shfl_down(u, 2, 32), u3 = __shfl_down(u, 3, 32);
+    const float sum = __fadd_rn(__fadd_rn(u, u1), __fadd_rn(u2, u3));        // lane 0
+    if (lane == 0 && valid) {
         float v = __fmul_rn(__fsub_rn(sum, offset[m]), scales[n]);
         const size_t o = (size_t)m * N + n;
         if (bias) v = __fadd_rn(v, bias[n]);
@@ -213,8 +282,7 @@ __global__ __launch_bounds__(256) void quantize_blocks(int8_t *__restrict__ xq, 
         // the chain's bits. Each lane quantizes its own element; the int32 sum is exact in any
         // order.
         const int lane = threadIdx.x & 31, group = threadIdx.x >> 5;
-        for (int b = group; b < nb; b += 8) {
-            const float v = row[(size_t)b * 32 + lane];
+        auto one_block = [&](int b, float v) {
             float mag = fabsf(v);
 #pragma unroll
             for (int off = 1; off < 32; off <<= 1) {
@@ -233,7 +301,22 @@ __global__ __launch_bounds__(256) void quantize_blocks(int8_t *__restrict__ xq, 
                 xs[(size_t)m * nb + b] = scale;
                 terms[b] = __fmul_rn((float)sum, scale);
             }
+        };
+        // a group's blocks b = group + 8 i: the first kHeldBlocks loaded before any is waited on
+        // (K up to 5120 at once), the rest one after another
+        constexpr int kHeldBlocks = 20;
+        float held[kHeldBlocks];
+#pragma unroll
+        for (int i = 0; i < kHeldBlocks; ++i) {
+            const int b = group + 8 * i;
+            held[i] = b < nb ? row[(size_t)b * 32 + lane] : 0.0f;
         }
+#pragma unroll
+        for (int i = 0; i < kHeldBlocks; ++i) {
+            const int b = group + 8 * i;
+            if (b < nb) one_block(b, held[i]);
+        }
+        for (int b = group + 8 * kHeldBlocks; b < nb; b += 8) one_block(b, row[(size_t)b * 32 + lane]);
     } else {
         for (int b = threadIdx.x; b < nb; b += 256) {
             const float *v = row + (size_t)b * block;
@@ -475,12 +558,16 @@ NC_EXPORT int32_t nc_matmul_i8(void **p, const int64_t *s) {
     NC_REQUIRE(s[0] >= 0 && s[0] < 65536 && s[1] >= 0 && s[1] < (1 << 24) && s[2] > 0 && s[2] <= 16384,
                "nc_matmul_i8: bad shape (K at most 16384)");
     if (s[0] == 0 || s[1] == 0) return NC_OK;
-    // the model's widths, x 16-byte aligned: the row staged in 16-byte pieces, each lane's weights ahead
+    // the model's widths, x 16-byte aligned: a chain a lane, the row staged in 16-byte pieces
     const bool whole = ((uintptr_t)p[1] & 15) == 0;
-    const auto kernel = whole && s[2] == 896    ? matmul_i8_f32<7>
-                        : whole && s[2] == 4864 ? matmul_i8_f32<38>
-                                                : matmul_i8_f32<0>;
-    hipLaunchKernelGGL(kernel, dim3((unsigned)((s[1] + 7) / 8), (unsigned)s[0]), dim3(64),
+    if (whole && (s[2] == 896 || s[2] == 4864)) {
+        const auto kernel = s[2] == 896 ? matmul_i8_lanes<7> : matmul_i8_lanes<38>;
+        hipLaunchKernelGGL(kernel, dim3((unsigned)((s[1] + 7) / 8), (unsigned)s[0]), dim3(256), 0, nc::stream(),
+                           (float *)p[0], (const float *)p[1], (const int8_t *)p[2], (const float *)p[4],
+                           (const float *)p[5], (const float *)p[6], (int)s[1]);
+        return nc::launched("matmul_i8_lanes");
+    }
+    hipLaunchKernelGGL(matmul_i8_f32, dim3((unsigned)((s[1] + 7) / 8), (unsigned)s[0]), dim3(64),
                        (size_t)s[2] * sizeof(float), nc::stream(), (float *)p[0], (const float *)p[1],
                        (const int8_t *)p[2], (const int8_t *)p[3], (const float *)p[4], (const float *)p[5],
                        (const float *)p[6], (int)s[0], (int)s[1], (int)s[2]);
@@ -497,9 +584,17 @@ NC_EXPORT int32_t nc_matmul_i8_vnni(void **p, const int64_t *s) {
                    (block & (block - 1)) == 0 && K % block == 0,
                "nc_matmul_i8_vnni: bad shape (block a power of two >= 32 dividing K)");
     if (M == 0 || N == 0) return NC_OK;
+    // the model's widths, xq 16-byte aligned: a chain a lane, the row staged in 16-byte pieces
+    if (((uintptr_t)p[1] & 15) == 0 && (K == 896 || K == 4864)) {
+        const auto kernel = K == 896 ? matmul_i8_vnni_lanes<7> : matmul_i8_vnni_lanes<38>;
+        hipLaunchKernelGGL(kernel, dim3((unsigned)((N + 7) / 8), (unsigned)M), dim3(256), 0, nc::stream(),
+                           (float *)p[0], (const int8_t *)p[1], (const float *)p[2], (const float *)p[3],
+                           (const int8_t *)p[4], (const float *)p[6], (const float *)p[7], (const float *)p[8],
+                           (int)N, __builtin_ctzll((unsigned long long)block));
+        return nc::launched("matmul_i8_vnni_lanes");
+    }
     const size_t lds = (size_t)((K + 15) / 16) * 16 + (size_t)(K / block) * sizeof(float);
-    const auto kernel = K == 896 ? matmul_i8_vnni<7> : K == 4864 ? matmul_i8_vnni<38> : matmul_i8_vnni<0>;
-    hipLaunchKernelGGL(kernel, dim3((unsigned)((N + 7) / 8), (unsigned)M), dim3(64), lds, nc::stream(),
+    hipLaunchKernelGGL(matmul_i8_vnni, dim3((unsigned)((N + 7) / 8), (unsigned)M), dim3(64), lds, nc::stream(),
                        (float *)p[0], (const int8_t *)p[1], (const float *)p[2], (const float *)p[3],
                        (const int8_t *)p[4], (const int8_t *)p[5], (const float *)p[6], (const float *)p[7],
                        (const float *)p[8], (int)M, (int)N, (int)K, (int)block);

@@ -414,18 +414,22 @@ class Qwen2:
             self._project(w["o"], self.ctx, self.x, m, H, Q, residual=self.x)
             hip.call("nc_rms_norm_index_order", [self.normed, self.x, w["g2"]], [m, H, eps])
             self._project(w["gate"], self.normed, self.gate, m, I, H)
-            self._project(w["up"], self.normed, self.up, m, I, H)
+            self._project(w["up"], self.normed, self.up, m, I, H, quantized=True)
             hip.call("nc_silu_mul", [self.h, self.gate, self.up], [m * I])
             self._project(w["down"], self.h, self.x, m, H, I, residual=self.x)
 
-    def _project(self, weight, x, y, m: int, n: int, k: int, bias=None, residual=None) -> None:
+    def _project(self, weight, x, y, m: int, n: int, k: int, bias=None, residual=None,
+                 quantized: bool = False) -> None:
+        """One projection in the reference's mode; ``quantized``: int8-vnni's blocks of ``x`` are
+        those the previous call left (the same input: the up projection after the gate)."""
         q, s, packed = weight
         if self.quantization == "f32":        # the reference's float32 linear: k in order, then + bias
             hip.call("nc_lm_head", [y, None, x, packed, None, bias, residual], [m, n, k, 0])
         elif self.quantization == "int8":
             hip.call("nc_matmul_i8", [y, x, packed, q, s, bias, residual], [m, n, k])
         else:
-            hip.call("nc_quantize_blocks", [self.xq, self.xsb, self.xoff, x], [m, k, BLOCK])
+            if not quantized:
+                hip.call("nc_quantize_blocks", [self.xq, self.xsb, self.xoff, x], [m, k, BLOCK])
             hip.call("nc_matmul_i8_vnni", [y, self.xq, self.xsb, self.xoff, packed, q, s, bias, residual],
                      [m, n, k, BLOCK])
 

@@ -65,6 +65,24 @@ def test_block_quantizer_is_the_references(gpu, golden):
     assert np.array_equal(bits(off.numpy()), bits(golden["g3_quant_offset"][:, 0]))
 
 
+@pytest.mark.parametrize("m,k,block", [(1, 896, 32), (2, 4864, 32), (3, 5120, 32), (2, 6400, 32), (1, 16384, 32),
+                                       (2, 4864, 64)])
+def test_block_quantizer_at_every_width_is_the_oracle(gpu, m, k, block):
+    """Rows whose blocks a workgroup holds at once (up to 5120 values) and longer ones whose
+    later blocks it loads one after another, and blocks of 64: bit for bit with the oracle."""
+    from nanocompile_amd import kernels
+    print(f"quantize_blocks m={m} k={k} block={block}", flush=True)
+    rng = np.random.default_rng(k + m)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[rng.random(x.shape) < 0.01] *= 30
+    x[:, :block] = 0.0                                   # an all-zero block: scale 1
+    xq, xs, off = kernels.quantize_blocks(x, block)
+    eq, es, eoff = R.quantize_blocks(x, block)
+    assert np.array_equal(xq.numpy(), eq)
+    assert np.array_equal(bits(xs.numpy()), bits(es))
+    assert np.array_equal(bits(off.numpy()), bits(eoff[:, 0]))
+
+
 def test_block_quantizer_on_special_values(gpu):
     """Blocks of 32 built to separate a block's maximum taken in another grouping or order:
     +0 against -0, tied magnitudes of both signs, an infinity, subnormals, and (in the first
@@ -90,7 +108,8 @@ def test_block_quantizer_on_special_values(gpu):
     assert np.isnan(xs[0, 5]) and np.all(xq[0, 160:] == 127) and np.isnan(off[0])
 
 
-@pytest.mark.parametrize("k,n,m", [(896, 896, 1), (4864, 896, 2), (896, 4864, 5), (128, 40, 3), (64, 8, 2)])
+@pytest.mark.parametrize("k,n,m", [(896, 896, 1), (4864, 896, 2), (896, 4864, 5), (128, 40, 3), (64, 8, 2),
+                                   (896, 100, 2), (4864, 13, 1)])
 def test_modes_at_model_shapes_match_the_host_restatement(gpu, host, k, n, m):
     """Model widths the golden set does not cover, with bias and residual epilogues."""
     from nanocompile_amd import kernels
