@@ -58,17 +58,12 @@ __global__ __launch_bounds__(256) void matmul_i8_lanes(float *__restrict__ y, co
     {   // the row in 16-byte pieces, all in flight at once (rows of x start at multiples of 512 bytes)
         const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)m * K);
         float4 *s4 = reinterpret_cast<float4 *>(sx);
-        float4 v[PER];
+        float4 v[PER];                           // clamped reads: every load issued before any wait
 #pragma unroll
-        for (int u = 0; u < PER; ++u) {
-            const int i = threadIdx.x + 256 * u;
-            if (i < PIECES) v[u] = x4[i];
-        }
+        for (int u = 0; u < PER; ++u) v[u] = x4[min((int)threadIdx.x + 256 * u, PIECES - 1)];
 #pragma unroll
-        for (int u = 0; u < PER; ++u) {
-            const int i = threadIdx.x + 256 * u;
-            if (i < PIECES) s4[i] = v[u];
-        }
+        for (int u = 0; u < PER; ++u) s4[min((int)threadIdx.x + 256 * u, PIECES - 1)] = v[u];   // the last piece
+                                                                  // written again with its own value
     }
     __syncthreads();
     const int lane = threadIdx.x & 31, c = lane >> 3, l = lane & 7;
@@ -219,18 +214,14 @@ __global__ __launch_bounds__(256) void matmul_i8_vnni_lanes(float *__restrict__ 
     {   // the row's bytes in 16-byte pieces, all in flight at once, and its block scales
         const int4 *x16 = reinterpret_cast<const int4 *>(xq + (size_t)m * K);
         int4 *s16 = reinterpret_cast<int4 *>(sxq);
-        int4 v[PER];
+        int4 v[PER];                             // clamped reads: every load issued before any wait
 #pragma unroll
-        for (int u = 0; u < PER; ++u) {
-            const int i = threadIdx.x + 256 * u;
-            if (i < PIECES) v[u] = x16[i];
-        }
-        for (int i = threadIdx.x; i < nb; i += 256) sxs[i] = xs[(size_t)m * nb + i];
-#pragma unroll
-        for (int u = 0; u < PER; ++u) {
-            const int i = threadIdx.x + 256 * u;
-            if (i < PIECES) s16[i] = v[u];
-        }
+        for (int u = 0; u < PER; ++u) v[u] = x16[min((int)threadIdx.x + 256 * u, PIECES - 1)];
+        static_assert(K / 32 <= 256, "a block scale a thread");
+        const float sv = xs[(size_t)m * nb + min((int)threadIdx.x, nb - 1)];   // nb <= K / 32
+        sxs[min((int)threadIdx.x, nb - 1)] = sv;       // stores unconditional too (the last ones written
+#pragma unroll                                          // again with their own values), so no load sinks
+        for (int u = 0; u < PER; ++u) s16[min((int)threadIdx.x + 256 * u, PIECES - 1)] = v[u];
     }
     __syncthreads();
     const int lane = threadIdx.x & 31, c = lane >> 3, l = lane & 7;
@@ -309,10 +300,12 @@ __global__ __launch_bounds__(256) void quantize_blocks(int8_t *__restrict__ xq, 
 #pragma unroll
         for (int i = 0; i < kHeldBlocks; ++i) {
             const int b = group + 8 * i;
-            held[i] = b < nb ? row[(size_t)b * 32 + lane] : 0.0f;
+            held[i] = row[(size_t)min(b, nb - 1) * 32 + lane];     // clamped: no load waits on another
         }
 #pragma unroll
-        for (int i = 0; i < kHeldBlocks; ++i) {
+        for (int i = 0; i < kHeldBlocks; ++i) asm volatile("" : "+v"(held[i]));   // every value here before
+#pragma unroll                                                                   // any block runs, so no
+        for (int i = 0; i < kHeldBlocks; ++i) {                                  // load sinks into one
             const int b = group + 8 * i;
             if (b < nb) one_block(b, held[i]);
         }
@@ -364,8 +357,8 @@ __global__ __launch_bounds__(256) void rms_norm_index_order(float *__restrict__ 
 #pragma unroll
     for (int j = 0; j < kHeld; ++j) {
         const int k = threadIdx.x + j * blockDim.x;
-        xv[j] = k < K ? row[k] : 0.0f;
-        gv[j] = k < K ? gamma[k] : 0.0f;
+        xv[j] = row[min(k, K - 1)];              // clamped reads: no load waits on another
+        gv[j] = gamma[min(k, K - 1)];
     }
 #pragma unroll
     for (int j = 0; j < kHeld; ++j) {
