@@ -867,12 +867,13 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=NEW_TOKENS - 1)
     parser.add_argument("--warmup", type=int, default=1)
     parser.add_argument("--workload", choices=("decode", "gemv", "kernels", "generated", "generated5", "generated4",
-                                               "gemms"),
+                                               "gemms", "modes"),
                         default="decode",
                         help="kernels: each decode-step kernel launched eagerly at past 383 (for counter passes); "
                              "generated / generated5 / generated4: config 2's generated programs / config 5's generated "
                              "decode step, default and tuned, launched eagerly (for kernel traces); gemms: config 4's "
-                             "int8 GEMMs, every MFMA tile, against the vendor library's int8 GEMM")
+                             "int8 GEMMs, every MFMA tile, against the vendor library's int8 GEMM; modes: config 5 in "
+                             "the reference's int8 and int8-vnni modes alone (with --no-graph, launched eagerly)")
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-blocks", action="store_true", help="skip the per-block measurements (configs 2-4)")
     parser.add_argument("--no-graph", action="store_true",
@@ -917,6 +918,14 @@ def main() -> int:
     if args.workload == "kernels":
         print(json.dumps({"workload": "config 5's decode-step kernels, eager, past 383",
                           "kernels": decode_kernels()}), flush=True)
+        return 0
+    if args.workload == "modes":
+        from nanocompile_amd.models.config import QWEN25_05B, random_weights
+        weights = random_weights(QWEN25_05B, seed=0)
+        prompt = [int(t) for t in np.random.default_rng(1).integers(0, QWEN25_05B.vocab_size, PROMPT)]
+        print(json.dumps({"workload": "config 5 in the reference's own modes, 256 greedy tokens after the "
+                                      "128-token prompt" + (", eager" if args.no_graph else ""),
+                          **reference_modes(weights, prompt, 0, graph=not args.no_graph)}), flush=True)
         return 0
     g = gpu_gemv(20 if args.workload == "decode" else args.steps, 3)
     log(f"gemv: stacked {g['stacked_gbps']:.0f} GB/s, single {g['single_us']:.2f} us")
