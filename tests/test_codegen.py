@@ -298,7 +298,9 @@ def test_hoisted_workgroup_item_stages_nothing_only_its_hoisted_pass_reads():
     assert launch.hoist and launch.stage == ()
     src = codegen_hip.render_kernel(kernel, launch, pv)
     body = src[:src.index("_unstaged")]
-    assert "nc_s1" not in body and body.count("__syncthreads();") == 3
+    # two barriers an item: after the products pass, and before the next item's pass overwrites them
+    # (none before the pass: the lead wave hands it nothing)
+    assert "nc_s1" not in body and body.count("__syncthreads();") == 2
     _, unhoisted = gpu_schedule.apply(q.kernels[pv], calls[pv], base)
     assert [st.param for st in unhoisted.stage] == [1]
 
