@@ -174,6 +174,17 @@ int32_t nc_matmul_i8_token_swiglu(void **p, const int64_t *s);
  *     bias f32[N] or NULL, residual f32[M,N] or NULL];  s: [M, N, K] (K <= 16384) */
 int32_t nc_matmul_i8(void **p, const int64_t *s);
 
+/* rms_norm (nc_rms_norm_index_order, nn.py:34-38) of x's rows, then matmul_i8
+ * (as nc_matmul_i8, lower.py:298-360) of the normalized rows, in one launch: every
+ * workgroup normalizes its row the same way, so the result is bit for bit the two
+ * calls'; it saves the norm's launch and its round trip through memory. At the
+ * model's widths only (K 896 or 4864, x 16-byte aligned); y and residual must not
+ * be x.
+ * p: [y f32[M,N], x f32[M,K], packed i8, q i8[N,K], scales f32[N],
+ *     bias f32[N] or NULL, residual f32[M,N] or NULL, gamma f32[K]];
+ * s: [M, N, K, eps as float32 bits] */
+int32_t nc_matmul_i8_normed(void **p, const int64_t *s);
+
 /* matmul_i8_vnni: per-block int8 activations (xq, xs, offset from
  * nc_quantize_blocks) times int8 weights, each block's byte dots in the
  * reference's Dp4 order with its +128 offset (lower.py:363-397), the block

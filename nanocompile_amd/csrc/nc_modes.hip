@@ -41,18 +41,26 @@ __device__ __forceinline__ int8_t byte_of(const i8x16 &v, int i) {
     return (int8_t)((v.w[i >> 2] >> (8 * (i & 3))) & 0xff);
 }
 
+// A serial chain over LDS (one thread's sum in index order) reads this many values ahead of its
+// steps, so it waits on LDS once a batch rather than once a step.
+constexpr int kChainBatch = 64;
+
 // The model's widths (K = 128 QUADS) with a chain a lane: 32 lanes a row, lane 8c + l running
 // accumulator 8c + l alone (elements 32 k0 + 8c + l, k0 in order), so a workgroup of 8 rows has
 // four waves where the four-chains-a-lane form has one; lane 8c + l takes byte 4 kk + c of group
 // l's 16-byte pieces (the four lanes of a group read the same piece). The tree's levels are
 // shuffles in the tree's order: h[l] = (acc[l] + acc[8+l]) + (acc[16+l] + acc[24+l]),
 // u[j] = h[j] + h[j+4], total = (u0 + u1) + (u2 + u3).
+// gamma non-null: the row is first normalized as rms_norm_index_order does (every workgroup
+// the same sum of squares in index order, so the same bits), the norm's launch saved.
 template <int QUADS>
 __global__ __launch_bounds__(256) void matmul_i8_lanes(float *__restrict__ y, const float *__restrict__ x,
                                                        const int8_t *__restrict__ packed,
                                                        const float *__restrict__ scales, const float *__restrict__ bias,
-                                                       const float *__restrict__ residual, int N) {
+                                                       const float *__restrict__ residual, int N,
+                                                       const float *__restrict__ gamma, float eps) {
     constexpr int K = 128 * QUADS, PIECES = 32 * QUADS, PER = (PIECES + 255) / 256;
+    constexpr int GPER = (K + 255) / 256;
     __shared__ __align__(16) float sx[K];
     const int m = blockIdx.y;
     {   // the row in 16-byte pieces, all in flight at once (rows of x start at multiples of 512 bytes)
@@ -66,6 +74,44 @@ __global__ __launch_bounds__(256) void matmul_i8_lanes(float *__restrict__ y, co
                                                                   // written again with its own value
     }
     __syncthreads();
+    if (gamma) {
+        // rms_norm_index_order on the staged row: squares across the workgroup, the adds in
+        // index order in thread 0, then (x * (1 / sqrt(ss / K + eps))) * gamma
+        __shared__ __align__(16) float sq[K];
+        __shared__ float rcp_shared;
+        float gv[GPER];
+#pragma unroll
+        for (int j = 0; j < GPER; ++j) gv[j] = gamma[min((int)threadIdx.x + 256 * j, K - 1)];
+#pragma unroll
+        for (int j = 0; j < GPER; ++j) {
+            const int k = min((int)threadIdx.x + 256 * j, K - 1);
+            sq[k] = __fmul_rn(sx[k], sx[k]);
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float ss = 0.0f;
+            for (int k = 0; k < K; k += kChainBatch) {         // K is a multiple of the batch
+                float t[kChainBatch];
+#pragma unroll
+                for (int u = 0; u < kChainBatch; ++u) t[u] = sq[k + u];
+#pragma unroll
+                for (int u = 0; u < kChainBatch; ++u) ss = __fadd_rn(ss, t[u]);
+            }
+            rcp_shared = nc::div_rn(1.0f, nc::sqrt_rn(__fadd_rn(nc::div_rn(ss, (float)K), eps)));
+        }
+        __syncthreads();
+        const float rcp = rcp_shared;
+        float nv[GPER];
+#pragma unroll
+        for (int j = 0; j < GPER; ++j) {
+            const int k = min((int)threadIdx.x + 256 * j, K - 1);
+            nv[j] = __fmul_rn(__fmul_rn(sx[k], rcp), gv[j]);
+        }
+        __syncthreads();                                 // every read of the raw row before any write
+#pragma unroll
+        for (int j = 0; j < GPER; ++j) sx[min((int)threadIdx.x + 256 * j, K - 1)] = nv[j];
+        __syncthreads();
+    }
     const int lane = threadIdx.x & 31, c = lane >> 3, l = lane & 7;
     const int n = blockIdx.x * 8 + (int)(threadIdx.x >> 5);
     const bool valid = n < N;
@@ -252,9 +298,6 @@ __global__ __launch_bounds__(256) void matmul_i8_vnni_lanes(float *__restrict__ 
     }
 }
 
-// A serial chain over LDS (one thread's sum in index order) reads this many values ahead of its
-// steps, so it waits on LDS once a batch rather than once a step.
-constexpr int kChainBatch = 64;
 
 // quantize.py:102-124: per block of `block` values, scale = max|x| / 127 (1 if
 // zero), xq = clamp(round(x / scale)); offset = 128 * sum over blocks, in
@@ -557,7 +600,7 @@ NC_EXPORT int32_t nc_matmul_i8(void **p, const int64_t *s) {
         const auto kernel = s[2] == 896 ? matmul_i8_lanes<7> : matmul_i8_lanes<38>;
         hipLaunchKernelGGL(kernel, dim3((unsigned)((s[1] + 7) / 8), (unsigned)s[0]), dim3(256), 0, nc::stream(),
                            (float *)p[0], (const float *)p[1], (const int8_t *)p[2], (const float *)p[4],
-                           (const float *)p[5], (const float *)p[6], (int)s[1]);
+                           (const float *)p[5], (const float *)p[6], (int)s[1], (const float *)nullptr, 0.0f);
         return nc::launched("matmul_i8_lanes");
     }
     hipLaunchKernelGGL(matmul_i8_f32, dim3((unsigned)((s[1] + 7) / 8), (unsigned)s[0]), dim3(64),
@@ -565,6 +608,24 @@ NC_EXPORT int32_t nc_matmul_i8(void **p, const int64_t *s) {
                        (const int8_t *)p[2], (const int8_t *)p[3], (const float *)p[4], (const float *)p[5],
                        (const float *)p[6], (int)s[0], (int)s[1], (int)s[2]);
     return nc::launched("matmul_i8_f32");
+}
+
+// rms_norm_index_order then matmul_i8 in one launch, at the model's widths (x 16-byte aligned).
+// p: [y f32[M,N], x f32[M,K], packed i8, q i8[N,K], scales f32[N], bias | NULL, residual | NULL,
+//     gamma f32[K]];  s: [M, N, K, eps as float32 bits]
+NC_EXPORT int32_t nc_matmul_i8_normed(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3] && p[4] && p[7], "nc_matmul_i8_normed: null operand");
+    NC_REQUIRE(s[0] >= 0 && s[0] < 65536 && s[1] >= 0 && s[1] < (1 << 24) && (s[2] == 896 || s[2] == 4864) &&
+                   ((uintptr_t)p[1] & 15) == 0,
+               "nc_matmul_i8_normed: bad shape (K 896 or 4864, x 16-byte aligned)");
+    NC_REQUIRE(p[6] != p[1] && p[0] != p[1], "nc_matmul_i8_normed: y and the residual may not be x");
+    if (s[0] == 0 || s[1] == 0) return NC_OK;
+    const auto kernel = s[2] == 896 ? matmul_i8_lanes<7> : matmul_i8_lanes<38>;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)((s[1] + 7) / 8), (unsigned)s[0]), dim3(256), 0, nc::stream(),
+                       (float *)p[0], (const float *)p[1], (const int8_t *)p[2], (const float *)p[4],
+                       (const float *)p[5], (const float *)p[6], (int)s[1], (const float *)p[7],
+                       nc::bits_to_float(s[3]));
+    return nc::launched("matmul_i8_lanes (normed)");
 }
 
 // The reference's matmul_i8_vnni: y = (sum_b xs[b] * Dp4 sums - offset) * scales in its order.

@@ -405,8 +405,11 @@ class Qwen2:
         eps = float_bits(c.rms_norm_eps)
         for i, w in enumerate(self.layers):
             kc, vc = cache.layer(i)
-            hip.call("nc_rms_norm_index_order", [self.normed, self.x, w["g1"]], [m, H, eps])
-            self._project(w["qkv"], self.normed, self.qkv, m, W, H, bias=w["qkv_b"])
+            if self._fused_norm(H):                # the norm inside the projection: the same bits
+                self._project_normed(w["qkv"], w["g1"], self.qkv, m, W, H, eps, bias=w["qkv_b"])
+            else:
+                hip.call("nc_rms_norm_index_order", [self.normed, self.x, w["g1"]], [m, H, eps])
+                self._project(w["qkv"], self.normed, self.qkv, m, W, H, bias=w["qkv_b"])
             hip.call("nc_rope_append", [self.qkv, kc, vc, self.inv_freq, pos, cache.rope],
                      [m, heads, kv, D, past, cache.capacity])
             hip.call("nc_attention_index_order", [self.ctx, self.qkv, kc, vc, pos],
@@ -417,6 +420,18 @@ class Qwen2:
             self._project(w["up"], self.normed, self.up, m, I, H, quantized=True)
             hip.call("nc_silu_mul", [self.h, self.gate, self.up], [m * I])
             self._project(w["down"], self.h, self.x, m, H, I, residual=self.x)
+
+    def _fused_norm(self, k: int) -> bool:
+        """Whether int8 mode's qkv projection takes the first norm in (nc_matmul_i8_normed, the
+        model's widths; the residual stream is 256-byte aligned in the arena). Only there: its
+        144 workgroups repeat the norm's chain in one round, where the gate and up projections'
+        608 each would repeat it over several (measured slower)."""
+        return self.quantization == "int8" and k in (896, 4864)
+
+    def _project_normed(self, weight, gamma, y, m: int, n: int, k: int, eps: int, bias=None) -> None:
+        """rms_norm_index_order of the residual stream, then matmul_i8, in one launch."""
+        q, s, packed = weight
+        hip.call("nc_matmul_i8_normed", [y, self.x, packed, q, s, bias, None, gamma], [m, n, k, eps])
 
     def _project(self, weight, x, y, m: int, n: int, k: int, bias=None, residual=None,
                  quantized: bool = False) -> None:

@@ -179,3 +179,29 @@ def test_attention_index_order_is_the_oracle(gpu, host, m, past, heads, kv, d):
                  [m, heads, kv, d, 0 if where is not None else past, capacity, float_bits(scale)])
         hip.sync()
         assert np.array_equal(bits(ctx.numpy()), bits(want)), where is not None
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1152, 896), (3, 4864, 896), (2, 896, 4864), (5, 100, 896)])
+def test_matmul_i8_normed_is_the_norm_then_the_matmul(gpu, m, n, k):
+    """The int8 mode's fused rms_norm + matmul_i8 against the two calls, bit for bit."""
+    from nanocompile_amd import hip, kernels
+    from nanocompile_amd.hip import DeviceArray
+    from nanocompile_amd.kernels import float_bits
+    print(f"matmul_i8_normed m={m} n={n} k={k}", flush=True)
+    rng = np.random.default_rng(m * n + k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[rng.random(x.shape) < 0.01] *= 20
+    g = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    q, s = R.quantize_int8(w)
+    dx, dg = DeviceArray.from_host(x), DeviceArray.from_host(g)
+    normed = DeviceArray((m, k), np.float32)
+    hip.call("nc_rms_norm_index_order", [normed, dx, dg], [m, k, float_bits(1e-6)])
+    want = kernels.matmul_i8(normed, q, s, bias=b).numpy()
+    dq, ds, db = DeviceArray.from_host(q), DeviceArray.from_host(s), DeviceArray.from_host(b)
+    packed = DeviceArray.from_host(kernels.pack_chains(q))
+    y = DeviceArray((m, n), np.float32)
+    hip.call("nc_matmul_i8_normed", [y, dx, packed, dq, ds, db, None, dg], [m, n, k, float_bits(1e-6)])
+    hip.sync()
+    assert np.array_equal(bits(y.numpy()), bits(want))
