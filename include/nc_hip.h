@@ -200,6 +200,15 @@ int32_t nc_matmul_i8_vnni(void **p, const int64_t *s);
  * p: [xq i8[M,K], xs f32[M,K/block], offset f32[M], x f32[M,K]];  s: [M, K, block] */
 int32_t nc_quantize_blocks(void **p, const int64_t *s);
 
+/* rms_norm (nc_rms_norm_index_order, nn.py:34-38) of x's rows, then the block
+ * quantizer (as nc_quantize_blocks, quantize.py:102-124, blocks of 32) of the
+ * normalized rows, in one launch and one workgroup a row: bit for bit the two
+ * calls', the norm's launch and its round trip through memory saved (int8-vnni's
+ * norms feed nothing else).
+ * p: [xq i8[M,K], xs f32[M,K/32], offset f32[M], x f32[M,K], gamma f32[K]];
+ * s: [M, K, eps as float32 bits] (K a multiple of 64, at most 1024) */
+int32_t nc_quantize_blocks_normed(void **p, const int64_t *s);
+
 /* The reference's rms_norm in its own order (nn.py:34-38 as fusion.py:631-650
  * emits it: the row's sum of squares in index order), for the reference modes,
  * whose int8-vnni activations round after every norm and so need its bits.

@@ -299,6 +299,85 @@ __global__ __launch_bounds__(256) void matmul_i8_vnni_lanes(float *__restrict__ 
 }
 
 
+// One block of 32 on the 32 lanes of a group, lane `lane` holding element `lane` (v): the
+// block's maximum magnitude as an ordered tree of the chain's NaN-propagating step (see
+// quantize_blocks), the lane's element quantized, the int32 sum of the block's values (exact in
+// any order); lane 0 writes the scale and the block's term of the offset.
+__device__ __forceinline__ void block32(float v, int lane, int8_t *q_out, float *scale_out, float *term_out) {
+    float mag = fabsf(v);
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) {
+        const float other = __shfl_xor(mag, off, 32);
+        const bool left = (lane & off) == 0;
+        mag = nc::nan_max(left ? mag : other, left ? other : mag);
+    }
+    mag = nc::nan_max(0.0f, mag);
+    const float scale = nc::token_scale(mag);
+    const int8_t qv = nc::quantize_value(v, scale);
+    q_out[lane] = qv;
+    int32_t sum = qv;
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) sum += __shfl_xor(sum, off, 32);
+    if (lane == 0) {
+        *scale_out = scale;
+        *term_out = __fmul_rn((float)sum, scale);
+    }
+}
+
+// rms_norm_index_order of a row of K <= 1024 (a multiple of 64), then quantize_blocks of the
+// normalized row with blocks of 32, in one workgroup: the norm's bits (the sum of squares in
+// index order in thread 0, then (x * (1 / sqrt(ss / K + eps))) * gamma) and the quantizer's.
+__global__ __launch_bounds__(256) void quantize_blocks_normed(int8_t *__restrict__ xq, float *__restrict__ xs,
+                                                              float *__restrict__ offset, const float *__restrict__ x,
+                                                              const float *__restrict__ gamma, int K, float eps) {
+    extern __shared__ __align__(16) float nsmem[];           // the row's squares, then its normed values
+    float *nrow = nsmem, *terms = nsmem + K;                 // and a term per block
+    __shared__ float rcp_shared;
+    const int m = blockIdx.x, nb = K / 32;
+    const float *row = x + (size_t)m * K;
+    float xv[4], gv[4];                                      // clamped reads: all issued before any wait
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int k = min((int)threadIdx.x + 256 * j, K - 1);
+        xv[j] = row[k];
+        gv[j] = gamma[k];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int k = threadIdx.x + 256 * j;
+        if (k < K) nrow[k] = __fmul_rn(xv[j], xv[j]);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float ss = 0.0f;
+        for (int k = 0; k < K; k += kChainBatch) {
+            float t[kChainBatch];
+#pragma unroll
+            for (int u = 0; u < kChainBatch; ++u) t[u] = nrow[k + u];
+#pragma unroll
+            for (int u = 0; u < kChainBatch; ++u) ss = __fadd_rn(ss, t[u]);
+        }
+        rcp_shared = nc::div_rn(1.0f, nc::sqrt_rn(__fadd_rn(nc::div_rn(ss, (float)K), eps)));
+    }
+    __syncthreads();                                         // thread 0's reads of the squares are done
+    const float rcp = rcp_shared;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int k = threadIdx.x + 256 * j;
+        if (k < K) nrow[k] = __fmul_rn(__fmul_rn(xv[j], rcp), gv[j]);
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 31, group = threadIdx.x >> 5;
+    for (int b = group; b < nb; b += 8)
+        block32(nrow[b * 32 + lane], lane, xq + (size_t)m * K + (size_t)b * 32, xs + (size_t)m * nb + b, terms + b);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float total = 0.0f;
+        for (int b = 0; b < nb; ++b) total = __fadd_rn(total, terms[b]);
+        offset[m] = __fmul_rn(total, 128.0f);
+    }
+}
+
 // quantize.py:102-124: per block of `block` values, scale = max|x| / 127 (1 if
 // zero), xq = clamp(round(x / scale)); offset = 128 * sum over blocks, in
 // order, of f32(sum of the block's xq) * scale.
@@ -317,24 +396,7 @@ __global__ __launch_bounds__(256) void quantize_blocks(int8_t *__restrict__ xq, 
         // order.
         const int lane = threadIdx.x & 31, group = threadIdx.x >> 5;
         auto one_block = [&](int b, float v) {
-            float mag = fabsf(v);
-#pragma unroll
-            for (int off = 1; off < 32; off <<= 1) {
-                const float other = __shfl_xor(mag, off, 32);
-                const bool left = (lane & off) == 0;
-                mag = nc::nan_max(left ? mag : other, left ? other : mag);
-            }
-            mag = nc::nan_max(0.0f, mag);
-            const float scale = nc::token_scale(mag);
-            const int8_t qv = nc::quantize_value(v, scale);
-            xq[(size_t)m * K + (size_t)b * 32 + lane] = qv;
-            int32_t sum = qv;
-#pragma unroll
-            for (int off = 1; off < 32; off <<= 1) sum += __shfl_xor(sum, off, 32);
-            if (lane == 0) {
-                xs[(size_t)m * nb + b] = scale;
-                terms[b] = __fmul_rn((float)sum, scale);
-            }
+            block32(v, lane, xq + (size_t)m * K + (size_t)b * 32, xs + (size_t)m * nb + b, terms + b);
         };
         // a group's blocks b = group + 8 i: the first kHeldBlocks loaded before any is waited on
         // (K up to 5120 at once), the rest one after another
@@ -653,6 +715,19 @@ NC_EXPORT int32_t nc_matmul_i8_vnni(void **p, const int64_t *s) {
                        (const int8_t *)p[4], (const int8_t *)p[5], (const float *)p[6], (const float *)p[7],
                        (const float *)p[8], (int)M, (int)N, (int)K, (int)block);
     return nc::launched("matmul_i8_vnni");
+}
+
+// p: [xq i8[M,K], xs f32[M,K/32], offset f32[M], x f32[M,K], gamma f32[K]];
+// s: [M, K, eps as float32 bits] (K a multiple of 64, at most 1024; blocks of 32)
+NC_EXPORT int32_t nc_quantize_blocks_normed(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3] && p[4], "nc_quantize_blocks_normed: null operand");
+    NC_REQUIRE(s[0] >= 0 && s[0] < (1 << 30) && s[1] > 0 && s[1] <= 1024 && s[1] % 64 == 0,
+               "nc_quantize_blocks_normed: bad shape (K a multiple of 64, at most 1024)");
+    if (s[0] == 0) return NC_OK;
+    hipLaunchKernelGGL(quantize_blocks_normed, dim3((unsigned)s[0]), dim3(256),
+                       (size_t)(s[1] + s[1] / 32) * sizeof(float), nc::stream(), (int8_t *)p[0], (float *)p[1],
+                       (float *)p[2], (const float *)p[3], (const float *)p[4], (int)s[1], nc::bits_to_float(s[2]));
+    return nc::launched("quantize_blocks_normed");
 }
 
 // p: [xq i8[M,K], xs f32[M,K/block], offset f32[M], x f32[M,K]];  s: [M, K, block]

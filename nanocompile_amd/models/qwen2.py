@@ -407,6 +407,9 @@ class Qwen2:
             kc, vc = cache.layer(i)
             if self._fused_norm(H):                # the norm inside the projection: the same bits
                 self._project_normed(w["qkv"], w["g1"], self.qkv, m, W, H, eps, bias=w["qkv_b"])
+            elif self._normed_blocks(H):           # the norm inside the block quantizer: the same bits
+                hip.call("nc_quantize_blocks_normed", [self.xq, self.xsb, self.xoff, self.x, w["g1"]], [m, H, eps])
+                self._project(w["qkv"], None, self.qkv, m, W, H, bias=w["qkv_b"], quantized=True)
             else:
                 hip.call("nc_rms_norm_index_order", [self.normed, self.x, w["g1"]], [m, H, eps])
                 self._project(w["qkv"], self.normed, self.qkv, m, W, H, bias=w["qkv_b"])
@@ -415,8 +418,12 @@ class Qwen2:
             hip.call("nc_attention_index_order", [self.ctx, self.qkv, kc, vc, pos],
                      [m, heads, kv, D, past, cache.capacity, float_bits(self.scale)])
             self._project(w["o"], self.ctx, self.x, m, H, Q, residual=self.x)
-            hip.call("nc_rms_norm_index_order", [self.normed, self.x, w["g2"]], [m, H, eps])
-            self._project(w["gate"], self.normed, self.gate, m, I, H)
+            if self._normed_blocks(H):
+                hip.call("nc_quantize_blocks_normed", [self.xq, self.xsb, self.xoff, self.x, w["g2"]], [m, H, eps])
+                self._project(w["gate"], None, self.gate, m, I, H, quantized=True)
+            else:
+                hip.call("nc_rms_norm_index_order", [self.normed, self.x, w["g2"]], [m, H, eps])
+                self._project(w["gate"], self.normed, self.gate, m, I, H)
             self._project(w["up"], self.normed, self.up, m, I, H, quantized=True)
             hip.call("nc_silu_mul", [self.h, self.gate, self.up], [m * I])
             self._project(w["down"], self.h, self.x, m, H, I, residual=self.x)
@@ -427,6 +434,11 @@ class Qwen2:
         144 workgroups repeat the norm's chain in one round, where the gate and up projections'
         608 each would repeat it over several (measured slower)."""
         return self.quantization == "int8" and k in (896, 4864)
+
+    def _normed_blocks(self, k: int) -> bool:
+        """Whether int8-vnni's norms run inside the block quantizer that follows them
+        (nc_quantize_blocks_normed: one workgroup a row, so nothing is repeated)."""
+        return self.quantization == "int8-vnni" and k <= 1024 and k % 64 == 0
 
     def _project_normed(self, weight, gamma, y, m: int, n: int, k: int, eps: int, bias=None) -> None:
         """rms_norm_index_order of the residual stream, then matmul_i8, in one launch."""

@@ -205,3 +205,25 @@ def test_matmul_i8_normed_is_the_norm_then_the_matmul(gpu, m, n, k):
     hip.call("nc_matmul_i8_normed", [y, dx, packed, dq, ds, db, None, dg], [m, n, k, float_bits(1e-6)])
     hip.sync()
     assert np.array_equal(bits(y.numpy()), bits(want))
+
+
+@pytest.mark.parametrize("m,k", [(1, 896), (3, 896), (2, 1024), (4, 64)])
+def test_quantize_blocks_normed_is_the_norm_then_the_quantizer(gpu, m, k):
+    """int8-vnni's fused rms_norm + block quantizer against the two calls, bit for bit."""
+    from nanocompile_amd import hip, kernels
+    from nanocompile_amd.hip import DeviceArray
+    from nanocompile_amd.kernels import float_bits
+    print(f"quantize_blocks_normed m={m} k={k}", flush=True)
+    rng = np.random.default_rng(m * 7 + k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[rng.random(x.shape) < 0.01] *= 20
+    g = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    dx, dg = DeviceArray.from_host(x), DeviceArray.from_host(g)
+    normed = DeviceArray((m, k), np.float32)
+    hip.call("nc_rms_norm_index_order", [normed, dx, dg], [m, k, float_bits(1e-6)])
+    eq, es, eoff = (a.numpy() for a in kernels.quantize_blocks(normed, 32))
+    xq, xs, off = DeviceArray((m, k), np.int8), DeviceArray((m, k // 32), np.float32), DeviceArray((m,), np.float32)
+    hip.call("nc_quantize_blocks_normed", [xq, xs, off, dx, dg], [m, k, float_bits(1e-6)])
+    hip.sync()
+    assert np.array_equal(xq.numpy(), eq)
+    assert np.array_equal(bits(xs.numpy()), bits(es)) and np.array_equal(bits(off.numpy()), bits(eoff))
