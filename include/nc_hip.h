@@ -185,6 +185,13 @@ int32_t nc_matmul_i8(void **p, const int64_t *s);
  * s: [M, N, K, eps as float32 bits] */
 int32_t nc_matmul_i8_normed(void **p, const int64_t *s);
 
+/* The up projection with SwiGLU (nn.py:41-54, nc_silu_mul's operations) in its
+ * epilogue: h = silu(gate) * matmul_i8(x, up), bit for bit the two calls'. At the
+ * model's widths (K 896 or 4864, x 16-byte aligned; h not x).
+ * p: [h f32[M,N], x f32[M,K], packed i8, q i8[N,K], scales f32[N], gate f32[M,N]];
+ * s: [M, N, K] */
+int32_t nc_matmul_i8_silu(void **p, const int64_t *s);
+
 /* matmul_i8_vnni: per-block int8 activations (xq, xs, offset from
  * nc_quantize_blocks) times int8 weights, each block's byte dots in the
  * reference's Dp4 order with its +128 offset (lower.py:363-397), the block
@@ -193,6 +200,12 @@ int32_t nc_matmul_i8_normed(void **p, const int64_t *s);
  *     (pack_chains_vnni), q i8[N,K], scales f32[N], bias or NULL, residual or NULL];
  * s: [M, N, K, block] (block a power of two >= 32 dividing K) */
 int32_t nc_matmul_i8_vnni(void **p, const int64_t *s);
+
+/* matmul_i8_vnni of the up projection with SwiGLU in its epilogue, as
+ * nc_matmul_i8_silu (K 896 or 4864, xq 16-byte aligned).
+ * p: [h f32[M,N], xq i8[M,K], xs f32[M,K/block], offset f32[M], packed i8, q i8[N,K],
+ *     scales f32[N], gate f32[M,N]];  s: [M, N, K, block] */
+int32_t nc_matmul_i8_vnni_silu(void **p, const int64_t *s);
 
 /* The block activation quantizer of matmul_i8_vnni (quantize.py:102-124):
  * per block of K, xs = max|x| / 127 (1 for an all-zero block), xq = round(x / xs),

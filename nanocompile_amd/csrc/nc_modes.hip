@@ -21,6 +21,7 @@
 // Elements past the last whole 32-block (or 128-block) are read from the
 // plain row-major weights, in the reference's order.
 #include "nc_common.h"
+#include "nc_epilogue.h"
 #include "nc_math.h"
 
 namespace {
@@ -58,7 +59,8 @@ __global__ __launch_bounds__(256) void matmul_i8_lanes(float *__restrict__ y, co
                                                        const int8_t *__restrict__ packed,
                                                        const float *__restrict__ scales, const float *__restrict__ bias,
                                                        const float *__restrict__ residual, int N,
-                                                       const float *__restrict__ gamma, float eps) {
+                                                       const float *__restrict__ gamma, float eps,
+                                                       const float *__restrict__ gate) {
     constexpr int K = 128 * QUADS, PIECES = 32 * QUADS, PER = (PIECES + 255) / 256;
     constexpr int GPER = (K + 255) / 256;
     __shared__ __align__(16) float sx[K];
@@ -138,7 +140,7 @@ __global__ __launch_bounds__(256) void matmul_i8_lanes(float *__restrict__ y, co
         const size_t o = (size_t)m * N + n;
         if (bias) v = __fadd_rn(v, bias[n]);
         if (residual) v = __fadd_rn(residual[o], v);
-        y[o] = v;
+        y[o] = gate ? nc::silu_mul(gate[o], v) : v;               // the up projection: silu(gate) * up
     }
 }
 
@@ -251,7 +253,8 @@ __global__ __launch_bounds__(256) void matmul_i8_vnni_lanes(float *__restrict__ 
                                                             const int8_t *__restrict__ packed,
                                                             const float *__restrict__ scales,
                                                             const float *__restrict__ bias,
-                                                            const float *__restrict__ residual, int N, int shift) {
+                                                            const float *__restrict__ residual, int N, int shift,
+                                                            const float *__restrict__ gate) {
     constexpr int K = 128 * STRIDES, PIECES = K / 16, PER = (PIECES + 255) / 256;
     const int block = 1 << shift;                                // a power of two: g / block = g >> shift
     __shared__ __align__(16) int8_t sxq[K];
@@ -294,7 +297,7 @@ __global__ __launch_bounds__(256) void matmul_i8_vnni_lanes(float *__restrict__ 
         const size_t o = (size_t)m * N + n;
         if (bias) v = __fadd_rn(v, bias[n]);
         if (residual) v = __fadd_rn(residual[o], v);
-        y[o] = v;
+        y[o] = gate ? nc::silu_mul(gate[o], v) : v;               // the up projection: silu(gate) * up
     }
 }
 
@@ -662,7 +665,8 @@ NC_EXPORT int32_t nc_matmul_i8(void **p, const int64_t *s) {
         const auto kernel = s[2] == 896 ? matmul_i8_lanes<7> : matmul_i8_lanes<38>;
         hipLaunchKernelGGL(kernel, dim3((unsigned)((s[1] + 7) / 8), (unsigned)s[0]), dim3(256), 0, nc::stream(),
                            (float *)p[0], (const float *)p[1], (const int8_t *)p[2], (const float *)p[4],
-                           (const float *)p[5], (const float *)p[6], (int)s[1], (const float *)nullptr, 0.0f);
+                           (const float *)p[5], (const float *)p[6], (int)s[1], (const float *)nullptr, 0.0f,
+                           (const float *)nullptr);
         return nc::launched("matmul_i8_lanes");
     }
     hipLaunchKernelGGL(matmul_i8_f32, dim3((unsigned)((s[1] + 7) / 8), (unsigned)s[0]), dim3(64),
@@ -686,8 +690,25 @@ NC_EXPORT int32_t nc_matmul_i8_normed(void **p, const int64_t *s) {
     hipLaunchKernelGGL(kernel, dim3((unsigned)((s[1] + 7) / 8), (unsigned)s[0]), dim3(256), 0, nc::stream(),
                        (float *)p[0], (const float *)p[1], (const int8_t *)p[2], (const float *)p[4],
                        (const float *)p[5], (const float *)p[6], (int)s[1], (const float *)p[7],
-                       nc::bits_to_float(s[3]));
+                       nc::bits_to_float(s[3]), (const float *)nullptr);
     return nc::launched("matmul_i8_lanes (normed)");
+}
+
+// matmul_i8 of the up projection with SwiGLU in its epilogue: h = silu(gate) * (x @ up.T),
+// nc_silu_mul's operations on the projection's value (the model's widths, x 16-byte aligned).
+// p: [h f32[M,N], x f32[M,K], packed i8, q i8[N,K], scales f32[N], gate f32[M,N]];  s: [M, N, K]
+NC_EXPORT int32_t nc_matmul_i8_silu(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3] && p[4] && p[5], "nc_matmul_i8_silu: null operand");
+    NC_REQUIRE(s[0] >= 0 && s[0] < 65536 && s[1] >= 0 && s[1] < (1 << 24) && (s[2] == 896 || s[2] == 4864) &&
+                   ((uintptr_t)p[1] & 15) == 0 && p[0] != p[1],
+               "nc_matmul_i8_silu: bad shape (K 896 or 4864, x 16-byte aligned, h not x)");
+    if (s[0] == 0 || s[1] == 0) return NC_OK;
+    const auto kernel = s[2] == 896 ? matmul_i8_lanes<7> : matmul_i8_lanes<38>;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)((s[1] + 7) / 8), (unsigned)s[0]), dim3(256), 0, nc::stream(),
+                       (float *)p[0], (const float *)p[1], (const int8_t *)p[2], (const float *)p[4],
+                       (const float *)nullptr, (const float *)nullptr, (int)s[1], (const float *)nullptr, 0.0f,
+                       (const float *)p[5]);
+    return nc::launched("matmul_i8_lanes (silu)");
 }
 
 // The reference's matmul_i8_vnni: y = (sum_b xs[b] * Dp4 sums - offset) * scales in its order.
@@ -706,7 +727,7 @@ NC_EXPORT int32_t nc_matmul_i8_vnni(void **p, const int64_t *s) {
         hipLaunchKernelGGL(kernel, dim3((unsigned)((N + 7) / 8), (unsigned)M), dim3(256), 0, nc::stream(),
                            (float *)p[0], (const int8_t *)p[1], (const float *)p[2], (const float *)p[3],
                            (const int8_t *)p[4], (const float *)p[6], (const float *)p[7], (const float *)p[8],
-                           (int)N, __builtin_ctzll((unsigned long long)block));
+                           (int)N, __builtin_ctzll((unsigned long long)block), (const float *)nullptr);
         return nc::launched("matmul_i8_vnni_lanes");
     }
     const size_t lds = (size_t)((K + 15) / 16) * 16 + (size_t)(K / block) * sizeof(float);
@@ -715,6 +736,25 @@ NC_EXPORT int32_t nc_matmul_i8_vnni(void **p, const int64_t *s) {
                        (const int8_t *)p[4], (const int8_t *)p[5], (const float *)p[6], (const float *)p[7],
                        (const float *)p[8], (int)M, (int)N, (int)K, (int)block);
     return nc::launched("matmul_i8_vnni");
+}
+
+// matmul_i8_vnni of the up projection with SwiGLU in its epilogue (as nc_matmul_i8_silu).
+// p: [h f32[M,N], xq i8[M,K], xs f32[M,K/block], offset f32[M], packed i8, q i8[N,K], scales f32[N],
+//     gate f32[M,N]];  s: [M, N, K, block] (K 896 or 4864, xq 16-byte aligned)
+NC_EXPORT int32_t nc_matmul_i8_vnni_silu(void **p, const int64_t *s) {
+    NC_REQUIRE(p && s && p[0] && p[1] && p[2] && p[3] && p[4] && p[5] && p[6] && p[7],
+               "nc_matmul_i8_vnni_silu: null operand");
+    const int64_t M = s[0], N = s[1], K = s[2], block = s[3];
+    NC_REQUIRE(M >= 0 && M < 65536 && N >= 0 && N < (1 << 24) && (K == 896 || K == 4864) && block >= 32 &&
+                   (block & (block - 1)) == 0 && K % block == 0 && ((uintptr_t)p[1] & 15) == 0,
+               "nc_matmul_i8_vnni_silu: bad shape (K 896 or 4864, block a power of two >= 32 dividing K)");
+    if (M == 0 || N == 0) return NC_OK;
+    const auto kernel = K == 896 ? matmul_i8_vnni_lanes<7> : matmul_i8_vnni_lanes<38>;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)((N + 7) / 8), (unsigned)M), dim3(256), 0, nc::stream(),
+                       (float *)p[0], (const int8_t *)p[1], (const float *)p[2], (const float *)p[3],
+                       (const int8_t *)p[4], (const float *)p[6], (const float *)nullptr, (const float *)nullptr,
+                       (int)N, __builtin_ctzll((unsigned long long)block), (const float *)p[7]);
+    return nc::launched("matmul_i8_vnni_lanes (silu)");
 }
 
 // p: [xq i8[M,K], xs f32[M,K/32], offset f32[M], x f32[M,K], gamma f32[K]];

@@ -424,8 +424,16 @@ class Qwen2:
             else:
                 hip.call("nc_rms_norm_index_order", [self.normed, self.x, w["g2"]], [m, H, eps])
                 self._project(w["gate"], self.normed, self.gate, m, I, H)
-            self._project(w["up"], self.normed, self.up, m, I, H, quantized=True)
-            hip.call("nc_silu_mul", [self.h, self.gate, self.up], [m * I])
+            if self._silu_epilogue(H):               # SwiGLU in the up projection's epilogue: the same bits
+                q, s, packed = w["up"]
+                if self.quantization == "int8":
+                    hip.call("nc_matmul_i8_silu", [self.h, self.normed, packed, q, s, self.gate], [m, I, H])
+                else:
+                    hip.call("nc_matmul_i8_vnni_silu", [self.h, self.xq, self.xsb, self.xoff, packed, q, s,
+                                                        self.gate], [m, I, H, BLOCK])
+            else:
+                self._project(w["up"], self.normed, self.up, m, I, H, quantized=True)
+                hip.call("nc_silu_mul", [self.h, self.gate, self.up], [m * I])
             self._project(w["down"], self.h, self.x, m, H, I, residual=self.x)
 
     def _fused_norm(self, k: int) -> bool:
@@ -434,6 +442,11 @@ class Qwen2:
         144 workgroups repeat the norm's chain in one round, where the gate and up projections'
         608 each would repeat it over several (measured slower)."""
         return self.quantization == "int8" and k in (896, 4864)
+
+    def _silu_epilogue(self, k: int) -> bool:
+        """Whether the reference modes' up projection applies SwiGLU in its epilogue
+        (nc_matmul_i8_silu, nc_matmul_i8_vnni_silu: the model's widths)."""
+        return self.quantization in ("int8", "int8-vnni") and k in (896, 4864)
 
     def _normed_blocks(self, k: int) -> bool:
         """Whether int8-vnni's norms run inside the block quantizer that follows them

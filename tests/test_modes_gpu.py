@@ -227,3 +227,35 @@ def test_quantize_blocks_normed_is_the_norm_then_the_quantizer(gpu, m, k):
     hip.sync()
     assert np.array_equal(xq.numpy(), eq)
     assert np.array_equal(bits(xs.numpy()), bits(es)) and np.array_equal(bits(off.numpy()), bits(eoff))
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 4864, 896), (3, 100, 896), (2, 896, 4864)])
+def test_up_projection_with_swiglu_is_the_projection_then_silu_mul(gpu, m, n, k):
+    """The reference modes' up projection with silu(gate) * up in its epilogue, int8 and
+    int8-vnni, against the projection then nc_silu_mul, bit for bit."""
+    from nanocompile_amd import hip, kernels
+    from nanocompile_amd.hip import DeviceArray
+    print(f"matmul_i8(_vnni)_silu m={m} n={n} k={k}", flush=True)
+    rng = np.random.default_rng(m + n + k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    gate = (rng.standard_normal((m, n)) * 3).astype(np.float32)
+    gate[0, :4] = [0.0, -0.0, 80.0, -80.0]
+    q, s = R.quantize_int8(w)
+    dx, dq, ds, dgate = (DeviceArray.from_host(a) for a in (x, q, s, gate))
+    for mode in ("int8", "int8-vnni"):
+        if mode == "int8":
+            up = kernels.matmul_i8(x, q, s)
+            packed = DeviceArray.from_host(kernels.pack_chains(q))
+            h = DeviceArray((m, n), np.float32)
+            hip.call("nc_matmul_i8_silu", [h, dx, packed, dq, ds, dgate], [m, n, k])
+        else:
+            xq, xs, off = kernels.quantize_blocks(x, 32)
+            up = kernels.matmul_i8_vnni(xq, xs, off, q, s, 32)
+            packed = DeviceArray.from_host(kernels.pack_chains_vnni(q))
+            h = DeviceArray((m, n), np.float32)
+            hip.call("nc_matmul_i8_vnni_silu", [h, xq, xs, off, packed, dq, ds, dgate], [m, n, k, 32])
+        want = DeviceArray((m, n), np.float32)
+        hip.call("nc_silu_mul", [want, dgate, up], [m * n])
+        hip.sync()
+        assert np.array_equal(bits(h.numpy()), bits(want.numpy())), mode
