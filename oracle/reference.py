@@ -104,7 +104,8 @@ def quantize_blocks(x: np.ndarray, block: int = 32) -> tuple[np.ndarray, np.ndar
     groups = x.reshape(lead + (blocks, block))
     magnitude = np.max(np.where(F32(0) <= groups, groups, -groups), axis=-1)
     scale = np.where(magnitude <= 0, F32(1.0), (magnitude / F32(INT8_MAX)).astype(F32)).astype(F32)
-    rounded = round_half_away((groups / scale[..., None]).astype(F32))
+    with np.errstate(invalid="ignore"):            # a NaN block's scale is NaN: its values, as C's
+        rounded = round_half_away((groups / scale[..., None]).astype(F32))
     values = clamp_int8(rounded)
     block_sums = values.astype(np.int32).sum(-1).astype(F32)
     terms = (block_sums * scale).astype(F32)
